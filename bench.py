@@ -1,0 +1,310 @@
+"""Scattered H2D gather benchmark on one MI355X.
+
+Workload (one "step"): gather 8192 tokens x 4 KiB (32 MiB) scattered at 2x
+stride in pinned host memory, in a seeded random order, into one contiguous
+HBM buffer.  Also measured in the same run: 2048 x 64 KiB (KV-cache pages),
+2048 x {512 B, 1 KiB, 2 KiB}, the contiguous-copy link peak, per-token
+hipMemcpyAsync, and the CPU ParallelGather restatement on the host cores.
+Timing: W warm-up + K timed iterations, P50 (examples/04_benchmark.cu:58-90).
+GB/s = bytes / (us * 1e3).
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 15] [--only zc|direct|...]
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import gfd_amd  # noqa: E402
+
+PCIE_GEN5_X16_GBPS = 32.0 * 16 * 128.0 / 130.0 / 8.0  # 63.0 GB/s per direction
+METRIC = "scattered H2D GB/s + % of PCIe5 x16 peak at 8192x4KB and 2048x64KB"
+PD = ctypes.POINTER(ctypes.c_double)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def p50(x):
+    return float(np.percentile(np.asarray(x, dtype=np.float64), 50))
+
+
+def gbps(nbytes, us):
+    return nbytes / (us * 1e3) if us > 0 else 0.0
+
+
+class Layout:
+    """n tokens of t bytes at 2t stride in pinned host memory, seeded order."""
+
+    def __init__(self, oracle, n, t, flags=gfd_amd.HOST_DEFAULT):
+        self.n, self.t, self.stride = n, t, 2 * t
+        self.bytes = n * t
+        self.host = gfd_amd.HostBuffer(n * self.stride, flags)
+        oracle.fill_tokens(self.host.array, n, t, self.stride)
+        self.perm = oracle.permutation(n)
+        self.expected = oracle.expected_gather(self.host.array, self.perm, t, self.stride)
+        self.src_addrs = np.uint64(self.host.ptr) + self.perm.astype(np.uint64) * np.uint64(self.stride)
+        self.dst = gfd_amd.DeviceBuffer(self.bytes)
+        self.table = gfd_amd.DeviceBuffer(n * 8)
+        self.table.upload(self.src_addrs)
+        self.entries = gfd_amd.make_entries(self.src_addrs, self.dst.ptr, t)
+        tok = np.zeros((n, 2), np.uint64)
+        tok[:, 0] = self.src_addrs
+        tok[:, 1] = np.arange(n, dtype=np.uint64)
+        self.tokens = gfd_amd.DeviceBuffer(tok.nbytes)
+        self.tokens.upload(tok)
+
+    def verify(self, what):
+        self.dst_ok = bool((self.dst.download() == self.expected).all())
+        if not self.dst_ok:
+            raise SystemExit("PARITY FAILURE: %s (%d x %d)" % (what, self.n, self.t))
+        self.dst.fill(0)
+        return True
+
+
+def host_info():
+    import platform
+
+    info = {"logical_cpus": os.cpu_count(), "allowed_cpus": len(os.sched_getaffinity(0))}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                info["cpu_model"] = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        info["numa_nodes"] = open("/sys/devices/system/node/online").read().strip()
+    except OSError:
+        pass
+    info["machine"] = platform.machine()
+    return info
+
+
+def cpu_baseline(oracle, seconds, info):
+    """The reference CPU ParallelGather restated (oracle/oracle.c), timed on
+    this host's cores: 8192 x 4 KiB into a pinned staging buffer."""
+    allowed = sorted(os.sched_getaffinity(0))
+    workers = max(0, min(15, len(allowed) - 1))
+    cpus = allowed[:workers + 1]
+    n, t = 8192, 4096
+    src = gfd_amd.HostBuffer(n * 2 * t)
+    oracle.fill_tokens(src.array, n, t, 2 * t)
+    perm = oracle.permutation(n)
+    staging = gfd_amd.HostBuffer(n * t)
+    entries = oracle.make_entries(src.ptr, 0, perm, t, 2 * t)
+    pool = oracle.GatherPool(workers, cpus)
+    try:
+        pool.gather(entries, n, staging.array, 0)
+        if not (staging.array == oracle.expected_gather(src.array, perm, t, 2 * t)).all():
+            raise SystemExit("PARITY FAILURE: CPU baseline")
+        times = []
+        t_end = time.time() + seconds
+        while time.time() < t_end:
+            times.extend(pool.time(entries, n, staging.array, 0, 20).tolist())
+    finally:
+        pool.close()
+        os.sched_setaffinity(0, allowed)
+    us = p50(times)
+    return {
+        "value": round(gbps(n * t, us), 3), "unit": "GB/s", "cores": workers + 1, "kind": "port",
+        "sample": "8192 x 4KiB ParallelGather into pinned staging, %d iterations (%.0f s), P50 %.1f us, "
+                  "W=%d workers + caller on CPUs %s, AVX-512=%s" % (
+                      len(times), seconds, us, workers, cpus, oracle.has_avx512()),
+    }
+
+
+def bench_peak(nbytes, iters, warmup):
+    src = gfd_amd.HostBuffer(nbytes)
+    src.array[:] = 1
+    dst = gfd_amd.DeviceBuffer(nbytes)
+    out = {}
+    for ns in (1, 4):
+        t = np.zeros(iters)
+        rc = gfd_amd.lib().gfd_bench_memcpy_contiguous(dst.ptr, src.ptr, nbytes, ns, warmup, iters,
+                                                       t.ctypes.data_as(PD))
+        assert rc == 0, gfd_amd.lib().gfd_last_error()
+        out["%d_stream" % ns] = round(gbps(nbytes, p50(t)), 3)
+    return out
+
+
+def run_zero_copy(L, iters, warmup):
+    wall = np.zeros(iters)
+    ev = np.zeros(iters)
+    rc = gfd_amd.lib().gfd_bench_zero_copy_tokens(L.table.ptr, L.dst.ptr, L.t, L.n, warmup, iters,
+                                                  wall.ctypes.data_as(PD), ev.ctypes.data_as(PD))
+    assert rc == 0, gfd_amd.lib().gfd_last_error()
+    L.verify("zero-copy")
+    return {"us_p50": round(p50(wall), 2), "GBps": round(gbps(L.bytes, p50(wall)), 3),
+            "kernel_us_mean": round(float(ev.mean()), 2), "kernel_us_p50": round(p50(ev), 2),
+            "kernel_GBps": round(gbps(L.bytes, float(ev.mean())), 3)}
+
+
+def run_direct(poller, L, iters, warmup):
+    t = np.zeros(iters)
+    rc = gfd_amd.lib().gfd_bench_submit_direct(poller._h, ctypes.cast(L.entries, ctypes.c_void_p), L.n, warmup,
+                                               iters, t.ctypes.data_as(PD))
+    assert rc == 0, gfd_amd.lib().gfd_last_error()
+    L.verify("direct")
+    return {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3)}
+
+
+def run_memcpy_n(L, iters, warmup):
+    t = np.zeros(iters)
+    rc = gfd_amd.lib().gfd_bench_memcpy_per_token(L.dst.ptr, L.src_addrs.ctypes.data, L.n, L.t, warmup, iters,
+                                                  t.ctypes.data_as(PD))
+    assert rc == 0, gfd_amd.lib().gfd_last_error()
+    L.verify("memcpy per token")
+    return {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3)}
+
+
+class QueueRig:
+    def __init__(self, region_bytes):
+        self.q = gfd_amd.DescriptorQueue()
+        self.p = gfd_amd.CpuPollingThread(self.q, None, None, region_bytes, numa_node=-1)
+        assert self.p.init_copy_engine(), "queue poller init failed"
+        self.p.start()
+        self.base = ctypes.c_uint64(0)
+
+    def run(self, L, iters, warmup):
+        t = np.zeros(iters)
+        rc = gfd_amd.lib().gfd_bench_queue(self.q.ptr, L.tokens.ptr, L.dst.ptr, L.n, L.t, ctypes.byref(self.base),
+                                           warmup, iters, 10_000_000, t.ctypes.data_as(PD))
+        assert rc == 0, gfd_amd.lib().gfd_last_error()
+        L.verify("queue")
+        return {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3)}
+
+    def close(self):
+        self.p.stop()
+        self.p.close()
+        self.q.free()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=15)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", default="", help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this path has no multi-GPU step (each GPU gathers over its own "
+              "PCIe link); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    only = set(x for x in args.only.split(",") if x)
+    want = (lambda k: not only or k in only)
+    K, W = args.steps, args.warmup
+
+    import oracle
+
+    info = host_info()
+    log("host:", info)
+    result = {}
+    cpu = None
+    if want("cpu") and args.cpu_seconds > 0:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(oracle, args.cpu_seconds, info)
+        log("cpu baseline:", cpu)
+
+    assert gfd_amd.device_count() > 0, "no GPU visible"
+    gfd_amd.lib().gfd_set_device(0)
+
+    peak = {}
+    if want("peak"):
+        log("contiguous peak ...")
+        peak = bench_peak(128 << 20, K, W)
+        log("peak:", peak)
+    peak_meas = max(peak.values()) if peak else None
+
+    main_cfg = (8192, 4096)
+    kv_cfg = (2048, 65536)
+    small = [(2048, 512), (2048, 1024), (2048, 2048)]
+    region_max = 2048 * 65536 * 2
+    direct = gfd_amd.CpuPollingThread(None, None, None, region_max, numa_node=-1)
+    assert direct.init_direct_ce(), "init_direct_ce failed"
+    dinfo = direct.info()
+    log("direct poller:", dinfo)
+    queue = QueueRig(region_max) if want("queue") else None
+
+    def run_cfg(n, t, methods):
+        L = Layout(oracle, n, t)
+        r = {"tokens": n, "token_bytes": t, "bytes": L.bytes}
+        if "zc" in methods and want("zc"):
+            r["zero_copy"] = run_zero_copy(L, K, W)
+            log("  %dx%d zero-copy: %s" % (n, t, r["zero_copy"]))
+        if "direct" in methods and want("direct"):
+            r["direct"] = run_direct(direct, L, K, W)
+            log("  %dx%d direct: %s" % (n, t, r["direct"]))
+        if "queue" in methods and queue is not None:
+            r["queue"] = queue.run(L, K, W)
+            log("  %dx%d queue: %s" % (n, t, r["queue"]))
+        if "memcpy" in methods and want("memcpy"):
+            r["memcpy_per_token"] = run_memcpy_n(L, max(5, K // 5), 2)
+            log("  %dx%d memcpy(N): %s" % (n, t, r["memcpy_per_token"]))
+        del L
+        return r
+
+    allm = ("zc", "direct", "queue", "memcpy")
+    log("8192 x 4KB ...")
+    r_main = run_cfg(*main_cfg, allm)
+    r_kv = run_cfg(*kv_cfg, allm) if want("kv") else None
+    r_small = [run_cfg(n, t, allm) for n, t in small] if want("small") else []
+    if queue:
+        queue.close()
+    direct.close()
+
+    def frac(v):
+        return {"of_theoretical": round(v / PCIE_GEN5_X16_GBPS, 4),
+                "of_measured": round(v / peak_meas, 4) if peak_meas else None}
+
+    head = r_main.get("direct") or r_main.get("zero_copy") or {}
+    value = head.get("GBps", 0.0)
+    zc = r_main.get("zero_copy")
+    roofline = None
+    if zc:
+        ach = zc["kernel_GBps"]
+        roofline = {"bound": "pcie", "kernel": "zc_gather_tokens16", "achieved": ach,
+                    "peak": round(PCIE_GEN5_X16_GBPS, 2), "unit": "GB/s",
+                    "frac": round(ach / PCIE_GEN5_X16_GBPS, 4), "traffic": None,
+                    "peak_measured": peak_meas,
+                    "frac_of_measured": round(ach / peak_meas, 4) if peak_meas else None,
+                    "algorithmic_bytes_per_launch": r_main["bytes"],
+                    "hbm_write_GBps": ach, "hbm_write_frac": round(ach / 8000.0, 5)}
+    for r in [r_main, r_kv] + r_small:
+        if not r:
+            continue
+        for k in ("zero_copy", "direct", "queue", "memcpy_per_token"):
+            if k in r:
+                r[k].update(frac(r[k]["GBps"]))
+    result = {
+        "metric": METRIC, "value": round(value, 3), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(head.get("us_p50", 0.0) / 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic: xorshift64 token bytes (seed 0x9E3779B97F4A7C15), 2x stride, 0xEE gaps, "
+                "Fisher-Yates order (seed 0xD1B54A32D192ED03); every method's output memcmp-checked",
+        "config": {"workload": "GFD Direct (CpuPollingThread::submit_direct): 8192 x 4KiB scattered pinned-host "
+                               "tokens -> contiguous HBM (32 MiB), P50 of %d" % K,
+                   "tokens": 8192, "token_bytes": 4096, "stride": "2x", "parallelism": "single GPU"},
+        "pcie_peak": {"theoretical_GBps": round(PCIE_GEN5_X16_GBPS, 2), "measured_contiguous_GBps": peak},
+        "roofline": roofline, "cpu_baseline": cpu,
+        "results_8192x4KB": r_main, "results_2048x64KB": r_kv, "results_small": r_small,
+        "direct_setup": {k: dinfo[k] for k in ("numa_node", "num_gather_workers", "worker_cpus", "poller_cpu",
+                                               "num_ce_channels", "direct_chunk_bytes", "gather_slice_bytes")},
+        "host": info,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

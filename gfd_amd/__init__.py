@@ -1,0 +1,371 @@
+"""gfd_amd — MI355X-native GFD: scattered host-to-HBM gather.
+
+Python mirror of the reference's host API (``include/gfd/cpu_polling.h``,
+``include/gfd/staging_pool.h``), bound over the C-ABI in
+``include/gfd_capi.h`` (``libgfd_amd.so``).  The library must be built
+(``python -m gfd_amd.builder``); importing this package without it raises
+ImportError — there is no CPU fallback.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgfd_amd.so")
+
+__all__ = [
+    "lib", "SGEntry", "HostBuffer", "DeviceBuffer", "CpuPollingThread", "StagingPool",
+    "DescriptorQueue", "zero_copy_gather_tokens", "zero_copy_gather", "GfdError",
+    "HOST_DEFAULT", "HOST_COHERENT", "HOST_NONCOHERENT", "HOST_NUMA_USER", "QUEUE_SIZE",
+]
+
+HOST_DEFAULT, HOST_COHERENT, HOST_NONCOHERENT, HOST_NUMA_USER = 0, 1, 2, 4
+QUEUE_SIZE = 16384
+MAX_BATCH_SIZE = 8192
+BATCH_THRESHOLD = 4096
+BATCH_THRESHOLD_SMALL = 1024
+FLAG_LAST_IN_BATCH, FLAG_URGENT, FLAG_LAST_IN_TILE, FLAG_LAST_CHUNK_IN_TILE = 1, 2, 4, 8
+
+
+class GfdError(RuntimeError):
+    pass
+
+
+class SGEntry(ctypes.Structure):
+    """gfd_sg_entry / gfd::SGEntry: 24 bytes {u64 dst, u64 src, u64 size}."""
+
+    _fields_ = [("dst", ctypes.c_uint64), ("src", ctypes.c_uint64), ("size", ctypes.c_uint64)]
+
+
+class TokenInfo(ctypes.Structure):
+    _fields_ = [("cpu_addr", ctypes.c_uint64), ("token_id", ctypes.c_uint32), ("expert_id", ctypes.c_uint32)]
+
+
+class PollerStats(ctypes.Structure):
+    _fields_ = [
+        ("descriptors_processed", ctypes.c_uint64), ("batches_submitted", ctypes.c_uint64),
+        ("coalesced_entries", ctypes.c_uint64), ("staging_batches", ctypes.c_uint64),
+        ("total_bytes_copied", ctypes.c_double), ("gather_us", ctypes.c_uint64),
+        ("dma_wait_us", ctypes.c_uint64), ("dma_submit_us", ctypes.c_uint64),
+        ("queue_read_us", ctypes.c_uint64),
+    ]
+
+
+class PollerInfo(ctypes.Structure):
+    _fields_ = [
+        ("device", ctypes.c_int), ("numa_node", ctypes.c_int), ("num_gather_workers", ctypes.c_int),
+        ("poller_cpu", ctypes.c_int), ("worker_cpus", ctypes.c_int * 16), ("num_ce_channels", ctypes.c_int),
+        ("num_staging_buffers", ctypes.c_int), ("staging_buffer_size", ctypes.c_uint64),
+        ("direct_chunk_bytes", ctypes.c_uint64), ("gather_slice_bytes", ctypes.c_uint64),
+    ]
+
+
+_lib = None
+_SIGNATURES = {}
+
+
+def _declare(L):
+    c_int, c_u32, c_u64, c_sz, vp, c_dbl = (ctypes.c_int, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_size_t,
+                                             ctypes.c_void_p, ctypes.c_double)
+    pvp = ctypes.POINTER(ctypes.c_void_p)
+    pd = ctypes.POINTER(ctypes.c_double)
+    sig = {
+        "gfd_version": ([], ctypes.c_char_p),
+        "gfd_last_error": ([], ctypes.c_char_p),
+        "gfd_device_count": ([ctypes.POINTER(c_int)], c_int),
+        "gfd_set_device": ([c_int], c_int),
+        "gfd_device_synchronize": ([], c_int),
+        "gfd_host_alloc": ([pvp, c_sz, ctypes.c_uint], c_int),
+        "gfd_host_free": ([vp], c_int),
+        "gfd_device_alloc": ([pvp, c_sz], c_int),
+        "gfd_device_free": ([vp], c_int),
+        "gfd_memcpy_h2d": ([vp, vp, c_sz], c_int),
+        "gfd_memcpy_d2h": ([vp, vp, c_sz], c_int),
+        "gfd_memset_device": ([vp, c_int, c_sz], c_int),
+        "gfd_stream_create": ([pvp], c_int),
+        "gfd_stream_destroy": ([vp], c_int),
+        "gfd_stream_synchronize": ([vp], c_int),
+        "gfd_event_create": ([pvp], c_int),
+        "gfd_event_destroy": ([vp], c_int),
+        "gfd_event_record": ([vp, vp], c_int),
+        "gfd_event_synchronize": ([vp], c_int),
+        "gfd_event_elapsed_ms": ([ctypes.POINTER(ctypes.c_float), vp, vp], c_int),
+        "gfd_poller_create": ([vp, vp, vp, c_sz, c_int, c_int, c_int, c_int, c_int, c_int], vp),
+        "gfd_poller_destroy": ([vp], None),
+        "gfd_poller_init_copy_engine": ([vp], c_int),
+        "gfd_poller_init_direct_ce": ([vp], c_int),
+        "gfd_poller_submit_direct": ([vp, vp, c_int], c_dbl),
+        "gfd_poller_set_tiled_queue": ([vp, vp], None),
+        "gfd_poller_set_sg_task_queue": ([vp, vp], None),
+        "gfd_poller_start": ([vp], None),
+        "gfd_poller_stop": ([vp], None),
+        "gfd_poller_get_stats": ([vp, ctypes.POINTER(PollerStats)], c_int),
+        "gfd_poller_reset_stats": ([vp], None),
+        "gfd_poller_get_info": ([vp, ctypes.POINTER(PollerInfo)], c_int),
+        "gfd_poller_set_direct_chunk_bytes": ([vp, c_u64], None),
+        "gfd_poller_set_gather_slice_bytes": ([vp, c_u64], None),
+        "gfd_host_gather": ([vp, c_int, vp, c_u64, c_u64, c_int, vp], c_int),
+        "gfd_staging_pool_init": ([c_int, c_sz, c_int], c_int),
+        "gfd_staging_pool_shutdown": ([], None),
+        "gfd_zero_copy_gather_tokens": ([vp, vp, c_u32, c_int, vp], c_int),
+        "gfd_zero_copy_gather": ([vp, c_int, vp], c_int),
+        "gfd_queue_alloc": ([pvp], c_int),
+        "gfd_queue_free": ([vp], c_int),
+        "gfd_queue_submit_tokens": ([vp, vp, vp, c_int, c_u32, c_u64, vp], c_int),
+        "gfd_queue_wait": ([vp, c_u64, c_u64, vp, vp], c_int),
+        "gfd_bench_memcpy_per_token": ([vp, vp, c_int, c_u32, c_int, c_int, pd], c_int),
+        "gfd_bench_memcpy_contiguous": ([vp, vp, c_sz, c_int, c_int, c_int, pd], c_int),
+        "gfd_bench_submit_direct": ([vp, vp, c_int, c_int, c_int, pd], c_int),
+        "gfd_bench_zero_copy_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
+        "gfd_bench_queue": ([vp, vp, vp, c_int, c_u32, ctypes.POINTER(c_u64), c_int, c_int, c_u64, pd], c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    return sig
+
+
+def lib():
+    """Load libgfd_amd.so (ImportError if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError("libgfd_amd.so is not built (run: python -m gfd_amd.builder)")
+        L = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+        _SIGNATURES.update(_declare(L))
+        _lib = L
+    return _lib
+
+
+def bound_symbols():
+    """Names of every C-ABI function this package binds."""
+    return sorted(_SIGNATURES)
+
+
+def _check(rc, what):
+    if rc != 0:
+        msg = lib().gfd_last_error().decode(errors="replace")
+        raise GfdError("%s failed (%d): %s" % (what, rc, msg))
+
+
+# ------------------------------------------------------------------ memory
+
+class HostBuffer:
+    """Pinned host memory (hipHostMalloc) with a numpy uint8 view."""
+
+    def __init__(self, nbytes, flags=HOST_DEFAULT):
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        _check(lib().gfd_host_alloc(ctypes.byref(p), max(self.nbytes, 1), flags), "gfd_host_alloc")
+        self.ptr = p.value
+        self.array = np.ctypeslib.as_array((ctypes.c_uint8 * max(self.nbytes, 1)).from_address(self.ptr))[:self.nbytes]
+
+    def free(self):
+        if self.ptr:
+            self.array = None
+            lib().gfd_host_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class DeviceBuffer:
+    """HBM allocation (hipMalloc)."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        _check(lib().gfd_device_alloc(ctypes.byref(p), max(self.nbytes, 1)), "gfd_device_alloc")
+        self.ptr = p.value
+
+    def fill(self, value):
+        _check(lib().gfd_memset_device(self.ptr, value, self.nbytes), "gfd_memset_device")
+
+    def upload(self, arr, offset=0):
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes
+        _check(lib().gfd_memcpy_h2d(self.ptr + offset, arr.ctypes.data, arr.nbytes), "gfd_memcpy_h2d")
+
+    def download(self, nbytes=None, offset=0):
+        n = self.nbytes - offset if nbytes is None else int(nbytes)
+        out = np.empty(n, dtype=np.uint8)
+        _check(lib().gfd_memcpy_d2h(out.ctypes.data, self.ptr + offset, n), "gfd_memcpy_d2h")
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().gfd_device_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def synchronize():
+    _check(lib().gfd_device_synchronize(), "gfd_device_synchronize")
+
+
+def device_count():
+    n = ctypes.c_int(0)
+    rc = lib().gfd_device_count(ctypes.byref(n))
+    return n.value if rc == 0 else 0
+
+
+def make_entries(src_addrs, dst_base, token_size):
+    """SGEntry array: entry j = {dst_base + j*token_size, src_addrs[j], token_size}."""
+    src_addrs = np.asarray(src_addrs, dtype=np.uint64)
+    n = len(src_addrs)
+    arr = (SGEntry * max(n, 1))()
+    a = np.frombuffer(arr, dtype=np.uint64).reshape(-1, 3)[:n]
+    a[:, 0] = np.uint64(dst_base) + np.arange(n, dtype=np.uint64) * np.uint64(token_size)
+    a[:, 1] = src_addrs
+    a[:, 2] = token_size
+    return arr
+
+
+# ------------------------------------------------------------ host classes
+
+class StagingPool:
+    """gfd::StagingPool::instance() (reference include/gfd/staging_pool.h)."""
+
+    @staticmethod
+    def init(num_gpus, buf_size, numa_node=0):
+        return lib().gfd_staging_pool_init(num_gpus, buf_size, numa_node) == 0
+
+    @staticmethod
+    def shutdown():
+        lib().gfd_staging_pool_shutdown()
+
+
+class CpuPollingThread:
+    """gfd::CpuPollingThread (reference include/gfd/cpu_polling.h:19-84)."""
+
+    def __init__(self, queue=None, gpu_base=None, cpu_base=None, total_cpu_size=0, use_ce=True, numa_node=0,
+                 core_offset=0, num_ce_channels=0, exclusive_core_base=-1, exclusive_core_count=0):
+        q = getattr(queue, "ptr", queue)
+        self._h = lib().gfd_poller_create(q, gpu_base, cpu_base, total_cpu_size, int(bool(use_ce)), numa_node,
+                                          core_offset, num_ce_channels, exclusive_core_base,
+                                          exclusive_core_count)
+        if not self._h:
+            raise GfdError("gfd_poller_create failed")
+
+    def init_copy_engine(self):
+        return lib().gfd_poller_init_copy_engine(self._h) == 0
+
+    def init_direct_ce(self):
+        return lib().gfd_poller_init_direct_ce(self._h) == 0
+
+    def submit_direct(self, entries, count=None):
+        if count is None:
+            count = len(entries)
+        return lib().gfd_poller_submit_direct(self._h, ctypes.cast(entries, ctypes.c_void_p), count)
+
+    def set_tiled_queue(self, tq):
+        lib().gfd_poller_set_tiled_queue(self._h, getattr(tq, "ptr", tq))
+
+    def set_sg_task_queue(self, sq):
+        lib().gfd_poller_set_sg_task_queue(self._h, getattr(sq, "ptr", sq))
+
+    def start(self):
+        lib().gfd_poller_start(self._h)
+
+    def stop(self):
+        lib().gfd_poller_stop(self._h)
+
+    def stats(self):
+        s = PollerStats()
+        lib().gfd_poller_get_stats(self._h, ctypes.byref(s))
+        return {k: getattr(s, k) for k, _ in PollerStats._fields_}
+
+    def reset_stats(self):
+        lib().gfd_poller_reset_stats(self._h)
+
+    def info(self):
+        i = PollerInfo()
+        lib().gfd_poller_get_info(self._h, ctypes.byref(i))
+        d = {k: getattr(i, k) for k, _ in PollerInfo._fields_}
+        d["worker_cpus"] = list(i.worker_cpus)[: i.num_gather_workers]
+        return d
+
+    def set_direct_chunk_bytes(self, b):
+        lib().gfd_poller_set_direct_chunk_bytes(self._h, b)
+
+    def set_gather_slice_bytes(self, b):
+        lib().gfd_poller_set_gather_slice_bytes(self._h, b)
+
+    def close(self):
+        if self._h:
+            lib().gfd_poller_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DescriptorQueue:
+    """gfd::DescriptorQueue in fine-grained host memory."""
+
+    def __init__(self):
+        p = ctypes.c_void_p()
+        _check(lib().gfd_queue_alloc(ctypes.byref(p)), "gfd_queue_alloc")
+        self.ptr = p.value
+        base = self.ptr + QUEUE_SIZE * 64
+        self._idx = np.ctypeslib.as_array((ctypes.c_uint64 * 3).from_address(base))
+
+    @property
+    def write_idx(self):
+        return int(self._idx[0])
+
+    @property
+    def read_idx(self):
+        return int(self._idx[1])
+
+    @property
+    def done_idx(self):
+        return int(self._idx[2])
+
+    def free(self):
+        if self.ptr:
+            self._idx = None
+            lib().gfd_queue_free(self.ptr)
+            self.ptr = None
+
+
+def host_gather(entries, count, out, chunk_bytes=0, slice_bytes=0, num_workers=0):
+    """Run the product's gather engine on the host only; returns the chunk
+    completion order (see gfd_host_gather in include/gfd_capi.h)."""
+    out_ptr = out.ctypes.data if isinstance(out, np.ndarray) else out
+    total = sum(int(entries[i].size) for i in range(count)) if count else 0
+    nchunks = max(1, -(-total // chunk_bytes)) if chunk_bytes else 1
+    order = np.full(nchunks, -1, dtype=np.int32)
+    _check(lib().gfd_host_gather(ctypes.cast(entries, ctypes.c_void_p), count, out_ptr, chunk_bytes, slice_bytes,
+                                 num_workers, order.ctypes.data), "gfd_host_gather")
+    return order
+
+
+def zero_copy_gather_tokens(src_addrs_ptr, dst_ptr, token_size, num_tokens, stream=None):
+    _check(lib().gfd_zero_copy_gather_tokens(src_addrs_ptr, dst_ptr, token_size, num_tokens, stream),
+           "gfd_zero_copy_gather_tokens")
+
+
+def zero_copy_gather(entries_ptr, count, stream=None):
+    _check(lib().gfd_zero_copy_gather(entries_ptr, count, stream), "gfd_zero_copy_gather")
+
+
+def build(verbose=False):
+    """Compile libgfd_amd.so for gfx950 (see gfd_amd/builder.py)."""
+    from . import builder
+
+    return builder.build(verbose=verbose)

@@ -1,0 +1,91 @@
+#pragma once
+// GatherEngine: a pool of pinned, spinning worker threads that copy scattered
+// host tokens into a contiguous pinned staging buffer with non-temporal
+// stores, and report finished chunks in order so the caller can start the
+// SDMA copy of each chunk while later chunks are still being gathered.
+//
+// Role in the reference: CpuPollingThread::parallel_gather +
+// gather_worker_loop (src/parallel_gather.cpp:44-116).  The reference splits
+// the entries statically into W+1 ranges and joins once; here the
+// destination byte range is cut into chunks, chunks into slices, and all
+// threads claim slices in order from one atomic counter, so chunk 0 is
+// finished by every thread together and its copy can start after a fraction
+// of the total gather time.
+#include <atomic>
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <thread>
+#include <vector>
+
+#include "gfd/copy_engine.h"
+
+namespace gfd {
+
+// Non-temporal copy: unaligned 64-byte loads, 64-byte-aligned streaming stores,
+// memcpy head/tail.  Does not fence; callers fence before publishing.
+void stream_copy(void* dst, const void* src, size_t n);
+void store_fence();
+
+class GatherEngine {
+public:
+    // One worker per CPU in worker_cpus (negative id: unpinned).
+    explicit GatherEngine(const std::vector<int>& worker_cpus);
+    ~GatherEngine();
+    GatherEngine(const GatherEngine&) = delete;
+    GatherEngine& operator=(const GatherEngine&) = delete;
+
+    int num_workers() const { return (int)threads_.size(); }
+    void set_slice_bytes(size_t b) { slice_bytes_ = b < 4096 ? 4096 : b; }
+    size_t slice_bytes() const { return slice_bytes_; }
+    // Whether the calling thread copies slices too (default: only when there
+    // are fewer than two workers, so the caller stays free to issue copies).
+    void set_caller_copies(int mode) { caller_copies_ = mode; }
+
+    using ChunkFn = void (*)(void* ctx, int chunk, size_t offset, size_t bytes);
+
+    // Precondition: the entries' destinations are contiguous in order
+    // (entry i starts where entry i-1 ends).  Writes entry i's bytes to
+    // staging + (entries[i].dst - entries[0].dst).  The destination range
+    // [0, total) is cut into chunks of chunk_bytes; on_chunk(ctx, c, off, len)
+    // is called on the calling thread, in chunk order, once chunk c's bytes
+    // are written and fenced.  Returns after every worker has left the job.
+    void run(const SGEntry* entries, int count, size_t total, char* staging,
+             size_t chunk_bytes, ChunkFn on_chunk, void* ctx);
+
+private:
+    struct Slice {
+        int entry;        // entry holding the slice's first byte
+        size_t entry_off; // offset of that byte inside the entry
+        size_t off;       // staging offset of the slice
+        size_t len;
+        int chunk;
+    };
+    struct alignas(64) WorkerState {
+        std::atomic<uint64_t> done_epoch{0};
+        char pad[56];
+    };
+
+    void worker_main(int w, int cpu);
+    void do_slices();
+    void copy_slice(const Slice& s);
+
+    std::vector<std::thread> threads_;
+    std::unique_ptr<WorkerState[]> wstate_;
+    alignas(64) std::atomic<uint64_t> epoch_{0};
+    alignas(64) std::atomic<bool> running_{true};
+    alignas(64) std::atomic<int> next_slice_{0};
+
+    // current job (written by the caller before the epoch bump)
+    const SGEntry* entries_ = nullptr;
+    int count_ = 0;
+    char* staging_ = nullptr;
+    std::vector<Slice> slices_;
+    std::unique_ptr<std::atomic<int>[]> remaining_;
+    int remaining_cap_ = 0;
+
+    size_t slice_bytes_ = 128 * 1024;
+    int caller_copies_ = -1;
+};
+
+}  // namespace gfd

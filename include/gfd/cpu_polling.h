@@ -1,0 +1,222 @@
+#pragma once
+// CpuPollingThread: the host side of GFD.  Public interface as in
+// include/gfd/cpu_polling.h:19-84 of the reference:
+//   * submit_direct()  — the CPU hands an SG list straight in ("GFD Direct");
+//   * start()/stop()   — a pinned thread polls the descriptor ring that GPU
+//                        kernels fill ("GFD Queue"), batches contiguous runs and
+//                        signals completion through done_idx / per-tile /
+//                        per-list signals.
+// Both gather scattered host tokens into pinned staging memory with a pool of
+// NUMA-local worker threads and stream the staging to HBM over several SDMA
+// channels.
+//
+// Threading: init_copy_engine()/init_direct_ce() must run on a thread that can
+// use the GPU; the polling thread makes the device current itself.
+// submit_direct() may run concurrently with the polling thread: the gather
+// workers are shared under a mutex and each path has its own staging and its
+// own copy channels.
+#include <atomic>
+#include <cstring>
+#include <mutex>
+#include <thread>
+#include <utility>
+#include <vector>
+
+#include "gfd/copy_engine.h"
+#include "gfd/tiled_queue.h"
+
+namespace gfd {
+
+// Upper bound on gather worker threads (not counting the calling thread).
+constexpr int MAX_GATHER_WORKERS = 15;
+// Worker count the reference used when no core range was given.
+constexpr int NUM_GATHER_WORKERS = 7;
+
+struct SGTaskQueue;
+class GatherEngine;
+
+class CpuPollingThread {
+public:
+    // queue:          descriptor ring in fine-grained host memory (may be null
+    //                 for direct-only use)
+    // gpu_base:       base of the HBM destination region (informational)
+    // cpu_base/total_cpu_size: the host source region; staging buffers are
+    //                 sized to total_cpu_size
+    // use_ce:         false = no SDMA (kept for API compatibility; rejected)
+    // numa_node:      host node for staging and workers; -1 = the GPU's node
+    // core_offset:    kept for API compatibility (ignored: CPUs are chosen from
+    //                 the node's CPU list and the process affinity mask)
+    // num_ce_channels: copy channels per manager (0 = DEFAULT_CE_CHANNELS)
+    // exclusive_core_base/count: explicit CPU range for poller + workers
+    CpuPollingThread(DescriptorQueue* queue, void* gpu_base, void* cpu_base,
+                     size_t total_cpu_size, bool use_ce = true, int numa_node = 0,
+                     int core_offset = 0, int num_ce_channels = 0,
+                     int exclusive_core_base = -1, int exclusive_core_count = 0);
+    ~CpuPollingThread();
+    CpuPollingThread(const CpuPollingThread&) = delete;
+    CpuPollingThread& operator=(const CpuPollingThread&) = delete;
+
+    // Channels, staging buffers, gather workers, signal stream.
+    bool init_copy_engine();
+
+    // Separate copy channels and staging for submit_direct().
+    bool init_direct_ce();
+
+    // Gather `count` entries into HBM and block until they have landed.
+    // Returns the wall time in microseconds, or -1 on error.
+    // Paths (src/direct_submit.cpp:37-145):
+    //   src and dst contiguous      -> one copy split over the channels
+    //   dst contiguous, src scattered, total <= staging
+    //                               -> pipelined gather: the workers fill
+    //                                  staging chunk by chunk and each finished
+    //                                  chunk is copied at once on the next channel
+    //   otherwise                   -> one async copy per entry
+    double submit_direct(const SGEntry* entries, int count);
+
+    void set_tiled_queue(TiledQueue* tq) { tiled_queue_ = tq; }
+    void set_sg_task_queue(SGTaskQueue* sq) { sg_queue_ = sq; }
+
+    void start();
+    void stop();
+
+    uint64_t get_descriptors_processed() const { return descriptors_processed_.load(std::memory_order_relaxed); }
+    uint64_t get_batches_submitted() const { return batches_submitted_.load(std::memory_order_relaxed); }
+    uint64_t get_coalesced_entries() const { return coalesced_entries_.load(std::memory_order_relaxed); }
+    uint64_t get_staging_batches() const { return staging_batches_.load(std::memory_order_relaxed); }
+    double get_total_bytes_copied() const { return (double)total_bytes_copied_.load(std::memory_order_relaxed); }
+    const CopyEngineManager& get_ce_manager() const { return ce_manager_; }
+    bool is_ce_mode() const { return use_ce_; }
+    uint64_t get_gather_us() const { return total_gather_us_.load(std::memory_order_relaxed); }
+    uint64_t get_dma_wait_us() const { return total_dma_wait_us_.load(std::memory_order_relaxed); }
+    uint64_t get_dma_submit_us() const { return total_dma_submit_us_.load(std::memory_order_relaxed); }
+    uint64_t get_queue_read_us() const { return total_queue_read_us_.load(std::memory_order_relaxed); }
+
+    void reset_stats() {
+        descriptors_processed_.store(0, std::memory_order_relaxed);
+        batches_submitted_.store(0, std::memory_order_relaxed);
+        coalesced_entries_.store(0, std::memory_order_relaxed);
+        staging_batches_.store(0, std::memory_order_relaxed);
+        total_bytes_copied_.store(0, std::memory_order_relaxed);
+        total_gather_us_.store(0, std::memory_order_relaxed);
+        total_dma_wait_us_.store(0, std::memory_order_relaxed);
+        total_dma_submit_us_.store(0, std::memory_order_relaxed);
+        total_queue_read_us_.store(0, std::memory_order_relaxed);
+        std::memset(tile_progress_, 0, sizeof(tile_progress_));
+        std::memset(tile_marked_, 0, sizeof(tile_marked_));
+    }
+
+    // ---- MI355X additions -------------------------------------------------
+    int num_gather_workers() const;
+    const std::vector<int>& worker_cpus() const { return worker_cpus_; }
+    int poller_cpu() const { return poller_cpu_; }
+    int numa_node() const { return numa_node_; }
+    int device() const { return device_; }
+    // Chunk size of the pipelined direct path (bytes of payload per copy).
+    void set_direct_chunk_bytes(size_t b) { direct_chunk_bytes_ = b ? b : 1; }
+    size_t direct_chunk_bytes() const { return direct_chunk_bytes_; }
+    // Gather slice size (bytes a thread copies per work item).
+    void set_gather_slice_bytes(size_t b);
+    size_t gather_slice_bytes() const { return slice_bytes_; }
+    size_t staging_buffer_size() const { return staging_buffer_size_; }
+    int num_staging_buffers() const { return num_staging_bufs_; }
+
+    // Host-side effects to apply once a batch's copies have completed.
+    struct CompletionSlot {
+        gfd_event_t event = nullptr;
+        uint64_t done_value = 0;
+        std::vector<std::pair<uint32_t, uint64_t>> host_tiles;  // (tile, progress)
+        uint32_t lists_done = 0;
+        void clear() {
+            host_tiles.clear();
+            lists_done = 0;
+        }
+    };
+
+private:
+    struct CompletionFifo;
+
+    void polling_loop();
+    void flush_batch(Descriptor* batch, int& batch_count, uint32_t& or_flags);
+    bool process_batch(Descriptor* batch, int count);
+    void process_batch_tiled(Descriptor* batch, int count, uint64_t cur_read);
+    void process_batch_sg(Descriptor* batch, int count, uint64_t cur_read);
+    void submit_list(const SGEntry* e, int count, size_t total);
+    bool gather_through_staging(const SGEntry* e, int count, size_t total);
+    void copy_runs(const SGEntry* e, int count);
+    void publish_done(uint64_t value);
+    void push_completion(uint64_t done_value);
+    void drain_completions(bool block);
+    void finish_slot(CompletionSlot& s);
+    bool start_workers();
+    bool choose_cpus();
+
+    CompletionFifo* fifo_ = nullptr;
+    CompletionSlot s_pending_;
+    std::vector<SGEntry> sg_scratch_;
+    std::vector<SGEntry> run_scratch_;
+    std::vector<uint32_t> tile_scratch_;
+    uint64_t tile_marked_[MAX_TILES] = {};
+    size_t slice_bytes_ = 0;
+
+    DescriptorQueue* queue_;
+    TiledQueue* tiled_queue_ = nullptr;
+    SGTaskQueue* sg_queue_ = nullptr;
+    void* gpu_base_;
+    void* cpu_base_;
+    size_t total_cpu_size_;
+    bool use_ce_;
+    int numa_node_;
+    int core_offset_;
+    int num_ce_channels_;
+    int exclusive_core_base_;
+    int exclusive_core_count_;
+    int device_ = 0;
+
+    CopyEngineManager ce_manager_;
+    CopyEngineManager direct_ce_manager_;
+    gfd_stream_t signal_stream_ = nullptr;
+
+    // Queue-path staging: rotating buffers, each guarded by an event.
+    static constexpr int NUM_STAGING_BUFS = 5;
+    char* staging_bufs_[NUM_STAGING_BUFS] = {};
+    gfd_event_t staging_events_[NUM_STAGING_BUFS] = {};
+    bool staging_event_pending_[NUM_STAGING_BUFS] = {};
+    size_t staging_buffer_size_ = 0;
+    int num_staging_bufs_ = 0;
+    int staging_cur_ = 0;
+    int staging_pool_set_ = -1;
+    bool staging_owned_ = false;
+
+    // Direct-path staging (one buffer of total_cpu_size bytes).
+    char* direct_staging_ = nullptr;
+    size_t direct_staging_size_ = 0;
+    size_t direct_chunk_bytes_ = 2u << 20;
+
+    bool has_async_dma_ = false;
+    uint64_t latest_async_read_ = 0;
+
+    // Tiled / SG completion signalling.
+    uint64_t tile_progress_[MAX_TILES] = {};
+
+    // Gather workers shared by both paths.
+    GatherEngine* gather_ = nullptr;
+    std::mutex gather_mutex_;
+    std::vector<int> worker_cpus_;
+    int poller_cpu_ = -1;
+    bool cpus_chosen_ = false;
+
+    std::atomic<bool> running_{false};
+    std::thread thread_;
+
+    std::atomic<uint64_t> descriptors_processed_{0};
+    std::atomic<uint64_t> batches_submitted_{0};
+    std::atomic<uint64_t> coalesced_entries_{0};
+    std::atomic<uint64_t> staging_batches_{0};
+    std::atomic<uint64_t> total_bytes_copied_{0};
+    std::atomic<uint64_t> total_gather_us_{0};
+    std::atomic<uint64_t> total_dma_wait_us_{0};
+    std::atomic<uint64_t> total_dma_submit_us_{0};
+    std::atomic<uint64_t> total_queue_read_us_{0};
+};
+
+}  // namespace gfd

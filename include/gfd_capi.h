@@ -1,0 +1,165 @@
+/*
+ * gfd_capi.h — the C-ABI drop-in boundary of the MI355X GFD library
+ * (libgfd_amd.so).  Plain pointers and sizes only; every function that can
+ * fail returns 0 on success and a nonzero HIP/GFD error code otherwise
+ * (gfd_last_error() gives a message for the calling thread).
+ *
+ * The C++ API in the include/gfd/ headers is the primary interface (same class names
+ * and signatures as the reference's include/gfd).  These entry points wrap it
+ * for FFI callers (ctypes, cgo, JNI) and are what the Python package binds.
+ * Each declaration names the reference interface it replaces.
+ */
+#ifndef GFD_CAPI_H
+#define GFD_CAPI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One host->device request; same 24-byte layout as gfd::SGEntry
+ * (reference include/gfd/copy_engine.h:29-33: {CUdeviceptr dst; const void* src; size_t size}). */
+typedef struct gfd_sg_entry {
+    uint64_t dst;
+    uint64_t src;
+    uint64_t size;
+} gfd_sg_entry;
+
+typedef void* gfd_poller_t;
+
+/* Counters of CpuPollingThread (reference include/gfd/cpu_polling.h:60-71). */
+typedef struct gfd_poller_stats {
+    uint64_t descriptors_processed;
+    uint64_t batches_submitted;
+    uint64_t coalesced_entries;
+    uint64_t staging_batches;
+    double total_bytes_copied;
+    uint64_t gather_us;
+    uint64_t dma_wait_us;
+    uint64_t dma_submit_us;
+    uint64_t queue_read_us;
+} gfd_poller_stats;
+
+/* Resources the poller chose (no reference counterpart; reported by the bench). */
+typedef struct gfd_poller_info {
+    int device;
+    int numa_node;
+    int num_gather_workers;
+    int poller_cpu;
+    int worker_cpus[16];
+    int num_ce_channels;
+    int num_staging_buffers;
+    uint64_t staging_buffer_size;
+    uint64_t direct_chunk_bytes;
+    uint64_t gather_slice_bytes;
+} gfd_poller_info;
+
+const char* gfd_version(void);
+const char* gfd_last_error(void);
+
+/* ---- runtime plumbing (the reference calls the CUDA runtime directly) ---- */
+int gfd_device_count(int* n);
+int gfd_set_device(int dev);
+int gfd_device_synchronize(void);
+/* flags: 0 default (pinned, coarse-grained), 1 coherent (fine-grained),
+ * 2 non-coherent, 4 follow the thread's NUMA policy.
+ * Replaces cudaHostAlloc / cudaMallocHost (examples/04_benchmark.cu:348). */
+int gfd_host_alloc(void** p, size_t bytes, unsigned flags);
+int gfd_host_free(void* p);
+int gfd_device_alloc(void** p, size_t bytes);           /* cudaMalloc */
+int gfd_device_free(void* p);
+int gfd_memcpy_h2d(void* dst, const void* src, size_t n);
+int gfd_memcpy_d2h(void* dst, const void* src, size_t n);
+int gfd_memset_device(void* dst, int value, size_t n);
+int gfd_stream_create(void** stream);                   /* non-blocking, default priority */
+int gfd_stream_destroy(void* stream);
+int gfd_stream_synchronize(void* stream);
+int gfd_event_create(void** event);                     /* timing enabled */
+int gfd_event_destroy(void* event);
+int gfd_event_record(void* event, void* stream);
+int gfd_event_synchronize(void* event);
+int gfd_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ---- CpuPollingThread (reference include/gfd/cpu_polling.h:21-84) ---- */
+/* CpuPollingThread::CpuPollingThread (cpu_polling.h:21-30); numa_node -1 = GPU-local. */
+gfd_poller_t gfd_poller_create(void* queue, void* gpu_base, void* cpu_base, size_t total_cpu_size,
+                               int use_ce, int numa_node, int core_offset, int num_ce_channels,
+                               int exclusive_core_base, int exclusive_core_count);
+void gfd_poller_destroy(gfd_poller_t p);                             /* ~CpuPollingThread */
+int gfd_poller_init_copy_engine(gfd_poller_t p);                     /* init_copy_engine (:33) -> 0/err */
+int gfd_poller_init_direct_ce(gfd_poller_t p);                       /* init_direct_ce (:43) */
+/* submit_direct (cpu_polling.h:36-40, src/direct_submit.cpp:28): blocks until
+ * the data is in HBM; returns elapsed microseconds, or -1 on error. */
+double gfd_poller_submit_direct(gfd_poller_t p, const gfd_sg_entry* entries, int count);
+void gfd_poller_set_tiled_queue(gfd_poller_t p, void* tiled_queue);  /* set_tiled_queue (:48) */
+void gfd_poller_set_sg_task_queue(gfd_poller_t p, void* sg_queue);   /* set_sg_task_queue (:53) */
+void gfd_poller_start(gfd_poller_t p);                               /* start (:56) */
+void gfd_poller_stop(gfd_poller_t p);                                /* stop (:57) */
+int gfd_poller_get_stats(gfd_poller_t p, gfd_poller_stats* out);     /* get_* (:60-71) */
+void gfd_poller_reset_stats(gfd_poller_t p);                         /* reset_stats (:73) */
+int gfd_poller_get_info(gfd_poller_t p, gfd_poller_info* out);
+/* Tuning of the pipelined direct path (no reference counterpart). */
+void gfd_poller_set_direct_chunk_bytes(gfd_poller_t p, uint64_t bytes);
+void gfd_poller_set_gather_slice_bytes(gfd_poller_t p, uint64_t bytes);
+
+/* Host-only gather (no GPU): the staging step of the pipelined direct path.
+ * Entries must have contiguous destinations; entry i lands at
+ * out + (entries[i].dst - entries[0].dst).  chunk_order (optional, capacity
+ * ceil(total/chunk_bytes)) receives the chunk indices in the order they were
+ * reported complete.  num_workers threads plus the caller.  (Reference
+ * counterpart: CpuPollingThread::parallel_gather, src/parallel_gather.cpp:74.) */
+int gfd_host_gather(const gfd_sg_entry* entries, int count, void* out, uint64_t chunk_bytes,
+                    uint64_t slice_bytes, int num_workers, int* chunk_order);
+
+/* ---- StagingPool (reference include/gfd/staging_pool.h:50,176) ---- */
+int gfd_staging_pool_init(int num_gpus, size_t buf_size, int numa_node);
+void gfd_staging_pool_shutdown(void);
+
+/* ---- zero-copy gather kernels (no reference counterpart: the GPU-initiated
+ * form of the same gather contract) ---- */
+/* dst + j*token_size <- src_addrs[j] (token_size bytes), j < num_tokens.
+ * src_addrs: device-readable table (HBM or pinned host); tokens in pinned host memory. */
+int gfd_zero_copy_gather_tokens(const uint64_t* src_addrs, void* dst, uint32_t token_size,
+                                int num_tokens, void* stream);
+/* Arbitrary SG list (device-readable array of entries, disjoint destinations). */
+int gfd_zero_copy_gather(const gfd_sg_entry* entries, int count, void* stream);
+
+/* ---- GFD Queue mode (reference include/gfd/device.cuh, examples/04_benchmark.cu:31-54) ---- */
+/* DescriptorQueue in fine-grained host memory, zeroed. */
+int gfd_queue_alloc(void** queue);
+int gfd_queue_free(void* queue);
+/* bench_gfd_submit_kernel (examples/04_benchmark.cu:31-46): descriptor j =
+ * {tokens[j].cpu_addr, gpu_dst + j*token_size, token_size, LAST_IN_BATCH on the last}
+ * at slot base_slot + j, one wave64 lane per descriptor. */
+int gfd_queue_submit_tokens(void* queue, const void* tokens, void* gpu_dst, int num_tokens,
+                            uint32_t token_size, uint64_t base_slot, void* stream);
+/* bench_gfd_wait_kernel (examples/04_benchmark.cu:49-54) with a bound: spins
+ * until done_idx >= expected_done or timeout_us elapses; *status (device or
+ * host-visible int) receives 0 on completion, 1 on timeout. */
+int gfd_queue_wait(void* queue, uint64_t expected_done, uint64_t timeout_us, int* status,
+                   void* stream);
+
+/* ---- measurement helpers (examples/04_benchmark.cu:92-115 and the peak
+ * reference copy); fill times_us[iters] with wall times ---- */
+int gfd_bench_memcpy_per_token(void* dst, const uint64_t* src_addrs, int num_tokens,
+                               uint32_t token_size, int warmup, int iters, double* times_us);
+int gfd_bench_memcpy_contiguous(void* dst, const void* src, size_t bytes, int num_streams,
+                                int warmup, int iters, double* times_us);
+int gfd_bench_submit_direct(gfd_poller_t p, const gfd_sg_entry* entries, int count, int warmup,
+                            int iters, double* times_us);
+/* Zero-copy tokens kernel: wall time launch->sync and HIP-event kernel time. */
+int gfd_bench_zero_copy_tokens(const uint64_t* src_addrs, void* dst, uint32_t token_size,
+                               int num_tokens, int warmup, int iters, double* wall_us,
+                               double* event_us);
+/* Queue mode: submit kernel + wait kernel, wall time launch->device sync. */
+int gfd_bench_queue(void* queue, const void* tokens, void* gpu_dst, int num_tokens,
+                    uint32_t token_size, uint64_t* base_slot, int warmup, int iters,
+                    uint64_t timeout_us, double* times_us);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GFD_CAPI_H */

@@ -1,0 +1,106 @@
+"""CPU-only checks of the C-ABI library: it loads, exports every declared
+symbol, and its host-side gather engine matches the oracle byte for byte."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import gfd_amd
+import oracle
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "gfd_capi.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gfd_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_reports_version():
+    assert gfd_amd.lib().gfd_version().startswith(b"gfd-amd")
+
+
+def test_every_declared_symbol_is_exported():
+    L = ctypes.CDLL(gfd_amd.LIB_PATH)
+    names = declared_functions()
+    assert len(names) > 40
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_python_binds_only_declared_symbols():
+    gfd_amd.lib()
+    assert set(gfd_amd.bound_symbols()) <= set(declared_functions())
+    assert set(declared_functions()) - set(gfd_amd.bound_symbols()) == set()
+
+
+def test_struct_layouts_match_header():
+    assert ctypes.sizeof(gfd_amd.SGEntry) == 24
+    assert ctypes.sizeof(gfd_amd.TokenInfo) == 16
+    assert ctypes.sizeof(oracle.SGEntry) == 24
+
+
+def _layout(n, t, stride=None):
+    stride = stride or 2 * t
+    region = np.empty(n * stride, np.uint8)
+    oracle.fill_tokens(region, n, t, stride)
+    perm = oracle.permutation(n)
+    return region, perm, stride
+
+
+@pytest.mark.parametrize("workers", [0, 1, 2, 7])
+@pytest.mark.parametrize("n,t,chunk,slice_", [
+    (256, 4096, 64 << 10, 16 << 10),     # the 256 x 4 KB CPU layout
+    (256, 4096, 1 << 20, 128 << 10),     # one chunk
+    (97, 1000, 10000, 4096),             # ragged: tokens cross chunk and slice edges
+    (8, 65536, 100000, 4096),            # tokens larger than chunks
+    (1, 12, 0, 0),                       # single tiny entry
+])
+def test_host_gather_matches_oracle(workers, n, t, chunk, slice_):
+    region, perm, stride = _layout(n, t)
+    base = 1 << 44
+    entries = gfd_amd.make_entries(region.ctypes.data + perm.astype(np.uint64) * np.uint64(stride), base, t)
+    out = np.full(n * t + 128, 0x5A, np.uint8)
+    order = gfd_amd.host_gather(entries, n, out, chunk_bytes=chunk, slice_bytes=slice_, num_workers=workers)
+    assert (out[:n * t] == oracle.expected_gather(region, perm, t, stride)).all()
+    assert (out[n * t:] == 0x5A).all()
+    assert order.tolist() == list(range(len(order)))  # chunks reported in order
+
+
+def test_host_gather_mixed_sizes():
+    rng = np.random.default_rng(7)
+    sizes = rng.integers(1, 9000, 300)
+    src = rng.integers(0, 256, int(sizes.sum()) * 2, dtype=np.uint8)
+    offs = np.concatenate([[0], np.cumsum(sizes * 2)[:-1]])
+    n = len(sizes)
+    entries = (gfd_amd.SGEntry * n)()
+    dst = 0
+    expect = np.empty(int(sizes.sum()), np.uint8)
+    for i in range(n):
+        entries[i].dst = 4096 + dst
+        entries[i].src = src.ctypes.data + int(offs[i])
+        entries[i].size = int(sizes[i])
+        expect[dst:dst + sizes[i]] = src[offs[i]:offs[i] + sizes[i]]
+        dst += int(sizes[i])
+    out = np.zeros(dst, np.uint8)
+    gfd_amd.host_gather(entries, n, out, chunk_bytes=50000, slice_bytes=8192, num_workers=3)
+    assert (out == expect).all()
+
+
+def test_host_gather_rejects_scattered_destinations():
+    a = np.zeros(64, np.uint8)
+    entries = (gfd_amd.SGEntry * 2)()
+    entries[0].dst, entries[0].src, entries[0].size = 0, a.ctypes.data, 16
+    entries[1].dst, entries[1].src, entries[1].size = 32, a.ctypes.data, 16
+    with pytest.raises(gfd_amd.GfdError):
+        gfd_amd.host_gather(entries, 2, np.zeros(64, np.uint8), num_workers=1)
+
+
+def test_host_gather_empty_is_noop():
+    out = np.full(16, 3, np.uint8)
+    gfd_amd.host_gather((gfd_amd.SGEntry * 1)(), 0, out, num_workers=2)
+    assert (out == 3).all()

@@ -1,0 +1,253 @@
+"""GPU parity: every gather path of libgfd_amd.so against the oracle,
+byte-exact, on seeded scattered layouts (tokens at 2x stride in pinned host
+memory, Fisher-Yates order) and the reference examples' known-answer pattern.
+Each destination buffer has a sentinel tail that must survive (no overrun)."""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+import gfd_amd
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = 0xCD
+TAIL = 4096
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert gfd_amd.device_count() > 0, "no GPU visible to libgfd_amd.so"
+    assert gfd_amd.lib().gfd_set_device(0) == 0
+
+
+class Layout:
+    def __init__(self, n, t, flags=gfd_amd.HOST_DEFAULT, stride=None):
+        self.n, self.t = n, t
+        self.stride = stride or 2 * t
+        self.host = gfd_amd.HostBuffer(n * self.stride, flags)
+        oracle.fill_tokens(self.host.array, n, t, self.stride)
+        self.perm = oracle.permutation(n)
+        self.expected = oracle.expected_gather(self.host.array, self.perm, t, self.stride)
+        self.src_addrs = (np.uint64(self.host.ptr) + self.perm.astype(np.uint64) * np.uint64(self.stride))
+        self.dst = gfd_amd.DeviceBuffer(n * t + TAIL)
+        self.dst.fill(SENTINEL)
+
+    def check(self):
+        got = self.dst.download()
+        n_bad = int(np.count_nonzero(got[:self.n * self.t] != self.expected))
+        assert n_bad == 0, "%d mismatched bytes" % n_bad
+        assert (got[self.n * self.t:] == SENTINEL).all(), "write past the destination range"
+
+    def reset(self):
+        self.dst.fill(SENTINEL)
+
+
+ZC_CASES = [(256, 4096), (8192, 4096), (2048, 65536), (2048, 512), (2048, 1024), (2048, 2048),
+            (97, 1000), (3, 48), (1, 16), (5, 12)]
+
+
+@pytest.mark.parametrize("n,t", ZC_CASES)
+def test_zero_copy_tokens_parity(n, t):
+    log("zero_copy_tokens n=%d t=%d" % (n, t))
+    L = Layout(n, t)
+    table = gfd_amd.DeviceBuffer(n * 8)
+    table.upload(L.src_addrs)
+    gfd_amd.zero_copy_gather_tokens(table.ptr, L.dst.ptr, t, n)
+    gfd_amd.synchronize()
+    L.check()
+
+
+def test_zero_copy_tokens_coherent_source_and_host_table():
+    # Fine-grained source and a page table read from pinned host memory.
+    log("zero_copy_tokens coherent")
+    L = Layout(1024, 4096, flags=gfd_amd.HOST_COHERENT)
+    table = gfd_amd.HostBuffer(1024 * 8)
+    table.array.view(np.uint64)[:] = L.src_addrs
+    gfd_amd.zero_copy_gather_tokens(table.ptr, L.dst.ptr, 4096, 1024)
+    gfd_amd.synchronize()
+    L.check()
+
+
+def test_zero_copy_tokens_zero_count_is_noop():
+    L = Layout(4, 64)
+    gfd_amd.zero_copy_gather_tokens(None, L.dst.ptr, 64, 0)
+    gfd_amd.synchronize()
+    assert (L.dst.download() == SENTINEL).all()
+
+
+def _ragged_entries(dst_base, src_base, rng, count, max_size):
+    sizes = rng.integers(1, max_size, count)
+    src_offs = np.cumsum(np.concatenate([[3], sizes[:-1] * 2 + rng.integers(0, 40, count - 1)]))
+    dst_offs = np.cumsum(np.concatenate([[0], sizes[:-1] + rng.integers(0, 24, count - 1)]))
+    return sizes, src_offs, dst_offs
+
+
+@pytest.mark.parametrize("where", ["device", "host"])
+def test_zero_copy_sg_generic_ragged(where):
+    log("zero_copy_sg ragged (%s entries)" % where)
+    rng = np.random.default_rng(11)
+    count = 700
+    sizes, src_offs, dst_offs = _ragged_entries(0, 0, rng, count, 9000)
+    src = gfd_amd.HostBuffer(int(src_offs[-1] + sizes[-1] + 64))
+    src.array[:] = rng.integers(0, 256, src.nbytes, dtype=np.uint8)
+    dst_len = int(dst_offs[-1] + sizes[-1])
+    dst = gfd_amd.DeviceBuffer(dst_len + TAIL)
+    dst.fill(SENTINEL)
+    entries = (gfd_amd.SGEntry * count)()
+    expect = np.full(dst_len + TAIL, SENTINEL, np.uint8)
+    for i in range(count):
+        entries[i].dst = dst.ptr + int(dst_offs[i])
+        entries[i].src = src.ptr + int(src_offs[i])
+        entries[i].size = int(sizes[i])
+        expect[dst_offs[i]:dst_offs[i] + sizes[i]] = src.array[src_offs[i]:src_offs[i] + sizes[i]]
+    raw = np.frombuffer(entries, np.uint8)
+    if where == "device":
+        tab = gfd_amd.DeviceBuffer(raw.nbytes)
+        tab.upload(raw)
+    else:
+        tab = gfd_amd.HostBuffer(raw.nbytes)
+        tab.array[:] = raw
+    gfd_amd.zero_copy_gather(tab.ptr, count, None)
+    gfd_amd.synchronize()
+    assert (dst.download() == expect).all()
+
+
+def test_zero_copy_sg_matches_tokens_layout():
+    log("zero_copy_sg tokens layout")
+    L = Layout(2048, 4096)
+    entries = gfd_amd.make_entries(L.src_addrs, L.dst.ptr, 4096)
+    raw = np.frombuffer(entries, np.uint8)
+    tab = gfd_amd.DeviceBuffer(raw.nbytes)
+    tab.upload(raw)
+    gfd_amd.zero_copy_gather(tab.ptr, 2048, None)
+    gfd_amd.synchronize()
+    L.check()
+
+
+# ----------------------------------------------------------- GFD Direct
+
+@pytest.fixture(scope="module")
+def direct_poller():
+    region = 2048 * 65536 * 2  # largest layout below
+    p = gfd_amd.CpuPollingThread(None, None, None, region, numa_node=-1)
+    assert p.init_direct_ce()
+    log("direct poller: %s" % p.info())
+    yield p
+    p.close()
+
+
+DIRECT_CASES = [(256, 4096, 2 << 20), (8192, 4096, 2 << 20), (8192, 4096, 256 << 10), (2048, 65536, 2 << 20),
+                (2048, 512, 2 << 20), (2048, 1024, 64 << 10), (2048, 2048, 2 << 20), (97, 1000, 10000),
+                (40, 4096, 2 << 20)]
+
+
+@pytest.mark.parametrize("n,t,chunk", DIRECT_CASES)
+def test_submit_direct_parity(direct_poller, n, t, chunk):
+    log("submit_direct n=%d t=%d chunk=%d" % (n, t, chunk))
+    L = Layout(n, t)
+    direct_poller.set_direct_chunk_bytes(chunk)
+    entries = gfd_amd.make_entries(L.src_addrs, L.dst.ptr, t)
+    for rep in range(2):
+        us = direct_poller.submit_direct(entries, n)
+        assert us > 0
+        L.check()
+        L.reset()
+    direct_poller.set_direct_chunk_bytes(2 << 20)
+
+
+def test_submit_direct_reference_kat(direct_poller):
+    # examples/02_direct_transfer.cu:50-54,117-129: token i = i & 0xFF.
+    log("submit_direct KAT")
+    n, t = 1024, 4096
+    host = gfd_amd.HostBuffer(n * 2 * t)
+    a = host.array.reshape(n, 2 * t)
+    a[:, :t] = (np.arange(n) & 0xFF).astype(np.uint8)[:, None]
+    a[:, t:] = oracle.GAP_BYTE
+    dst = gfd_amd.DeviceBuffer(n * t)
+    srcs = np.uint64(host.ptr) + np.arange(n, dtype=np.uint64) * np.uint64(2 * t)
+    entries = gfd_amd.make_entries(srcs, dst.ptr, t)
+    assert direct_poller.submit_direct(entries, n) > 0
+    assert (dst.download() == np.repeat((np.arange(n) & 0xFF).astype(np.uint8), t)).all()
+
+
+def test_submit_direct_contiguous_and_scattered_dst(direct_poller):
+    log("submit_direct contiguous / scattered dst")
+    # fully contiguous source and destination (single split copy)
+    host = gfd_amd.HostBuffer(16 << 20)
+    host.array[:] = np.random.default_rng(3).integers(0, 256, host.nbytes, dtype=np.uint8)
+    dst = gfd_amd.DeviceBuffer(16 << 20)
+    n, t = 4096, 4096
+    srcs = np.uint64(host.ptr) + np.arange(n, dtype=np.uint64) * np.uint64(t)
+    entries = gfd_amd.make_entries(srcs, dst.ptr, t)
+    assert direct_poller.submit_direct(entries, n) > 0
+    assert (dst.download() == host.array).all()
+    # destinations with gaps: one copy per entry
+    n2 = 64
+    dst2 = gfd_amd.DeviceBuffer(n2 * 2 * t)
+    dst2.fill(SENTINEL)
+    e2 = (gfd_amd.SGEntry * n2)()
+    expect = np.full(n2 * 2 * t, SENTINEL, np.uint8)
+    for i in range(n2):
+        j = (i * 37) % n2
+        e2[i].dst = dst2.ptr + i * 2 * t
+        e2[i].src = host.ptr + j * t
+        e2[i].size = t
+        expect[i * 2 * t:i * 2 * t + t] = host.array[j * t:(j + 1) * t]
+    assert direct_poller.submit_direct(e2, n2) > 0
+    assert (dst2.download() == expect).all()
+
+
+def test_submit_direct_rejects_empty(direct_poller):
+    assert direct_poller.submit_direct((gfd_amd.SGEntry * 1)(), 0) == -1.0
+
+
+def test_memcpy_per_token_baseline_parity():
+    log("memcpy per token")
+    L = Layout(512, 4096)
+    t = np.zeros(1)
+    rc = gfd_amd.lib().gfd_bench_memcpy_per_token(L.dst.ptr, L.src_addrs.ctypes.data, L.n, L.t, 0, 1,
+                                                  t.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    assert rc == 0
+    L.check()
+
+
+# ------------------------------------------------------------- GFD Queue
+
+@pytest.mark.parametrize("n,t", [(2048, 512), (2048, 2048), (8192, 4096), (1, 4096), (300, 1000)])
+def test_queue_mode_parity(n, t):
+    log("queue n=%d t=%d" % (n, t))
+    L = Layout(n, t)
+    q = gfd_amd.DescriptorQueue()
+    p = gfd_amd.CpuPollingThread(q, L.dst.ptr, L.host.ptr, L.host.nbytes, numa_node=-1)
+    try:
+        assert p.init_copy_engine()
+        p.start()
+        tokens = np.zeros((n, 2), np.uint64)
+        tokens[:, 0] = L.src_addrs
+        tokens[:, 1] = np.arange(n, dtype=np.uint64)  # token_id, expert_id = 0
+        dtok = gfd_amd.DeviceBuffer(tokens.nbytes)
+        dtok.upload(tokens)
+        base = ctypes.c_uint64(0)
+        times = np.zeros(2)
+        for rep in range(2):
+            rc = gfd_amd.lib().gfd_bench_queue(q.ptr, dtok.ptr, L.dst.ptr, n, t, ctypes.byref(base), 0, 1,
+                                               10_000_000, times.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+            assert rc == 0, gfd_amd.lib().gfd_last_error()
+            assert base.value == n * (rep + 1)
+            L.check()
+            L.reset()
+        assert q.done_idx == base.value and q.read_idx == base.value
+        s = p.stats()
+        assert s["descriptors_processed"] == 2 * n
+    finally:
+        p.stop()
+        p.close()
+        q.free()
