@@ -109,9 +109,14 @@ def cpu_baseline(oracle, seconds, info):
         if not (staging.array == oracle.expected_gather(src.array, perm, t, 2 * t)).all():
             raise SystemExit("PARITY FAILURE: CPU baseline")
         times = []
-        t_end = time.time() + seconds
+        t_start = time.time()
+        t_end = t_start + seconds
+        t_log = t_start + 2.5
         while time.time() < t_end:
             times.extend(pool.time(entries, n, staging.array, 0, 20).tolist())
+            if time.time() > t_log:
+                log("  cpu baseline: %d gathers, P50 %.1f us so far" % (len(times), p50(times)))
+                t_log += 2.5
     finally:
         pool.close()
         os.sched_setaffinity(0, allowed)
@@ -134,7 +139,15 @@ def bench_peak(nbytes, iters, warmup):
         rc = gfd_amd.lib().gfd_bench_memcpy_contiguous(dst.ptr, src.ptr, nbytes, ns, warmup, iters,
                                                        t.ctypes.data_as(PD))
         assert rc == 0, gfd_amd.lib().gfd_last_error()
-        out["%d_stream" % ns] = round(gbps(nbytes, p50(t)), 3)
+        out["hip_%d_stream" % ns] = round(gbps(nbytes, p50(t)), 3)
+    mask = ctypes.c_uint32(0)
+    for ch, pin in ((1, 1), (2, 1), (4, 1), (2, 0)):
+        t = np.zeros(iters)
+        rc = gfd_amd.lib().gfd_bench_sdma_contiguous(dst.ptr, src.ptr, nbytes, ch, pin, warmup, iters,
+                                                     t.ctypes.data_as(PD), ctypes.byref(mask))
+        assert rc == 0, gfd_amd.lib().gfd_last_error()
+        out["sdma_%dch_%s" % (ch, "pinned" if pin else "auto")] = round(gbps(nbytes, p50(t)), 3)
+    out["sdma_engine_mask"] = "0x%x" % mask.value
     return out
 
 
@@ -225,44 +238,49 @@ def main():
         log("contiguous peak ...")
         peak = bench_peak(128 << 20, K, W)
         log("peak:", peak)
-    peak_meas = max(peak.values()) if peak else None
+    peak_meas = max(v for v in peak.values() if isinstance(v, float)) if peak else None
 
     main_cfg = (8192, 4096)
     kv_cfg = (2048, 65536)
     small = [(2048, 512), (2048, 1024), (2048, 2048)]
     region_max = 2048 * 65536 * 2
+    cfgs = [main_cfg] + ([kv_cfg] if want("kv") else []) + (small if want("small") else [])
+    res = {c: {"tokens": c[0], "token_bytes": c[1], "bytes": c[0] * c[1]} for c in cfgs}
+
+    # Phase 1: zero-copy kernel, GFD Direct and per-token copies.  Only the
+    # direct poller's gather workers exist (the queue poller is not created
+    # yet), so the two pollers never compete for the host cores.
     direct = gfd_amd.CpuPollingThread(None, None, None, region_max, numa_node=-1)
     assert direct.init_direct_ce(), "init_direct_ce failed"
     dinfo = direct.info()
     log("direct poller:", dinfo)
-    queue = QueueRig(region_max) if want("queue") else None
-
-    def run_cfg(n, t, methods):
+    for n, t in cfgs:
         L = Layout(oracle, n, t)
-        r = {"tokens": n, "token_bytes": t, "bytes": L.bytes}
-        if "zc" in methods and want("zc"):
+        r = res[(n, t)]
+        if want("zc"):
             r["zero_copy"] = run_zero_copy(L, K, W)
             log("  %dx%d zero-copy: %s" % (n, t, r["zero_copy"]))
-        if "direct" in methods and want("direct"):
+        if want("direct"):
             r["direct"] = run_direct(direct, L, K, W)
             log("  %dx%d direct: %s" % (n, t, r["direct"]))
-        if "queue" in methods and queue is not None:
-            r["queue"] = queue.run(L, K, W)
-            log("  %dx%d queue: %s" % (n, t, r["queue"]))
-        if "memcpy" in methods and want("memcpy"):
+        if want("memcpy"):
             r["memcpy_per_token"] = run_memcpy_n(L, max(5, K // 5), 2)
             log("  %dx%d memcpy(N): %s" % (n, t, r["memcpy_per_token"]))
         del L
-        return r
-
-    allm = ("zc", "direct", "queue", "memcpy")
-    log("8192 x 4KB ...")
-    r_main = run_cfg(*main_cfg, allm)
-    r_kv = run_cfg(*kv_cfg, allm) if want("kv") else None
-    r_small = [run_cfg(n, t, allm) for n, t in small] if want("small") else []
-    if queue:
-        queue.close()
     direct.close()
+
+    # Phase 2: GFD Queue (GPU-submitted descriptors + CPU poller).
+    if want("queue"):
+        queue = QueueRig(region_max)
+        for n, t in cfgs:
+            L = Layout(oracle, n, t)
+            res[(n, t)]["queue"] = queue.run(L, K, W)
+            log("  %dx%d queue: %s" % (n, t, res[(n, t)]["queue"]))
+            del L
+        queue.close()
+    r_main = res[main_cfg]
+    r_kv = res.get(kv_cfg)
+    r_small = [res[c] for c in small if c in res]
 
     def frac(v):
         return {"of_theoretical": round(v / PCIE_GEN5_X16_GBPS, 4),

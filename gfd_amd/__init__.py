@@ -116,6 +116,7 @@ def _declare(L):
         "gfd_queue_wait": ([vp, c_u64, c_u64, vp, vp], c_int),
         "gfd_bench_memcpy_per_token": ([vp, vp, c_int, c_u32, c_int, c_int, pd], c_int),
         "gfd_bench_memcpy_contiguous": ([vp, vp, c_sz, c_int, c_int, c_int, pd], c_int),
+        "gfd_bench_sdma_contiguous": ([vp, vp, c_sz, c_int, c_int, c_int, c_int, pd, ctypes.POINTER(c_u32)], c_int),
         "gfd_bench_submit_direct": ([vp, vp, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_zero_copy_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
         "gfd_bench_queue": ([vp, vp, vp, c_int, c_u32, ctypes.POINTER(c_u64), c_int, c_int, c_u64, pd], c_int),

@@ -19,7 +19,7 @@ ARCH = os.environ.get("GFD_OFFLOAD_ARCH", "gfx950")
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 CXX = os.environ.get("CXX", "g++")
 
-INCLUDES = ["-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
+INCLUDES = ["-I" + os.path.join(ROOT, "include"), "-I" + CSRC, "-I/opt/rocm/include"]
 HIP_FLAGS = [
     "--offload-arch=" + ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall",
     # packed fp32 instructions are not to be generated for this target
@@ -65,7 +65,8 @@ def build(verbose=False):
             if warn and verbose:
                 print(warn, file=sys.stderr)
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "--offload-arch=" + ARCH, "-shared", "-o", tmp] + objs + ["-lpthread"]
+    cmd = [HIPCC, "--offload-arch=" + ARCH, "-shared", "-o", tmp] + objs + [
+        "-L/opt/rocm/lib", "-lhsa-runtime64", "-Wl,-rpath,/opt/rocm/lib", "-lpthread"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed: %s\n%s\n%s" % (" ".join(cmd), r.stdout, r.stderr))

@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "gather_engine.h"
+#include "sdma.h"
 #include "gfd/cpu_polling.h"
 #include "gfd/hip_shim.h"
 #include "gfd/sg_task_queue.h"
@@ -268,6 +269,42 @@ int gfd_bench_memcpy_contiguous(void* dst, const void* src, size_t bytes, int ns
     }
     for (int i = 0; i < ns; i++) gfd_hip_stream_destroy(st[i]);
     return rc ? fail(rc, "contiguous copy") : 0;
+}
+
+int gfd_bench_sdma_contiguous(void* dst, const void* src, size_t bytes, int channels, int pin, int warmup,
+                              int iters, double* times_us, uint32_t* engine_mask) {
+    int dev = 0;
+    gfd_hip_get_device(&dev);
+    gfd::SdmaQueue q;
+    int st = q.init(dev, channels, pin);
+    if (st) {
+        g_last_error = "SDMA init failed";
+        return st;
+    }
+    if (engine_mask) *engine_mask = q.engine_mask();
+    if (channels < 1) channels = 1;
+    const size_t per = ((bytes + channels - 1) / channels + 4095) & ~(size_t)4095;
+    for (int it = -warmup; it < iters; it++) {
+        auto t0 = std::chrono::steady_clock::now();
+        for (int c = 0; c < channels; c++) {
+            size_t off = (size_t)c * per;
+            if (off >= bytes) break;
+            size_t len = std::min(per, bytes - off);
+            st = q.copy(c, (uint64_t)(uintptr_t)dst + off, (const char*)src + off, len);
+            if (st) {
+                q.wait_all();
+                g_last_error = "SDMA copy failed";
+                return st;
+            }
+        }
+        if (q.wait_all()) {
+            g_last_error = "SDMA copy reported an error";
+            return -1;
+        }
+        auto t1 = std::chrono::steady_clock::now();
+        if (it >= 0) times_us[it] = elapsed_us(t0, t1);
+    }
+    return 0;
 }
 
 int gfd_bench_submit_direct(gfd_poller_t p, const gfd_sg_entry* entries, int count, int warmup, int iters,

@@ -2,24 +2,26 @@
 // (declaration: include/gfd/cpu_polling.h).
 //
 // Reference behaviour kept (src/cpu_polling.cpp:37-490,
-// src/batch_processor.cpp:448-723):
+// src/batch_processor.cpp:307-723):
 //   * a descriptor is consumed when sequence == read_idx + 1 (acquire); the
 //     poller zeroes sequence (release) and advances read_idx;
 //   * batches close at BATCH_THRESHOLD entries (BATCH_THRESHOLD_SMALL when the
 //     first entry is <= 2 KB), at MAX_BATCH_SIZE, on LAST_IN_BATCH / URGENT /
-//     LAST_IN_TILE, or after a 4096-pause gap with no new descriptor;
-//   * a dst-contiguous, equal-size, src-scattered batch is gathered into the
-//     next of NUM_STAGING_BUFS rotating pinned buffers and copied as one range;
-//   * done_idx only ever moves forward and only past slots whose copies have
-//     completed.
+//     LAST_IN_TILE (tiled and SG modes), or after a 4096-pause gap with no
+//     new descriptor;
+//   * a dst-contiguous, src-scattered batch is gathered into the next of
+//     NUM_STAGING_BUFS rotating pinned buffers and copied as one range;
+//   * done_idx only moves forward, and only past slots whose copies finished;
+//   * tiled mode: per-tile cumulative progress; SG mode: one list at a time,
+//     d_list_done[list_id] = 1 after the list's copies.
 // MI355X design differences:
-//   * done_idx is advanced per batch as soon as that batch's copies finish (a
-//     FIFO of completion events recorded on a signal stream that waits on all
-//     copy channels), not only when the ring goes idle;
-//   * the batch gather is pipelined: staging chunks are copied as soon as the
-//     worker pool finishes them;
-//   * per-list / per-tile signals are stream-ordered 8-byte writes into HBM
-//     queued behind the data copies (hipStreamWriteValue64).
+//   * copies are SDMA transfers tracked by fences (no GPU stream is involved,
+//     so a kernel spinning on done_idx can never block them);
+//   * done_idx advances per batch as soon as that batch's copies finish;
+//   * batch gathers are pipelined: each staging chunk is copied as soon as the
+//     worker pool has filled it;
+//   * HBM flags are 8-byte SDMA writes chained behind the data copies on the
+//     engine; flags in host memory are written by this thread on completion.
 #include "gfd/cpu_polling.h"
 
 #include <immintrin.h>
@@ -35,9 +37,17 @@
 #include "gfd/pcie_topology.h"
 #include "gfd/sg_task_queue.h"
 #include "gfd/staging_pool.h"
-#include "poller_internal.h"
 
 namespace gfd {
+
+// Ring of completion points, oldest at `tail`.
+struct CpuPollingThread::CompletionFifo {
+    static constexpr int N = 64;
+    CompletionSlot slots[N];
+    int head = 0;
+    int tail = 0;
+    int count = 0;
+};
 
 namespace {
 
@@ -63,6 +73,20 @@ void pin_self(int cpu) {
     CPU_ZERO(&cs);
     CPU_SET(cpu, &cs);
     pthread_setaffinity_np(pthread_self(), sizeof(cs), &cs);
+}
+
+struct ChunkCtx {
+    CopyEngineManager* ce;
+    DevicePtr dst0;
+    const char* staging;
+    int channels;
+    int err;
+};
+
+void issue_chunk(void* p, int chunk, size_t off, size_t len) {
+    ChunkCtx* c = (ChunkCtx*)p;
+    int e = c->ce->submit_on_channel(chunk % c->channels, c->dst0 + off, c->staging + off, len);
+    if (e && !c->err) c->err = e;
 }
 
 }  // namespace
@@ -93,21 +117,8 @@ CpuPollingThread::~CpuPollingThread() {
     gfd_hip_set_device(device_);
     ce_manager_.wait_completion();
     direct_ce_manager_.wait_completion();
-    if (signal_stream_) {
-        gfd_hip_stream_synchronize(signal_stream_);
-        gfd_hip_stream_destroy(signal_stream_);
-        signal_stream_ = nullptr;
-    }
-    for (int b = 0; b < NUM_STAGING_BUFS; b++) {
-        if (staging_events_[b]) gfd_hip_event_destroy(staging_events_[b]);
-        staging_events_[b] = nullptr;
-    }
-    if (fifo_) {
-        for (auto& s : fifo_->slots)
-            if (s.event) gfd_hip_event_destroy(s.event);
-        delete fifo_;
-        fifo_ = nullptr;
-    }
+    delete fifo_;
+    fifo_ = nullptr;
     if (staging_pool_set_ >= 0) {
         StagingPool::instance().release_buffers(staging_pool_set_);
         staging_pool_set_ = -1;
@@ -117,6 +128,8 @@ CpuPollingThread::~CpuPollingThread() {
     for (int b = 0; b < NUM_STAGING_BUFS; b++) staging_bufs_[b] = nullptr;
     StagingPool::free_pinned(direct_staging_);
     direct_staging_ = nullptr;
+    if (signal_values_) gfd_hip_host_free(signal_values_);
+    signal_values_ = nullptr;
     ce_manager_.shutdown();
     direct_ce_manager_.shutdown();
 }
@@ -155,7 +168,7 @@ bool CpuPollingThread::start_workers() {
 
 bool CpuPollingThread::init_copy_engine() {
     if (!use_ce_) {
-        GFD_LOG_ERROR("use_ce=false is not supported: copies always use the SDMA channels\n");
+        GFD_LOG_ERROR("use_ce=false is not supported: copies always use the SDMA engines\n");
         return false;
     }
     if (gfd_hip_set_device(device_) != 0) return false;
@@ -164,12 +177,13 @@ bool CpuPollingThread::init_copy_engine() {
         GFD_LOG_ERROR("copy engine init failed\n");
         return false;
     }
-    if (!signal_stream_ && gfd_hip_stream_create(&signal_stream_) != 0) {
-        GFD_LOG_ERROR("signal stream creation failed\n");
-        return false;
+    if (!signal_values_) {
+        if (gfd_hip_host_alloc((void**)&signal_values_, sizeof(uint64_t) * SIGNAL_SLOTS, GFD_HOST_DEFAULT) != 0) {
+            GFD_LOG_ERROR("signal value buffer allocation failed\n");
+            return false;
+        }
+        std::memset(signal_values_, 0, sizeof(uint64_t) * SIGNAL_SLOTS);
     }
-    for (auto& s : fifo_->slots)
-        if (!s.event && gfd_hip_event_create(&s.event, 0) != 0) return false;
 
     staging_buffer_size_ = total_cpu_size_;
     int got = 0;
@@ -195,11 +209,9 @@ bool CpuPollingThread::init_copy_engine() {
         staging_owned_ = true;
     }
     num_staging_bufs_ = got;
-    for (int b = 0; b < got; b++) {
-        if (!staging_events_[b] && gfd_hip_event_create(&staging_events_[b], 0) != 0) return false;
-        staging_event_pending_[b] = false;
-    }
-    GFD_LOG_INFO("queue staging: %d x %zu bytes (NUMA %d)\n", got, staging_buffer_size_, numa_node_);
+    for (int b = 0; b < NUM_STAGING_BUFS; b++) staging_fence_[b] = 0;
+    GFD_LOG_INFO("queue staging: %d x %zu bytes (NUMA %d), %d copy channel(s), SDMA engines 0x%x\n", got,
+                 staging_buffer_size_, numa_node_, ce_manager_.num_channels(), ce_manager_.sdma_engine_mask());
     return start_workers();
 }
 
@@ -207,6 +219,10 @@ void CpuPollingThread::start() {
     if (running_.load(std::memory_order_acquire)) return;
     if (!queue_) {
         GFD_LOG_ERROR("start(): no descriptor queue\n");
+        return;
+    }
+    if (!ce_manager_.is_initialized()) {
+        GFD_LOG_ERROR("start(): init_copy_engine() has not succeeded\n");
         return;
     }
     running_.store(true, std::memory_order_release);
@@ -223,27 +239,18 @@ void CpuPollingThread::publish_done(uint64_t value) {
     if (value > cur) __atomic_store_n(&queue_->done_idx, value, __ATOMIC_RELEASE);
 }
 
-// Record a completion point for everything submitted so far on the copy
-// channels; it publishes done_idx = done_value (and the tiles / lists noted in
-// the slot) once the GPU passes it.
+// Completion point for everything issued so far: once those copies finish,
+// done_idx = done_value and the pending host-side flags are written.
 void CpuPollingThread::push_completion(uint64_t done_value) {
     CompletionFifo& f = *fifo_;
     while (f.count == CompletionFifo::N) drain_completions(true);
     CompletionSlot& s = f.slots[f.head];
-    if (ce_manager_.make_stream_wait_on_all(signal_stream_) != 0 ||
-        gfd_hip_event_record(s.event, signal_stream_) != 0) {
-        // Could not record: wait for everything and publish directly.
-        ce_manager_.wait_completion();
-        gfd_hip_stream_synchronize(signal_stream_);
-        finish_slot(s_pending_);
-        publish_done(done_value);
-        s_pending_.clear();
-        return;
-    }
+    s.fence = ce_manager_.fence();
     s.done_value = done_value;
-    s.host_tiles.swap(s_pending_.host_tiles);
-    s.lists_done = s_pending_.lists_done;
-    s_pending_.clear();
+    s.host_tiles.swap(pending_.host_tiles);
+    s.host_lists.swap(pending_.host_lists);
+    s.lists_done = pending_.lists_done;
+    pending_.clear();
     f.head = (f.head + 1) % CompletionFifo::N;
     f.count++;
 }
@@ -252,10 +259,11 @@ void CpuPollingThread::finish_slot(CompletionSlot& s) {
     if (tiled_queue_)
         for (auto& tv : s.host_tiles)
             __atomic_store_n(&tiled_queue_->tile_chunk_done[tv.first], tv.second, __ATOMIC_RELEASE);
-    s.host_tiles.clear();
-    if (sg_queue_ && s.lists_done)
-        __atomic_fetch_add(&sg_queue_->lists_completed, (uint64_t)s.lists_done, __ATOMIC_RELEASE);
-    s.lists_done = 0;
+    if (sg_queue_) {
+        for (uint32_t id : s.host_lists) __atomic_store_n(&sg_queue_->d_list_done[id], 1ull, __ATOMIC_RELEASE);
+        if (s.lists_done) __atomic_fetch_add(&sg_queue_->lists_completed, (uint64_t)s.lists_done, __ATOMIC_RELEASE);
+    }
+    s.clear();
 }
 
 // Publish every completed slot in order; with `block`, wait for the oldest.
@@ -263,12 +271,10 @@ void CpuPollingThread::drain_completions(bool block) {
     CompletionFifo& f = *fifo_;
     while (f.count > 0) {
         CompletionSlot& s = f.slots[f.tail];
-        int q = gfd_hip_event_query(s.event);
-        if (q == 1) {
+        if (!ce_manager_.fence_done(s.fence)) {
             if (!block) return;
-            while ((q = gfd_hip_event_query(s.event)) == 1) cpu_relax();
+            if (ce_manager_.wait_fence(s.fence) != 0) GFD_LOG_ERROR("a copy reported an error\n");
         }
-        if (q != 0) GFD_LOG_ERROR("completion event error %d\n", q);
         finish_slot(s);
         publish_done(s.done_value);
         f.tail = (f.tail + 1) % CompletionFifo::N;
@@ -303,6 +309,7 @@ void CpuPollingThread::polling_loop() {
         Descriptor* d = &queue_->entries[read % QUEUE_SIZE];
         uint64_t seq = __atomic_load_n(&d->sequence, __ATOMIC_ACQUIRE);
         if (seq == read + 1) {
+            const uint64_t t0 = now_us();
             do {
                 take(d);
                 read++;
@@ -313,6 +320,7 @@ void CpuPollingThread::polling_loop() {
                 d = &queue_->entries[read % QUEUE_SIZE];
                 seq = __atomic_load_n(&d->sequence, __ATOMIC_ACQUIRE);
             } while (seq == read + 1);
+            total_queue_read_us_.fetch_add(now_us() - t0, std::memory_order_relaxed);
             const bool urgent = (or_flags & (FLAG_LAST_IN_BATCH | FLAG_URGENT | FLAG_LAST_IN_TILE)) != 0;
             if (n >= threshold || n >= MAX_BATCH_SIZE || urgent) flush_batch(batch.data(), n, or_flags);
         } else if (n > 0) {
@@ -362,34 +370,15 @@ void CpuPollingThread::flush_batch(Descriptor* batch, int& count, uint32_t& or_f
     or_flags = 0;
 }
 
-namespace {
-
-struct ChunkCtx {
-    CopyEngineManager* ce;
-    DevicePtr dst0;
-    const char* staging;
-    int channels;
-    int err;
-};
-
-void issue_chunk(void* p, int chunk, size_t off, size_t len) {
-    ChunkCtx* c = (ChunkCtx*)p;
-    int e = c->ce->submit_on_channel(chunk % c->channels, c->dst0 + off, c->staging + off, len);
-    if (e && !c->err) c->err = e;
-}
-
-}  // namespace
-
-// Copy a run list: maximal runs contiguous in both src and dst become one copy.
+// One copy per maximal run that is contiguous in both src and dst.
 void CpuPollingThread::copy_runs(const SGEntry* e, int count) {
-    int i = 0;
     std::vector<SGEntry>& runs = run_scratch_;
     runs.clear();
+    int i = 0;
     while (i < count) {
         SGEntry r = e[i];
         int j = i + 1;
-        while (j < count && e[j].dst == r.dst + r.size &&
-               (const char*)e[j].src == (const char*)r.src + r.size) {
+        while (j < count && e[j].dst == r.dst + r.size && (const char*)e[j].src == (const char*)r.src + r.size) {
             r.size += e[j].size;
             j++;
         }
@@ -401,26 +390,21 @@ void CpuPollingThread::copy_runs(const SGEntry* e, int count) {
     coalesced_entries_.fetch_add(runs.size(), std::memory_order_relaxed);
 }
 
-// Gather a dst-contiguous list through the next staging buffer; true if done.
+// Gather a dst-contiguous list through the next staging buffer; false if it
+// does not fit (the caller then copies runs directly).
 bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_t total) {
     if (num_staging_bufs_ == 0 || total > staging_buffer_size_ || !gather_) return false;
     const int cur = staging_cur_;
-    uint64_t t0 = now_us();
-    if (staging_event_pending_[cur]) {
-        gfd_hip_event_synchronize(staging_events_[cur]);
-        staging_event_pending_[cur] = false;
-    }
-    uint64_t t1 = now_us();
+    const uint64_t t0 = now_us();
+    if (ce_manager_.wait_fence(staging_fence_[cur]) != 0) GFD_LOG_ERROR("staging copy reported an error\n");
+    const uint64_t t1 = now_us();
     ChunkCtx ctx{&ce_manager_, e[0].dst, staging_bufs_[cur], ce_manager_.num_channels(), 0};
     {
         std::lock_guard<std::mutex> lock(gather_mutex_);
         gather_->run(e, count, total, staging_bufs_[cur], direct_chunk_bytes_, issue_chunk, &ctx);
     }
-    uint64_t t2 = now_us();
-    // The staging buffer is free again once every channel has passed this point.
-    ce_manager_.make_stream_wait_on_all(signal_stream_);
-    gfd_hip_event_record(staging_events_[cur], signal_stream_);
-    staging_event_pending_[cur] = true;
+    const uint64_t t2 = now_us();
+    staging_fence_[cur] = ce_manager_.fence();
     staging_cur_ = (cur + 1) % num_staging_bufs_;
     total_dma_wait_us_.fetch_add(t1 - t0, std::memory_order_relaxed);
     total_gather_us_.fetch_add(t2 - t1, std::memory_order_relaxed);
@@ -428,6 +412,25 @@ bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_
     coalesced_entries_.fetch_add(count, std::memory_order_relaxed);
     if (ctx.err) GFD_LOG_ERROR("staging copy submission failed (%d)\n", ctx.err);
     return true;
+}
+
+// Route one list: contiguous on both sides -> one copy; dst contiguous ->
+// staged gather; otherwise coalesced runs.
+void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total) {
+    const uint64_t t0 = now_us();
+    bool dst_contig = true, src_contig = true;
+    for (int i = 1; i < count && (dst_contig || src_contig); i++) {
+        if (e[i].dst != e[i - 1].dst + e[i - 1].size) dst_contig = false;
+        if ((const char*)e[i].src != (const char*)e[i - 1].src + e[i - 1].size) src_contig = false;
+    }
+    if (count == 1 || (dst_contig && src_contig)) {
+        SGEntry one{e[0].dst, e[0].src, total};
+        ce_manager_.submit_scatter_gather(&one, 1);
+        coalesced_entries_.fetch_add(1, std::memory_order_relaxed);
+    } else if (!(dst_contig && gather_through_staging(e, count, total))) {
+        copy_runs(e, count);
+    }
+    total_dma_submit_us_.fetch_add(now_us() - t0, std::memory_order_relaxed);
 }
 
 bool CpuPollingThread::process_batch(Descriptor* batch, int count) {
@@ -447,76 +450,75 @@ bool CpuPollingThread::process_batch(Descriptor* batch, int count) {
     return true;
 }
 
-// Route one list: contiguous on both sides -> one copy; dst contiguous ->
-// staged gather; otherwise coalesced runs.
-void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total) {
-    uint64_t t0 = now_us();
-    bool dst_contig = true, src_contig = true;
-    for (int i = 1; i < count; i++) {
-        if (e[i].dst != e[i - 1].dst + e[i - 1].size) dst_contig = false;
-        if ((const char*)e[i].src != (const char*)e[i - 1].src + e[i - 1].size) src_contig = false;
-        if (!dst_contig && !src_contig) break;
-    }
-    if (count == 1 || (dst_contig && src_contig)) {
-        SGEntry one{e[0].dst, e[0].src, total};
-        ce_manager_.submit_scatter_gather(&one, 1);
-        coalesced_entries_.fetch_add(1, std::memory_order_relaxed);
-    } else if (!(dst_contig && gather_through_staging(e, count, total))) {
-        copy_runs(e, count);
-    }
-    total_dma_submit_us_.fetch_add(now_us() - t0, std::memory_order_relaxed);
+// 8-byte store of `value` into HBM at `dst`, ordered on the copy engines after
+// every copy with fence >= after_begin issued so far.
+void CpuPollingThread::signal_device_u64(uint64_t* dst, uint64_t value, uint64_t after_begin) {
+    const int slot = signal_next_;
+    signal_next_ = (signal_next_ + 1) % SIGNAL_SLOTS;
+    ce_manager_.wait_fence(signal_fence_[slot]);  // previous use of this value slot has finished
+    signal_values_[slot] = value;
+    const uint64_t end = ce_manager_.fence();
+    if (ce_manager_.submit_after((DevicePtr)(uintptr_t)dst, &signal_values_[slot], sizeof(uint64_t), after_begin,
+                                 end) != 0)
+        GFD_LOG_ERROR("flag write submission failed\n");
+    signal_fence_[slot] = ce_manager_.fence();
 }
 
-// Tiled mode: entries carry tile_id in user_data >> 32.  Every tile's
-// cumulative progress is written after this batch's copies complete.
+// Tiled mode: entries carry tile_id in user_data >> 32.  Every tile touched by
+// the batch gets its cumulative progress written after the batch's copies.
 void CpuPollingThread::process_batch_tiled(Descriptor* batch, int count, uint64_t cur_read) {
     (void)cur_read;
+    const uint64_t f0 = ce_manager_.fence();
     process_batch(batch, count);
     std::vector<uint32_t>& touched = tile_scratch_;
     touched.clear();
     for (int i = 0; i < count; i++) {
-        uint32_t tid = (uint32_t)(batch[i].user_data >> 32);
+        const uint32_t tid = (uint32_t)(batch[i].user_data >> 32);
         if (tid >= (uint32_t)MAX_TILES) continue;
         if (tile_progress_[tid]++ == tile_marked_[tid]) touched.push_back(tid);
     }
+    if (tile_done_on_device_ < 0)
+        tile_done_on_device_ = tiled_queue_->d_tile_chunk_done ? gfd_hip_pointer_is_device(tiled_queue_->d_tile_chunk_done) : 0;
     for (uint32_t tid : touched) {
         tile_marked_[tid] = tile_progress_[tid];
-        if (tiled_queue_->d_tile_chunk_done) {
-            ce_manager_.make_stream_wait_on_all(signal_stream_);
-            gfd_hip_stream_write_u64(signal_stream_, (uint64_t)(uintptr_t)(tiled_queue_->d_tile_chunk_done + tid),
-                                     tile_progress_[tid]);
-        } else {
-            s_pending_.host_tiles.emplace_back(tid, tile_progress_[tid]);
-        }
+        if (tiled_queue_->d_tile_chunk_done && tile_done_on_device_)
+            signal_device_u64(tiled_queue_->d_tile_chunk_done + tid, tile_progress_[tid], f0);
+        else
+            pending_.host_tiles.emplace_back(tid, tile_progress_[tid]);
     }
 }
 
 // SG mode: entries carry list_id in user_data >> 32; each list is copied on
-// its own and d_list_done[list_id] = 1 is written behind its copies.
+// its own and d_list_done[list_id] = 1 once its copies have finished.
 void CpuPollingThread::process_batch_sg(Descriptor* batch, int count, uint64_t cur_read) {
     (void)cur_read;
-    std::vector<SGEntry>& sg = sg_scratch_;
+    if (list_done_on_device_ < 0)
+        list_done_on_device_ = sg_queue_->d_list_done ? gfd_hip_pointer_is_device(sg_queue_->d_list_done) : 0;
+    std::vector<SGEntry> list;
     int i = 0;
     while (i < count) {
         const uint32_t list_id = (uint32_t)(batch[i].user_data >> 32);
         int j = i;
         size_t total = 0;
-        sg.clear();
+        list.clear();
         while (j < count && (uint32_t)(batch[j].user_data >> 32) == list_id) {
-            sg.push_back(SGEntry{batch[j].dst_addr, (const void*)(uintptr_t)batch[j].src_addr, batch[j].size});
+            list.push_back(SGEntry{batch[j].dst_addr, (const void*)(uintptr_t)batch[j].src_addr, batch[j].size});
             total += batch[j].size;
             j++;
         }
-        submit_list(sg.data(), (int)sg.size(), total);
+        const uint64_t f0 = ce_manager_.fence();
+        submit_list(list.data(), (int)list.size(), total);
         total_bytes_copied_.fetch_add(total, std::memory_order_relaxed);
         descriptors_processed_.fetch_add(j - i, std::memory_order_relaxed);
         batches_submitted_.fetch_add(1, std::memory_order_relaxed);
         const bool list_end = (batch[j - 1].flags & FLAG_LAST_IN_TILE) != 0;
-        if (list_end && sg_queue_ && sg_queue_->d_list_done && list_id < (uint32_t)MAX_SG_LISTS) {
-            ce_manager_.make_stream_wait_on_all(signal_stream_);
-            gfd_hip_stream_write_u64(signal_stream_, (uint64_t)(uintptr_t)(sg_queue_->d_list_done + list_id), 1);
+        if (list_end && sg_queue_->d_list_done && list_id < (uint32_t)MAX_SG_LISTS) {
+            if (list_done_on_device_)
+                signal_device_u64(sg_queue_->d_list_done + list_id, 1, f0);
+            else
+                pending_.host_lists.push_back(list_id);
         }
-        if (list_end) s_pending_.lists_done++;
+        if (list_end) pending_.lists_done++;
         i = j;
     }
 }

@@ -104,7 +104,7 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
         err = direct_ce_manager_.submit_scatter_gather(entries, count);
     }
 
-    int werr = direct_ce_manager_.wait_completion();
+    const int werr = direct_ce_manager_.wait_completion();
     const auto t1 = std::chrono::steady_clock::now();
     if (err || werr) {
         GFD_LOG_ERROR("submit_direct: copy failed (%d / %d)\n", err, werr);

@@ -2,10 +2,15 @@
 #include "gather_engine.h"
 
 #include <immintrin.h>
+#include <linux/futex.h>
 #include <pthread.h>
 #include <sched.h>
+#include <sys/syscall.h>
+#include <unistd.h>
 
 #include <algorithm>
+#include <climits>
+#include <cstdlib>
 #include <cstring>
 
 namespace gfd {
@@ -75,6 +80,25 @@ void stream_copy(void* dst, const void* src, size_t n) {
 
 void store_fence() { _mm_sfence(); }
 
+namespace {
+
+void futex_wait(std::atomic<uint32_t>* addr, uint32_t expected) {
+    syscall(SYS_futex, reinterpret_cast<uint32_t*>(addr), FUTEX_WAIT_PRIVATE, expected, nullptr, nullptr, 0);
+}
+
+void futex_wake_all(std::atomic<uint32_t>* addr) {
+    syscall(SYS_futex, reinterpret_cast<uint32_t*>(addr), FUTEX_WAKE_PRIVATE, INT32_MAX, nullptr, nullptr, 0);
+}
+
+// Pause iterations an idle worker spins before it sleeps (a few hundred
+// microseconds: long enough to bridge back-to-back gathers).
+unsigned spin_limit() {
+    const char* v = std::getenv("GFD_GATHER_SPIN");
+    return (v && *v) ? (unsigned)std::strtoul(v, nullptr, 0) : 20000u;
+}
+
+}  // namespace
+
 GatherEngine::GatherEngine(const std::vector<int>& worker_cpus) {
     wstate_.reset(new WorkerState[worker_cpus.size() ? worker_cpus.size() : 1]);
     for (size_t w = 0; w < worker_cpus.size(); w++)
@@ -82,11 +106,15 @@ GatherEngine::GatherEngine(const std::vector<int>& worker_cpus) {
 }
 
 GatherEngine::~GatherEngine() {
-    running_.store(false, std::memory_order_release);
+    running_.store(false, std::memory_order_seq_cst);
+    epoch_.fetch_add(1, std::memory_order_seq_cst);
+    futex_wake_all(&epoch_);
     for (auto& t : threads_)
         if (t.joinable()) t.join();
 }
 
+// Spin on the job counter, then sleep on it: idle workers give their cores
+// back to the application and the poller instead of burning them.
 void GatherEngine::worker_main(int w, int cpu) {
     if (cpu >= 0) {
         cpu_set_t cs;
@@ -94,20 +122,32 @@ void GatherEngine::worker_main(int w, int cpu) {
         CPU_SET(cpu, &cs);
         pthread_setaffinity_np(pthread_self(), sizeof(cs), &cs);
     }
-    uint64_t seen = 0;
-    unsigned idle = 0;
-    while (running_.load(std::memory_order_acquire)) {
-        uint64_t e = epoch_.load(std::memory_order_acquire);
+    const unsigned spin = spin_limit();
+    uint32_t seen = 0;
+    for (;;) {
+        const uint32_t e = epoch_.load(std::memory_order_acquire);
+        if (!running_.load(std::memory_order_acquire)) break;
         if (e != seen) {
             seen = e;
             do_slices();
             wstate_[w].done_epoch.store(e, std::memory_order_release);
-            idle = 0;
             continue;
         }
-        cpu_relax();
-        // After a long idle stretch, let other runnable threads in.
-        if (++idle > (1u << 16)) sched_yield();
+        bool moved = false;
+        for (unsigned i = 0; i < spin; i++) {
+            cpu_relax();
+            if (epoch_.load(std::memory_order_relaxed) != seen) {
+                moved = true;
+                break;
+            }
+        }
+        if (moved) continue;
+        // Dekker handshake with run(): either run() sees sleepers_ > 0 and
+        // wakes us, or we see the new epoch here and do not sleep.
+        sleepers_.fetch_add(1, std::memory_order_seq_cst);
+        if (epoch_.load(std::memory_order_seq_cst) == seen && running_.load(std::memory_order_seq_cst))
+            futex_wait(&epoch_, seen);
+        sleepers_.fetch_sub(1, std::memory_order_seq_cst);
     }
 }
 
@@ -190,7 +230,8 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
 
     const int nw = num_workers();
     const bool caller_copy = caller_copies_ >= 0 ? (caller_copies_ != 0 || nw == 0) : (nw < 2);
-    const uint64_t ep = epoch_.fetch_add(1, std::memory_order_acq_rel) + 1;
+    const uint32_t ep = epoch_.fetch_add(1, std::memory_order_seq_cst) + 1;
+    if (sleepers_.load(std::memory_order_seq_cst) > 0) futex_wake_all(&epoch_);
     const int ns = (int)slices_.size();
 
     int ready = 0;

@@ -62,8 +62,8 @@ private:
         int chunk;
     };
     struct alignas(64) WorkerState {
-        std::atomic<uint64_t> done_epoch{0};
-        char pad[56];
+        std::atomic<uint32_t> done_epoch{0};
+        char pad[60];
     };
 
     void worker_main(int w, int cpu);
@@ -72,7 +72,9 @@ private:
 
     std::vector<std::thread> threads_;
     std::unique_ptr<WorkerState[]> wstate_;
-    alignas(64) std::atomic<uint64_t> epoch_{0};
+    // Job counter; 32-bit so idle workers can sleep on it with a futex.
+    alignas(64) std::atomic<uint32_t> epoch_{0};
+    alignas(64) std::atomic<int> sleepers_{0};
     alignas(64) std::atomic<bool> running_{true};
     alignas(64) std::atomic<int> next_slice_{0};
 

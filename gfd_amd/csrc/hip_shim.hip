@@ -114,3 +114,12 @@ int gfd_hip_memset_d8(uint64_t dst, int value, size_t bytes) {
 extern "C" int gfd_hip_stream_write_u64(gfd_stream_t s, uint64_t dst, uint64_t value) {
     return (int)hipStreamWriteValue64((hipStream_t)s, (void*)(uintptr_t)dst, value, 0);
 }
+
+extern "C" int gfd_hip_pointer_is_device(const void* p) {
+    hipPointerAttribute_t a;
+    if (!p || hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return a.type == hipMemoryTypeDevice ? 1 : 0;
+}

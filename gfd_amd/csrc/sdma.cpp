@@ -1,0 +1,187 @@
+// SdmaQueue (see sdma.h).
+#include "sdma.h"
+
+#include <hsa/hsa.h>
+#include <hsa/hsa_ext_amd.h>
+#include <immintrin.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "gfd/hip_shim.h"
+#include "gfd/log.h"
+
+namespace gfd {
+
+namespace {
+
+constexpr size_t kRing = 4096;  // in-flight copies before the issuer waits
+
+struct AgentSearch {
+    uint32_t bdf;
+    uint32_t domain;
+    hsa_agent_t gpu{0};
+    hsa_agent_t cpu{0};
+    bool have_gpu = false;
+    bool have_cpu = false;
+    int gpu_index = 0;
+    int want_index = 0;
+    hsa_agent_t nth_gpu{0};
+    bool have_nth = false;
+};
+
+hsa_status_t visit_agent(hsa_agent_t a, void* p) {
+    AgentSearch* s = (AgentSearch*)p;
+    hsa_device_type_t type;
+    if (hsa_agent_get_info(a, HSA_AGENT_INFO_DEVICE, &type) != HSA_STATUS_SUCCESS) return HSA_STATUS_SUCCESS;
+    if (type == HSA_DEVICE_TYPE_CPU && !s->have_cpu) {
+        s->cpu = a;
+        s->have_cpu = true;
+    } else if (type == HSA_DEVICE_TYPE_GPU) {
+        uint32_t bdf = 0, dom = 0;
+        hsa_agent_get_info(a, (hsa_agent_info_t)HSA_AMD_AGENT_INFO_BDFID, &bdf);
+        hsa_agent_get_info(a, (hsa_agent_info_t)HSA_AMD_AGENT_INFO_DOMAIN, &dom);
+        if (bdf == s->bdf && dom == s->domain && !s->have_gpu) {
+            s->gpu = a;
+            s->have_gpu = true;
+        }
+        if (s->gpu_index == s->want_index) {
+            s->nth_gpu = a;
+            s->have_nth = true;
+        }
+        s->gpu_index++;
+    }
+    return HSA_STATUS_SUCCESS;
+}
+
+inline hsa_signal_t sig(uint64_t h) {
+    hsa_signal_t s;
+    s.handle = h;
+    return s;
+}
+
+}  // namespace
+
+SdmaQueue::SdmaQueue() = default;
+
+SdmaQueue::~SdmaQueue() {
+    if (!inited_) return;
+    wait_all();
+    for (uint64_t h : signals_)
+        if (h) hsa_signal_destroy(sig(h));
+    hsa_shut_down();
+}
+
+int SdmaQueue::init(int device, int channels, int pin_engines) {
+    if (inited_) return 0;
+    hsa_status_t st = hsa_init();  // reference-counted; HIP holds its own reference
+    if (st != HSA_STATUS_SUCCESS) return (int)st;
+    AgentSearch s;
+    s.want_index = device;
+    char bus[64] = {0};
+    unsigned dom = 0, b = 0, d = 0, f = 0;
+    if (gfd_hip_pci_bus_id(bus, sizeof(bus), device) == 0 && std::sscanf(bus, "%x:%x:%x.%x", &dom, &b, &d, &f) == 4) {
+        s.bdf = (b << 8) | (d << 3) | f;
+        s.domain = dom;
+    } else {
+        s.bdf = 0xFFFFFFFFu;
+        s.domain = 0xFFFFFFFFu;
+    }
+    hsa_iterate_agents(visit_agent, &s);
+    if (!s.have_cpu || !(s.have_gpu || s.have_nth)) {
+        GFD_LOG_ERROR("SDMA: HSA agents for device %d not found\n", device);
+        hsa_shut_down();
+        return (int)HSA_STATUS_ERROR_INVALID_AGENT;
+    }
+    gpu_agent_ = s.have_gpu ? s.gpu.handle : s.nth_gpu.handle;
+    cpu_agent_ = s.cpu.handle;
+    hsa_agent_t gpu{gpu_agent_}, cpu{cpu_agent_};
+    engine_mask_ = 0;
+    hsa_amd_memory_copy_engine_status(gpu, cpu, &engine_mask_);
+    engines_.clear();
+    for (uint32_t m = engine_mask_; m; m &= m - 1) engines_.push_back(m & (~m + 1));
+    channels_ = channels > 0 ? channels : 1;
+    pin_ = pin_engines && !engines_.empty();
+    signals_.assign(kRing, 0);
+    for (size_t i = 0; i < kRing; i++) {
+        hsa_signal_t h;
+        st = hsa_signal_create(0, 0, nullptr, &h);
+        if (st != HSA_STATUS_SUCCESS) return (int)st;
+        signals_[i] = h.handle;
+    }
+    next_seq_ = tail_ = 0;
+    error_ = 0;
+    inited_ = true;
+    GFD_LOG_DEBUG("SDMA: engines mask 0x%x, %d channel(s), pinned=%d\n", engine_mask_, channels_, (int)pin_);
+    return 0;
+}
+
+uint64_t SdmaQueue::retire() {
+    while (tail_ < next_seq_) {
+        hsa_signal_value_t v = hsa_signal_load_scacquire(sig(signals_[tail_ % kRing]));
+        if (v > 0) break;
+        if (v < 0) error_ = -1;
+        tail_++;
+    }
+    return tail_;
+}
+
+int SdmaQueue::wait(uint64_t seq_end) {
+    if (seq_end > next_seq_) seq_end = next_seq_;
+    while (retire() < seq_end) {
+        hsa_signal_t s = sig(signals_[tail_ % kRing]);
+        hsa_signal_wait_scacquire(s, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX, HSA_WAIT_STATE_ACTIVE);
+    }
+    return error_ ? -1 : 0;
+}
+
+bool SdmaQueue::host_source_ok(const void* p, size_t n) {
+    const uintptr_t lo = (uintptr_t)p, hi = lo + n;
+    if (lo >= ok_lo_ && hi <= ok_hi_) return true;
+    hsa_amd_pointer_info_t info;
+    std::memset(&info, 0, sizeof(info));
+    info.size = sizeof(info);
+    if (hsa_amd_pointer_info(const_cast<void*>(p), &info, nullptr, nullptr, nullptr) != HSA_STATUS_SUCCESS)
+        return false;
+    if (info.type != HSA_EXT_POINTER_TYPE_HSA && info.type != HSA_EXT_POINTER_TYPE_LOCKED) return false;
+    const uintptr_t base = (uintptr_t)info.hostBaseAddress;
+    if (!base || lo < base || hi > base + info.sizeInBytes) return false;
+    ok_lo_ = base;
+    ok_hi_ = base + info.sizeInBytes;
+    return true;
+}
+
+int SdmaQueue::copy(int channel, uint64_t dst, const void* src, size_t bytes, uint64_t* seq,
+                    const uint64_t* deps, int ndeps) {
+    if (!inited_) return (int)HSA_STATUS_ERROR_NOT_INITIALIZED;
+    // Reuse of a ring slot requires its previous copy to be finished.
+    if (next_seq_ - tail_ >= kRing) {
+        if (wait(next_seq_ - kRing + 1) != 0) return -1;
+    }
+    const uint64_t s = next_seq_;
+    hsa_signal_t cs = sig(signals_[s % kRing]);
+    hsa_signal_store_relaxed(cs, 1);
+    hsa_signal_t dep_sigs[16];
+    uint32_t nd = 0;
+    for (int i = 0; i < ndeps && nd < 16; i++)
+        if (deps[i] >= tail_ && deps[i] < s) dep_sigs[nd++] = sig(signals_[deps[i] % kRing]);
+    hsa_agent_t gpu{gpu_agent_}, cpu{cpu_agent_};
+    hsa_status_t st;
+    if (pin_) {
+        const uint32_t eng = engines_[(size_t)channel % engines_.size()];
+        st = hsa_amd_memory_async_copy_on_engine((void*)(uintptr_t)dst, gpu, src, cpu, bytes, nd,
+                                                 nd ? dep_sigs : nullptr, cs, (hsa_amd_sdma_engine_id_t)eng, true);
+    } else {
+        st = hsa_amd_memory_async_copy((void*)(uintptr_t)dst, gpu, src, cpu, bytes, nd, nd ? dep_sigs : nullptr, cs);
+    }
+    if (st != HSA_STATUS_SUCCESS) {
+        hsa_signal_store_relaxed(cs, 0);
+        return (int)st;
+    }
+    next_seq_ = s + 1;
+    if (seq) *seq = s;
+    return 0;
+}
+
+}  // namespace gfd

@@ -1,0 +1,81 @@
+#pragma once
+// SdmaQueue: host-to-HBM copies issued straight to the GPU's SDMA engines
+// through the HSA runtime (hsa_amd_memory_async_copy[_on_engine]) with one
+// HSA completion signal per copy.
+//
+// Why not HIP streams: a HIP stream's markers and cross-stream waits are AQL
+// packets on one of the process's few hardware compute queues.  When a GPU
+// kernel spins on a host-written completion flag (queue-mode waits, the
+// warp-specialised transfer waves) and a stream of the poller shares that
+// hardware queue, the poller's packets sit behind the spinning kernel and
+// never run.  SDMA copies with HSA signals never touch a compute queue, and
+// the host learns of completion by reading the signals.
+//
+// Copies get consecutive sequence numbers; retire() advances the completed
+// prefix.  Channels map to SDMA engines reported by
+// hsa_amd_memory_copy_engine_status (channel i -> i-th available engine), or
+// to runtime-chosen engines when engine pinning is off.
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+namespace gfd {
+
+class SdmaQueue {
+public:
+    SdmaQueue();
+    ~SdmaQueue();
+    SdmaQueue(const SdmaQueue&) = delete;
+    SdmaQueue& operator=(const SdmaQueue&) = delete;
+
+    // Find the HSA agents of HIP device `device` and the host; set up
+    // `channels` channels.  pin_engines: 1 = one SDMA engine per channel,
+    // 0 = let the runtime choose.  Returns 0 or an HSA status.
+    int init(int device, int channels, int pin_engines);
+    bool ok() const { return inited_; }
+    int num_channels() const { return channels_; }
+    int num_engines() const { return (int)engines_.size(); }
+    uint32_t engine_mask() const { return engine_mask_; }
+
+    // Enqueue one host->device copy (or device<-host flag write) on a channel.
+    // deps: copies (by sequence number) that must finish first (GPU-side wait).
+    // Returns 0 or an HSA status; *seq receives the copy's sequence number.
+    int copy(int channel, uint64_t dst, const void* src, size_t bytes, uint64_t* seq = nullptr,
+             const uint64_t* deps = nullptr, int ndeps = 0);
+
+    uint64_t issued() const { return next_seq_; }
+    // Advance past completed copies; returns the first sequence number not yet
+    // known complete (every copy below it has finished).
+    uint64_t retire();
+    bool done(uint64_t seq_end) { return retire() >= seq_end; }
+    // Block until every copy with sequence < seq_end has finished.  Returns 0,
+    // or -1 if a copy reported an error.
+    int wait(uint64_t seq_end);
+    int wait_all() { return wait(next_seq_); }
+    // Sticky: nonzero once any copy reported failure.
+    int error() const { return error_; }
+
+    // True if [p, p + n) lies in host memory the runtime has pinned and mapped
+    // for the GPU (hipHostMalloc / registered), i.e. a legal SDMA source.
+    // Pageable memory is not: the caller must copy it another way.
+    bool host_source_ok(const void* p, size_t n);
+
+private:
+    struct Slot;
+    int grow();
+
+    bool inited_ = false;
+    int channels_ = 0;
+    bool pin_ = false;
+    uint64_t gpu_agent_ = 0;
+    uint64_t cpu_agent_ = 0;
+    uint32_t engine_mask_ = 0;
+    std::vector<uint32_t> engines_;
+    std::vector<uint64_t> signals_;  // ring of hsa_signal_t handles
+    uint64_t next_seq_ = 0;
+    uint64_t tail_ = 0;  // all seq < tail_ complete
+    int error_ = 0;
+    uintptr_t ok_lo_ = 0, ok_hi_ = 0;  // last pinned range found
+};
+
+}  // namespace gfd

@@ -1,12 +1,15 @@
 #pragma once
-// CopyEngineManager: asynchronous host-to-HBM copies on several SDMA-backed
-// HIP streams (include/gfd/copy_engine.h:23-98 and src/copy_engine.cpp:13-208
+// CopyEngineManager: asynchronous host-to-HBM copies on the GPU's SDMA
+// engines (include/gfd/copy_engine.h:23-98 and src/copy_engine.cpp:13-208
 // of the reference, re-designed for ROCm).
 //
-// On MI355X a hipMemcpyAsync from pinned host memory to HBM runs on an SDMA
-// engine; copies on different streams can run on different engines.  The
-// manager owns `num_channels` non-blocking streams (default priority: no
-// priority streams are created) and one completion event per stream.
+// Default backend: copies are issued straight to SDMA engines through the HSA
+// runtime (one engine per channel when the engines can be pinned), each with
+// an HSA completion signal; completion is tracked by sequence number
+// ("fences").  Nothing is placed on a GPU compute queue, so copies and
+// completion tracking keep running while GPU kernels spin on host-written
+// flags.  The HIP-stream backend (GFD_COPY_BACKEND=hip) issues hipMemcpyAsync
+// on per-channel non-blocking streams instead.
 #include <cstddef>
 #include <cstdint>
 
@@ -19,7 +22,7 @@ namespace gfd {
 // reference).  It must stay an integer: gathers compute `dst - min_dst`.
 using DevicePtr = uint64_t;
 
-// 0 on success, otherwise the HIP error code.
+// 0 on success, otherwise the HIP / HSA error code.
 using Status = int;
 constexpr Status GFD_SUCCESS = 0;
 
@@ -33,10 +36,10 @@ constexpr Status GFD_SUCCESS = 0;
         }                                                                       \
     } while (0)
 
-// Upper bound on copy channels (streams) per manager.  The default used when
-// init() is given 0 is DEFAULT_CE_CHANNELS.
+// Upper bound on copy channels per manager; DEFAULT_CE_CHANNELS when init()
+// is given 0.
 constexpr int MAX_CE_CHANNELS = 8;
-constexpr int DEFAULT_CE_CHANNELS = 4;
+constexpr int DEFAULT_CE_CHANNELS = 2;
 
 constexpr int MAX_SG_ENTRIES_PER_BATCH = 8192;
 
@@ -49,16 +52,21 @@ struct SGEntry {
 };
 static_assert(sizeof(SGEntry) == 24, "SGEntry must be 24 bytes");
 
+class SdmaQueue;
+
 class CopyEngineManager {
 public:
+    enum Backend { BACKEND_SDMA = 0, BACKEND_HIP = 1 };
+
     CopyEngineManager();
     ~CopyEngineManager();
     CopyEngineManager(const CopyEngineManager&) = delete;
     CopyEngineManager& operator=(const CopyEngineManager&) = delete;
 
-    // Create the channel streams and events on `device` (the reference takes a
-    // CUcontext; HIP has one primary context per device).
-    // num_channels: 0 = DEFAULT_CE_CHANNELS, clamped to MAX_CE_CHANNELS.
+    // Set up the channels on `device` (the reference takes a CUcontext; HIP
+    // has one primary context per device).  num_channels: 0 = default.
+    // The backend comes from GFD_COPY_BACKEND (sdma | hip; default sdma) and
+    // engine pinning from GFD_SDMA_PIN (1 default, 0 = runtime's choice).
     Status init(int device, int num_channels = 0);
     void shutdown();
 
@@ -72,18 +80,32 @@ public:
     // range of entries (src/copy_engine.cpp:103-131).
     Status submit_scatter_gather(const SGEntry* entries, int count);
 
-    // Enqueue one copy on a given channel (used by the pipelined direct path).
+    // Enqueue one copy on a given channel.
     Status submit_on_channel(int channel, DevicePtr dst, const void* src, size_t size);
 
-    // Block until every copy submitted since the last wait has completed.
+    // Enqueue a small copy that starts only after the copies with fence
+    // numbers in [after_begin, after_end) have finished (ordered on the copy
+    // engines, no host wait).  Used for completion flags in HBM.
+    Status submit_after(DevicePtr dst, const void* src, size_t size, uint64_t after_begin,
+                        uint64_t after_end);
+
+    // Fences: every copy gets the next fence number.  fence() is the number the
+    // next copy will get; fence_done(f) is true once every copy below f has
+    // finished.
+    uint64_t fence() const;
+    bool fence_done(uint64_t f);
+    Status wait_fence(uint64_t f);
+
+    // Block until every copy submitted so far has completed.
     Status wait_completion();
     Status submit_and_wait(const SGEntry* entries, int count);
 
-    // Record `event` on the channel used by the most recent submission.
+    // Reference API: record `event` after the most recent copy.  SDMA backend:
+    // waits for the copies on the host, after which the event counts as passed.
     Status record_event_on_last_stream(gfd_event_t event);
 
-    // Make `stream` wait (on the GPU, not the CPU) for every channel with
-    // outstanding copies.
+    // Reference API: make `stream` wait for every outstanding copy.  SDMA
+    // backend: waits on the host (the stream then has nothing to wait for).
     Status make_stream_wait_on_all(gfd_stream_t stream);
 
     uint64_t get_total_submissions() const { return total_submissions_; }
@@ -93,10 +115,16 @@ public:
     bool is_initialized() const { return initialized_; }
     int num_channels() const { return num_channels_; }
     int device() const { return device_; }
-    gfd_stream_t stream(int ch) const { return streams_[ch]; }
+    Backend backend() const { return backend_; }
+    int num_sdma_engines() const;
+    uint32_t sdma_engine_mask() const;
 
 private:
+    Status issue(int ch, DevicePtr dst, const void* src, size_t size);
+
     int device_ = 0;
+    Backend backend_ = BACKEND_SDMA;
+    SdmaQueue* sdma_ = nullptr;
     gfd_stream_t streams_[MAX_CE_CHANNELS] = {};
     gfd_event_t events_[MAX_CE_CHANNELS] = {};
     int num_channels_ = DEFAULT_CE_CHANNELS;
@@ -104,6 +132,7 @@ private:
     int next_channel_ = 0;
     int last_channel_ = 0;
     uint32_t dirty_mask_ = 0;
+    uint64_t hip_fence_ = 0;
 
     uint64_t total_submissions_ = 0;
     uint64_t total_entries_ = 0;

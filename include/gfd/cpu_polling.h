@@ -4,17 +4,16 @@
 //   * submit_direct()  — the CPU hands an SG list straight in ("GFD Direct");
 //   * start()/stop()   — a pinned thread polls the descriptor ring that GPU
 //                        kernels fill ("GFD Queue"), batches contiguous runs and
-//                        signals completion through done_idx / per-tile /
-//                        per-list signals.
+//                        signals completion through done_idx and per-tile /
+//                        per-list flags.
 // Both gather scattered host tokens into pinned staging memory with a pool of
-// NUMA-local worker threads and stream the staging to HBM over several SDMA
-// channels.
+// worker threads and stream the staging to HBM over SDMA engines.
 //
 // Threading: init_copy_engine()/init_direct_ce() must run on a thread that can
 // use the GPU; the polling thread makes the device current itself.
 // submit_direct() may run concurrently with the polling thread: the gather
-// workers are shared under a mutex and each path has its own staging and its
-// own copy channels.
+// workers are shared under a mutex and each path has its own staging buffers
+// and its own copy channels.
 #include <atomic>
 #include <cstring>
 #include <mutex>
@@ -42,11 +41,12 @@ public:
     // gpu_base:       base of the HBM destination region (informational)
     // cpu_base/total_cpu_size: the host source region; staging buffers are
     //                 sized to total_cpu_size
-    // use_ce:         false = no SDMA (kept for API compatibility; rejected)
+    // use_ce:         false = no copy engines (kept for API compatibility;
+    //                 init_copy_engine() then fails)
     // numa_node:      host node for staging and workers; -1 = the GPU's node
     // core_offset:    kept for API compatibility (ignored: CPUs are chosen from
     //                 the node's CPU list and the process affinity mask)
-    // num_ce_channels: copy channels per manager (0 = DEFAULT_CE_CHANNELS)
+    // num_ce_channels: copy channels per manager (0 = default)
     // exclusive_core_base/count: explicit CPU range for poller + workers
     CpuPollingThread(DescriptorQueue* queue, void* gpu_base, void* cpu_base,
                      size_t total_cpu_size, bool use_ce = true, int numa_node = 0,
@@ -56,7 +56,7 @@ public:
     CpuPollingThread(const CpuPollingThread&) = delete;
     CpuPollingThread& operator=(const CpuPollingThread&) = delete;
 
-    // Channels, staging buffers, gather workers, signal stream.
+    // Copy channels, staging buffers, gather workers.
     bool init_copy_engine();
 
     // Separate copy channels and staging for submit_direct().
@@ -70,7 +70,7 @@ public:
     //                               -> pipelined gather: the workers fill
     //                                  staging chunk by chunk and each finished
     //                                  chunk is copied at once on the next channel
-    //   otherwise                   -> one async copy per entry
+    //   otherwise                   -> one copy per maximal contiguous run
     double submit_direct(const SGEntry* entries, int count);
 
     void set_tiled_queue(TiledQueue* tq) { tiled_queue_ = tq; }
@@ -91,6 +91,7 @@ public:
     uint64_t get_dma_submit_us() const { return total_dma_submit_us_.load(std::memory_order_relaxed); }
     uint64_t get_queue_read_us() const { return total_queue_read_us_.load(std::memory_order_relaxed); }
 
+    // Only between runs (the polling thread stopped or idle).
     void reset_stats() {
         descriptors_processed_.store(0, std::memory_order_relaxed);
         batches_submitted_.store(0, std::memory_order_relaxed);
@@ -111,23 +112,26 @@ public:
     int poller_cpu() const { return poller_cpu_; }
     int numa_node() const { return numa_node_; }
     int device() const { return device_; }
-    // Chunk size of the pipelined direct path (bytes of payload per copy).
+    const CopyEngineManager& get_direct_ce_manager() const { return direct_ce_manager_; }
+    // Chunk size of the pipelined gather (payload bytes per copy).
     void set_direct_chunk_bytes(size_t b) { direct_chunk_bytes_ = b ? b : 1; }
     size_t direct_chunk_bytes() const { return direct_chunk_bytes_; }
-    // Gather slice size (bytes a thread copies per work item).
+    // Gather slice size (bytes one thread copies per work item).
     void set_gather_slice_bytes(size_t b);
     size_t gather_slice_bytes() const { return slice_bytes_; }
     size_t staging_buffer_size() const { return staging_buffer_size_; }
     int num_staging_buffers() const { return num_staging_bufs_; }
 
-    // Host-side effects to apply once a batch's copies have completed.
+    // Host-side effects applied once a batch's copies have completed.
     struct CompletionSlot {
-        gfd_event_t event = nullptr;
-        uint64_t done_value = 0;
-        std::vector<std::pair<uint32_t, uint64_t>> host_tiles;  // (tile, progress)
+        uint64_t fence = 0;       // every copy below this fence belongs to the batch or earlier
+        uint64_t done_value = 0;  // done_idx to publish
+        std::vector<std::pair<uint32_t, uint64_t>> host_tiles;  // (tile, progress) for host flags
+        std::vector<uint32_t> host_lists;                       // list ids for host flags
         uint32_t lists_done = 0;
         void clear() {
             host_tiles.clear();
+            host_lists.clear();
             lists_done = 0;
         }
     };
@@ -143,20 +147,13 @@ private:
     void submit_list(const SGEntry* e, int count, size_t total);
     bool gather_through_staging(const SGEntry* e, int count, size_t total);
     void copy_runs(const SGEntry* e, int count);
+    void signal_device_u64(uint64_t* dst, uint64_t value, uint64_t after_begin);
     void publish_done(uint64_t value);
     void push_completion(uint64_t done_value);
     void drain_completions(bool block);
     void finish_slot(CompletionSlot& s);
     bool start_workers();
     bool choose_cpus();
-
-    CompletionFifo* fifo_ = nullptr;
-    CompletionSlot s_pending_;
-    std::vector<SGEntry> sg_scratch_;
-    std::vector<SGEntry> run_scratch_;
-    std::vector<uint32_t> tile_scratch_;
-    uint64_t tile_marked_[MAX_TILES] = {};
-    size_t slice_bytes_ = 0;
 
     DescriptorQueue* queue_;
     TiledQueue* tiled_queue_ = nullptr;
@@ -174,13 +171,12 @@ private:
 
     CopyEngineManager ce_manager_;
     CopyEngineManager direct_ce_manager_;
-    gfd_stream_t signal_stream_ = nullptr;
 
-    // Queue-path staging: rotating buffers, each guarded by an event.
+    // Queue-path staging: rotating buffers; a buffer is reused once the
+    // copies out of it (fence) have finished.
     static constexpr int NUM_STAGING_BUFS = 5;
     char* staging_bufs_[NUM_STAGING_BUFS] = {};
-    gfd_event_t staging_events_[NUM_STAGING_BUFS] = {};
-    bool staging_event_pending_[NUM_STAGING_BUFS] = {};
+    uint64_t staging_fence_[NUM_STAGING_BUFS] = {};
     size_t staging_buffer_size_ = 0;
     int num_staging_bufs_ = 0;
     int staging_cur_ = 0;
@@ -192,11 +188,26 @@ private:
     size_t direct_staging_size_ = 0;
     size_t direct_chunk_bytes_ = 2u << 20;
 
-    bool has_async_dma_ = false;
-    uint64_t latest_async_read_ = 0;
+    // Pinned source values for flag writes into HBM (ring; a slot is reused
+    // only after its copy has finished, which the fence order guarantees once
+    // the ring has wrapped past completed fences).
+    static constexpr int SIGNAL_SLOTS = 4096;
+    uint64_t* signal_values_ = nullptr;
+    uint64_t signal_fence_[SIGNAL_SLOTS] = {};
+    int signal_next_ = 0;
+    int list_done_on_device_ = -1;  // -1 unknown, 0 host memory, 1 HBM
+    int tile_done_on_device_ = -1;
 
-    // Tiled / SG completion signalling.
+    // Tiled / SG completion bookkeeping.
     uint64_t tile_progress_[MAX_TILES] = {};
+    uint64_t tile_marked_[MAX_TILES] = {};
+
+    CompletionFifo* fifo_ = nullptr;
+    CompletionSlot pending_;
+    std::vector<SGEntry> sg_scratch_;
+    std::vector<SGEntry> run_scratch_;
+    std::vector<uint32_t> tile_scratch_;
+    size_t slice_bytes_ = 0;
 
     // Gather workers shared by both paths.
     GatherEngine* gather_ = nullptr;

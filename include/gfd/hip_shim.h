@@ -60,3 +60,8 @@ extern "C" {
 // per-tile / per-list completion signals after the data copies).
 int gfd_hip_stream_write_u64(gfd_stream_t s, uint64_t dst, uint64_t value);
 }
+
+extern "C" {
+// 1 if `p` is device (HBM) memory, 0 if host / unknown.
+int gfd_hip_pointer_is_device(const void* p);
+}

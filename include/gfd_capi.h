@@ -147,6 +147,10 @@ int gfd_bench_memcpy_per_token(void* dst, const uint64_t* src_addrs, int num_tok
                                uint32_t token_size, int warmup, int iters, double* times_us);
 int gfd_bench_memcpy_contiguous(void* dst, const void* src, size_t bytes, int num_streams,
                                 int warmup, int iters, double* times_us);
+/* One contiguous copy split over `channels` SDMA channels (engines pinned when
+ * pin != 0, else runtime-chosen); also reports the engine mask. */
+int gfd_bench_sdma_contiguous(void* dst, const void* src, size_t bytes, int channels, int pin,
+                              int warmup, int iters, double* times_us, uint32_t* engine_mask);
 int gfd_bench_submit_direct(gfd_poller_t p, const gfd_sg_entry* entries, int count, int warmup,
                             int iters, double* times_us);
 /* Zero-copy tokens kernel: wall time launch->sync and HIP-event kernel time. */

@@ -227,8 +227,13 @@ static void* worker_main(void* p) {
     while (atomic_load_explicit(&pool->running, memory_order_acquire)) {
         if (atomic_load_explicit(&t->has_work, memory_order_acquire)) {
             copy_range(t->entries, t->start, t->end, t->staging, t->min_dst);
-            atomic_store_explicit(&t->done, 1, memory_order_release);
+            /* Clear has_work BEFORE raising done.  The reference stores done
+             * first (src/parallel_gather.cpp:66-67); a caller that sees done
+             * can then publish the next task before the late has_work = false
+             * lands, and that store erases the new task (the caller waits
+             * forever).  Output bytes are unaffected by the order. */
             atomic_store_explicit(&t->has_work, 0, memory_order_release);
+            atomic_store_explicit(&t->done, 1, memory_order_release);
         } else {
             _mm_pause();
         }

@@ -104,3 +104,28 @@ def test_host_gather_empty_is_noop():
     out = np.full(16, 3, np.uint8)
     gfd_amd.host_gather((gfd_amd.SGEntry * 1)(), 0, out, num_workers=2)
     assert (out == 3).all()
+
+
+def test_host_gather_with_sleeping_workers():
+    # GFD_GATHER_SPIN=0: idle workers sleep on the job counter at once, so every
+    # gather has to wake them (futex path) and still produce the same bytes.
+    import subprocess
+    import sys
+
+    code = (
+        "import numpy as np, gfd_amd, oracle, time\n"
+        "n, t = 512, 4096\n"
+        "region = np.empty(n * 2 * t, np.uint8); oracle.fill_tokens(region, n, t, 2 * t)\n"
+        "perm = oracle.permutation(n)\n"
+        "e = gfd_amd.make_entries(region.ctypes.data + perm.astype(np.uint64) * np.uint64(2 * t), 0, t)\n"
+        "exp = oracle.expected_gather(region, perm, t, 2 * t)\n"
+        "for k in range(5):\n"
+        "    out = np.zeros(n * t, np.uint8)\n"
+        "    gfd_amd.host_gather(e, n, out, chunk_bytes=256 << 10, slice_bytes=32 << 10, num_workers=4)\n"
+        "    assert (out == exp).all()\n"
+        "    time.sleep(0.01)\n"
+        "print('ok')\n"
+    )
+    env = dict(os.environ, GFD_GATHER_SPIN="0", PYTHONPATH=ROOT)
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stderr

@@ -250,3 +250,23 @@ def test_rmsnorm_closed_forms():
     assert np.allclose(np.mean(y1.astype(np.float64) ** 2, 1), 1.0, atol=1e-5)
     w2 = rng.standard_normal(256).astype(np.float32)
     assert np.allclose(oracle.rmsnorm_rows(x, w2, 0.0), y1 * w2, atol=1e-5)
+
+
+@pytest.mark.timeout(120)
+def test_pool_back_to_back_gathers_do_not_lose_tasks():
+    # Regression for the task hand-off order: thousands of back-to-back
+    # gathers must all complete (a worker that clears has_work after raising
+    # done can erase the next task and stall the caller).
+    n, t = 64, 4096
+    region = np.empty(n * 2 * t, np.uint8)
+    oracle.fill_tokens(region, n, t, 2 * t)
+    perm = oracle.permutation(n)
+    entries = oracle.make_entries(region.ctypes.data, 0, perm, t, 2 * t)
+    staging = np.zeros(n * t, np.uint8)
+    pool = oracle.GatherPool(7)
+    try:
+        times = pool.time(entries, n, staging, 0, 3000)
+    finally:
+        pool.close()
+    assert len(times) == 3000
+    assert (staging == oracle.expected_gather(region, perm, t, 2 * t)).all()
