@@ -61,6 +61,10 @@ class PollerInfo(ctypes.Structure):
     ]
 
 
+TRACE_DTYPE = np.dtype([("t_ns", np.uint64), ("kind", np.uint32), ("a", np.uint32), ("b", np.uint64)])
+TRACE_KINDS = {1: "batch_first", 2: "flush", 3: "issued", 4: "done", 5: "gap_flush", 6: "direct_begin",
+               7: "chunk", 8: "direct_end"}
+
 _lib = None
 _SIGNATURES = {}
 
@@ -103,6 +107,8 @@ def _declare(L):
         "gfd_poller_get_stats": ([vp, ctypes.POINTER(PollerStats)], c_int),
         "gfd_poller_reset_stats": ([vp], None),
         "gfd_poller_get_info": ([vp, ctypes.POINTER(PollerInfo)], c_int),
+        "gfd_poller_set_trace": ([vp, c_int], None),
+        "gfd_poller_read_trace": ([vp, vp, c_int], c_int),
         "gfd_poller_set_direct_chunk_bytes": ([vp, c_u64], None),
         "gfd_poller_set_gather_slice_bytes": ([vp, c_u64], None),
         "gfd_host_gather": ([vp, c_int, vp, c_u64, c_u64, c_int, vp], c_int),
@@ -297,6 +303,15 @@ class CpuPollingThread:
         d["worker_cpus"] = list(i.worker_cpus)[: i.num_gather_workers]
         return d
 
+    def set_trace(self, on=True):
+        lib().gfd_poller_set_trace(self._h, int(bool(on)))
+
+    def read_trace(self, max_events=16384):
+        """Drain the timeline trace: structured array (t_ns, kind, a, b)."""
+        buf = np.zeros(max_events, dtype=TRACE_DTYPE)
+        n = lib().gfd_poller_read_trace(self._h, buf.ctypes.data, max_events)
+        return buf[:n]
+
     def set_direct_chunk_bytes(self, b):
         lib().gfd_poller_set_direct_chunk_bytes(self._h, b)
 
@@ -349,11 +364,11 @@ def host_gather(entries, count, out, chunk_bytes=0, slice_bytes=0, num_workers=0
     completion order (see gfd_host_gather in include/gfd_capi.h)."""
     out_ptr = out.ctypes.data if isinstance(out, np.ndarray) else out
     total = sum(int(entries[i].size) for i in range(count)) if count else 0
-    nchunks = max(1, -(-total // chunk_bytes)) if chunk_bytes else 1
+    nchunks = (max(1, -(-total // chunk_bytes)) if chunk_bytes else 1) + 1
     order = np.full(nchunks, -1, dtype=np.int32)
     _check(lib().gfd_host_gather(ctypes.cast(entries, ctypes.c_void_p), count, out_ptr, chunk_bytes, slice_bytes,
                                  num_workers, order.ctypes.data), "gfd_host_gather")
-    return order
+    return order[order >= 0]
 
 
 def zero_copy_gather_tokens(src_addrs_ptr, dst_ptr, token_size, num_tokens, stream=None):

@@ -171,6 +171,16 @@ int gfd_poller_get_info(gfd_poller_t p, gfd_poller_info* out) {
     return 0;
 }
 
+void gfd_poller_set_trace(gfd_poller_t p, int on) {
+    if (p) P(p)->set_trace(on != 0);
+}
+
+int gfd_poller_read_trace(gfd_poller_t p, gfd_trace_event* out, int max) {
+    static_assert(sizeof(gfd_trace_event) == sizeof(gfd::CpuPollingThread::TraceEvent), "trace event layout");
+    if (!p || !out || max <= 0) return 0;
+    return P(p)->read_trace(reinterpret_cast<gfd::CpuPollingThread::TraceEvent*>(out), max);
+}
+
 void gfd_poller_set_direct_chunk_bytes(gfd_poller_t p, uint64_t b) {
     if (p) P(p)->set_direct_chunk_bytes(b);
 }

@@ -76,6 +76,7 @@ void pin_self(int cpu) {
 }
 
 struct ChunkCtx {
+    CpuPollingThread* self;
     CopyEngineManager* ce;
     DevicePtr dst0;
     const char* staging;
@@ -87,6 +88,7 @@ void issue_chunk(void* p, int chunk, size_t off, size_t len) {
     ChunkCtx* c = (ChunkCtx*)p;
     int e = c->ce->submit_on_channel(chunk % c->channels, c->dst0 + off, c->staging + off, len);
     if (e && !c->err) c->err = e;
+    c->self->trace(CpuPollingThread::TRACE_CHUNK, (uint32_t)chunk, len);
 }
 
 }  // namespace
@@ -108,6 +110,7 @@ CpuPollingThread::CpuPollingThread(DescriptorQueue* queue, void* gpu_base, void*
     gfd_hip_get_device(&device_);
     direct_chunk_bytes_ = env_size("GFD_DIRECT_CHUNK_BYTES", direct_chunk_bytes_);
     fifo_ = new CompletionFifo();
+    if (env_size("GFD_TRACE", 0)) set_trace(true);
 }
 
 CpuPollingThread::~CpuPollingThread() {
@@ -135,6 +138,31 @@ CpuPollingThread::~CpuPollingThread() {
 }
 
 int CpuPollingThread::num_gather_workers() const { return gather_ ? gather_->num_workers() : 0; }
+
+void CpuPollingThread::set_trace(bool on) {
+    std::lock_guard<std::mutex> lock(trace_mutex_);
+    if (on && trace_buf_.empty()) trace_buf_.resize(TRACE_CAP);
+    trace_on_.store(on, std::memory_order_release);
+}
+
+void CpuPollingThread::trace(uint32_t kind, uint32_t a, uint64_t b) {
+    if (!trace_on_.load(std::memory_order_relaxed)) return;
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    std::lock_guard<std::mutex> lock(trace_mutex_);
+    if (trace_buf_.empty()) return;
+    if (trace_head_ - trace_tail_ == (uint64_t)TRACE_CAP) trace_tail_++;  // overwrite the oldest
+    trace_buf_[trace_head_ % TRACE_CAP] = TraceEvent{(uint64_t)ts.tv_sec * 1000000000ull + (uint64_t)ts.tv_nsec,
+                                                     kind, a, b};
+    trace_head_++;
+}
+
+int CpuPollingThread::read_trace(TraceEvent* out, int max) {
+    std::lock_guard<std::mutex> lock(trace_mutex_);
+    int n = 0;
+    while (n < max && trace_tail_ < trace_head_) out[n++] = trace_buf_[trace_tail_++ % TRACE_CAP];
+    return n;
+}
 
 void CpuPollingThread::set_gather_slice_bytes(size_t b) {
     slice_bytes_ = b;
@@ -277,6 +305,7 @@ void CpuPollingThread::drain_completions(bool block) {
         }
         finish_slot(s);
         publish_done(s.done_value);
+        trace(TRACE_DONE, 0, s.done_value);
         f.tail = (f.tail + 1) % CompletionFifo::N;
         f.count--;
         block = false;  // only the oldest is waited for
@@ -304,22 +333,29 @@ void CpuPollingThread::polling_loop() {
         n++;
     };
 
+    // read_idx lives in the same cache line as done_idx, which GPU waiters
+    // poll over PCIe: it is published once per run of consumed descriptors
+    // rather than once per descriptor, so the line is not bounced per entry.
+    uint64_t read = queue_->read_idx;
     while (running_.load(std::memory_order_acquire)) {
-        uint64_t read = queue_->read_idx;
         Descriptor* d = &queue_->entries[read % QUEUE_SIZE];
         uint64_t seq = __atomic_load_n(&d->sequence, __ATOMIC_ACQUIRE);
         if (seq == read + 1) {
             const uint64_t t0 = now_us();
+            if (n == 0) {
+                if (gather_) gather_->prewake();  // wake workers while the batch is read
+                trace(TRACE_BATCH_FIRST, (uint32_t)(read % QUEUE_SIZE), read);
+            }
             do {
                 take(d);
                 read++;
-                __atomic_store_n(&queue_->read_idx, read, __ATOMIC_RELEASE);
                 if (n == 1) threshold = batch[0].size <= 2048 ? BATCH_THRESHOLD_SMALL : BATCH_THRESHOLD;
                 if (n >= threshold || n >= MAX_BATCH_SIZE) break;
                 if (per_chunk_flush && (or_flags & FLAG_LAST_IN_TILE)) break;
                 d = &queue_->entries[read % QUEUE_SIZE];
                 seq = __atomic_load_n(&d->sequence, __ATOMIC_ACQUIRE);
             } while (seq == read + 1);
+            __atomic_store_n(&queue_->read_idx, read, __ATOMIC_RELEASE);
             total_queue_read_us_.fetch_add(now_us() - t0, std::memory_order_relaxed);
             const bool urgent = (or_flags & (FLAG_LAST_IN_BATCH | FLAG_URGENT | FLAG_LAST_IN_TILE)) != 0;
             if (n >= threshold || n >= MAX_BATCH_SIZE || urgent) flush_batch(batch.data(), n, or_flags);
@@ -332,7 +368,10 @@ void CpuPollingThread::polling_loop() {
                     break;
                 }
             }
-            if (!filled) flush_batch(batch.data(), n, or_flags);
+            if (!filled) {
+                trace(TRACE_GAP_FLUSH, (uint32_t)n, read);
+                flush_batch(batch.data(), n, or_flags);
+            }
         } else if (fifo_->count > 0) {
             drain_completions(false);
             cpu_relax();
@@ -343,11 +382,11 @@ void CpuPollingThread::polling_loop() {
 
     // Drain what is already committed, then wait for every copy.
     for (;;) {
-        uint64_t read = queue_->read_idx;
         Descriptor* d = &queue_->entries[read % QUEUE_SIZE];
         if (__atomic_load_n(&d->sequence, __ATOMIC_ACQUIRE) != read + 1) break;
         take(d);
-        __atomic_store_n(&queue_->read_idx, read + 1, __ATOMIC_RELEASE);
+        read++;
+        __atomic_store_n(&queue_->read_idx, read, __ATOMIC_RELEASE);
         if (n >= MAX_BATCH_SIZE) flush_batch(batch.data(), n, or_flags);
     }
     flush_batch(batch.data(), n, or_flags);
@@ -357,6 +396,11 @@ void CpuPollingThread::polling_loop() {
 void CpuPollingThread::flush_batch(Descriptor* batch, int& count, uint32_t& or_flags) {
     if (count == 0) return;
     const uint64_t cur_read = queue_->read_idx;
+    if (trace_on_.load(std::memory_order_relaxed)) {
+        uint64_t bytes = 0;
+        for (int i = 0; i < count; i++) bytes += batch[i].size;
+        trace(TRACE_FLUSH, (uint32_t)count, bytes);
+    }
     if (sg_queue_ && (or_flags & FLAG_LAST_IN_TILE)) {
         process_batch_sg(batch, count, cur_read);
     } else if (tiled_queue_) {
@@ -364,6 +408,7 @@ void CpuPollingThread::flush_batch(Descriptor* batch, int& count, uint32_t& or_f
     } else {
         process_batch(batch, count);
     }
+    trace(TRACE_ISSUED, 0, ce_manager_.fence());
     push_completion(cur_read);
     drain_completions(false);
     count = 0;
@@ -398,7 +443,7 @@ bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_
     const uint64_t t0 = now_us();
     if (ce_manager_.wait_fence(staging_fence_[cur]) != 0) GFD_LOG_ERROR("staging copy reported an error\n");
     const uint64_t t1 = now_us();
-    ChunkCtx ctx{&ce_manager_, e[0].dst, staging_bufs_[cur], ce_manager_.num_channels(), 0};
+    ChunkCtx ctx{this, &ce_manager_, e[0].dst, staging_bufs_[cur], ce_manager_.num_channels(), 0};
     {
         std::lock_guard<std::mutex> lock(gather_mutex_);
         gather_->run(e, count, total, staging_bufs_[cur], direct_chunk_bytes_, issue_chunk, &ctx);

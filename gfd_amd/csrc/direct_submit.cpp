@@ -23,6 +23,7 @@ namespace gfd {
 namespace {
 
 struct DirectCtx {
+    CpuPollingThread* self;
     CopyEngineManager* ce;
     DevicePtr dst0;
     const char* staging;
@@ -34,6 +35,7 @@ void direct_chunk(void* p, int chunk, size_t off, size_t len) {
     DirectCtx* c = (DirectCtx*)p;
     int e = c->ce->submit_on_channel(chunk % c->channels, c->dst0 + off, c->staging + off, len);
     if (e && !c->err) c->err = e;
+    c->self->trace(CpuPollingThread::TRACE_CHUNK, (uint32_t)chunk, len);
 }
 
 constexpr size_t kContiguousSplitMin = 8u << 20;  // split one contiguous copy above this
@@ -62,6 +64,7 @@ bool CpuPollingThread::init_direct_ce() {
 double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
     if (!direct_ce_manager_.is_initialized() || count <= 0 || !entries) return -1.0;
     const auto t0 = std::chrono::steady_clock::now();
+    if (gather_) gather_->prewake();  // workers wake while the list is inspected
     if (direct_ce_manager_.pin_context() != 0) return -1.0;
 
     size_t total = 0;
@@ -73,6 +76,7 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
             src_contig = false;
     }
 
+    trace(TRACE_DIRECT_BEGIN, (uint32_t)count, total);
     int err = 0;
     const int nch = direct_ce_manager_.num_channels();
     if (dst_contig && src_contig) {
@@ -89,7 +93,7 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
     } else if (dst_contig && direct_staging_ && total <= direct_staging_size_) {
         std::lock_guard<std::mutex> lock(gather_mutex_);
         if (gather_) {
-            DirectCtx ctx{&direct_ce_manager_, entries[0].dst, direct_staging_, nch, 0};
+            DirectCtx ctx{this, &direct_ce_manager_, entries[0].dst, direct_staging_, nch, 0};
             gather_->run(entries, count, total, direct_staging_, direct_chunk_bytes_, direct_chunk, &ctx);
             err = ctx.err;
         } else {
@@ -106,6 +110,7 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
 
     const int werr = direct_ce_manager_.wait_completion();
     const auto t1 = std::chrono::steady_clock::now();
+    trace(TRACE_DIRECT_END, 0, (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count());
     if (err || werr) {
         GFD_LOG_ERROR("submit_direct: copy failed (%d / %d)\n", err, werr);
         return -1.0;

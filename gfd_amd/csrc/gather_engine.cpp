@@ -90,17 +90,23 @@ void futex_wake_all(std::atomic<uint32_t>* addr) {
     syscall(SYS_futex, reinterpret_cast<uint32_t*>(addr), FUTEX_WAKE_PRIVATE, INT32_MAX, nullptr, nullptr, 0);
 }
 
-// Pause iterations an idle worker spins before it sleeps (a few hundred
-// microseconds: long enough to bridge back-to-back gathers).
-unsigned spin_limit() {
-    const char* v = std::getenv("GFD_GATHER_SPIN");
-    return (v && *v) ? (unsigned)std::strtoul(v, nullptr, 0) : 20000u;
+// Microseconds an idle worker spins before it sleeps: long enough to bridge
+// the copy tail between back-to-back gathers (GFD_GATHER_SPIN_US).
+uint64_t spin_limit_ns() {
+    const char* v = std::getenv("GFD_GATHER_SPIN_US");
+    const uint64_t us = (v && *v) ? (uint64_t)std::strtoull(v, nullptr, 0) : 1000u;
+    return us * 1000u;
+}
+
+inline uint64_t mono_ns() {
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (uint64_t)ts.tv_sec * 1000000000ull + (uint64_t)ts.tv_nsec;
 }
 
 }  // namespace
 
 GatherEngine::GatherEngine(const std::vector<int>& worker_cpus) {
-    wstate_.reset(new WorkerState[worker_cpus.size() ? worker_cpus.size() : 1]);
     for (size_t w = 0; w < worker_cpus.size(); w++)
         threads_.emplace_back(&GatherEngine::worker_main, this, (int)w, worker_cpus[w]);
 }
@@ -113,33 +119,42 @@ GatherEngine::~GatherEngine() {
         if (t.joinable()) t.join();
 }
 
-// Spin on the job counter, then sleep on it: idle workers give their cores
-// back to the application and the poller instead of burning them.
+// Job hand-off.  run() builds the job, sets open_, bumps epoch_ and wakes
+// sleepers; when every chunk is complete it clears open_ and returns without
+// waiting for the workers.  A worker joins a job by raising active_ and then
+// checking open_; run() rebuilds job state only after active_ has dropped to
+// zero.  With sequentially consistent operations on both counters, a worker
+// either is counted before run() looks (and run() waits for it) or sees open_
+// cleared and leaves without touching the job.
 void GatherEngine::worker_main(int w, int cpu) {
+    (void)w;
     if (cpu >= 0) {
         cpu_set_t cs;
         CPU_ZERO(&cs);
         CPU_SET(cpu, &cs);
         pthread_setaffinity_np(pthread_self(), sizeof(cs), &cs);
     }
-    const unsigned spin = spin_limit();
-    uint32_t seen = 0;
+    const uint64_t spin_ns = spin_limit_ns();
+    uint32_t seen = epoch_.load(std::memory_order_acquire);
     for (;;) {
-        const uint32_t e = epoch_.load(std::memory_order_acquire);
         if (!running_.load(std::memory_order_acquire)) break;
+        const uint32_t e = epoch_.load(std::memory_order_acquire);
         if (e != seen) {
             seen = e;
-            do_slices();
-            wstate_[w].done_epoch.store(e, std::memory_order_release);
+            active_.fetch_add(1, std::memory_order_seq_cst);
+            if (open_.load(std::memory_order_seq_cst)) do_slices();
+            active_.fetch_sub(1, std::memory_order_seq_cst);
             continue;
         }
         bool moved = false;
-        for (unsigned i = 0; i < spin; i++) {
+        const uint64_t t_end = mono_ns() + spin_ns;
+        for (unsigned i = 1;; i++) {
             cpu_relax();
             if (epoch_.load(std::memory_order_relaxed) != seen) {
                 moved = true;
                 break;
             }
+            if ((i & 255) == 0 && mono_ns() >= t_end) break;
         }
         if (moved) continue;
         // Dekker handshake with run(): either run() sees sleepers_ > 0 and
@@ -149,6 +164,10 @@ void GatherEngine::worker_main(int w, int cpu) {
             futex_wait(&epoch_, seen);
         sleepers_.fetch_sub(1, std::memory_order_seq_cst);
     }
+}
+
+void GatherEngine::prewake() {
+    if (sleepers_.load(std::memory_order_seq_cst) > 0) futex_wake_all(&epoch_);
 }
 
 void GatherEngine::copy_slice(const Slice& s) {
@@ -170,10 +189,11 @@ void GatherEngine::copy_slice(const Slice& s) {
     }
 }
 
+// Claim and copy slices until none are left.  Returns after the last claim.
 void GatherEngine::do_slices() {
-    const int ns = (int)slices_.size();
+    const int ns = num_slices_;
     for (;;) {
-        int s = next_slice_.fetch_add(1, std::memory_order_relaxed);
+        const int s = next_slice_.fetch_add(1, std::memory_order_relaxed);
         if (s >= ns) break;
         copy_slice(slices_[s]);
         store_fence();
@@ -184,8 +204,20 @@ void GatherEngine::do_slices() {
 void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* staging,
                        size_t chunk_bytes, ChunkFn on_chunk, void* ctx) {
     if (count <= 0 || total == 0) return;
-    if (chunk_bytes == 0) chunk_bytes = total;
-    const int nchunks = (int)((total + chunk_bytes - 1) / chunk_bytes);
+    if (chunk_bytes == 0 || chunk_bytes > total) chunk_bytes = total;
+    // Workers still inside the previous job must leave before its state changes.
+    while (active_.load(std::memory_order_seq_cst) != 0) cpu_relax();
+
+    // Chunk edges: a short first chunk gets the first copy going early.
+    size_t first = first_chunk_bytes_ ? first_chunk_bytes_ : chunk_bytes / 8;
+    if (first < 64 * 1024) first = 64 * 1024;
+    if (first > chunk_bytes) first = chunk_bytes;
+    chunk_end_.clear();
+    for (size_t end = first;; end += chunk_bytes) {
+        chunk_end_.push_back(std::min(end, total));
+        if (end >= total) break;
+    }
+    const int nchunks = (int)chunk_end_.size();
 
     // Cut the destination stream into slices that never cross a chunk edge.
     slices_.clear();
@@ -193,17 +225,17 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     size_t eo = 0;
     size_t pos = 0;
     for (int c = 0; c < nchunks; c++) {
-        size_t cend = std::min(total, (size_t)(c + 1) * chunk_bytes);
+        const size_t cend = chunk_end_[c];
         while (pos < cend) {
             while (e < count && eo == entries[e].size) {  // skip spent / empty entries
                 e++;
                 eo = 0;
             }
-            size_t len = std::min(slice_bytes_, cend - pos);
+            const size_t len = std::min(slice_bytes_, cend - pos);
             slices_.push_back(Slice{e, eo, pos, len, c});
             size_t adv = len;
             while (adv) {
-                size_t avail = entries[e].size - eo;
+                const size_t avail = entries[e].size - eo;
                 if (avail > adv) {
                     eo += adv;
                     adv = 0;
@@ -226,25 +258,26 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     entries_ = entries;
     count_ = count;
     staging_ = staging;
+    num_slices_ = (int)slices_.size();
     next_slice_.store(0, std::memory_order_relaxed);
 
     const int nw = num_workers();
-    const bool caller_copy = caller_copies_ >= 0 ? (caller_copies_ != 0 || nw == 0) : (nw < 2);
-    const uint32_t ep = epoch_.fetch_add(1, std::memory_order_seq_cst) + 1;
+    const bool caller_copy = caller_copies_ != 0 || nw == 0;
+    open_.store(true, std::memory_order_seq_cst);
+    epoch_.fetch_add(1, std::memory_order_seq_cst);
     if (sleepers_.load(std::memory_order_seq_cst) > 0) futex_wake_all(&epoch_);
-    const int ns = (int)slices_.size();
+    const int ns = num_slices_;
 
     int ready = 0;
     while (ready < nchunks) {
         if (remaining_[ready].load(std::memory_order_acquire) == 0) {
-            size_t off = (size_t)ready * chunk_bytes;
-            size_t len = std::min(chunk_bytes, total - off);
-            on_chunk(ctx, ready, off, len);
+            const size_t off = ready ? chunk_end_[ready - 1] : 0;
+            on_chunk(ctx, ready, off, chunk_end_[ready] - off);
             ready++;
             continue;
         }
         if (caller_copy) {
-            int s = next_slice_.fetch_add(1, std::memory_order_relaxed);
+            const int s = next_slice_.fetch_add(1, std::memory_order_relaxed);
             if (s < ns) {
                 copy_slice(slices_[s]);
                 store_fence();
@@ -254,8 +287,7 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
         }
         cpu_relax();
     }
-    for (int w = 0; w < nw; w++)
-        while (wstate_[w].done_epoch.load(std::memory_order_acquire) != ep) cpu_relax();
+    open_.store(false, std::memory_order_seq_cst);
 }
 
 }  // namespace gfd

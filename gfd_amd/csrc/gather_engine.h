@@ -38,18 +38,27 @@ public:
     int num_workers() const { return (int)threads_.size(); }
     void set_slice_bytes(size_t b) { slice_bytes_ = b < 4096 ? 4096 : b; }
     size_t slice_bytes() const { return slice_bytes_; }
-    // Whether the calling thread copies slices too (default: only when there
-    // are fewer than two workers, so the caller stays free to issue copies).
-    void set_caller_copies(int mode) { caller_copies_ = mode; }
+    // Whether the calling thread copies slices too (default yes: between
+    // chunk hand-offs it claims slices like a worker, so a gather never waits
+    // on a worker that is still waking up).
+    void set_caller_copies(bool on) { caller_copies_ = on; }
+    // Size of the first chunk (0 = chunk_bytes / 8, at least 64 KiB): a short
+    // first chunk starts the first copy early.
+    void set_first_chunk_bytes(size_t b) { first_chunk_bytes_ = b; }
+
+    // Wake sleeping workers ahead of a job (they spin again until it comes).
+    void prewake();
 
     using ChunkFn = void (*)(void* ctx, int chunk, size_t offset, size_t bytes);
 
     // Precondition: the entries' destinations are contiguous in order
     // (entry i starts where entry i-1 ends).  Writes entry i's bytes to
     // staging + (entries[i].dst - entries[0].dst).  The destination range
-    // [0, total) is cut into chunks of chunk_bytes; on_chunk(ctx, c, off, len)
-    // is called on the calling thread, in chunk order, once chunk c's bytes
-    // are written and fenced.  Returns after every worker has left the job.
+    // [0, total) is cut into chunks (a short first chunk, then chunk_bytes
+    // each); on_chunk(ctx, c, off, len) is called on the calling thread, in
+    // chunk order, once chunk c's bytes are written and fenced.  Returns as
+    // soon as every chunk has been handed to on_chunk.  Not reentrant: one
+    // caller at a time.
     void run(const SGEntry* entries, int count, size_t total, char* staging,
              size_t chunk_bytes, ChunkFn on_chunk, void* ctx);
 
@@ -61,20 +70,16 @@ private:
         size_t len;
         int chunk;
     };
-    struct alignas(64) WorkerState {
-        std::atomic<uint32_t> done_epoch{0};
-        char pad[60];
-    };
-
     void worker_main(int w, int cpu);
     void do_slices();
     void copy_slice(const Slice& s);
 
     std::vector<std::thread> threads_;
-    std::unique_ptr<WorkerState[]> wstate_;
     // Job counter; 32-bit so idle workers can sleep on it with a futex.
     alignas(64) std::atomic<uint32_t> epoch_{0};
     alignas(64) std::atomic<int> sleepers_{0};
+    alignas(64) std::atomic<int> active_{0};   // workers inside a job
+    alignas(64) std::atomic<bool> open_{false};  // job state valid to read
     alignas(64) std::atomic<bool> running_{true};
     alignas(64) std::atomic<int> next_slice_{0};
 
@@ -83,11 +88,14 @@ private:
     int count_ = 0;
     char* staging_ = nullptr;
     std::vector<Slice> slices_;
+    int num_slices_ = 0;
+    std::vector<size_t> chunk_end_;
     std::unique_ptr<std::atomic<int>[]> remaining_;
     int remaining_cap_ = 0;
 
     size_t slice_bytes_ = 128 * 1024;
-    int caller_copies_ = -1;
+    size_t first_chunk_bytes_ = 0;
+    bool caller_copies_ = true;
 };
 
 }  // namespace gfd

@@ -16,7 +16,10 @@ namespace gfd {
 
 namespace {
 
-constexpr size_t kRing = 4096;  // in-flight copies before the issuer waits
+// In-flight copies before the issuer waits.  The signals are polled, never
+// slept on, so they are created without interrupt events: the driver's
+// per-process event pool is small and HIP and profilers need it too.
+constexpr size_t kRing = 1024;
 
 struct AgentSearch {
     uint32_t bdf;
@@ -70,13 +73,20 @@ SdmaQueue::~SdmaQueue() {
     wait_all();
     for (uint64_t h : signals_)
         if (h) hsa_signal_destroy(sig(h));
-    hsa_shut_down();
+    if (own_hsa_) hsa_shut_down();
 }
 
 int SdmaQueue::init(int device, int channels, int pin_engines) {
     if (inited_) return 0;
-    hsa_status_t st = hsa_init();  // reference-counted; HIP holds its own reference
-    if (st != HSA_STATUS_SUCCESS) return (int)st;
+    // HIP has normally initialised the runtime already; only take a reference
+    // of our own when it has not.
+    uint16_t major = 0;
+    if (hsa_system_get_info(HSA_SYSTEM_INFO_VERSION_MAJOR, &major) != HSA_STATUS_SUCCESS) {
+        hsa_status_t st0 = hsa_init();
+        if (st0 != HSA_STATUS_SUCCESS) return (int)st0;
+        own_hsa_ = true;
+    }
+    hsa_status_t st = HSA_STATUS_SUCCESS;
     AgentSearch s;
     s.want_index = device;
     char bus[64] = {0};
@@ -91,7 +101,8 @@ int SdmaQueue::init(int device, int channels, int pin_engines) {
     hsa_iterate_agents(visit_agent, &s);
     if (!s.have_cpu || !(s.have_gpu || s.have_nth)) {
         GFD_LOG_ERROR("SDMA: HSA agents for device %d not found\n", device);
-        hsa_shut_down();
+        if (own_hsa_) hsa_shut_down();
+        own_hsa_ = false;
         return (int)HSA_STATUS_ERROR_INVALID_AGENT;
     }
     gpu_agent_ = s.have_gpu ? s.gpu.handle : s.nth_gpu.handle;
@@ -106,7 +117,9 @@ int SdmaQueue::init(int device, int channels, int pin_engines) {
     signals_.assign(kRing, 0);
     for (size_t i = 0; i < kRing; i++) {
         hsa_signal_t h;
-        st = hsa_signal_create(0, 0, nullptr, &h);
+        // GPU_ONLY: a plain memory signal without an interrupt event; the
+        // host still reads it (load / spin-wait), it just is never woken.
+        st = hsa_amd_signal_create(0, 0, nullptr, HSA_AMD_SIGNAL_AMD_GPU_ONLY, &h);
         if (st != HSA_STATUS_SUCCESS) return (int)st;
         signals_[i] = h.handle;
     }

@@ -65,6 +65,7 @@ private:
     int grow();
 
     bool inited_ = false;
+    bool own_hsa_ = false;
     int channels_ = 0;
     bool pin_ = false;
     uint64_t gpu_agent_ = 0;

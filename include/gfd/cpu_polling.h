@@ -122,6 +122,29 @@ public:
     size_t staging_buffer_size() const { return staging_buffer_size_; }
     int num_staging_buffers() const { return num_staging_bufs_; }
 
+    // Timeline trace (off by default; GFD_TRACE=1 or set_trace(true)).
+    // Timestamps are CLOCK_MONOTONIC nanoseconds.
+    enum TraceKind : uint32_t {
+        TRACE_BATCH_FIRST = 1,  // first descriptor of a batch consumed: a = slot, b = read_idx
+        TRACE_FLUSH = 2,        // batch handed to the copy path: a = entries, b = bytes
+        TRACE_ISSUED = 3,       // batch copies issued: b = fence after them
+        TRACE_DONE = 4,         // done_idx published: b = value
+        TRACE_GAP_FLUSH = 5,    // partial batch flushed after a gap: a = entries
+        TRACE_DIRECT_BEGIN = 6, // submit_direct entered: a = entries, b = bytes
+        TRACE_CHUNK = 7,        // a staging chunk's copy issued: a = chunk, b = bytes
+        TRACE_DIRECT_END = 8,   // submit_direct returns: b = elapsed ns
+    };
+    struct TraceEvent {
+        uint64_t t_ns;
+        uint32_t kind;
+        uint32_t a;
+        uint64_t b;
+    };
+    void set_trace(bool on);
+    // Move up to `max` recorded events (oldest first) into `out`; returns the count.
+    int read_trace(TraceEvent* out, int max);
+    void trace(uint32_t kind, uint32_t a, uint64_t b);
+
     // Host-side effects applied once a batch's copies have completed.
     struct CompletionSlot {
         uint64_t fence = 0;       // every copy below this fence belongs to the batch or earlier
@@ -218,6 +241,13 @@ private:
 
     std::atomic<bool> running_{false};
     std::thread thread_;
+
+    static constexpr int TRACE_CAP = 16384;
+    std::vector<TraceEvent> trace_buf_;
+    uint64_t trace_head_ = 0;
+    uint64_t trace_tail_ = 0;
+    std::atomic<bool> trace_on_{false};
+    std::mutex trace_mutex_;
 
     std::atomic<uint64_t> descriptors_processed_{0};
     std::atomic<uint64_t> batches_submitted_{0};

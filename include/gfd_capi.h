@@ -100,6 +100,18 @@ void gfd_poller_stop(gfd_poller_t p);                                /* stop (:5
 int gfd_poller_get_stats(gfd_poller_t p, gfd_poller_stats* out);     /* get_* (:60-71) */
 void gfd_poller_reset_stats(gfd_poller_t p);                         /* reset_stats (:73) */
 int gfd_poller_get_info(gfd_poller_t p, gfd_poller_info* out);
+/* Timeline trace of the poller and direct path (no reference counterpart):
+ * t_ns (CLOCK_MONOTONIC), kind (1 batch-first, 2 flush, 3 issued, 4 done,
+ * 5 gap-flush, 6 direct-begin, 7 chunk, 8 direct-end), a, b as documented in
+ * include/gfd/cpu_polling.h.  read_trace drains up to max events. */
+typedef struct gfd_trace_event {
+    uint64_t t_ns;
+    uint32_t kind;
+    uint32_t a;
+    uint64_t b;
+} gfd_trace_event;
+void gfd_poller_set_trace(gfd_poller_t p, int on);
+int gfd_poller_read_trace(gfd_poller_t p, gfd_trace_event* out, int max);
 /* Tuning of the pipelined direct path (no reference counterpart). */
 void gfd_poller_set_direct_chunk_bytes(gfd_poller_t p, uint64_t bytes);
 void gfd_poller_set_gather_slice_bytes(gfd_poller_t p, uint64_t bytes);
@@ -107,8 +119,8 @@ void gfd_poller_set_gather_slice_bytes(gfd_poller_t p, uint64_t bytes);
 /* Host-only gather (no GPU): the staging step of the pipelined direct path.
  * Entries must have contiguous destinations; entry i lands at
  * out + (entries[i].dst - entries[0].dst).  chunk_order (optional, capacity
- * ceil(total/chunk_bytes)) receives the chunk indices in the order they were
- * reported complete.  num_workers threads plus the caller.  (Reference
+ * ceil(total/chunk_bytes) + 1: the first chunk is shorter) receives the chunk
+ * indices in the order they were reported complete.  num_workers threads plus the caller.  (Reference
  * counterpart: CpuPollingThread::parallel_gather, src/parallel_gather.cpp:74.) */
 int gfd_host_gather(const gfd_sg_entry* entries, int count, void* out, uint64_t chunk_bytes,
                     uint64_t slice_bytes, int num_workers, int* chunk_order);

@@ -107,7 +107,7 @@ def test_host_gather_empty_is_noop():
 
 
 def test_host_gather_with_sleeping_workers():
-    # GFD_GATHER_SPIN=0: idle workers sleep on the job counter at once, so every
+    # GFD_GATHER_SPIN_US=0: idle workers sleep on the job counter at once, so every
     # gather has to wake them (futex path) and still produce the same bytes.
     import subprocess
     import sys
@@ -126,6 +126,6 @@ def test_host_gather_with_sleeping_workers():
         "    time.sleep(0.01)\n"
         "print('ok')\n"
     )
-    env = dict(os.environ, GFD_GATHER_SPIN="0", PYTHONPATH=ROOT)
+    env = dict(os.environ, GFD_GATHER_SPIN_US="0", PYTHONPATH=ROOT)
     r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stderr
