@@ -63,7 +63,8 @@ class PollerInfo(ctypes.Structure):
 
 TRACE_DTYPE = np.dtype([("t_ns", np.uint64), ("kind", np.uint32), ("a", np.uint32), ("b", np.uint64)])
 TRACE_KINDS = {1: "batch_first", 2: "flush", 3: "issued", 4: "done", 5: "gap_flush", 6: "direct_begin",
-               7: "chunk", 8: "direct_end"}
+               7: "chunk", 8: "direct_end", 9: "gather_entry", 10: "gather_idle", 11: "gather_published",
+               12: "gather_first_slice", 13: "gather_built"}
 
 _lib = None
 _SIGNATURES = {}

@@ -149,11 +149,15 @@ void CpuPollingThread::trace(uint32_t kind, uint32_t a, uint64_t b) {
     if (!trace_on_.load(std::memory_order_relaxed)) return;
     timespec ts;
     clock_gettime(CLOCK_MONOTONIC, &ts);
+    trace_at((uint64_t)ts.tv_sec * 1000000000ull + (uint64_t)ts.tv_nsec, kind, a, b);
+}
+
+void CpuPollingThread::trace_at(uint64_t t_ns, uint32_t kind, uint32_t a, uint64_t b) {
+    if (!trace_on_.load(std::memory_order_relaxed)) return;
     std::lock_guard<std::mutex> lock(trace_mutex_);
     if (trace_buf_.empty()) return;
     if (trace_head_ - trace_tail_ == (uint64_t)TRACE_CAP) trace_tail_++;  // overwrite the oldest
-    trace_buf_[trace_head_ % TRACE_CAP] = TraceEvent{(uint64_t)ts.tv_sec * 1000000000ull + (uint64_t)ts.tv_nsec,
-                                                     kind, a, b};
+    trace_buf_[trace_head_ % TRACE_CAP] = TraceEvent{t_ns, kind, a, b};
     trace_head_++;
 }
 
@@ -173,7 +177,16 @@ bool CpuPollingThread::choose_cpus() {
     if (cpus_chosen_) return true;
     GpuTopology topo = discover_gpu_topology(device_);
     if (numa_node_ < 0) numa_node_ = topo.numa_node;
-    int cap = (int)env_size("GFD_NUM_GATHER_WORKERS", MAX_GATHER_WORKERS);
+    // Default worker count: with an explicit core range, the reference rule
+    // (up to 15); otherwise half of the CPUs this process may use, so the
+    // application thread, the GPU runtime's threads and the poller keep cores
+    // of their own (a handful of AVX-512 streams already outrun the link).
+    int dflt = MAX_GATHER_WORKERS;
+    if (!(exclusive_core_base_ >= 0 && exclusive_core_count_ > 0)) {
+        const int avail = (int)allowed_cpus().size();
+        dflt = std::max(1, std::min(MAX_GATHER_WORKERS, avail / 2));
+    }
+    int cap = (int)env_size("GFD_NUM_GATHER_WORKERS", (size_t)dflt);
     if (cap > MAX_GATHER_WORKERS) cap = MAX_GATHER_WORKERS;
     std::vector<int> cpus = pick_cpus(topo, 1 + cap, exclusive_core_base_, exclusive_core_count_);
     if (cpus.empty()) cpus.push_back(-1);

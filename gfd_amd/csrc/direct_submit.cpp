@@ -69,11 +69,11 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
 
     size_t total = 0;
     for (int i = 0; i < count; i++) total += entries[i].size;
-    bool dst_contig = true, src_contig = true;
-    for (int i = 1; i < count && (dst_contig || src_contig); i++) {
-        if (entries[i].dst != entries[i - 1].dst + entries[i - 1].size) dst_contig = false;
-        if ((const char*)entries[i].src != (const char*)entries[i - 1].src + entries[i - 1].size)
-            src_contig = false;
+    bool dst_contig = true, src_contig = true, uniform = true;
+    for (int i = 1; i < count; i++) {
+        dst_contig &= entries[i].dst == entries[i - 1].dst + entries[i - 1].size;
+        src_contig &= (const char*)entries[i].src == (const char*)entries[i - 1].src + entries[i - 1].size;
+        uniform &= entries[i].size == entries[0].size;
     }
 
     trace(TRACE_DIRECT_BEGIN, (uint32_t)count, total);
@@ -94,8 +94,17 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
         std::lock_guard<std::mutex> lock(gather_mutex_);
         if (gather_) {
             DirectCtx ctx{this, &direct_ce_manager_, entries[0].dst, direct_staging_, nch, 0};
-            gather_->run(entries, count, total, direct_staging_, direct_chunk_bytes_, direct_chunk, &ctx);
+            gather_->run(entries, count, total, direct_staging_, direct_chunk_bytes_, direct_chunk, &ctx,
+                         uniform ? 1 : 0);
             err = ctx.err;
+            if (trace_on_.load(std::memory_order_relaxed)) {
+                const GatherEngine::RunTimes rt = gather_->last_run();
+                trace_at(rt.entry, TRACE_GATHER_ENTRY, 0, 0);
+                trace_at(rt.idle, TRACE_GATHER_IDLE, 0, 0);
+                trace_at(rt.built, TRACE_GATHER_BUILT, 0, 0);
+                trace_at(rt.published, TRACE_GATHER_PUBLISHED, (uint32_t)rt.sleepers, 0);
+                trace_at(rt.first_slice, TRACE_GATHER_FIRST_SLICE, (uint32_t)rt.copiers, 0);
+            }
         } else {
             size_t off = 0;
             for (int i = 0; i < count; i++) {

@@ -167,6 +167,7 @@ void GatherEngine::worker_main(int w, int cpu) {
 }
 
 void GatherEngine::prewake() {
+    last_prewake_ns_ = mono_ns();
     if (sleepers_.load(std::memory_order_seq_cst) > 0) futex_wake_all(&epoch_);
 }
 
@@ -192,21 +193,35 @@ void GatherEngine::copy_slice(const Slice& s) {
 // Claim and copy slices until none are left.  Returns after the last claim.
 void GatherEngine::do_slices() {
     const int ns = num_slices_;
+    bool counted = false;
     for (;;) {
         const int s = next_slice_.fetch_add(1, std::memory_order_relaxed);
         if (s >= ns) break;
         copy_slice(slices_[s]);
         store_fence();
+        note_slice(counted);
         remaining_[slices_[s].chunk].fetch_sub(1, std::memory_order_release);
     }
 }
 
+void GatherEngine::note_slice(bool& counted) {
+    if (counted) return;
+    counted = true;
+    copiers_.fetch_add(1, std::memory_order_relaxed);
+    uint64_t z = 0;
+    first_slice_ns_.compare_exchange_strong(z, mono_ns(), std::memory_order_relaxed);
+}
+
 void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* staging,
-                       size_t chunk_bytes, ChunkFn on_chunk, void* ctx) {
+                       size_t chunk_bytes, ChunkFn on_chunk, void* ctx, int uniform_hint) {
     if (count <= 0 || total == 0) return;
+    times_.entry = mono_ns();
     if (chunk_bytes == 0 || chunk_bytes > total) chunk_bytes = total;
     // Workers still inside the previous job must leave before its state changes.
     while (active_.load(std::memory_order_seq_cst) != 0) cpu_relax();
+    times_.idle = mono_ns();
+    first_slice_ns_.store(0, std::memory_order_relaxed);
+    copiers_.store(0, std::memory_order_relaxed);
 
     // Chunk edges: a short first chunk gets the first copy going early.
     size_t first = first_chunk_bytes_ ? first_chunk_bytes_ : chunk_bytes / 8;
@@ -220,29 +235,44 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     const int nchunks = (int)chunk_end_.size();
 
     // Cut the destination stream into slices that never cross a chunk edge.
+    // The first chunk uses finer slices so every thread shares it and the
+    // first copy starts as early as possible.
+    const size_t esz = entries[0].size;
+    bool uniform = uniform_hint > 0;
+    if (uniform_hint < 0) {
+        uniform = true;
+        for (int i = 1; i < count && uniform; i++) uniform = entries[i].size == esz;
+    }
+    uniform = uniform && esz > 0;
+    const size_t first_slice = std::max<size_t>(16 * 1024, std::min(slice_bytes_, chunk_end_[0] / 16));
     slices_.clear();
     int e = 0;
     size_t eo = 0;
     size_t pos = 0;
     for (int c = 0; c < nchunks; c++) {
         const size_t cend = chunk_end_[c];
+        const size_t sb = c == 0 ? first_slice : slice_bytes_;
         while (pos < cend) {
-            while (e < count && eo == entries[e].size) {  // skip spent / empty entries
-                e++;
-                eo = 0;
-            }
-            const size_t len = std::min(slice_bytes_, cend - pos);
-            slices_.push_back(Slice{e, eo, pos, len, c});
-            size_t adv = len;
-            while (adv) {
-                const size_t avail = entries[e].size - eo;
-                if (avail > adv) {
-                    eo += adv;
-                    adv = 0;
-                } else {
-                    adv -= avail;
+            const size_t len = std::min(sb, cend - pos);
+            if (uniform) {
+                slices_.push_back(Slice{(int)(pos / esz), pos % esz, pos, len, c});
+            } else {
+                while (e < count && eo == entries[e].size) {  // skip spent / empty entries
                     e++;
                     eo = 0;
+                }
+                slices_.push_back(Slice{e, eo, pos, len, c});
+                size_t adv = len;
+                while (adv) {
+                    const size_t avail = entries[e].size - eo;
+                    if (avail > adv) {
+                        eo += adv;
+                        adv = 0;
+                    } else {
+                        adv -= avail;
+                        e++;
+                        eo = 0;
+                    }
                 }
             }
             pos += len;
@@ -263,10 +293,17 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
 
     const int nw = num_workers();
     const bool caller_copy = caller_copies_ != 0 || nw == 0;
+    times_.built = mono_ns();
     open_.store(true, std::memory_order_seq_cst);
     epoch_.fetch_add(1, std::memory_order_seq_cst);
-    if (sleepers_.load(std::memory_order_seq_cst) > 0) futex_wake_all(&epoch_);
+    times_.sleepers = sleepers_.load(std::memory_order_seq_cst);
+    // Workers are helpers: the caller can finish the job alone.  If they were
+    // woken just before (prewake), do not pay for a second wake syscall here;
+    // a worker that fell asleep in between simply sits this job out.
+    if (times_.sleepers > 0 && times_.built - last_prewake_ns_ > 200000ull) futex_wake_all(&epoch_);
     const int ns = num_slices_;
+    times_.published = mono_ns();
+    bool counted = false;
 
     int ready = 0;
     while (ready < nchunks) {
@@ -281,6 +318,7 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
             if (s < ns) {
                 copy_slice(slices_[s]);
                 store_fence();
+                note_slice(counted);
                 remaining_[slices_[s].chunk].fetch_sub(1, std::memory_order_release);
                 continue;
             }
@@ -288,6 +326,8 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
         cpu_relax();
     }
     open_.store(false, std::memory_order_seq_cst);
+    times_.first_slice = first_slice_ns_.load(std::memory_order_relaxed);
+    times_.copiers = copiers_.load(std::memory_order_relaxed);
 }
 
 }  // namespace gfd

@@ -49,6 +49,15 @@ public:
     // Wake sleeping workers ahead of a job (they spin again until it comes).
     void prewake();
 
+    // CLOCK_MONOTONIC ns of the last run(): entry, after the wait for the
+    // previous job's workers, job published, first slice finished (by any
+    // thread), and number of threads that copied at least one slice.
+    struct RunTimes {
+        uint64_t entry, idle, built, published, first_slice;
+        int copiers, sleepers;
+    };
+    RunTimes last_run() const { return times_; }
+
     using ChunkFn = void (*)(void* ctx, int chunk, size_t offset, size_t bytes);
 
     // Precondition: the entries' destinations are contiguous in order
@@ -59,8 +68,10 @@ public:
     // chunk order, once chunk c's bytes are written and fenced.  Returns as
     // soon as every chunk has been handed to on_chunk.  Not reentrant: one
     // caller at a time.
+    // uniform_hint: 1 = every entry has the same size (slices are placed by
+    // division), 0 = not, -1 = check.
     void run(const SGEntry* entries, int count, size_t total, char* staging,
-             size_t chunk_bytes, ChunkFn on_chunk, void* ctx);
+             size_t chunk_bytes, ChunkFn on_chunk, void* ctx, int uniform_hint = -1);
 
 private:
     struct Slice {
@@ -73,6 +84,7 @@ private:
     void worker_main(int w, int cpu);
     void do_slices();
     void copy_slice(const Slice& s);
+    void note_slice(bool& counted);
 
     std::vector<std::thread> threads_;
     // Job counter; 32-bit so idle workers can sleep on it with a futex.
@@ -92,6 +104,11 @@ private:
     std::vector<size_t> chunk_end_;
     std::unique_ptr<std::atomic<int>[]> remaining_;
     int remaining_cap_ = 0;
+
+    RunTimes times_{};
+    uint64_t last_prewake_ns_ = 0;
+    std::atomic<uint64_t> first_slice_ns_{0};
+    std::atomic<int> copiers_{0};
 
     size_t slice_bytes_ = 128 * 1024;
     size_t first_chunk_bytes_ = 0;

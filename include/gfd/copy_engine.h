@@ -39,7 +39,7 @@ constexpr Status GFD_SUCCESS = 0;
 // Upper bound on copy channels per manager; DEFAULT_CE_CHANNELS when init()
 // is given 0.
 constexpr int MAX_CE_CHANNELS = 8;
-constexpr int DEFAULT_CE_CHANNELS = 2;
+constexpr int DEFAULT_CE_CHANNELS = 4;
 
 constexpr int MAX_SG_ENTRIES_PER_BATCH = 8192;
 

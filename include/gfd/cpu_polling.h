@@ -133,6 +133,11 @@ public:
         TRACE_DIRECT_BEGIN = 6, // submit_direct entered: a = entries, b = bytes
         TRACE_CHUNK = 7,        // a staging chunk's copy issued: a = chunk, b = bytes
         TRACE_DIRECT_END = 8,   // submit_direct returns: b = elapsed ns
+        TRACE_GATHER_ENTRY = 9,        // gather job entered
+        TRACE_GATHER_IDLE = 10,        // previous job's workers have left
+        TRACE_GATHER_PUBLISHED = 11,   // job visible to the workers: a = workers asleep at that moment
+        TRACE_GATHER_FIRST_SLICE = 12, // first slice copied: a = threads that copied
+        TRACE_GATHER_BUILT = 13,       // job state built (slices cut)
     };
     struct TraceEvent {
         uint64_t t_ns;
@@ -144,6 +149,7 @@ public:
     // Move up to `max` recorded events (oldest first) into `out`; returns the count.
     int read_trace(TraceEvent* out, int max);
     void trace(uint32_t kind, uint32_t a, uint64_t b);
+    void trace_at(uint64_t t_ns, uint32_t kind, uint32_t a, uint64_t b);
 
     // Host-side effects applied once a batch's copies have completed.
     struct CompletionSlot {
