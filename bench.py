@@ -209,7 +209,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=15)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", default="", help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small")
+    ap.add_argument("--only", default="",
+                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small (calib: add a 32 MiB D2D copy)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this path has no multi-GPU step (each GPU gathers over its own "
@@ -232,6 +233,17 @@ def main():
 
     assert gfd_amd.device_count() > 0, "no GPU visible"
     gfd_amd.lib().gfd_set_device(0)
+
+    if "calib" in only:
+        # Reference kernel for the FETCH_SIZE / WRITE_SIZE counters: a device
+        # to device copy of 32 MiB (the runtime's blit kernel), 5 launches.
+        a = gfd_amd.DeviceBuffer(32 << 20)
+        b = gfd_amd.DeviceBuffer(32 << 20)
+        a.fill(1)
+        for _ in range(5):
+            gfd_amd.lib().gfd_memcpy_d2d(b.ptr, a.ptr, 32 << 20)
+        gfd_amd.synchronize()
+        log("calibration copies done: 5 x 32 MiB device-to-device")
 
     peak = {}
     if want("peak"):

@@ -87,6 +87,7 @@ def _declare(L):
         "gfd_device_free": ([vp], c_int),
         "gfd_memcpy_h2d": ([vp, vp, c_sz], c_int),
         "gfd_memcpy_d2h": ([vp, vp, c_sz], c_int),
+        "gfd_memcpy_d2d": ([vp, vp, c_sz], c_int),
         "gfd_memset_device": ([vp, c_int, c_sz], c_int),
         "gfd_stream_create": ([pvp], c_int),
         "gfd_stream_destroy": ([vp], c_int),

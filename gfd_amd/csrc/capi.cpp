@@ -65,6 +65,10 @@ int gfd_memcpy_d2h(void* dst, const void* src, size_t n) {
     CAPI_CHECK(gfd_hip_memcpy_d2h(dst, (uint64_t)(uintptr_t)src, n), "hipMemcpy D2H");
     return 0;
 }
+int gfd_memcpy_d2d(void* dst, const void* src, size_t n) {
+    CAPI_CHECK(gfd_hip_memcpy_d2d((uint64_t)(uintptr_t)dst, (uint64_t)(uintptr_t)src, n), "hipMemcpy D2D");
+    return 0;
+}
 int gfd_memset_device(void* dst, int value, size_t n) {
     CAPI_CHECK(gfd_hip_memset_d8((uint64_t)(uintptr_t)dst, value, n), "hipMemset");
     return 0;

@@ -8,10 +8,14 @@
 //   * Each lane moves 16 bytes per load (global_load_dwordx4); a wave covers
 //     1 KiB of one token per instruction, so every PCIe read request is a
 //     full, contiguous cache-line group.
-//   * Each lane keeps U independent 16-byte loads in flight before it stores
-//     anything, so a 256-thread workgroup has 4*U KiB of host reads
-//     outstanding; with a few thousand waves resident that is far above the
-//     link's bandwidth-latency product (about 64 GB/s x 2 us = 128 KiB).
+//   * Each lane keeps U = 4 independent 16-byte loads in flight before it
+//     stores, and the grid is 2 workgroups per CU (512 on MI355X) looping over
+//     the data: 512 x 256 x 4 x 16 B = 8 MiB of host reads can be outstanding,
+//     far above the link's bandwidth-latency product (about 64 GB/s x 2 us).
+//     More concurrency is slower, not faster: with 16 workgroups per CU the
+//     kernel drops from 56 to 52 GB/s, because many more distinct host pages
+//     are in flight at once (measured over 0.5-32 workgroups per CU and
+//     U = 1-16; 2 and 4 are the optimum for 512 B - 64 KiB tokens).
 //   * Stores are plain 16-byte stores to HBM (coalesced, contiguous).
 //   * Token source addresses come from a per-token table (the KV block/page
 //     table), normally resident in HBM; lanes of one token read the same
@@ -168,7 +172,8 @@ int cu_count() {
     return g_cu_count;
 }
 
-constexpr int kUnroll = 8;
+constexpr int kUnroll = 4;
+constexpr int kBlocksPerCU = 2;
 
 }  // namespace
 
@@ -179,7 +184,7 @@ extern "C" int gfd_zero_copy_gather_tokens(const uint64_t* src_addrs, void* dst,
     if (num_tokens == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
     const uint64_t total = (uint64_t)num_tokens * token_size;
-    const int max_blocks = cu_count() * 16;
+    const int max_blocks = cu_count() * kBlocksPerCU;
     if ((token_size & 15) == 0 && ((uintptr_t)dst & 15) == 0) {
         const uint64_t total_vecs = total >> 4;
         if (total_vecs >= (1ull << 31)) return (int)hipErrorInvalidValue;  // >= 32 GiB per call
@@ -202,13 +207,15 @@ extern "C" int gfd_zero_copy_gather(const gfd_sg_entry* entries, int count, void
     if (count < 0 || (count > 0 && !entries)) return (int)hipErrorInvalidValue;
     if (count == 0) return 0;
     hipStream_t st = (hipStream_t)stream;
-    // Aim for about 2048 busy waves; at most 64 entries per wave (one per lane).
-    int per_wave = (count + 2047) / 2048;
+    // One wave per entry batch, about 4 * 2 waves per CU in flight (the same
+    // concurrency as the page-table kernel); at most 64 entries per batch.
+    const int max_blocks = cu_count() * kBlocksPerCU;
+    const int target_waves = max_blocks * (kBlock / 64);
+    int per_wave = (count + target_waves - 1) / target_waves;
     if (per_wave < 1) per_wave = 1;
     if (per_wave > 64) per_wave = 64;
     const int waves = (count + per_wave - 1) / per_wave;
     int blocks = (waves + 3) / 4;
-    const int max_blocks = cu_count() * 16;
     if (blocks > max_blocks) blocks = max_blocks;
     hipLaunchKernelGGL(zc_gather_sg<4>, dim3(blocks), dim3(kBlock), 0, st, entries, count, per_wave);
     return (int)hipGetLastError();

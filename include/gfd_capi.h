@@ -72,6 +72,7 @@ int gfd_device_alloc(void** p, size_t bytes);           /* cudaMalloc */
 int gfd_device_free(void* p);
 int gfd_memcpy_h2d(void* dst, const void* src, size_t n);
 int gfd_memcpy_d2h(void* dst, const void* src, size_t n);
+int gfd_memcpy_d2d(void* dst, const void* src, size_t n);
 int gfd_memset_device(void* dst, int value, size_t n);
 int gfd_stream_create(void** stream);                   /* non-blocking, default priority */
 int gfd_stream_destroy(void* stream);
