@@ -27,6 +27,13 @@ sys.path.insert(0, ROOT)
 import gfd_amd  # noqa: E402
 
 PCIE_GEN5_X16_GBPS = 32.0 * 16 * 128.0 / 130.0 / 8.0  # 63.0 GB/s per direction
+
+# Bytes one zc_gather_tokens16 launch moves at 8192 x 4 KiB, from two
+# rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of `bench.py --only zc,calib`,
+# each scaled by the same counter on a 32 MiB device-to-device copy
+# (FETCH x 1.9986, WRITE x 1.0).  Reads are host-link reads through the L2's
+# external interface; writes land in HBM.
+ZC_TRAFFIC_8192x4KB = {"read_bytes": 33027 * 1024, "write_bytes": 32768 * 1024}
 METRIC = "scattered H2D GB/s + % of PCIe5 x16 peak at 8192x4KB and 2048x64KB"
 PD = ctypes.POINTER(ctypes.c_double)
 
@@ -306,7 +313,10 @@ def main():
         ach = zc["kernel_GBps"]
         roofline = {"bound": "pcie", "kernel": "zc_gather_tokens16", "achieved": ach,
                     "peak": round(PCIE_GEN5_X16_GBPS, 2), "unit": "GB/s",
-                    "frac": round(ach / PCIE_GEN5_X16_GBPS, 4), "traffic": None,
+                    "frac": round(ach / PCIE_GEN5_X16_GBPS, 4),
+                    "traffic": ZC_TRAFFIC_8192x4KB["read_bytes"] + ZC_TRAFFIC_8192x4KB["write_bytes"],
+                    "traffic_detail": dict(ZC_TRAFFIC_8192x4KB, algorithmic_read=r_main["bytes"] + 8 * r_main["tokens"],
+                                           algorithmic_write=r_main["bytes"]),
                     "peak_measured": peak_meas,
                     "frac_of_measured": round(ach / peak_meas, 4) if peak_meas else None,
                     "algorithmic_bytes_per_launch": r_main["bytes"],
