@@ -188,6 +188,74 @@ def run_memcpy_n(L, iters, warmup):
     return {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3)}
 
 
+def run_moe(oracle, iters, warmup, tokens=4096, experts=64, dim=7168):
+    """SG-MoE: top-2 of 64 experts per token on the GPU, per-expert row lists
+    built on the GPU, then the wave-specialised gather of the routed 14 KiB
+    bf16 rows from pinned host memory, with and without the RMSNorm consumer.
+    Times are HIP-event kernel times on the launch stream (P50)."""
+    L = gfd_amd.lib()
+    row_bytes, stride = dim * 2, dim * 4
+    vals = oracle.moe_token_values(tokens, dim)
+    host = gfd_amd.HostBuffer(tokens * stride)
+    host.array[:] = oracle.GAP_BYTE
+    host.array.reshape(tokens, stride)[:, :row_bytes] = vals.view(np.uint8).reshape(tokens, row_bytes)
+    logits = oracle.moe_logits(tokens, experts)
+    offsets, row_token = oracle.moe_lists(oracle.moe_top2(logits), experts)
+    weight = oracle.moe_weight(dim)
+    n = 2 * tokens
+    d_logits = gfd_amd.DeviceBuffer(logits.nbytes)
+    d_logits.upload(logits)
+    d_top2, d_rows = gfd_amd.DeviceBuffer(n * 4), gfd_amd.DeviceBuffer(n * 4)
+    d_off = gfd_amd.DeviceBuffer((experts + 1) * 4)
+    d_w = gfd_amd.DeviceBuffer(dim * 2)
+    d_w.upload(weight)
+    d_dst, d_out, d_err = gfd_amd.DeviceBuffer(n * row_bytes), gfd_amd.DeviceBuffer(n * row_bytes), gfd_amd.DeviceBuffer(4)
+    d_err.fill(0)
+    st, ea, eb = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    L.gfd_stream_create(ctypes.byref(st))
+    L.gfd_event_create(ctypes.byref(ea))
+    L.gfd_event_create(ctypes.byref(eb))
+
+    def timed(fn, count):
+        out = []
+        for i in range(-warmup, count):
+            L.gfd_event_record(ea, st)
+            fn()
+            L.gfd_event_record(eb, st)
+            L.gfd_event_synchronize(eb)
+            ms = ctypes.c_float(0)
+            L.gfd_event_elapsed_ms(ctypes.byref(ms), ea, eb)
+            if i >= 0:
+                out.append(ms.value * 1000.0)
+        return out
+
+    route_us = timed(lambda: gfd_amd.moe_route(d_logits.ptr, tokens, experts, d_top2.ptr, d_off.ptr, d_rows.ptr,
+                                               st), iters)
+    if not (d_rows.download().view(np.int32) == row_token).all():
+        raise SystemExit("PARITY FAILURE: MoE row lists")
+    res = {"tokens": tokens, "experts": experts, "rows": n, "row_bytes": row_bytes, "bytes": n * row_bytes,
+           "route_and_lists_us_p50": round(p50(route_us), 2)}
+    expect = vals[row_token]
+    for name, with_norm in (("transfer_only", False), ("overlapped_rmsnorm", True)):
+        t = timed(lambda: gfd_amd.sg_gather_rmsnorm(host.ptr, stride, tokens, d_rows.ptr, n, row_bytes, d_dst.ptr,
+                                                    d_out.ptr if with_norm else None, d_w.ptr, 1e-6, 0, d_err.ptr,
+                                                    st), iters)
+        if int(d_err.download().view(np.int32)[0]) != 0:
+            raise SystemExit("MoE gather reported an error")
+        if not (d_dst.download().view(np.uint16).reshape(n, dim) == expect).all():
+            raise SystemExit("PARITY FAILURE: MoE gathered rows (%s)" % name)
+        if with_norm:
+            ref = oracle.rmsnorm_rows(oracle.bf16_to_f32(expect), oracle.bf16_to_f32(weight), 1e-6)
+            got = oracle.bf16_to_f32(d_out.download().view(np.uint16).reshape(n, dim))
+            if not np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-6):
+                raise SystemExit("PARITY FAILURE: MoE RMSNorm outside bf16 tolerance")
+        res[name] = {"us_p50": round(p50(t), 2), "GBps": round(gbps(n * row_bytes, p50(t)), 3)}
+    L.gfd_event_destroy(ea)
+    L.gfd_event_destroy(eb)
+    L.gfd_stream_destroy(st)
+    return res
+
+
 class QueueRig:
     def __init__(self, region_bytes):
         self.q = gfd_amd.DescriptorQueue()
@@ -217,7 +285,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=15)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="",
-                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small (calib: add a 32 MiB D2D copy)")
+                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe (calib: add a 32 MiB D2D copy)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this path has no multi-GPU step (each GPU gathers over its own "
@@ -288,6 +356,12 @@ def main():
         del L
     direct.close()
 
+    r_moe = None
+    if want("moe"):
+        log("SG-MoE 4096 x 7168 bf16, top-2 of 64 ...")
+        r_moe = run_moe(oracle, K, W)
+        log("  sg-moe: %s" % r_moe)
+
     # Phase 2: GFD Queue (GPU-submitted descriptors + CPU poller).
     if want("queue"):
         queue = QueueRig(region_max)
@@ -338,7 +412,7 @@ def main():
                    "tokens": 8192, "token_bytes": 4096, "stride": "2x", "parallelism": "single GPU"},
         "pcie_peak": {"theoretical_GBps": round(PCIE_GEN5_X16_GBPS, 2), "measured_contiguous_GBps": peak},
         "roofline": roofline, "cpu_baseline": cpu,
-        "results_8192x4KB": r_main, "results_2048x64KB": r_kv, "results_small": r_small,
+        "results_8192x4KB": r_main, "results_2048x64KB": r_kv, "results_small": r_small, "results_sg_moe": r_moe,
         "direct_setup": {k: dinfo[k] for k in ("numa_node", "num_gather_workers", "worker_cpus", "poller_cpu",
                                                "num_ce_channels", "direct_chunk_bytes", "gather_slice_bytes")},
         "host": info,

@@ -118,6 +118,9 @@ def _declare(L):
         "gfd_staging_pool_shutdown": ([], None),
         "gfd_zero_copy_gather_tokens": ([vp, vp, c_u32, c_int, vp], c_int),
         "gfd_zero_copy_gather": ([vp, c_int, vp], c_int),
+        "gfd_moe_route": ([vp, c_int, c_int, vp, vp, vp, vp], c_int),
+        "gfd_sg_gather_rmsnorm": ([vp, c_u64, c_int, vp, c_int, c_u32, vp, vp, vp, ctypes.c_float, c_int, vp, vp],
+                                  c_int),
         "gfd_queue_alloc": ([pvp], c_int),
         "gfd_queue_free": ([vp], c_int),
         "gfd_queue_submit_tokens": ([vp, vp, vp, c_int, c_u32, c_u64, vp], c_int),
@@ -380,6 +383,17 @@ def zero_copy_gather_tokens(src_addrs_ptr, dst_ptr, token_size, num_tokens, stre
 
 def zero_copy_gather(entries_ptr, count, stream=None):
     _check(lib().gfd_zero_copy_gather(entries_ptr, count, stream), "gfd_zero_copy_gather")
+
+
+def moe_route(d_logits, num_tokens, num_experts, d_top2, d_offsets, d_row_token, stream=None):
+    _check(lib().gfd_moe_route(d_logits, num_tokens, num_experts, d_top2, d_offsets, d_row_token, stream),
+           "gfd_moe_route")
+
+
+def sg_gather_rmsnorm(host_base, token_stride, num_tokens, d_row_token, num_rows, row_bytes, d_dst, d_out=None,
+                      d_weight=None, eps=1e-6, num_blocks=0, d_error=None, stream=None):
+    _check(lib().gfd_sg_gather_rmsnorm(host_base, token_stride, num_tokens, d_row_token, num_rows, row_bytes, d_dst,
+                                       d_out, d_weight, eps, num_blocks, d_error, stream), "gfd_sg_gather_rmsnorm")
 
 
 def build(verbose=False):

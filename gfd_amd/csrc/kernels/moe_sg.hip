@@ -1,0 +1,293 @@
+// MoE-routed scattered gather with a wave-specialised RMSNorm consumer (gfx950).
+//
+// Role in the reference: the SG warp-specialised path (include/gfd/sg_warp_spec.cuh:
+// a transfer warp turns per-expert (src, dst, size) lists into copies, a compute
+// warp runs a functor on each list once it has landed; examples/09_sg_warp_spec.cu
+// builds the lists on the GPU).  Here the whole path stays on the GPU:
+//
+//   1. moe_top2_kernel   — top-2 experts per token from the logits (ties go to
+//                          the lower expert id), one wave64 per token.
+//   2. moe_lists_kernel  — one workgroup per expert builds its row list in token
+//                          order (stable; no atomics), plus the expert offsets.
+//                          Rows are packed expert-major.
+//   3. sg_gather_norm_kernel<P, C> — per workgroup, P producer waves read whole
+//                          rows straight from pinned host memory (16-byte loads
+//                          over PCIe), write them to HBM and into an LDS ring of
+//                          S row slots; C consumer waves wait on the slot flags
+//                          (LDS acquire + s_sleep), compute a bf16 RMSNorm of the
+//                          row in fp32 and write it to HBM, then free the slot.
+//                          C = 0 is the pure-transfer variant.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "gfd_capi.h"
+
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kSlots = 4;              // LDS ring depth per workgroup
+constexpr int kMaxRowBytes = 14336;    // 7168 bf16
+constexpr int kVecPerLane = kMaxRowBytes / (kWave * 16);  // 14
+constexpr uint64_t kSpinLimit = 1ull << 26;  // LDS flag polls before giving up
+
+// ---------------------------------------------------------------- routing
+
+__device__ __forceinline__ void wave_argmax(float& v, int& idx) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(v, off, kWave);
+        const int oi = __shfl_xor(idx, off, kWave);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void moe_top2_kernel(const float* __restrict__ logits, int num_tokens,
+                                                       int num_experts, int* __restrict__ top2) {
+    const int t = (int)((blockIdx.x * blockDim.x + threadIdx.x) / kWave);
+    const int lane = (int)(threadIdx.x % kWave);
+    if (t >= num_tokens) return;  // uniform per wave
+    const float x = lane < num_experts ? logits[(size_t)t * num_experts + lane] : -INFINITY;
+    float v = x;
+    int i = lane;
+    wave_argmax(v, i);
+    const int first = i;
+    v = (lane == first || lane >= num_experts) ? -INFINITY : x;
+    i = lane;
+    wave_argmax(v, i);
+    if (lane == 0) {
+        top2[2 * t] = first;
+        top2[2 * t + 1] = i;
+    }
+}
+
+// Workgroup e: offsets[e] = number of (token, choice) pairs routed to experts
+// below e; row_token[offsets[e] + k] = k-th token (in token order) routed to e.
+__global__ __launch_bounds__(256) void moe_lists_kernel(const int* __restrict__ top2, int num_tokens,
+                                                        int num_experts, int* __restrict__ offsets,
+                                                        int* __restrict__ row_token) {
+    __shared__ int wave_sum[4];
+    __shared__ int block_base;
+    const int e = (int)blockIdx.x;
+    const int tid = (int)threadIdx.x;
+    const int lane = tid % kWave, wave = tid / kWave;
+
+    // Offset of this expert: pairs routed to lower experts.
+    int below = 0;
+    for (int t = tid; t < num_tokens; t += 256) below += (top2[2 * t] < e) + (top2[2 * t + 1] < e);
+    for (int off = 32; off >= 1; off >>= 1) below += __shfl_xor(below, off, kWave);
+    if (lane == 0) wave_sum[wave] = below;
+    __syncthreads();
+    if (tid == 0) {
+        block_base = wave_sum[0] + wave_sum[1] + wave_sum[2] + wave_sum[3];
+        offsets[e] = block_base;
+        if (e == num_experts - 1) offsets[num_experts] = 2 * num_tokens;
+    }
+    __syncthreads();
+
+    // Stable placement: block-wide exclusive prefix over token order.
+    int running = block_base;
+    for (int base = 0; base < num_tokens; base += 256) {
+        const int t = base + tid;
+        const bool hit = t < num_tokens && (top2[2 * t] == e || top2[2 * t + 1] == e);
+        const uint64_t mask = __ballot(hit);
+        const int before_in_wave = __popcll(mask & ((1ull << lane) - 1ull));
+        __syncthreads();
+        if (lane == 0) wave_sum[wave] = __popcll(mask);
+        __syncthreads();
+        int before_waves = 0;
+        for (int w = 0; w < wave; w++) before_waves += wave_sum[w];
+        if (hit) row_token[running + before_waves + before_in_wave] = t;
+        running += wave_sum[0] + wave_sum[1] + wave_sum[2] + wave_sum[3];
+    }
+}
+
+// ------------------------------------------------------ gather + RMSNorm
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// Round-to-nearest-even fp32 -> bf16 (finite values).
+__device__ __forceinline__ uint32_t to_bf16(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ int lds_load_acquire(int* p) {
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void lds_store_release(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Wait until *flag == want; false if the spin limit ran out (the caller then
+// skips its row and reports the error instead of hanging the workgroup).
+__device__ __forceinline__ bool lds_wait(int* flag, int want) {
+    for (uint64_t n = 0; n < kSpinLimit; n++) {
+        if (lds_load_acquire(flag) == want) return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
+// Workgroup b owns rows [b*R/G, (b+1)*R/G) of the expert-major row order.
+// Row r copies token row_token[r] (host_base + token * token_stride,
+// row_bytes bytes) to dst + r * row_bytes; with C > 0 it also writes
+// RMSNorm(row) (bf16, weight w, epsilon eps) to out + r * row_bytes.
+template <int P, int C>
+__global__ __launch_bounds__(kWave*(P + C)) void sg_gather_norm_kernel(
+    const uint8_t* __restrict__ host_base, uint64_t token_stride, int num_tokens, const int* __restrict__ row_token,
+    int num_rows, uint32_t row_bytes, uint8_t* __restrict__ dst, uint8_t* __restrict__ out,
+    const uint16_t* __restrict__ weight, float eps, int* __restrict__ error_flag) {
+    __shared__ uint4 ring[C > 0 ? kSlots : 1][kVecPerLane * kWave];
+    __shared__ int slot_row[kSlots];
+    const int wave = (int)(threadIdx.x / kWave);
+    const int lane = (int)(threadIdx.x % kWave);
+    const int r0 = (int)(((int64_t)blockIdx.x * num_rows) / gridDim.x);
+    const int r1 = (int)(((int64_t)(blockIdx.x + 1) * num_rows) / gridDim.x);
+    const int rows = r1 - r0;
+    const int nvec = (int)(row_bytes / 16);  // multiple of 64 (checked on the host)
+    const int vpl = nvec / kWave;            // vectors per lane, <= kVecPerLane
+
+    if (C > 0) {
+        if (threadIdx.x < kSlots) slot_row[threadIdx.x] = 0;
+        __syncthreads();
+    }
+
+    if (wave < P) {
+        // ---------------- producer waves
+        for (int i = wave; i < rows; i += P) {
+            const int r = r0 + i;
+            const int s = i % kSlots;
+            if (C > 0 && !lds_wait(&slot_row[s], 0)) {
+                if (lane == 0) atomicOr(error_flag, 1);
+                return;
+            }
+            const int tok = row_token[r];
+            if (tok < 0 || tok >= num_tokens) {  // not a valid token: report, keep the ring moving
+                if (lane == 0) atomicOr(error_flag, 4);
+                if (C > 0) lds_store_release(&slot_row[s], i + 1);
+                continue;
+            }
+            const uint4* src = reinterpret_cast<const uint4*>(host_base + (uint64_t)tok * token_stride);
+            uint4* d = reinterpret_cast<uint4*>(dst + (uint64_t)r * row_bytes);
+            uint4 v[kVecPerLane];
+#pragma unroll
+            for (int k = 0; k < kVecPerLane; k++)
+                if (k < vpl) v[k] = src[k * kWave + lane];
+#pragma unroll
+            for (int k = 0; k < kVecPerLane; k++)
+                if (k < vpl) d[k * kWave + lane] = v[k];
+            if (C > 0) {
+#pragma unroll
+                for (int k = 0; k < kVecPerLane; k++)
+                    if (k < vpl) ring[s][k * kWave + lane] = v[k];
+                lds_store_release(&slot_row[s], i + 1);
+            }
+        }
+    } else if (C > 0) {
+        // ---------------- consumer waves
+        const int c = wave - P;
+        // This lane's weights: the same element positions in every row.
+        uint4 w[kVecPerLane];
+        const uint4* wv = reinterpret_cast<const uint4*>(weight);
+#pragma unroll
+        for (int k = 0; k < kVecPerLane; k++)
+            if (k < vpl) w[k] = wv[k * kWave + lane];
+        const float inv_dim = 1.0f / (float)(row_bytes / 2);
+        for (int i = c; i < rows; i += C) {
+            const int r = r0 + i;
+            const int s = i % kSlots;
+            if (!lds_wait(&slot_row[s], i + 1)) {
+                if (lane == 0) atomicOr(error_flag, 2);
+                return;
+            }
+            uint4 x[kVecPerLane];
+            float ss = 0.f;
+#pragma unroll
+            for (int k = 0; k < kVecPerLane; k++) {
+                if (k < vpl) {
+                    x[k] = ring[s][k * kWave + lane];
+                    const uint32_t q[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float a = bf16_lo(q[j]), b = bf16_hi(q[j]);
+                        ss += a * a + b * b;
+                    }
+                }
+            }
+            lds_store_release(&slot_row[s], 0);  // row is in registers: free the slot
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+            const float scale = 1.0f / sqrtf(ss * inv_dim + eps);
+            uint4* o = reinterpret_cast<uint4*>(out + (uint64_t)r * row_bytes);
+#pragma unroll
+            for (int k = 0; k < kVecPerLane; k++) {
+                if (k < vpl) {
+                    const uint32_t q[4] = {x[k].x, x[k].y, x[k].z, x[k].w};
+                    const uint32_t g[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+                    uint32_t y[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const float lo = bf16_lo(q[j]) * scale * bf16_lo(g[j]);
+                        const float hi = bf16_hi(q[j]) * scale * bf16_hi(g[j]);
+                        y[j] = to_bf16(lo) | (to_bf16(hi) << 16);
+                    }
+                    o[k * kWave + lane] = make_uint4(y[0], y[1], y[2], y[3]);
+                }
+            }
+        }
+    }
+}
+
+int g_cus = 0;
+int cus() {
+    if (!g_cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || g_cus <= 0)
+            g_cus = 256;
+    }
+    return g_cus;
+}
+
+}  // namespace
+
+extern "C" int gfd_moe_route(const float* logits, int num_tokens, int num_experts, int* top2, int* offsets,
+                             int* row_token, void* stream) {
+    if (num_tokens <= 0 || num_experts < 2 || num_experts > 64 || !logits || !top2 || !offsets || !row_token)
+        return (int)hipErrorInvalidValue;
+    hipStream_t st = (hipStream_t)stream;
+    const int waves_per_block = 256 / kWave;
+    hipLaunchKernelGGL(moe_top2_kernel, dim3((num_tokens + waves_per_block - 1) / waves_per_block), dim3(256), 0, st,
+                       logits, num_tokens, num_experts, top2);
+    hipLaunchKernelGGL(moe_lists_kernel, dim3(num_experts), dim3(256), 0, st, top2, num_tokens, num_experts, offsets,
+                       row_token);
+    return (int)hipGetLastError();
+}
+
+extern "C" int gfd_sg_gather_rmsnorm(const void* host_base, uint64_t token_stride, int num_tokens, const int* row_token,
+                                     int num_rows, uint32_t row_bytes, void* dst, void* out, const uint16_t* weight,
+                                     float eps, int num_blocks, int* error_flag, void* stream) {
+    if (num_rows < 0 || num_tokens <= 0 || !host_base || !row_token || !dst || !error_flag || row_bytes == 0 ||
+        row_bytes % (kWave * 16) != 0 || row_bytes > (uint32_t)kMaxRowBytes || (out && !weight))
+        return (int)hipErrorInvalidValue;
+    if (num_rows == 0) return 0;
+    if (num_blocks <= 0) num_blocks = cus();
+    if (num_blocks > num_rows) num_blocks = num_rows;
+    hipStream_t st = (hipStream_t)stream;
+    if (out) {
+        hipLaunchKernelGGL((sg_gather_norm_kernel<4, 4>), dim3(num_blocks), dim3(kWave * 8), 0, st,
+                           (const uint8_t*)host_base, token_stride, num_tokens, row_token, num_rows, row_bytes,
+                           (uint8_t*)dst, (uint8_t*)out, weight, eps, error_flag);
+    } else {
+        hipLaunchKernelGGL((sg_gather_norm_kernel<4, 0>), dim3(num_blocks), dim3(kWave * 4), 0, st,
+                           (const uint8_t*)host_base, token_stride, num_tokens, row_token, num_rows, row_bytes,
+                           (uint8_t*)dst, (uint8_t*)nullptr, weight, eps, error_flag);
+    }
+    return (int)hipGetLastError();
+}

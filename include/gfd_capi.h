@@ -139,6 +139,25 @@ int gfd_zero_copy_gather_tokens(const uint64_t* src_addrs, void* dst, uint32_t t
 /* Arbitrary SG list (device-readable array of entries, disjoint destinations). */
 int gfd_zero_copy_gather(const gfd_sg_entry* entries, int count, void* stream);
 
+/* ---- MoE-routed SG gather with a wave-specialised consumer (the SG
+ * warp-specialised path, reference include/gfd/sg_warp_spec.cuh and
+ * examples/09_sg_warp_spec.cu, kept entirely on the GPU) ---- */
+/* Top-2 experts per token of logits[num_tokens][num_experts] (fp32, HBM;
+ * ties -> lower expert id) into top2[2*num_tokens]; per-expert row lists in
+ * token order: offsets[num_experts+1], row_token[2*num_tokens] (expert-major). */
+int gfd_moe_route(const float* logits, int num_tokens, int num_experts, int* top2, int* offsets,
+                  int* row_token, void* stream);
+/* Row r: token row_token[r] (host_base + token*token_stride, row_bytes bytes,
+ * pinned host memory) -> dst + r*row_bytes (HBM).  out != NULL: producer waves
+ * fetch into an LDS ring and consumer waves write the bf16 RMSNorm
+ * x / sqrt(mean(x^2) + eps) * weight to out + r*row_bytes; out == NULL: pure
+ * transfer.  row_bytes a multiple of 1024, at most 14336.  *error_flag
+ * (device int, zeroed by the caller) receives nonzero bits on a bad token id
+ * or a stalled hand-off. */
+int gfd_sg_gather_rmsnorm(const void* host_base, uint64_t token_stride, int num_tokens,
+                          const int* row_token, int num_rows, uint32_t row_bytes, void* dst, void* out,
+                          const uint16_t* weight, float eps, int num_blocks, int* error_flag, void* stream);
+
 /* ---- GFD Queue mode (reference include/gfd/device.cuh, examples/04_benchmark.cu:31-54) ---- */
 /* DescriptorQueue in fine-grained host memory, zeroed. */
 int gfd_queue_alloc(void** queue);

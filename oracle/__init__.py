@@ -202,6 +202,28 @@ def bf16_to_f32(bits):
     return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
 
 
+def f32_to_bf16(x):
+    """Round-to-nearest-even fp32 -> bf16 bits (finite inputs)."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + np.uint64(0x7FFF) + ((u >> np.uint64(16)) & np.uint64(1))) >> np.uint64(16)
+    return r.astype(np.uint16)
+
+
+def moe_token_values(num_tokens, dim, seed=DATA_SEED):
+    """bf16 activations [num_tokens, dim]: successive xorshift64 outputs x ->
+    ((x >> 40) / 2**24) * 2 - 1, rounded to bf16 (finite, in [-1, 1])."""
+    x = xorshift64_seq(seed, num_tokens * dim)
+    u = (x >> np.uint64(40)).astype(np.float64) / float(1 << 24)
+    return f32_to_bf16((u * 2.0 - 1.0).astype(np.float32)).reshape(num_tokens, dim)
+
+
+def moe_weight(dim, seed=PERM_SEED):
+    """bf16 RMSNorm weight [dim]: 0.5 + ((x >> 40) / 2**24), rounded to bf16."""
+    x = xorshift64_seq(seed, dim)
+    u = (x >> np.uint64(40)).astype(np.float64) / float(1 << 24)
+    return f32_to_bf16((0.5 + u).astype(np.float32))
+
+
 def rmsnorm_rows(x_f32, weight_f32, eps):
     """y = x * w / sqrt(mean(x^2) + eps) per row, fp32 (textbook RMSNorm)."""
     x = np.asarray(x_f32, dtype=np.float32)

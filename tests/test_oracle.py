@@ -270,3 +270,20 @@ def test_pool_back_to_back_gathers_do_not_lose_tasks():
         pool.close()
     assert len(times) == 3000
     assert (staging == oracle.expected_gather(region, perm, t, 2 * t)).all()
+
+
+def test_bf16_rounding_known_values():
+    # Round-to-nearest-even: 1 + 2^-8 is halfway between bf16 1.0 and
+    # 1 + 2^-7 and goes to the even one; 1 + 3*2^-9 rounds up; the result of
+    # every representable bf16 value is itself.
+    x = np.array([1.0, 1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -9, -2.5, 0.0], np.float32)
+    assert oracle.f32_to_bf16(x).tolist() == [0x3F80, 0x3F80, 0x3F81, 0xC020, 0x0000]
+    allb = np.arange(0, 0x7F80, 7, dtype=np.uint16)
+    assert (oracle.f32_to_bf16(oracle.bf16_to_f32(allb)) == allb).all()
+
+
+def test_moe_token_values_and_weight_ranges():
+    v = oracle.bf16_to_f32(oracle.moe_token_values(16, 512))
+    assert v.min() >= -1.0 and v.max() <= 1.0 and np.isfinite(v).all()
+    w = oracle.bf16_to_f32(oracle.moe_weight(512))
+    assert w.min() >= 0.5 and w.max() <= 1.5
