@@ -61,6 +61,33 @@ class PollerInfo(ctypes.Structure):
     ]
 
 
+class DeviceSGEntry(ctypes.Structure):
+    """gfd_device_sg_entry / gfd::DeviceSGEntry: 24 bytes {u64 src, u64 dst, u32 size, u32 tag}."""
+
+    _fields_ = [("src", ctypes.c_uint64), ("dst", ctypes.c_uint64), ("size", ctypes.c_uint32),
+                ("tag", ctypes.c_uint32)]
+
+
+DEVICE_SG_ENTRY_DTYPE = np.dtype([("src", np.uint64), ("dst", np.uint64), ("size", np.uint32), ("tag", np.uint32)])
+
+
+class SessionResult(ctypes.Structure):
+    """gfd_session_result: a session's get_stats() plus kernel-reported counters."""
+
+    _fields_ = [("units_done", ctypes.c_uint64), ("bytes", ctypes.c_uint64), ("lists_done", ctypes.c_uint64),
+                ("error_bits", ctypes.c_uint64), ("elapsed_ms", ctypes.c_double), ("grid", ctypes.c_int),
+                ("block", ctypes.c_int), ("tokens_per_chunk", ctypes.c_int), ("chunks_per_tile", ctypes.c_int)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+MAX_TILES = 1024
+MAX_SG_LISTS = 512
+MAX_SG_POOL_ENTRIES = 16384
+SG_FLAG_NONE, SG_FLAG_HOST_SUBMITTED = 0, 1
+
+
 TRACE_DTYPE = np.dtype([("t_ns", np.uint64), ("kind", np.uint32), ("a", np.uint32), ("b", np.uint64)])
 TRACE_KINDS = {1: "batch_first", 2: "flush", 3: "issued", 4: "done", 5: "gap_flush", 6: "direct_begin",
                7: "chunk", 8: "direct_end", 9: "gather_entry", 10: "gather_idle", 11: "gather_published",
@@ -131,6 +158,18 @@ def _declare(L):
         "gfd_bench_submit_direct": ([vp, vp, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_zero_copy_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
         "gfd_bench_queue": ([vp, vp, vp, c_int, c_u32, ctypes.POINTER(c_u64), c_int, c_int, c_u64, pd], c_int),
+        "gfd_warp_spec_run": ([vp, vp, c_u32, c_u32, c_u32, c_u32, c_int, c_int, c_int, vp, c_int, pd,
+                               ctypes.POINTER(SessionResult)], c_int),
+        "gfd_sg_session_create": ([c_int, c_int, c_u32, pvp], c_int),
+        "gfd_sg_session_destroy": ([vp], None),
+        "gfd_sg_session_submit": ([vp, vp, c_u32, c_u32, c_u32], ctypes.c_int64),
+        "gfd_sg_session_launch": ([vp, vp, vp], c_int),
+        "gfd_sg_session_launch_gpu_submit": ([vp, vp, c_u32, c_u32, vp, vp], c_int),
+        "gfd_sg_session_synchronize": ([vp, c_u64], c_int),
+        "gfd_sg_session_reset": ([vp], c_int),
+        "gfd_sg_session_stats": ([vp, ctypes.POINTER(SessionResult)], c_int),
+        "gfd_sg_session_queue": ([vp], vp),
+        "gfd_bench_sg_session": ([vp, vp, c_u32, c_u32, c_int, c_int, pd], c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -394,6 +433,95 @@ def sg_gather_rmsnorm(host_base, token_stride, num_tokens, d_row_token, num_rows
                       d_weight=None, eps=1e-6, num_blocks=0, d_error=None, stream=None):
     _check(lib().gfd_sg_gather_rmsnorm(host_base, token_stride, num_tokens, d_row_token, num_rows, row_bytes, d_dst,
                                        d_out, d_weight, eps, num_blocks, d_error, stream), "gfd_sg_gather_rmsnorm")
+
+
+def warp_spec_run(cpu_src, gpu_dst, total_tokens, token_size, tokens_per_tile=128, tokens_per_chunk=0,
+                  double_buffer=False, per_tile_mode=False, num_blocks=0, token_sums=None, iters=1):
+    """WarpSpecSession (reference include/gfd/warp_spec_session.h:14-132) over
+    tokens [0, total_tokens): construct, then `iters` times launch +
+    synchronize.  token_sums: device float[total_tokens] for the per-token
+    sum consumer, or None for a no-op consumer.  Returns (result dict, kernel
+    times in ms)."""
+    res = SessionResult()
+    times = np.zeros(max(iters, 1), dtype=np.float64)
+    _check(lib().gfd_warp_spec_run(cpu_src, gpu_dst, total_tokens, token_size, tokens_per_tile, tokens_per_chunk,
+                                   int(bool(double_buffer)), int(bool(per_tile_mode)), num_blocks, token_sums, iters,
+                                   times.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), ctypes.byref(res)),
+           "gfd_warp_spec_run")
+    return res.as_dict(), times
+
+
+def device_sg_entries(src, dst, size, tag=0):
+    """Structured array of DeviceSGEntry rows (numpy, 24 bytes each)."""
+    src = np.asarray(src, dtype=np.uint64)
+    a = np.zeros(len(src), dtype=DEVICE_SG_ENTRY_DTYPE)
+    a["src"] = src
+    a["dst"] = np.asarray(dst, dtype=np.uint64)
+    a["size"] = size
+    a["tag"] = tag
+    return a
+
+
+class SGWarpSpecSession:
+    """gfd::SGWarpSpecSession (reference include/gfd/warp_spec_session.h:142-258,
+    src/sg_warp_spec_session.cpp) with the built-in consumers of the C-ABI."""
+
+    def __init__(self, num_compute_warps=1, num_blocks=0, idle_limit_ms=0):
+        h = ctypes.c_void_p()
+        _check(lib().gfd_sg_session_create(num_compute_warps, num_blocks, idle_limit_ms, ctypes.byref(h)),
+               "gfd_sg_session_create")
+        self._h = h.value
+
+    def submit_sg_list(self, entries, list_id, flags=SG_FLAG_HOST_SUBMITTED):
+        """entries: DEVICE_SG_ENTRY_DTYPE array.  Returns the ring index."""
+        entries = np.ascontiguousarray(entries, dtype=DEVICE_SG_ENTRY_DTYPE)
+        idx = lib().gfd_sg_session_submit(self._h, entries.ctypes.data if len(entries) else None, len(entries),
+                                          list_id, flags)
+        if idx < 0:
+            _check(1, "gfd_sg_session_submit")
+        return idx
+
+    def launch(self, list_sums=None, stream=None):
+        _check(lib().gfd_sg_session_launch(self._h, list_sums, stream), "gfd_sg_session_launch")
+
+    def launch_gpu_submit(self, d_entries, entries_per_list, num_lists, list_sums=None, stream=None):
+        _check(lib().gfd_sg_session_launch_gpu_submit(self._h, d_entries, entries_per_list, num_lists, list_sums,
+                                                      stream), "gfd_sg_session_launch_gpu_submit")
+
+    def synchronize(self, extra_gpu_lists=0):
+        _check(lib().gfd_sg_session_synchronize(self._h, extra_gpu_lists), "gfd_sg_session_synchronize")
+
+    def reset(self):
+        _check(lib().gfd_sg_session_reset(self._h), "gfd_sg_session_reset")
+
+    def stats(self):
+        r = SessionResult()
+        _check(lib().gfd_sg_session_stats(self._h, ctypes.byref(r)), "gfd_sg_session_stats")
+        return r.as_dict()
+
+    def queue_ptr(self):
+        return lib().gfd_sg_session_queue(self._h)
+
+    def bench(self, entries, entries_per_list, warmup=2, iters=10):
+        entries = np.ascontiguousarray(entries, dtype=DEVICE_SG_ENTRY_DTYPE)
+        t = np.zeros(iters, dtype=np.float64)
+        _check(lib().gfd_bench_sg_session(self._h, entries.ctypes.data, len(entries), entries_per_list, warmup, iters,
+                                          t.ctypes.data_as(ctypes.POINTER(ctypes.c_double))), "gfd_bench_sg_session")
+        return t
+
+    def close(self):
+        if self._h:
+            lib().gfd_sg_session_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+SgWarpSpecSession = SGWarpSpecSession
 
 
 def build(verbose=False):

@@ -12,6 +12,7 @@
 #include "gather_engine.h"
 #include "sdma.h"
 #include "gfd/cpu_polling.h"
+#include "capi_error.h"
 #include "gfd/hip_shim.h"
 #include "gfd/sg_task_queue.h"
 #include "gfd/staging_pool.h"
@@ -40,6 +41,8 @@ double elapsed_us(std::chrono::steady_clock::time_point a, std::chrono::steady_c
 }
 
 }  // namespace
+
+void gfd_internal_set_error(const char* what) { g_last_error = what ? what : ""; }
 
 extern "C" {
 

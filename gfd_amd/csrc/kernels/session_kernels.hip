@@ -1,0 +1,335 @@
+// Kernels and C-ABI entry points for the WarpSpec / SG-WarpSpec sessions.
+//
+// The device frameworks (include/gfd/warp_spec.h, sg_warp_spec.h) are
+// header-only templates a user instantiates with their own functor, exactly as
+// with the reference's GFD_WARP_SPEC_KERNEL / GFD_SG_WARP_SPEC_KERNEL.  This
+// file instantiates them with the functors the reference's own tests use
+// (per-token float sums: test/test_db_small_tiles.cu:18-31; a no-op consumer:
+// test/test_sg_e2e.cu:10-17; a GPU submitter wave:
+// test/test_sg_gpu_submit.cu:20-213) plus a per-list checksum consumer, so
+// FFI callers and the tests can drive the sessions end to end.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <vector>
+
+#include "gfd/sg_device_primitives.h"
+#include "gfd/sg_warp_spec.h"
+#include "gfd/warp_spec.h"
+#include "gfd/warp_spec_session.h"
+#include "capi_error.h"
+#include "gfd_capi.h"
+
+static_assert(sizeof(gfd_device_sg_entry) == sizeof(gfd::DeviceSGEntry), "gfd_device_sg_entry layout");
+static_assert(sizeof(gfd_session_result) % 8 == 0, "gfd_session_result layout");
+
+namespace {
+
+using gfd::sg_warp_spec::SGListView;
+using gfd::warp_spec::ChunkView;
+
+// Wave sum of a float; every lane gets the result.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_sum(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, o, 64);
+        const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), o, 64);
+        v += ((uint64_t)hi << 32) | lo;
+    }
+    return v;
+}
+
+// out[global token] = sum of the token's floats (test_db_small_tiles.cu:18-31),
+// summed by the whole wave with 16-byte loads from HBM.
+struct TokenSum {
+    float* out;
+    __device__ void operator()(ChunkView c) const {
+        const uint32_t nf = c.token_size / 4;
+        for (uint32_t i = 0; i < c.size; i++) {
+            const float* t = c.data<float>((int)i);
+            float s = 0.f;
+            for (uint32_t k = (uint32_t)c.lane_id; k < nf; k += 64) s += t[k];
+            s = wave_sum(s);
+            if (c.lane_id == 0) out[c.global_idx((int)i)] = s;
+        }
+    }
+};
+
+struct NullChunk {
+    __device__ void operator()(ChunkView) const {}
+};
+
+// list_sums[list_id] += sum of the list's landed bytes read as little-endian
+// u32 words (a trailing partial word adds its bytes one by one).  Integer
+// sums do not depend on the order of the adds.
+struct ListChecksum {
+    unsigned long long* list_sums;
+    __device__ void operator()(SGListView v) const {
+        uint64_t acc = 0;
+        for (uint32_t e = 0; e < v.count; e++) {
+            const gfd::DeviceSGEntry d = v.get_entry(e);
+            const uint8_t* p = reinterpret_cast<const uint8_t*>(d.dst_addr);
+            const uint32_t nw = d.size / 4;
+            if ((d.dst_addr & 3) == 0) {
+                const uint32_t* w = reinterpret_cast<const uint32_t*>(p);
+                for (uint32_t k = (uint32_t)v.lane_id; k < nw; k += 64) acc += w[k];
+            } else {
+                for (uint32_t k = (uint32_t)v.lane_id; k < nw; k += 64)
+                    acc += (uint32_t)p[4 * k] | ((uint32_t)p[4 * k + 1] << 8) | ((uint32_t)p[4 * k + 2] << 16) |
+                           ((uint32_t)p[4 * k + 3] << 24);
+            }
+            for (uint32_t b = nw * 4 + (uint32_t)v.lane_id; b < d.size; b += 64) acc += p[b];
+        }
+        acc = wave_sum(acc);
+        if (v.lane_id == 0 && v.list_id < (uint32_t)gfd::MAX_SG_LISTS)
+            atomicAdd(&list_sums[v.list_id], (unsigned long long)acc);
+    }
+};
+
+struct NullList {
+    __device__ void operator()(SGListView) const {}
+};
+
+GFD_WARP_SPEC_KERNEL(ws_token_sum_kernel, TokenSum)
+GFD_WARP_SPEC_KERNEL_DB(ws_token_sum_kernel_db, TokenSum)
+GFD_WARP_SPEC_KERNEL(ws_null_kernel, NullChunk)
+GFD_WARP_SPEC_KERNEL_DB(ws_null_kernel_db, NullChunk)
+GFD_SG_WARP_SPEC_KERNEL(sg_checksum_kernel, ListChecksum)
+GFD_SG_WARP_SPEC_KERNEL(sg_null_kernel, NullList)
+
+// Transfer (wave 0) + compute (wave 1) + submitter (wave 2) per workgroup, as
+// test/test_sg_gpu_submit.cu:20-213: workgroup b submits lists b, b + grid,
+// ... (list i = entries [i*epl, (i+1)*epl) of d_entries), waits for all
+// num_lists to land, then sets terminate.
+template <typename F>
+__global__ void sg_gpu_submit_kernel(gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq, F fn,
+                                     const gfd::DeviceSGEntry* d_entries, uint32_t epl, uint32_t num_lists) {
+    gfd::sg_warp_spec::_sg_transfer_warp_loop(dq, sq, fn);  // waves 0 and 1 run here; wave 2 returns
+    if (gfd::wave::wave_id() != 2) return;
+    gfd::SGDeviceCounters* cnt = gfd::sg_device_counters(sq);
+    for (uint32_t l = blockIdx.x; l < num_lists; l += gridDim.x) {
+        if (gfd::sg::sg_submit_list(sq, d_entries + (uint64_t)l * epl, epl, l, gfd::SG_FLAG_NONE) == ~0ull) {
+            if (gfd::wave::lane_id() == 0)
+                __hip_atomic_fetch_or(&cnt->error, gfd::SG_ERR_RING_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+    }
+    if (blockIdx.x == 0) {
+        gfd::sg::sg_wait_list_done(sq, num_lists);
+        gfd::sg::sg_terminate(sq);
+    }
+}
+
+int fail(int code, const char* what) {
+    gfd_internal_set_error(what);
+    return code ? code : (int)hipErrorInvalidValue;
+}
+
+void fill_ws_result(gfd::WarpSpecSession& s, const gfd::WarpSpecConfig& c, gfd_session_result* r) {
+    const auto st = s.get_stats();
+    r->units_done = st.descriptors_processed;
+    r->bytes = st.bytes_transferred;
+    r->lists_done = s.tiles_done();
+    r->error_bits = s.error_bits();
+    r->elapsed_ms = st.elapsed_ms;
+    const auto p = s.get_launch_params();
+    r->grid = (int)p.grid;
+    r->block = (int)p.block;
+    r->tokens_per_chunk = (int)c.effective_tokens_per_chunk();
+    r->chunks_per_tile = (int)c.chunks_per_tile();
+}
+
+gfd::SGWarpSpecSession* S(gfd_sg_session_t s) { return static_cast<gfd::SGWarpSpecSession*>(s); }
+
+}  // namespace
+
+extern "C" int gfd_warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t total_tokens, uint32_t token_size,
+                                 uint32_t tokens_per_tile, uint32_t tokens_per_chunk, int double_buffer,
+                                 int per_tile_mode, int num_blocks, float* token_sums, int iters,
+                                 double* kernel_ms, gfd_session_result* res) {
+    if (!cpu_src || !gpu_dst || total_tokens == 0 || token_size == 0 || iters < 1 || !res)
+        return fail(hipErrorInvalidValue, "gfd_warp_spec_run: invalid argument");
+    gfd::WarpSpecConfig c;
+    c.total_tokens = total_tokens;
+    c.token_size = token_size;
+    c.cpu_src = const_cast<void*>(cpu_src);
+    c.gpu_dst = gpu_dst;
+    c.tokens_per_tile = tokens_per_tile;
+    c.tokens_per_chunk = tokens_per_chunk;
+    c.double_buffer = double_buffer != 0;
+    c.per_tile_mode = per_tile_mode != 0;
+    c.num_blocks = num_blocks;
+    if (c.tokens_per_tile == 0 || c.effective_tokens_per_chunk() == 0 ||
+        c.tokens_per_tile % c.effective_tokens_per_chunk() != 0 || c.block_size() > 1024 ||
+        c.chunks_per_tile() > (uint32_t)gfd::warp_spec::MAX_CHUNKS_PER_TILE)
+        return fail(hipErrorInvalidValue, "gfd_warp_spec_run: tile / chunk shape not supported");
+    gfd::WarpSpecSession s(c);
+    if (!s.ok()) return fail(hipErrorInvalidValue, "gfd_warp_spec_run: session construction failed");
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
+        return fail(hipErrorOutOfMemory, "gfd_warp_spec_run: event creation failed");
+    int rc = 0;
+    const auto p = s.get_launch_params();
+    for (int it = 0; it < iters && rc == 0; it++) {
+        // launch() with the HIP events around the kernel alone: before_launch
+        // clears the signals with a blocking memset first.
+        s.before_launch(nullptr);
+        (void)hipEventRecord(e0, nullptr);
+        if (token_sums) {
+            if (c.double_buffer)
+                hipLaunchKernelGGL(ws_token_sum_kernel_db, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
+                                   p.cpu_base, TokenSum{token_sums});
+            else
+                hipLaunchKernelGGL(ws_token_sum_kernel, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
+                                   p.cpu_base, TokenSum{token_sums});
+        } else {
+            if (c.double_buffer)
+                hipLaunchKernelGGL(ws_null_kernel_db, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
+                                   p.cpu_base, NullChunk{});
+            else
+                hipLaunchKernelGGL(ws_null_kernel, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
+                                   p.cpu_base, NullChunk{});
+        }
+        (void)hipEventRecord(e1, nullptr);
+        const hipError_t le = hipGetLastError();
+        const bool ok = s.synchronize();
+        float ms = 0.f;
+        (void)hipEventElapsedTime(&ms, e0, e1);
+        if (kernel_ms) kernel_ms[it] = ms;
+        if (le != hipSuccess) rc = fail(le, "gfd_warp_spec_run: launch failed");
+        else if (!ok) rc = fail(hipErrorLaunchFailure, "gfd_warp_spec_run: kernel reported an error or missing tiles");
+    }
+    fill_ws_result(s, c, res);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc;
+}
+
+extern "C" int gfd_sg_session_create(int num_compute_warps, int num_blocks, uint32_t idle_limit_ms,
+                                     gfd_sg_session_t* out) {
+    if (!out) return fail(hipErrorInvalidValue, "gfd_sg_session_create: out is NULL");
+    gfd::SGWarpSpecConfig c;
+    c.num_compute_warps = num_compute_warps;
+    c.num_blocks = num_blocks;
+    c.idle_limit_ms = idle_limit_ms;
+    auto* s = new gfd::SGWarpSpecSession(c);
+    if (!s->ok()) {
+        delete s;
+        return fail(hipErrorInvalidValue, "gfd_sg_session_create: session construction failed");
+    }
+    *out = s;
+    return 0;
+}
+
+extern "C" void gfd_sg_session_destroy(gfd_sg_session_t s) { delete S(s); }
+
+extern "C" int64_t gfd_sg_session_submit(gfd_sg_session_t s, const gfd_device_sg_entry* entries, uint32_t count,
+                                         uint32_t list_id, uint32_t flags) {
+    if (!s) return -1;
+    const uint64_t idx =
+        S(s)->submit_sg_list(reinterpret_cast<const gfd::DeviceSGEntry*>(entries), count, list_id, flags);
+    if (idx == ~0ull) {
+        fail(hipErrorInvalidValue, "gfd_sg_session_submit: rejected (invalid argument, or ring / pool full)");
+        return -1;
+    }
+    return (int64_t)idx;
+}
+
+extern "C" int gfd_sg_session_launch(gfd_sg_session_t s, unsigned long long* list_sums, void* stream) {
+    if (!s) return fail(hipErrorInvalidValue, "gfd_sg_session_launch: NULL session");
+    if (list_sums) S(s)->launch(sg_checksum_kernel, ListChecksum{list_sums}, stream);
+    else S(s)->launch(sg_null_kernel, NullList{}, stream);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail(e, "gfd_sg_session_launch: launch failed");
+}
+
+extern "C" int gfd_sg_session_launch_gpu_submit(gfd_sg_session_t s, const gfd_device_sg_entry* d_entries,
+                                                uint32_t entries_per_list, uint32_t num_lists,
+                                                unsigned long long* list_sums, void* stream) {
+    if (!s || !d_entries || entries_per_list == 0 || num_lists == 0 ||
+        entries_per_list > (uint32_t)gfd::MAX_SG_POOL_ENTRIES || num_lists > (uint32_t)gfd::MAX_SG_LISTS)
+        return fail(hipErrorInvalidValue, "gfd_sg_session_launch_gpu_submit: invalid argument");
+    gfd::SGWarpSpecSession* p = S(s);
+    p->before_launch(stream);
+    const auto* ents = reinterpret_cast<const gfd::DeviceSGEntry*>(d_entries);
+    const dim3 grid((unsigned)p->num_blocks()), block(3 * 64);
+    if (list_sums)
+        hipLaunchKernelGGL(sg_gpu_submit_kernel<ListChecksum>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),
+                           p->get_sg_queue(), ListChecksum{list_sums}, ents, entries_per_list, num_lists);
+    else
+        hipLaunchKernelGGL(sg_gpu_submit_kernel<NullList>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),
+                           p->get_sg_queue(), NullList{}, ents, entries_per_list, num_lists);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail(e, "gfd_sg_session_launch_gpu_submit: launch failed");
+}
+
+extern "C" int gfd_sg_session_synchronize(gfd_sg_session_t s, uint64_t extra_gpu_lists) {
+    if (!s) return fail(hipErrorInvalidValue, "gfd_sg_session_synchronize: NULL session");
+    return S(s)->synchronize(extra_gpu_lists) ? 0 : fail(hipErrorLaunchFailure, "gfd_sg_session_synchronize: lists did not land or the kernel reported an error");
+}
+
+extern "C" int gfd_sg_session_reset(gfd_sg_session_t s) {
+    if (!s) return fail(hipErrorInvalidValue, "gfd_sg_session_reset: NULL session");
+    S(s)->reset();
+    return 0;
+}
+
+extern "C" int gfd_sg_session_stats(gfd_sg_session_t s, gfd_session_result* r) {
+    if (!s || !r) return fail(hipErrorInvalidValue, "gfd_sg_session_stats: invalid argument");
+    const auto st = S(s)->get_stats();
+    *r = gfd_session_result{};
+    r->units_done = st.descriptors_processed;
+    r->bytes = st.bytes_transferred;
+    r->lists_done = S(s)->lists_landed();
+    r->error_bits = S(s)->error_bits();
+    r->elapsed_ms = st.elapsed_ms;
+    r->grid = S(s)->num_blocks();
+    return 0;
+}
+
+extern "C" void* gfd_sg_session_queue(gfd_sg_session_t s) { return s ? (void*)S(s)->get_sg_queue() : nullptr; }
+
+// Host-submitted SG transfer timed from launch until the host has seen every
+// list land (done markers), then terminate + sync.  times_us[iters].
+extern "C" int gfd_bench_sg_session(gfd_sg_session_t s, const gfd_device_sg_entry* entries, uint32_t count,
+                                    uint32_t entries_per_list, int warmup, int iters, double* times_us) {
+    if (!s || !entries || count == 0 || entries_per_list == 0 || iters < 1 || !times_us ||
+        count > (uint32_t)gfd::MAX_SG_POOL_ENTRIES ||
+        (count + entries_per_list - 1) / entries_per_list > (uint32_t)gfd::MAX_SG_LISTS)
+        return fail(hipErrorInvalidValue,
+                    "gfd_bench_sg_session: invalid argument (at most 16384 entries in at most 512 lists)");
+    gfd::SGWarpSpecSession* p = S(s);
+    const uint32_t nl = (count + entries_per_list - 1) / entries_per_list;
+    for (int it = -warmup; it < iters; it++) {
+        p->reset();
+        for (uint32_t l = 0; l < nl; l++) {
+            const uint32_t b = l * entries_per_list, n = std::min(entries_per_list, count - b);
+            if (p->submit_sg_list(reinterpret_cast<const gfd::DeviceSGEntry*>(entries) + b, n, l) == ~0ull)
+                return fail(hipErrorInvalidValue, "gfd_bench_sg_session: submit rejected");
+        }
+        gfd::SGTaskQueue* sq = p->get_sg_queue();
+        const auto t0 = std::chrono::steady_clock::now();
+        p->launch(sg_null_kernel, NullList{}, nullptr);
+        // Spin until every list's done marker is up (bounded: 10 s).
+        bool all = false;
+        while (!all) {
+            all = true;
+            for (uint64_t i = 0; i < nl; i++)
+                if (__atomic_load_n(const_cast<uint64_t*>(&sq->lists[i].done), __ATOMIC_ACQUIRE) < i + 1) {
+                    all = false;
+                    break;
+                }
+            if (std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > 10.0) break;
+        }
+        const auto t1 = std::chrono::steady_clock::now();
+        if (!p->synchronize() || !all) return fail(hipErrorLaunchFailure, "gfd_bench_sg_session: lists did not land");
+        if (it >= 0) times_us[it] = std::chrono::duration<double, std::micro>(t1 - t0).count();
+    }
+    return 0;
+}

@@ -1,0 +1,351 @@
+// Host side of WarpSpecSession and SGWarpSpecSession (the reference's
+// src/warp_spec_session.cpp:8-142 and src/sg_warp_spec_session.cpp:9-186).
+//
+// The sessions own their queues (fine-grained host memory, so kernels read
+// them with system-scope loads) and HBM arrays (per-tile / per-list
+// completion words plus the device counters the kernels claim work from).
+// No CPU poller runs: the kernels' transfer waves move the data themselves.
+#include <algorithm>
+#include <chrono>
+#include <cstring>
+#include <thread>
+
+#include "gfd/log.h"
+#include "gfd/warp_spec_session.h"
+
+namespace gfd {
+
+namespace {
+
+int default_num_blocks() {
+    int dev = 0, n = 0;
+    gfd_hip_get_device(&dev);
+    if (gfd_hip_cu_count(&n, dev) != 0 || n <= 0) n = 1;
+    return n;
+}
+
+double ms_between(std::chrono::steady_clock::time_point a, std::chrono::steady_clock::time_point b) {
+    return std::chrono::duration<double, std::milli>(b - a).count();
+}
+
+uint64_t load_acquire(const volatile uint64_t* p) { return __atomic_load_n(const_cast<uint64_t*>(p), __ATOMIC_ACQUIRE); }
+void store_release(volatile uint64_t* p, uint64_t v) { __atomic_store_n(const_cast<uint64_t*>(p), v, __ATOMIC_RELEASE); }
+
+}  // namespace
+
+// ============================================================ WarpSpecSession
+
+WarpSpecSession::WarpSpecSession(const WarpSpecConfig& config) : config_(config) {
+    // Validation as src/warp_spec_session.cpp:11-23, plus the wave64 block limit.
+    if (config_.total_tokens == 0 || config_.token_size == 0) {
+        GFD_LOG_ERROR("WarpSpecSession: total_tokens and token_size must be > 0\n");
+        return;
+    }
+    const uint32_t chunk = config_.effective_tokens_per_chunk();
+    if (config_.tokens_per_tile == 0 || chunk == 0) {
+        GFD_LOG_ERROR("WarpSpecSession: tokens_per_tile and tokens_per_chunk must be > 0\n");
+        return;
+    }
+    if (config_.tokens_per_tile % chunk != 0) {
+        GFD_LOG_ERROR("WarpSpecSession: tokens_per_tile must be divisible by tokens_per_chunk\n");
+        return;
+    }
+    if (config_.block_size() > 1024) {
+        GFD_LOG_ERROR("WarpSpecSession: %u chunks per tile need %d threads (> 1024)\n", config_.chunks_per_tile(),
+                      config_.block_size());
+        return;
+    }
+    if (!config_.cpu_src || !config_.gpu_dst) {
+        GFD_LOG_ERROR("WarpSpecSession: cpu_src and gpu_dst are required\n");
+        return;
+    }
+    num_blocks_ = config_.num_blocks > 0 ? config_.num_blocks : default_num_blocks();
+
+    void* q = nullptr;
+    if (gfd_hip_host_alloc(&q, sizeof(TiledQueue), GFD_HOST_COHERENT) != 0) {
+        GFD_LOG_ERROR("WarpSpecSession: TiledQueue allocation failed\n");
+        return;
+    }
+    tq_ = static_cast<TiledQueue*>(q);
+    std::memset((void*)tq_, 0, sizeof(TiledQueue));
+    tq_->scheduler.total_tiles = config_.total_tiles();
+    tq_->scheduler.tokens_per_tile = config_.tokens_per_tile;
+    tq_->scheduler.tokens_per_chunk = chunk;
+    tq_->scheduler.chunks_per_tile = config_.chunks_per_tile();
+    tq_->scheduler.token_size = config_.token_size;
+
+    const size_t words = (size_t)MAX_TILES + TILE_DEVICE_COUNTER_WORDS;
+    void* d = nullptr;
+    if (gfd_hip_malloc(&d, words * sizeof(uint64_t)) != 0) {
+        GFD_LOG_ERROR("WarpSpecSession: device signal allocation failed\n");
+        return;
+    }
+    d_signals_ = static_cast<uint64_t*>(d);
+    gfd_hip_memset_d8((uint64_t)(uintptr_t)d_signals_, 0, words * sizeof(uint64_t));
+    tq_->d_tile_chunk_done = d_signals_;
+    ok_ = true;
+}
+
+WarpSpecSession::~WarpSpecSession() {
+    if (running_) synchronize();
+    if (d_signals_) gfd_hip_free(d_signals_);
+    if (tq_) gfd_hip_host_free(tq_);
+}
+
+WarpSpecSession::LaunchParams WarpSpecSession::get_launch_params() const {
+    LaunchParams p;
+    p.tq = tq_;
+    p.gpu_buffer = config_.gpu_dst;
+    p.cpu_base = config_.cpu_src;
+    p.grid = (unsigned)num_blocks_;
+    p.block = (unsigned)config_.block_size();
+    return p;
+}
+
+void WarpSpecSession::reset() {
+    if (running_) synchronize();
+    if (!tq_) return;
+    if (d_signals_)
+        gfd_hip_memset_d8((uint64_t)(uintptr_t)d_signals_, 0,
+                          ((size_t)MAX_TILES + TILE_DEVICE_COUNTER_WORDS) * sizeof(uint64_t));
+    std::memset((void*)tq_->tile_chunk_done, 0, sizeof(tq_->tile_chunk_done));
+    tq_->scheduler.next_tile = 0;
+    error_bits_ = 0;
+    tiles_done_ = 0;
+}
+
+void WarpSpecSession::before_launch(gfd_stream_t stream) {
+    reset();  // as the reference's launch (warp_spec_session.h:217)
+    stream_ = stream;
+    launch_time_ = std::chrono::steady_clock::now();
+    running_ = ok_;
+}
+
+bool WarpSpecSession::synchronize() {
+    if (!running_) return ok_ && error_bits_ == 0 && tiles_done_ == config_.total_tiles();
+    const int rc = gfd_hip_stream_synchronize(stream_);
+    last_elapsed_ms_ = ms_between(launch_time_, std::chrono::steady_clock::now());
+    running_ = false;
+    TileDeviceCounters c{};
+    if (rc == 0 && gfd_hip_memcpy_d2h(&c, (uint64_t)(uintptr_t)(d_signals_ + MAX_TILES), sizeof(c)) == 0) {
+        error_bits_ = c.error;
+        tiles_done_ = c.tiles_done;
+        // Host-visible progress mirror (tile_chunk_done, tiled_queue.h:41).
+        const uint32_t n = std::min<uint32_t>(config_.total_tiles(), (uint32_t)MAX_TILES);
+        if (n) gfd_hip_memcpy_d2h((void*)tq_->tile_chunk_done, (uint64_t)(uintptr_t)d_signals_, n * sizeof(uint64_t));
+        tq_->scheduler.next_tile = (uint32_t)std::min<uint64_t>(c.next_tile, config_.total_tiles());
+    } else {
+        GFD_LOG_ERROR("WarpSpecSession: synchronize failed: %s\n", gfd_hip_error_string(rc));
+        error_bits_ |= 1ull << 63;
+    }
+    if (error_bits_) GFD_LOG_ERROR("WarpSpecSession: kernel reported error bits 0x%llx\n", (unsigned long long)error_bits_);
+    return error_bits_ == 0 && tiles_done_ == config_.total_tiles();
+}
+
+WarpSpecSession::Stats WarpSpecSession::get_stats() const {
+    Stats s;
+    s.descriptors_processed = tiles_done_ * config_.tokens_per_tile;
+    s.bytes_transferred = s.descriptors_processed * (uint64_t)config_.token_size;
+    s.elapsed_ms = running_ ? ms_between(launch_time_, std::chrono::steady_clock::now()) : last_elapsed_ms_;
+    s.bandwidth_gbps = s.elapsed_ms > 0 ? (double)s.bytes_transferred / (s.elapsed_ms * 1e6) : 0.0;
+    return s;
+}
+
+// ========================================================== SGWarpSpecSession
+
+SGWarpSpecSession::SGWarpSpecSession(const SGWarpSpecConfig& config) : config_(config) {
+    if (config_.block_size() > 1024) {
+        GFD_LOG_ERROR("SGWarpSpecSession: %d compute waves exceed a 1024-thread workgroup\n", config_.num_compute_warps);
+        return;
+    }
+    num_blocks_ = config_.num_blocks > 0 ? config_.num_blocks : default_num_blocks();
+    void* q = nullptr;
+    if (gfd_hip_host_alloc(&q, sizeof(SGTaskQueue), GFD_HOST_COHERENT) != 0) {
+        GFD_LOG_ERROR("SGWarpSpecSession: SGTaskQueue allocation failed\n");
+        return;
+    }
+    sq_ = static_cast<SGTaskQueue*>(q);
+    std::memset((void*)sq_, 0, sizeof(SGTaskQueue));
+    sq_->idle_limit_ms = config_.idle_limit_ms;
+    if (gfd_hip_host_alloc(&q, sizeof(DescriptorQueue), GFD_HOST_COHERENT) != 0) {
+        GFD_LOG_ERROR("SGWarpSpecSession: DescriptorQueue allocation failed\n");
+        return;
+    }
+    dq_ = static_cast<DescriptorQueue*>(q);
+    std::memset((void*)dq_, 0, sizeof(DescriptorQueue));
+    const size_t words = (size_t)MAX_SG_LISTS + SG_DEVICE_COUNTER_WORDS;
+    void* d = nullptr;
+    if (gfd_hip_malloc(&d, words * sizeof(uint64_t)) != 0) {
+        GFD_LOG_ERROR("SGWarpSpecSession: d_list_done allocation failed\n");
+        return;
+    }
+    sq_->d_list_done = static_cast<uint64_t*>(d);
+    gfd_hip_memset_d8((uint64_t)(uintptr_t)d, 0, words * sizeof(uint64_t));
+    ok_ = true;
+}
+
+SGWarpSpecSession::~SGWarpSpecSession() {
+    if (running_) synchronize();
+    if (sq_) {
+        if (sq_->d_list_done) gfd_hip_free(sq_->d_list_done);
+        gfd_hip_host_free(sq_);
+    }
+    if (dq_) gfd_hip_host_free(dq_);
+}
+
+bool SGWarpSpecSession::list_done(uint64_t idx) const {
+    return load_acquire(&sq_->lists[idx % MAX_SG_LISTS].done) >= idx + 1;
+}
+
+void SGWarpSpecSession::retire_done() {
+    while (!pending_.empty() && list_done(pending_.front().idx)) pending_.pop_front();
+}
+
+bool SGWarpSpecSession::wait_until(const std::function<bool()>& cond, double limit_ms) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (uint32_t n = 0;; n++) {
+        if (cond()) return true;
+        if (n > 256) {
+            if (ms_between(t0, std::chrono::steady_clock::now()) > limit_ms) return false;
+            std::this_thread::sleep_for(std::chrono::microseconds(20));
+        }
+    }
+}
+
+double SGWarpSpecSession::wait_limit_ms() const {
+    return (config_.idle_limit_ms ? (double)config_.idle_limit_ms : 30000.0) + 10000.0;
+}
+
+uint64_t SGWarpSpecSession::submit_sg_list(const DeviceSGEntry* entries, uint32_t count, uint32_t list_id,
+                                           uint32_t flags) {
+    // src/sg_warp_spec_session.cpp:81-116, with backpressure: the ring slot's
+    // previous list and the pool entries being reused must have landed.
+    if (!ok_ || (count > 0 && !entries) || count > (uint32_t)MAX_SG_POOL_ENTRIES) {
+        GFD_LOG_ERROR("SGWarpSpecSession::submit_sg_list: invalid argument\n");
+        return ~0ull;
+    }
+    const uint64_t idx = sq_->list_alloc_idx;
+    const uint64_t pool = sq_->entry_alloc_idx;
+    retire_done();
+    auto room = [&]() {
+        retire_done();
+        if (idx >= (uint64_t)MAX_SG_LISTS && !list_done(idx - MAX_SG_LISTS)) return false;
+        return pending_.empty() || pool + count - pending_.front().pool_begin <= (uint64_t)MAX_SG_POOL_ENTRIES;
+    };
+    if (!room()) {
+        if (!running_) {
+            GFD_LOG_ERROR("SGWarpSpecSession::submit_sg_list: ring or pool full and no kernel running\n");
+            return ~0ull;
+        }
+        if (!wait_until(room, wait_limit_ms())) {
+            GFD_LOG_ERROR("SGWarpSpecSession::submit_sg_list: timed out waiting for ring / pool space\n");
+            return ~0ull;
+        }
+    }
+    for (uint32_t i = 0; i < count; i++) sq_->entries[(pool + i) % MAX_SG_POOL_ENTRIES] = entries[i];
+    SGList& l = sq_->lists[idx % MAX_SG_LISTS];
+    l.pool_offset = (uint32_t)(pool % MAX_SG_POOL_ENTRIES);
+    l.count = count;
+    l.list_id = list_id;
+    l.flags = flags;
+    store_release(&l.sequence, idx + 1);  // commit
+    sq_->entry_alloc_idx = pool + count;
+    sq_->list_alloc_idx = idx + 1;
+    pending_.push_back(Pending{idx, pool, count});
+    return idx;
+}
+
+void SGWarpSpecSession::before_launch(gfd_stream_t stream) {
+    if (running_) synchronize();
+    if (!ok_) return;
+    __atomic_store_n(&sq_->terminate, 0u, __ATOMIC_RELEASE);
+    sq_->lists_completed = 0;
+    dq_->write_idx = dq_->read_idx = dq_->done_idx = 0;
+    // Device counters: claims start at the first list no launch has consumed;
+    // GPU submitters allocate after the lists the host has already queued.
+    SGDeviceCounters c{};
+    c.list_claim = consumed_lists_;
+    c.list_alloc = sq_->list_alloc_idx;
+    c.entry_alloc = sq_->entry_alloc_idx;
+    c.entries_done = consumed_entries_;
+    c.list_known = consumed_lists_;
+    c.list_base = consumed_lists_;
+    gfd_hip_memset_d8((uint64_t)(uintptr_t)sq_->d_list_done, 0, MAX_SG_LISTS * sizeof(uint64_t));
+    gfd_hip_memcpy_h2d((uint64_t)(uintptr_t)sg_device_counters(sq_), &c, sizeof(c));
+    stream_ = stream;
+    launch_time_ = std::chrono::steady_clock::now();
+    running_ = true;
+}
+
+bool SGWarpSpecSession::synchronize(uint64_t extra_gpu_lists) {
+    if (!running_) return ok_ && error_bits_ == 0;
+    // As src/sg_warp_spec_session.cpp:118-139: every submitted list lands,
+    // then terminate releases the transfer waves.
+    const uint64_t host_end = sq_->list_alloc_idx;
+    bool landed = wait_until(
+        [&]() {
+            retire_done();
+            if (!pending_.empty()) return false;
+            for (uint64_t i = 0; i < extra_gpu_lists; i++)
+                if (!list_done(host_end + i)) return false;
+            return true;
+        },
+        wait_limit_ms());
+    __atomic_store_n(&sq_->terminate, 1u, __ATOMIC_RELEASE);
+    const int rc = gfd_hip_stream_synchronize(stream_);
+    last_elapsed_ms_ = ms_between(launch_time_, std::chrono::steady_clock::now());
+    running_ = false;
+    SGDeviceCounters c{};
+    if (rc != 0 || gfd_hip_memcpy_d2h(&c, (uint64_t)(uintptr_t)sg_device_counters(sq_), sizeof(c)) != 0) {
+        GFD_LOG_ERROR("SGWarpSpecSession: synchronize failed: %s\n", gfd_hip_error_string(rc));
+        error_bits_ |= 1ull << 63;
+        return false;
+    }
+    error_bits_ |= c.error;
+    entries_done_ = c.entries_done - consumed_entries_;
+    bytes_done_ = c.bytes_done;
+    lists_done_ = c.lists_done;
+    // Everything committed so far has been consumed (unless a wait gave up).
+    consumed_lists_ = std::max<uint64_t>((uint64_t)sq_->list_alloc_idx, c.list_alloc);
+    consumed_entries_ = std::max<uint64_t>((uint64_t)sq_->entry_alloc_idx, c.entry_alloc);
+    sq_->list_alloc_idx = consumed_lists_;
+    sq_->entry_alloc_idx = consumed_entries_;
+    sq_->list_read_idx = consumed_lists_;
+    sq_->entry_consumed_idx = consumed_entries_;
+    sq_->lists_completed = lists_done_;
+    retire_done();
+    if (!landed || !pending_.empty()) {
+        GFD_LOG_ERROR("SGWarpSpecSession: %zu submitted lists did not land\n", pending_.size());
+        pending_.clear();
+        landed = false;
+    }
+    if (error_bits_) GFD_LOG_ERROR("SGWarpSpecSession: kernel reported error bits 0x%llx\n", (unsigned long long)error_bits_);
+    return landed && error_bits_ == 0;
+}
+
+void SGWarpSpecSession::reset() {
+    if (running_) synchronize();
+    if (!sq_) return;
+    uint64_t* d = sq_->d_list_done;
+    const uint32_t idle = sq_->idle_limit_ms;
+    std::memset((void*)sq_, 0, sizeof(SGTaskQueue));
+    sq_->d_list_done = d;
+    sq_->idle_limit_ms = idle;
+    if (dq_) std::memset((void*)dq_, 0, sizeof(DescriptorQueue));
+    if (d)
+        gfd_hip_memset_d8((uint64_t)(uintptr_t)d, 0, ((size_t)MAX_SG_LISTS + SG_DEVICE_COUNTER_WORDS) * sizeof(uint64_t));
+    pending_.clear();
+    consumed_lists_ = consumed_entries_ = 0;
+    error_bits_ = entries_done_ = bytes_done_ = lists_done_ = 0;
+}
+
+SGWarpSpecSession::Stats SGWarpSpecSession::get_stats() const {
+    Stats s;
+    s.descriptors_processed = entries_done_;
+    s.bytes_transferred = bytes_done_;
+    s.elapsed_ms = running_ ? ms_between(launch_time_, std::chrono::steady_clock::now()) : last_elapsed_ms_;
+    s.bandwidth_gbps = s.elapsed_ms > 0 ? (double)s.bytes_transferred / (s.elapsed_ms * 1e6) : 0.0;
+    return s;
+}
+
+}  // namespace gfd

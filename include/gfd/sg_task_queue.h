@@ -5,6 +5,12 @@
 // fine-grained host memory; d_list_done lives in HBM).
 #include <cstdint>
 
+#ifdef __HIPCC__
+#define GFD_HD __host__ __device__
+#else
+#define GFD_HD
+#endif
+
 namespace gfd {
 
 constexpr int MAX_SG_LISTS = 512;
@@ -26,8 +32,12 @@ struct alignas(16) SGList {
     uint32_t count;
     uint32_t list_id;
     uint32_t flags;
-    volatile uint64_t sequence;  // ring slot + 1 when committed
-    uint64_t _pad;
+    volatile uint64_t sequence;  // ring slot + 1 when committed, 0 once claimed
+    // The reference's padding word.  Here it holds "ring index + 1" once the
+    // list's data has landed in HBM: a completion marker the host polls
+    // without reading device memory.  A ring slot is refilled only after the
+    // previous list in it is done, so per slot this value only grows.
+    volatile uint64_t done;
 };
 static_assert(sizeof(SGList) == 32, "SGList must be 32 bytes");
 
@@ -43,10 +53,48 @@ struct SGTaskQueue {
 
     alignas(64) volatile uint64_t lists_completed;
     volatile uint32_t terminate;
-    uint32_t _pad_term;
+    // The reference's padding word after `terminate`.  This build reads it as
+    // the transfer waves' idle limit in milliseconds (0 = 30 s): a wave that
+    // sees no committed list for that long gives up instead of spinning
+    // forever when the host never sets `terminate`.
+    uint32_t idle_limit_ms;
 
-    uint64_t* d_list_done;  // HBM, one u64 per list id
+    uint64_t* d_list_done;  // HBM, one u64 per list id (+ SGDeviceCounters after them)
 };
+
+// Claim / allocation counters kept in HBM right after d_list_done[MAX_SG_LISTS]
+// (sessions allocate MAX_SG_LISTS + SG_DEVICE_COUNTER_WORDS words).  GPU waves
+// update them with device-scope atomics, so no atomic operation ever crosses
+// PCIe into host memory.
+struct SGDeviceCounters {
+    uint64_t list_claim;      // next ring index a transfer wave claims
+    uint64_t list_alloc;      // next ring index a GPU submitter allocates
+    uint64_t entry_alloc;     // next pool index a GPU submitter allocates
+    // Entries landed, counted on from the first pool index of the launch, so
+    // entry_alloc - entries_done is the pool occupancy (exact while lists land
+    // in submission order, as the reference's entry_consumed_idx).
+    uint64_t entries_done;
+    uint64_t lists_done;      // lists landed during this launch
+    uint64_t error;           // nonzero: a bounded wait gave up (bit flags)
+    // Lowest ring index whose commit no transfer wave has seen yet.  Only the
+    // wave holding this index polls host memory; the others poll this word.
+    uint64_t list_known;
+    uint64_t stop;            // set once `terminate` has been seen: waiting waves exit
+    uint64_t list_base;       // first ring index of this launch
+    uint64_t bytes_done;      // bytes landed during this launch
+    uint64_t _pad[6];
+};
+constexpr int SG_DEVICE_COUNTER_WORDS = (int)(sizeof(SGDeviceCounters) / sizeof(uint64_t));
+
+// Bits of SGDeviceCounters::error.
+constexpr uint64_t SG_ERR_SLOT_WAIT = 1;     // transfer wave: the compute wave never freed an LDS slot
+constexpr uint64_t SG_ERR_COMPUTE_WAIT = 2;  // compute wave: the transfer wave never handed a list over
+constexpr uint64_t SG_ERR_RING_WAIT = 4;     // GPU submitter: a ring slot never became free
+static_assert(sizeof(SGDeviceCounters) == 128, "SGDeviceCounters is two cache lines");
+
+GFD_HD inline SGDeviceCounters* sg_device_counters(const SGTaskQueue* sq) {
+    return reinterpret_cast<SGDeviceCounters*>(sq->d_list_done + MAX_SG_LISTS);
+}
 
 namespace sg_compat {
 

@@ -1,0 +1,221 @@
+#pragma once
+// Wave-specialised scatter-gather framework (HIP sources only).  Same kernel
+// interface as the reference's include/gfd/sg_warp_spec.cuh:31-314:
+//
+//   struct MyCompute { __device__ void operator()(gfd::sg_warp_spec::SGListView v) { ... } };
+//   GFD_SG_WARP_SPEC_KERNEL(my_kernel, MyCompute);   // (DescriptorQueue*, SGTaskQueue*, MyCompute)
+//
+// Wave 0 of each workgroup is the transfer wave, wave 1 the compute wave;
+// further waves return from the loop right after its opening barrier, so a
+// kernel may call the loop from every wave and give the others work of its
+// own afterwards (a GPU submitter, for instance).
+//
+// The transfer wave claims the next ring index (device-scope atomic on an
+// HBM counter), waits for that list to be committed, copies every entry's
+// bytes from pinned host memory into HBM itself (zero-copy, 16-byte loads
+// over PCIe), marks the list done (d_list_done[list_id] in HBM, the header's
+// `done` word in host memory) and hands it to the compute wave through one of
+// two LDS slots, so the copy of the next list overlaps the compute of this
+// one.  The reference routes each list through descriptors and the CPU poller
+// instead; the DescriptorQueue argument is kept for the interface and unused.
+//
+// Waiting for commits: only the wave holding the lowest index whose commit no
+// wave has seen (SGDeviceCounters::list_known) reads host memory.  When its
+// list is committed it reads the next 64 sequences at once (one per lane) and
+// advances list_known past the committed run, releasing that many waiting
+// waves; the others poll list_known in HBM.  Idle waves thus put one read at
+// a time on PCIe instead of one per wave.
+#include "gfd/descriptor_queue.h"
+#include "gfd/sg_device_primitives.h"
+#include "gfd/sg_task_queue.h"
+#include "gfd/wave_ops.h"
+
+namespace gfd {
+namespace sg_warp_spec {
+
+// Read-only view of a list whose data is in HBM.
+struct SGListView {
+    uint32_t list_id;
+    uint32_t count;
+    uint32_t flags;
+    int lane_id;
+    uint32_t pool_offset;
+    const SGTaskQueue* sq;
+
+    __device__ __forceinline__ DeviceSGEntry get_entry(uint32_t idx) const {
+        return sq->entries[(pool_offset + idx) % MAX_SG_POOL_ENTRIES];
+    }
+    template <typename T>
+    __device__ __forceinline__ T* dst_ptr(uint32_t idx) const {
+        return reinterpret_cast<T*>(get_entry(idx).dst_addr);
+    }
+    __device__ __forceinline__ uint32_t entry_size(uint32_t idx) const { return get_entry(idx).size; }
+};
+
+struct _SGSlot {
+    uint32_t list_id, count, pool_offset, flags;
+    int seq;   // k + 1 once the k-th list of this slot is ready
+    int free;  // 1 while the slot may be (re)filled
+};
+
+__device__ __forceinline__ uint64_t _idle_limit_ticks(const SGTaskQueue* sq) {
+    const uint32_t ms = wave::load_system32(&sq->idle_limit_ms);
+    return (uint64_t)(ms ? ms : 30000u) * 100000ull;  // 100 MHz wall clock
+}
+
+// Wait until ring index idx is committed.  False once terminate (or the idle
+// limit) ends the wait with nothing committed.
+__device__ __forceinline__ bool _wait_committed(SGTaskQueue* sq, SGDeviceCounters* cnt, uint64_t idx,
+                                                uint64_t idle_ticks) {
+    const int lane = wave::lane_id();
+    const SGList& mine = sq->lists[idx % MAX_SG_LISTS];
+    const uint64_t t0 = wall_clock64();
+    uint32_t grace = 0;
+    for (;;) {
+        const uint64_t known = sg::load_dev(&cnt->list_known);
+        if (idx <= known) {
+            if (wave::load_system(&mine.sequence) == idx + 1) {
+                if (idx == known) {
+                    // Leader: find the committed run idx, idx+1, ... and publish it.
+                    const uint64_t j = idx + (uint64_t)lane;
+                    const bool c = wave::load_system(&sq->lists[j % MAX_SG_LISTS].sequence) == j + 1;
+                    const uint64_t mask = __ballot(c);
+                    const uint64_t run = (~mask == 0) ? 64 : (uint64_t)__builtin_ctzll(~mask);
+                    if (lane == 0)
+                        __hip_atomic_fetch_max(&cnt->list_known, idx + (run ? run : 1), __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                }
+                return true;
+            }
+            if (wave::load_system32(&sq->terminate) && ++grace > 64) {
+                if (lane == 0) __hip_atomic_store(&cnt->stop, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return false;
+            }
+            __builtin_amdgcn_s_sleep(4);
+        } else {
+            if (sg::load_dev(&cnt->stop)) return false;
+            __builtin_amdgcn_s_sleep(16);
+        }
+        if (wall_clock64() - t0 > idle_ticks) return false;
+    }
+}
+
+template <typename ComputeFn>
+__device__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTaskQueue* sq, ComputeFn compute_fn) {
+    (void)dq;
+    __shared__ _SGSlot slots[2];
+    __shared__ int terminated;
+    const int w = wave::wave_id();
+    const int lane = wave::lane_id();
+    if (threadIdx.x < 2) {
+        slots[threadIdx.x].seq = 0;
+        slots[threadIdx.x].free = 1;
+    }
+    if (threadIdx.x == 0) terminated = 0;
+    __syncthreads();
+
+    SGDeviceCounters* cnt = sg_device_counters(sq);
+    const bool has_compute = blockDim.x > (unsigned)wave::kWidth;
+
+    if (w == 0) {
+        // ---------------- transfer wave
+        const uint64_t idle_ticks = _idle_limit_ticks(sq);
+        for (uint64_t iter = 0;; iter++) {
+            const int s = (int)(iter & 1);
+            if (has_compute && !wave::wait_lds_eq(&slots[s].free, 1)) {
+                if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_SLOT_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            uint64_t idx = 0;
+            if (lane == 0) idx = sg::atomic_add_dev(&cnt->list_claim, 1);
+            idx = wave::broadcast0(idx);
+            if (!_wait_committed(sq, cnt, idx, idle_ticks)) break;
+            SGList& l = sq->lists[idx % MAX_SG_LISTS];
+            const uint32_t pool_offset = l.pool_offset, count = l.count, list_id = l.list_id, flags = l.flags;
+            if (lane == 0) wave::store_system(&l.sequence, 0);  // claimed
+
+            // Copy the list: lane i holds entry b+i's descriptor, the wave walks them.
+            uint64_t bytes = 0;
+            for (uint32_t b = 0; b < count; b += wave::kWidth) {
+                uint64_t md = 0, ms = 0, mn = 0;
+                if (b + lane < count) {
+                    const DeviceSGEntry e = sq->entries[(pool_offset + b + lane) % MAX_SG_POOL_ENTRIES];
+                    md = e.dst_addr;
+                    ms = e.src_addr;
+                    mn = e.size;
+                }
+                const uint32_t nb = count - b < (uint32_t)wave::kWidth ? count - b : (uint32_t)wave::kWidth;
+                for (uint32_t j = 0; j < nb; j++) {
+                    const uint64_t n = wave::readlane64(mn, (int)j);
+                    wave::copy<4>(wave::readlane64(md, (int)j), wave::readlane64(ms, (int)j), n);
+                    bytes += n;
+                }
+            }
+            wave::release_agent();  // the list's bytes are visible device-wide
+            if (lane == 0) {
+                if (list_id < (uint32_t)MAX_SG_LISTS)
+                    __hip_atomic_store(&sq->d_list_done[list_id], 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                sg::atomic_add_dev(&cnt->entries_done, count);
+                sg::atomic_add_dev(&cnt->bytes_done, bytes);
+                __hip_atomic_fetch_add(&cnt->lists_done, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                wave::store_system(&l.done, idx + 1);
+                if (has_compute) {
+                    slots[s].list_id = list_id;
+                    slots[s].count = count;
+                    slots[s].pool_offset = pool_offset;
+                    slots[s].flags = flags;
+                    slots[s].free = 0;
+                    wave::lds_store(&slots[s].seq, (int)(iter / 2) + 1);
+                }
+            }
+        }
+        if (lane == 0) wave::lds_store(&terminated, 1);
+    } else if (w == 1) {
+        // ---------------- compute wave: bounded by the transfer wave's idle
+        // limit (plus 1 s), the longest the transfer wave can stay silent.
+        const uint64_t limit = _idle_limit_ticks(sq) + 100000000ull;
+        for (uint64_t k = 0;; k++) {
+            const int s = (int)(k & 1);
+            const int want = (int)(k / 2) + 1;
+            bool ready = false;
+            const uint64_t t0 = wall_clock64();
+            for (;;) {
+                if (wave::lds_load(&slots[s].seq) == want) {
+                    ready = true;
+                    break;
+                }
+                if (wave::lds_load(&terminated)) {
+                    ready = wave::lds_load(&slots[s].seq) == want;
+                    break;
+                }
+                if (wall_clock64() - t0 > limit) {
+                    if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_COMPUTE_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            if (!ready) break;
+            wave::acquire_agent();
+            SGListView view;
+            view.list_id = slots[s].list_id;
+            view.count = slots[s].count;
+            view.flags = slots[s].flags;
+            view.lane_id = lane;
+            view.pool_offset = slots[s].pool_offset;
+            view.sq = sq;
+            compute_fn(view);
+            if (lane == 0) wave::lds_store(&slots[s].free, 1);
+        }
+    }
+    // further waves return to the caller
+}
+
+}  // namespace sg_warp_spec
+}  // namespace gfd
+
+// Kernel generation macro (block = 64 * (1 + compute waves) threads).
+#define GFD_SG_WARP_SPEC_KERNEL(kernel_name, ComputeFnType)                             \
+    __global__ void kernel_name(gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq,        \
+                                ComputeFnType compute_fn) {                             \
+        gfd::sg_warp_spec::_sg_transfer_warp_loop(dq, sq, compute_fn);                  \
+    }

@@ -27,4 +27,16 @@ struct TiledQueue {
     uint64_t* d_tile_chunk_done;                   // device-memory progress (preferred)
 };
 
+// Tile dispatch counter kept in HBM right after d_tile_chunk_done[MAX_TILES]
+// (sessions allocate MAX_TILES + TILE_DEVICE_COUNTER_WORDS words), so tile
+// claims are device-scope atomics instead of atomics into host memory.
+struct TileDeviceCounters {
+    uint64_t next_tile;
+    uint64_t tiles_done;
+    uint64_t error;  // nonzero: a bounded wait gave up
+    uint64_t _pad[5];
+};
+constexpr int TILE_DEVICE_COUNTER_WORDS = (int)(sizeof(TileDeviceCounters) / sizeof(uint64_t));
+static_assert(sizeof(TileDeviceCounters) == 64, "TileDeviceCounters is one cache line");
+
 }  // namespace gfd

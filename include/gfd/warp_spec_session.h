@@ -1,0 +1,230 @@
+#pragma once
+// Session managers for the wave-specialised frameworks (the reference's
+// include/gfd/warp_spec_session.h:14-258 and src/*_session.cpp: the same class
+// names, configuration fields and lifecycle: construct, launch(kernel, fn),
+// synchronize(), reset(), get_stats()).
+//
+// MI355X design: the kernels move the data themselves (zero-copy loads from
+// pinned host memory, see include/gfd/warp_spec.h and sg_warp_spec.h), so a
+// session owns queues and HBM counters but no CPU poller; get_poller()
+// returns nullptr.  launch() is a template defined for HIP translation units.
+#include <chrono>
+#include <cstdint>
+#include <deque>
+#include <functional>
+
+#include "gfd/cpu_polling.h"
+#include "gfd/hip_shim.h"
+#include "gfd/sg_task_queue.h"
+#include "gfd/tiled_queue.h"
+
+namespace gfd {
+
+struct WarpSpecConfig {
+    // required
+    uint32_t total_tokens = 0;
+    uint32_t token_size = 0;
+    void* cpu_src = nullptr;   // pinned host memory
+    void* gpu_dst = nullptr;   // HBM
+
+    // optional
+    uint32_t tokens_per_tile = 128;
+    uint32_t tokens_per_chunk = 0;  // 0 = automatic
+    int num_blocks = 0;             // 0 = one workgroup per CU
+    int numa_node = 0;              // kept for API compatibility
+    bool use_copy_engine = true;    // kept for API compatibility (data moves zero-copy)
+    bool double_buffer = false;
+    bool per_tile_mode = false;     // one chunk per tile
+
+    // Chunk size: about 64 KiB (tokens <= 512 B), 128 KiB, or 256 KiB (tokens
+    // >= 64 KiB) per chunk, a power of two, at least 4 tokens, and at most 8
+    // chunks per tile (4 with double buffering, so a workgroup stays within
+    // 1024 threads with 64-lane waves) — the reference's heuristic with the
+    // wave64 limit (include/gfd/warp_spec_session.h:33-52).
+    uint32_t effective_tokens_per_chunk() const {
+        if (per_tile_mode) return tokens_per_tile;
+        if (tokens_per_chunk > 0) return tokens_per_chunk;
+        uint64_t target = 128 * 1024;
+        if (token_size <= 512) target = 64 * 1024;
+        else if (token_size >= 65536) target = 256 * 1024;
+        uint32_t c = token_size ? (uint32_t)(target / token_size) : 1;
+        if (c < 4) c = 4;
+        if (c > tokens_per_tile) c = tokens_per_tile;
+        const uint32_t max_k = double_buffer ? 4 : 8;
+        const uint32_t min_c = tokens_per_tile / max_k;
+        if (min_c > 0 && c < min_c) c = min_c;
+        uint32_t p = 1;
+        while (p * 2 <= c) p *= 2;
+        return p;
+    }
+    uint32_t total_tiles() const { return tokens_per_tile ? total_tokens / tokens_per_tile : 0; }
+    uint32_t chunks_per_tile() const { return tokens_per_tile / effective_tokens_per_chunk(); }
+    // 1 transfer wave + K (or 2K) compute waves of 64 lanes.
+    int block_size() const {
+        const int k = (int)chunks_per_tile();
+        return (double_buffer ? 1 + 2 * k : 1 + k) * 64;
+    }
+};
+
+class WarpSpecSession {
+public:
+    explicit WarpSpecSession(const WarpSpecConfig& config);
+    ~WarpSpecSession();
+    WarpSpecSession(const WarpSpecSession&) = delete;
+    WarpSpecSession& operator=(const WarpSpecSession&) = delete;
+
+    // Launch a GFD_WARP_SPEC_KERNEL(_DB) kernel: (TiledQueue*, gpu_dst, cpu_src, fn).
+    template <typename KernelFn, typename ComputeFn>
+    void launch(KernelFn kernel, ComputeFn compute_fn, gfd_stream_t stream = nullptr);
+
+    struct LaunchParams {
+        TiledQueue* tq;
+        void* gpu_buffer;
+        const void* cpu_base;
+        unsigned grid;
+        unsigned block;
+    };
+    LaunchParams get_launch_params() const;
+
+    // Wait for the launch to finish.  False if the kernel reported a stalled
+    // hand-off or the stream returned an error.
+    bool synchronize();
+    // Clear tile progress and the tile counter for another launch.
+    void reset();
+
+    struct Stats {
+        uint64_t descriptors_processed;  // tokens landed
+        uint64_t bytes_transferred;
+        double elapsed_ms;
+        double bandwidth_gbps;
+    };
+    Stats get_stats() const;
+
+    TiledQueue* get_queue() const { return tq_; }
+    CpuPollingThread* get_poller() const { return nullptr; }
+    bool ok() const { return ok_; }
+    uint64_t error_bits() const { return error_bits_; }
+    uint64_t tiles_done() const { return tiles_done_; }
+
+    // Internal: called by launch().
+    void before_launch(gfd_stream_t stream);
+
+private:
+    WarpSpecConfig config_;
+    TiledQueue* tq_ = nullptr;
+    uint64_t* d_signals_ = nullptr;  // MAX_TILES progress words + TileDeviceCounters
+    int num_blocks_ = 0;
+    bool ok_ = false;
+    bool running_ = false;  // launched, not yet synchronized
+    gfd_stream_t stream_ = nullptr;
+    uint64_t error_bits_ = 0;
+    uint64_t tiles_done_ = 0;
+    std::chrono::steady_clock::time_point launch_time_;
+    double last_elapsed_ms_ = 0;
+};
+
+struct SGWarpSpecConfig {
+    int num_compute_warps = 0;  // compute waves per workgroup (0 -> 1, as in the reference)
+    int num_blocks = 0;         // 0 = one workgroup per CU
+    int numa_node = 0;          // kept for API compatibility
+    bool use_copy_engine = true;
+    int max_lists = MAX_SG_LISTS;
+    int max_entries = MAX_SG_POOL_ENTRIES;
+    uint32_t idle_limit_ms = 0;  // transfer waves give up after this long without a list (0 = 30 s)
+
+    int block_size() const { return (1 + (num_compute_warps > 0 ? num_compute_warps : 1)) * 64; }
+};
+
+class SGWarpSpecSession {
+public:
+    explicit SGWarpSpecSession(const SGWarpSpecConfig& config);
+    ~SGWarpSpecSession();
+    SGWarpSpecSession(const SGWarpSpecSession&) = delete;
+    SGWarpSpecSession& operator=(const SGWarpSpecSession&) = delete;
+
+    // Host submission: entries into the pool, header, release fence, commit.
+    // Blocks while the ring or the pool is full of lists not yet landed.
+    // Returns the list's ring index, or ~0 on a timeout / invalid argument.
+    uint64_t submit_sg_list(const DeviceSGEntry* entries, uint32_t count, uint32_t list_id,
+                            uint32_t flags = SG_FLAG_HOST_SUBMITTED);
+
+    SGTaskQueue* get_sg_queue() const { return sq_; }
+    DescriptorQueue* get_desc_queue() const { return dq_; }
+    CpuPollingThread* get_poller() const { return nullptr; }
+
+    // Launch a GFD_SG_WARP_SPEC_KERNEL kernel: (DescriptorQueue*, SGTaskQueue*, fn).
+    template <typename KernelFn, typename ComputeFn>
+    void launch(KernelFn kernel, ComputeFn compute_fn, gfd_stream_t stream = nullptr);
+
+    // Wait until every host-submitted list (plus `extra_gpu_lists` lists
+    // submitted by GPU waves during the launch) has landed, then terminate the
+    // transfer waves and wait for the kernel.  False on timeout or error.
+    bool synchronize(uint64_t extra_gpu_lists = 0);
+    void reset();
+
+    struct Stats {
+        uint64_t descriptors_processed;  // entries landed
+        uint64_t bytes_transferred;
+        double elapsed_ms;
+        double bandwidth_gbps;
+    };
+    Stats get_stats() const;
+
+    bool ok() const { return ok_; }
+    uint64_t error_bits() const { return error_bits_; }
+    uint64_t lists_landed() const { return lists_done_; }  // during the last launch
+    int num_blocks() const { return num_blocks_; }
+
+    // Internal: called by launch().
+    void before_launch(gfd_stream_t stream);
+
+private:
+    struct Pending {
+        uint64_t idx;
+        uint64_t pool_begin;
+        uint32_t count;
+    };
+    bool list_done(uint64_t idx) const;
+    void retire_done();
+    bool wait_until(const std::function<bool()>& cond, double limit_ms);
+    double wait_limit_ms() const;
+
+    SGWarpSpecConfig config_;
+    SGTaskQueue* sq_ = nullptr;
+    DescriptorQueue* dq_ = nullptr;
+    int num_blocks_ = 0;
+    bool ok_ = false;
+    bool running_ = false;
+    gfd_stream_t stream_ = nullptr;
+    uint64_t consumed_lists_ = 0;    // ring index where the next launch's claims start
+    uint64_t consumed_entries_ = 0;  // pool index every consumed list lies below
+    std::deque<Pending> pending_;    // host-submitted lists not yet seen landed, in order
+    uint64_t error_bits_ = 0;
+    uint64_t entries_done_ = 0, bytes_done_ = 0, lists_done_ = 0;  // last launch
+    std::chrono::steady_clock::time_point launch_time_;
+    double last_elapsed_ms_ = 0;
+};
+
+// The reference's spelling in the north-star text.
+using SgWarpSpecSession = SGWarpSpecSession;
+
+}  // namespace gfd
+
+#ifdef __HIPCC__
+#include <hip/hip_runtime.h>
+
+template <typename KernelFn, typename ComputeFn>
+void gfd::WarpSpecSession::launch(KernelFn kernel, ComputeFn compute_fn, gfd_stream_t stream) {
+    before_launch(stream);
+    const LaunchParams p = get_launch_params();
+    hipLaunchKernelGGL(kernel, dim3(p.grid), dim3(p.block), 0, (hipStream_t)stream, p.tq, p.gpu_buffer, p.cpu_base,
+                       compute_fn);
+}
+
+template <typename KernelFn, typename ComputeFn>
+void gfd::SGWarpSpecSession::launch(KernelFn kernel, ComputeFn compute_fn, gfd_stream_t stream) {
+    before_launch(stream);
+    hipLaunchKernelGGL(kernel, dim3(num_blocks_), dim3(config_.block_size()), 0, (hipStream_t)stream, dq_, sq_,
+                       compute_fn);
+}
+#endif

@@ -194,6 +194,76 @@ int gfd_bench_queue(void* queue, const void* tokens, void* gpu_dst, int num_toke
                     uint32_t token_size, uint64_t* base_slot, int warmup, int iters,
                     uint64_t timeout_us, double* times_us);
 
+/* ---- wave-specialised sessions (reference include/gfd/warp_spec_session.h,
+ * src/warp_spec_session.cpp, src/sg_warp_spec_session.cpp).  The C++ classes
+ * gfd::WarpSpecSession / gfd::SGWarpSpecSession are the primary API (kernels
+ * are instantiated from user functors); these entry points drive them with
+ * built-in consumers for FFI callers and tests. ---- */
+
+/* Same 24-byte layout as gfd::DeviceSGEntry (reference include/gfd/sg_task_queue.h:37-43). */
+typedef struct gfd_device_sg_entry {
+    uint64_t src;
+    uint64_t dst;
+    uint32_t size;
+    uint32_t tag;
+} gfd_device_sg_entry;
+
+/* get_stats() of a session (reference include/gfd/warp_spec_session.h:118-124)
+ * plus what the kernels report. */
+typedef struct gfd_session_result {
+    uint64_t units_done;  /* tokens (WarpSpec) or entries (SG) landed: descriptors_processed */
+    uint64_t bytes;       /* bytes_transferred */
+    uint64_t lists_done;  /* tiles (WarpSpec) or lists (SG) landed */
+    uint64_t error_bits;  /* nonzero: a bounded wait inside the kernel gave up */
+    double elapsed_ms;    /* launch -> synchronize, host clock */
+    int grid, block, tokens_per_chunk, chunks_per_tile;
+} gfd_session_result;
+
+/* WarpSpecSession over tokens [0, total_tokens) of cpu_src (pinned) -> gpu_dst
+ * (HBM): construct, then `iters` times reset + launch + synchronize.
+ * token_sums != NULL: the consumer writes each token's float sum to
+ * token_sums[t] (test/test_db_small_tiles.cu:18-31); NULL: no-op consumer.
+ * kernel_ms[iters] (optional) gets HIP-event times of each launch.
+ * Tokens past the last whole tile are not moved (as the reference). */
+int gfd_warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t total_tokens, uint32_t token_size,
+                      uint32_t tokens_per_tile, uint32_t tokens_per_chunk, int double_buffer,
+                      int per_tile_mode, int num_blocks, float* token_sums, int iters,
+                      double* kernel_ms, gfd_session_result* res);
+
+typedef void* gfd_sg_session_t;
+/* SGWarpSpecSession(SGWarpSpecConfig{num_compute_warps, num_blocks}); idle_limit_ms
+ * bounds how long transfer waves wait without a list (0 = 30 s). */
+int gfd_sg_session_create(int num_compute_warps, int num_blocks, uint32_t idle_limit_ms,
+                          gfd_sg_session_t* out);
+void gfd_sg_session_destroy(gfd_sg_session_t s);
+/* submit_sg_list (warp_spec_session.h:170-171): returns the ring index, or -1. */
+int64_t gfd_sg_session_submit(gfd_sg_session_t s, const gfd_device_sg_entry* entries, uint32_t count,
+                              uint32_t list_id, uint32_t flags);
+/* launch with the checksum consumer: list_sums[list_id] (device u64[512],
+ * zeroed by the caller) += sum of the list's landed bytes as LE u32 words
+ * (a trailing partial word adds its bytes); list_sums == NULL: no-op consumer
+ * (test/test_sg_e2e.cu:10-17). */
+int gfd_sg_session_launch(gfd_sg_session_t s, unsigned long long* list_sums, void* stream);
+/* Kernel with a submitter wave per workgroup (test/test_sg_gpu_submit.cu:20-213):
+ * list i = entries [i*entries_per_list, (i+1)*entries_per_list) of d_entries
+ * (device array), list_id i; the submitters set terminate once all landed. */
+int gfd_sg_session_launch_gpu_submit(gfd_sg_session_t s, const gfd_device_sg_entry* d_entries,
+                                     uint32_t entries_per_list, uint32_t num_lists,
+                                     unsigned long long* list_sums, void* stream);
+/* synchronize (sg_warp_spec_session.cpp:118-139): waits for every host-submitted
+ * list and `extra_gpu_lists` GPU-submitted lists to land, sets terminate,
+ * waits for the kernel.  Nonzero if lists did not land or the kernel
+ * reported an error. */
+int gfd_sg_session_synchronize(gfd_sg_session_t s, uint64_t extra_gpu_lists);
+int gfd_sg_session_reset(gfd_sg_session_t s);
+int gfd_sg_session_stats(gfd_sg_session_t s, gfd_session_result* out);
+void* gfd_sg_session_queue(gfd_sg_session_t s); /* get_sg_queue(): the SGTaskQueue */
+/* Host-submitted SG transfer (`count` entries in lists of entries_per_list,
+ * at most 16384 entries / 512 lists), no-op consumer: wall time from launch
+ * until every list's done marker is up, times_us[iters]. */
+int gfd_bench_sg_session(gfd_sg_session_t s, const gfd_device_sg_entry* entries, uint32_t count,
+                         uint32_t entries_per_list, int warmup, int iters, double* times_us);
+
 #ifdef __cplusplus
 }
 #endif

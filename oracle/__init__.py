@@ -18,6 +18,10 @@ Pins (tests/test_oracle.py):
   * moe_routing — brute-force top-2 on tiny inputs, tie rule checked on a
     planted tie, list sizes summing to 2*tokens, stability (token order).
   * rmsnorm — closed forms (constant rows, unit weights) and scale invariance.
+  * warp_spec_chunking — the chunk sizes the reference's heuristic gives for
+    its documented targets, plus the invariants (power of two, K <= 8, tile
+    divisible); warp_spec_expected — brute-force copy on tiny inputs;
+    u32_word_checksum — closed forms and a pure-Python loop.
 """
 import ctypes
 import os
@@ -229,3 +233,62 @@ def rmsnorm_rows(x_f32, weight_f32, eps):
     x = np.asarray(x_f32, dtype=np.float32)
     ms = np.mean(x.astype(np.float64) ** 2, axis=-1, keepdims=True)
     return (x / np.sqrt(ms + eps) * np.asarray(weight_f32, dtype=np.float32)).astype(np.float32)
+
+
+# ------------------------------------------------------------ sessions
+
+def warp_spec_chunking(token_size, tokens_per_tile=128, tokens_per_chunk=0, double_buffer=False,
+                       per_tile_mode=False):
+    """(tokens_per_chunk, chunks_per_tile, block threads) of a WarpSpecSession.
+
+    Restates the reference's WarpSpecConfig::effective_tokens_per_chunk
+    (include/gfd/warp_spec_session.h:33-52): ~64 KiB chunks for tokens
+    <= 512 B, ~256 KiB for tokens >= 64 KiB, else ~128 KiB; at least 4 tokens,
+    at most a tile, at most 8 chunks per tile, rounded down to a power of two.
+    With 64-lane waves a double-buffered workgroup (1 + 2K waves) stays within
+    1024 threads only for K <= 7, so the double-buffer limit is 4 chunks.
+    Blocks are 64 * (1 + K) or 64 * (1 + 2K) threads (warp_spec_session.h:59-62
+    with 64-lane waves).
+    """
+    if per_tile_mode:
+        c = tokens_per_tile
+    elif tokens_per_chunk > 0:
+        c = tokens_per_chunk
+    else:
+        target = 128 * 1024
+        if token_size <= 512:
+            target = 64 * 1024
+        elif token_size >= 65536:
+            target = 256 * 1024
+        c = max(4, target // token_size)
+        c = min(c, tokens_per_tile)
+        min_c = tokens_per_tile // (4 if double_buffer else 8)
+        if min_c > 0 and c < min_c:
+            c = min_c
+        p = 1
+        while p * 2 <= c:
+            p *= 2
+        c = p
+    k = tokens_per_tile // c
+    return c, k, 64 * (1 + (2 * k if double_buffer else k))
+
+
+def warp_spec_expected(src, dst_before, total_tokens, token_size, tokens_per_tile):
+    """Destination after a WarpSpecSession launch: tokens of whole tiles are
+    copied from the same offset of src; tokens past the last whole tile are
+    untouched (total_tiles = total_tokens / tokens_per_tile,
+    include/gfd/warp_spec_session.h:56)."""
+    out = np.array(dst_before, dtype=np.uint8, copy=True)
+    n = (total_tokens // tokens_per_tile) * tokens_per_tile * token_size
+    out[:n] = np.asarray(src, dtype=np.uint8)[:n]
+    return out
+
+
+def u32_word_checksum(buf):
+    """Sum (mod 2^64) of buf read as little-endian u32 words, plus the bytes
+    of a trailing partial word.  Order-free, so it pins what a consumer wave
+    saw of a landed list whatever order its lanes added in."""
+    b = np.ascontiguousarray(buf, dtype=np.uint8)
+    nw = b.size // 4
+    words = b[:nw * 4].view("<u4").astype(np.uint64)
+    return (int(words.sum(dtype=np.uint64)) + int(b[nw * 4:].astype(np.uint64).sum())) & MASK64

@@ -1,0 +1,299 @@
+"""GPU parity of the wave-specialised sessions (WarpSpecSession,
+SGWarpSpecSession) against the oracle: landed bytes are compared byte-exact,
+the consumers' results (per-token float sums, per-list u32-word checksums)
+exactly.  Cases follow the reference's own tests: test/test_db_small_tiles.cu
+(double-buffered tiles, sum = (t+1)*dim), test/test_sg_e2e.cu (one host list
+of 4 x 4 KiB floats i+1), test/test_sg_gpu_submit.cu (lists submitted by a
+GPU wave)."""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+import gfd_amd
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = 0xCD
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert gfd_amd.device_count() > 0, "no GPU visible to libgfd_amd.so"
+    assert gfd_amd.lib().gfd_set_device(0) == 0
+
+
+def random_host(nbytes, seed):
+    h = gfd_amd.HostBuffer(nbytes)
+    h.array[:] = np.random.default_rng(seed).integers(0, 256, nbytes, dtype=np.uint8)
+    return h
+
+
+# ------------------------------------------------------------ WarpSpecSession
+
+DB_CASES = [(tc * 32, 32, 16) for tc in (1, 2, 3, 4, 5, 7)] + \
+           [(tc * 16, 16, 16) for tc in (1, 2, 3, 5)] + \
+           [(tc * 64, 64, 16) for tc in (1, 2, 3)]
+
+
+@pytest.mark.parametrize("total,tile,chunk", DB_CASES)
+def test_warp_spec_db_small_tiles(total, tile, chunk):
+    """test/test_db_small_tiles.cu: token t = 256 floats of value t+1,
+    double-buffered, grid = min(CUs, tiles); each token's sum is (t+1)*256."""
+    log("warp_spec db total=%d tile=%d chunk=%d" % (total, tile, chunk))
+    dim = 256
+    host = gfd_amd.HostBuffer(total * dim * 4)
+    vals = host.array.view(np.float32).reshape(total, dim)
+    vals[:] = (np.arange(total, dtype=np.float32) + 1)[:, None]
+    dst = gfd_amd.DeviceBuffer(total * dim * 4)
+    dst.fill(0)
+    sums = gfd_amd.DeviceBuffer(total * 4)
+    sums.fill(0)
+    res, _ = gfd_amd.warp_spec_run(host.ptr, dst.ptr, total, dim * 4, tile, chunk, double_buffer=True,
+                                   num_blocks=total // tile, token_sums=sums.ptr)
+    got = sums.download().view(np.float32)
+    want = (np.arange(total, dtype=np.float32) + 1) * dim
+    assert (got == want).all(), "first bad token %d" % int(np.argmax(got != want))
+    assert (dst.download() == host.array).all()
+    c, k, block = oracle.warp_spec_chunking(dim * 4, tile, chunk, True)
+    assert (res["tokens_per_chunk"], res["chunks_per_tile"], res["block"]) == (c, k, block)
+    assert res["units_done"] == total and res["lists_done"] == total // tile and res["error_bits"] == 0
+
+
+WS_CASES = [
+    # total tokens, token bytes, tile, chunk (0 = auto), double buffer, per-tile mode, blocks (0 = per CU)
+    (8192, 4096, 128, 0, False, False, 0),
+    (8192, 4096, 128, 0, True, False, 0),
+    (1000, 4096, 128, 0, False, False, 0),      # 104 tokens past the last whole tile stay untouched
+    (2048, 16384, 128, 0, False, False, 64),
+    (512, 65536, 128, 0, True, False, 0),
+    (4096, 512, 128, 0, False, False, 0),
+    (4096, 1000, 64, 0, False, False, 3),       # token size not a multiple of 16
+    (1024, 4096, 128, 0, False, True, 0),       # per-tile mode, K = 1
+    (300, 48, 32, 8, True, False, 1),
+]
+
+
+@pytest.mark.parametrize("total,ts,tile,chunk,db,per_tile,blocks", WS_CASES)
+def test_warp_spec_parity(total, ts, tile, chunk, db, per_tile, blocks):
+    log("warp_spec total=%d ts=%d tile=%d chunk=%d db=%d per_tile=%d blocks=%d" %
+        (total, ts, tile, chunk, db, per_tile, blocks))
+    host = random_host(total * ts, seed=total * 31 + ts)
+    dst = gfd_amd.DeviceBuffer(total * ts + 4096)
+    dst.fill(SENTINEL)
+    before = dst.download()
+    res, times = gfd_amd.warp_spec_run(host.ptr, dst.ptr, total, ts, tile, chunk, db, per_tile, blocks, iters=2)
+    got = dst.download()
+    want = np.concatenate([oracle.warp_spec_expected(host.array, before[:total * ts], total, ts, tile),
+                           before[total * ts:]])
+    n_bad = int(np.count_nonzero(got != want))
+    assert n_bad == 0, "%d mismatched bytes" % n_bad
+    tiles = total // tile
+    assert res["lists_done"] == tiles and res["units_done"] == tiles * tile and res["error_bits"] == 0
+    c, k, block = oracle.warp_spec_chunking(ts, tile, chunk, db, per_tile)
+    assert (res["tokens_per_chunk"], res["chunks_per_tile"], res["block"]) == (c, k, block)
+    assert (times > 0).all()
+
+
+def test_warp_spec_rejects_oversized_block():
+    host = gfd_amd.HostBuffer(4096 * 64)
+    dst = gfd_amd.DeviceBuffer(4096 * 64)
+    # 16 chunks per tile double-buffered would need 64 * 33 threads
+    with pytest.raises(gfd_amd.GfdError):
+        gfd_amd.warp_spec_run(host.ptr, dst.ptr, 64, 4096, 64, 4, double_buffer=True)
+
+
+# --------------------------------------------------------- SGWarpSpecSession
+
+def entries_array(src, dst, size, tag=0):
+    return gfd_amd.device_sg_entries(src, dst, size, tag)
+
+
+def list_checksums(host_bytes, host_base, entries, list_ranges):
+    """Expected ListChecksum per list: u32-word checksum of each entry's source bytes."""
+    out = {}
+    for lid, (a, b) in list_ranges.items():
+        s = 0
+        for e in entries[a:b]:
+            off = int(e["src"]) - host_base
+            s += oracle.u32_word_checksum(host_bytes[off:off + int(e["size"])])
+        out[lid] = s & oracle.MASK64
+    return out
+
+
+def test_sg_e2e_single_list():
+    """test/test_sg_e2e.cu: 4 entries of 4 KiB, floats i+1, one list, one workgroup."""
+    log("sg e2e")
+    n, t = 4, 4096
+    host = gfd_amd.HostBuffer(n * t)
+    host.array.view(np.float32)[:] = np.arange(n * t // 4, dtype=np.float32) + 1
+    dst = gfd_amd.DeviceBuffer(n * t)
+    dst.fill(0)
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=1, idle_limit_ms=5000)
+    ent = entries_array(host.ptr + np.arange(n, dtype=np.uint64) * t, dst.ptr + np.arange(n, dtype=np.uint64) * t, t)
+    assert s.submit_sg_list(ent, list_id=0) == 0
+    s.launch()
+    s.synchronize()
+    assert (dst.download().view(np.float32) == host.array.view(np.float32)).all()
+    st = s.stats()
+    assert st["units_done"] == n and st["bytes"] == n * t and st["lists_done"] == 1 and st["error_bits"] == 0
+    s.close()
+
+
+def ragged_lists(rng, host, dst, n_lists, max_entries, max_size):
+    """Random lists of random-size entries at random source offsets, disjoint destinations."""
+    ents, ranges, off = [], {}, 0
+    for lid in range(n_lists):
+        k = int(rng.integers(1, max_entries + 1))
+        sizes = rng.integers(1, max_size + 1, k)
+        srcs = rng.integers(0, host.nbytes - max_size, k)
+        a = len(ents)
+        for sz, so in zip(sizes, srcs):
+            gap = int(rng.integers(0, 33))
+            ents.append((host.ptr + int(so), dst.ptr + off + gap, int(sz)))
+            off += gap + int(sz)
+        ranges[lid] = (a, len(ents))
+    assert off <= dst.nbytes
+    arr = entries_array([e[0] for e in ents], [e[1] for e in ents], [e[2] for e in ents])
+    return arr, ranges
+
+
+def expected_dst(host, dst_before, dst_ptr, arr):
+    out = dst_before.copy()
+    for e in arr:
+        so, do, n = int(e["src"]) - host.ptr, int(e["dst"]) - dst_ptr, int(e["size"])
+        out[do:do + n] = host.array[so:so + n]
+    return out
+
+
+@pytest.mark.parametrize("blocks,compute", [(1, 1), (8, 1), (0, 1), (0, 3)])
+def test_sg_ragged_lists_checksum(blocks, compute):
+    log("sg ragged blocks=%d compute=%d" % (blocks, compute))
+    rng = np.random.default_rng(100 + blocks * 7 + compute)
+    host = random_host(4 << 20, seed=blocks + 11)
+    dst = gfd_amd.DeviceBuffer(48 << 20)
+    dst.fill(SENTINEL)
+    before = dst.download()
+    arr, ranges = ragged_lists(rng, host, dst, n_lists=120, max_entries=90, max_size=9000)
+    sums = gfd_amd.DeviceBuffer(gfd_amd.MAX_SG_LISTS * 8)
+    sums.fill(0)
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=compute, num_blocks=blocks, idle_limit_ms=5000)
+    for lid, (a, b) in ranges.items():
+        s.submit_sg_list(arr[a:b], list_id=lid)
+    s.launch(list_sums=sums.ptr)
+    s.synchronize()
+    assert (dst.download() == expected_dst(host, before, dst.ptr, arr)).all()
+    got = sums.download().view(np.uint64)
+    want = list_checksums(host.array, host.ptr, arr, ranges)
+    for lid, v in want.items():
+        assert int(got[lid]) == v, "list %d checksum" % lid
+    st = s.stats()
+    assert st["units_done"] == len(arr) and st["bytes"] == int(arr["size"].sum()) and st["error_bits"] == 0
+    assert st["lists_done"] == len(ranges)
+    s.close()
+
+
+def test_sg_streaming_ring_and_pool_wrap():
+    """Lists submitted while the kernel runs: 700 lists (ring of 512) with
+    40 entries each (pool of 16384), so both wrap under backpressure."""
+    log("sg streaming wrap")
+    rng = np.random.default_rng(7)
+    t = 1024
+    n_lists, epl = 700, 40
+    n = n_lists * epl
+    host = random_host(n * t, seed=3)
+    perm = rng.permutation(n)
+    dst = gfd_amd.DeviceBuffer(n * t)
+    dst.fill(0)
+    arr = entries_array(host.ptr + perm.astype(np.uint64) * t, dst.ptr + np.arange(n, dtype=np.uint64) * t, t)
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=0, idle_limit_ms=5000)
+    s.launch()
+    for l in range(n_lists):
+        s.submit_sg_list(arr[l * epl:(l + 1) * epl], list_id=l % gfd_amd.MAX_SG_LISTS)
+    s.synchronize()
+    want = host.array.reshape(n, t)[perm].reshape(-1)
+    assert (dst.download() == want).all()
+    st = s.stats()
+    assert st["units_done"] == n and st["lists_done"] == n_lists and st["error_bits"] == 0
+    s.close()
+
+
+def test_sg_relaunch_and_reset():
+    """Indices carry over between launches without reset(); reset() restarts them."""
+    log("sg relaunch")
+    t, n = 2048, 64
+    host = random_host(3 * n * t, seed=21)
+    dst = gfd_amd.DeviceBuffer(3 * n * t)
+    dst.fill(0)
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=4, idle_limit_ms=5000)
+    idx = []
+    for r in range(3):
+        if r == 2:
+            s.reset()
+        base = r * n
+        ent = entries_array(host.ptr + (base + np.arange(n, dtype=np.uint64)) * t,
+                            dst.ptr + (base + np.arange(n, dtype=np.uint64)) * t, t)
+        idx.append(s.submit_sg_list(ent[: n // 2], list_id=2 * r))
+        idx.append(s.submit_sg_list(ent[n // 2:], list_id=2 * r + 1))
+        s.launch()
+        s.synchronize()
+        assert s.stats()["units_done"] == n
+    assert idx == [0, 1, 2, 3, 0, 1]
+    assert (dst.download() == host.array).all()
+    s.close()
+
+
+def test_sg_submit_without_kernel_rejects_when_ring_full():
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=1, idle_limit_ms=2000)
+    host = gfd_amd.HostBuffer(4096)
+    dst = gfd_amd.DeviceBuffer(4096)
+    ent = entries_array([host.ptr], [dst.ptr], 16)
+    for i in range(gfd_amd.MAX_SG_LISTS):
+        assert s.submit_sg_list(ent, list_id=i) == i
+    with pytest.raises(gfd_amd.GfdError):
+        s.submit_sg_list(ent, list_id=0)
+    # The queued lists still land once a kernel runs.
+    s.launch()
+    s.synchronize()
+    assert s.stats()["lists_done"] == gfd_amd.MAX_SG_LISTS
+    s.close()
+
+
+@pytest.mark.parametrize("blocks,n_lists,epl,t", [(1, 4, 8, 4096), (8, 64, 32, 2048), (0, 300, 16, 1000)])
+def test_sg_gpu_submit(blocks, n_lists, epl, t):
+    """test/test_sg_gpu_submit.cu: a submitter wave per workgroup builds the
+    lists on the GPU (entries from a device table), transfer waves land them,
+    the compute wave checksums each list."""
+    log("sg gpu submit blocks=%d lists=%d epl=%d t=%d" % (blocks, n_lists, epl, t))
+    n = n_lists * epl
+    host = gfd_amd.HostBuffer(n * t)
+    if t % 4 == 0:
+        host.array.view(np.float32)[:] = np.arange(n * t // 4, dtype=np.float32) + 1
+    else:
+        host.array[:] = np.random.default_rng(1).integers(0, 256, n * t, dtype=np.uint8)
+    dst = gfd_amd.DeviceBuffer(n * t)
+    dst.fill(0)
+    arr = entries_array(host.ptr + np.arange(n, dtype=np.uint64) * t, dst.ptr + np.arange(n, dtype=np.uint64) * t, t,
+                        tag=0)
+    d_ent = gfd_amd.DeviceBuffer(arr.nbytes)
+    d_ent.upload(arr.view(np.uint8))
+    sums = gfd_amd.DeviceBuffer(gfd_amd.MAX_SG_LISTS * 8)
+    sums.fill(0)
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=blocks, idle_limit_ms=5000)
+    s.launch_gpu_submit(d_ent.ptr, epl, n_lists, list_sums=sums.ptr)
+    s.synchronize(extra_gpu_lists=n_lists)
+    assert (dst.download() == host.array).all()
+    got = sums.download().view(np.uint64)
+    want = list_checksums(host.array, host.ptr, arr, {l: (l * epl, (l + 1) * epl) for l in range(n_lists)})
+    for lid, v in want.items():
+        assert int(got[lid]) == v, "list %d checksum" % lid
+    st = s.stats()
+    assert st["lists_done"] == n_lists and st["units_done"] == n and st["error_bits"] == 0
+    s.close()

@@ -287,3 +287,74 @@ def test_moe_token_values_and_weight_ranges():
     assert v.min() >= -1.0 and v.max() <= 1.0 and np.isfinite(v).all()
     w = oracle.bf16_to_f32(oracle.moe_weight(512))
     assert w.min() >= 0.5 and w.max() <= 1.5
+
+
+# ------------------------------------------------------------ sessions
+
+@pytest.mark.parametrize("token_size,db,expect", [
+    # ~128 KiB chunks: 4 KiB tokens -> 32 per chunk, 4 chunks per 128-token tile
+    (4096, False, (32, 4, 64 * 5)),
+    # small tokens aim at 64 KiB: 512 B -> 128 tokens = the whole tile
+    (512, False, (128, 1, 128)),
+    (256, False, (128, 1, 128)),
+    (1024, False, (128, 1, 128)),
+    (2048, False, (64, 2, 64 * 3)),
+    # 16 KiB tokens: 8 per chunk would be 16 chunks; the K <= 8 limit raises it to 16
+    (16384, False, (16, 8, 64 * 9)),
+    # large tokens aim at 256 KiB: 4 tokens, again raised to the K <= 8 floor
+    (65536, False, (16, 8, 64 * 9)),
+    # double buffering: K <= 4 keeps 1 + 2K waves within 1024 threads
+    (16384, True, (32, 4, 64 * 9)),
+    (4096, True, (32, 4, 64 * 9)),
+    (3000, False, (32, 4, 64 * 5)),   # 131072 // 3000 = 43 -> 32
+])
+def test_warp_spec_chunking_known(token_size, db, expect):
+    assert oracle.warp_spec_chunking(token_size, 128, 0, db) == expect
+
+
+def test_warp_spec_chunking_explicit_and_per_tile():
+    # test/test_db_small_tiles.cu: tile 32 / chunk 16 (K=2), 16/16 (K=1), 64/16 (K=4), double-buffered
+    assert oracle.warp_spec_chunking(1024, 32, 16, True) == (16, 2, 64 * 5)
+    assert oracle.warp_spec_chunking(1024, 16, 16, True) == (16, 1, 64 * 3)
+    assert oracle.warp_spec_chunking(1024, 64, 16, True) == (16, 4, 64 * 9)
+    assert oracle.warp_spec_chunking(4096, 128, 0, False, per_tile_mode=True) == (128, 1, 128)
+
+
+def test_warp_spec_chunking_invariants():
+    for T in (16, 32, 64, 128, 256, 512):
+        for ts in (16, 100, 512, 513, 4096, 5000, 65535, 65536, 1 << 20):
+            for db in (False, True):
+                c, k, block = oracle.warp_spec_chunking(ts, T, 0, db)
+                assert c & (c - 1) == 0 and T % c == 0 and k * c == T
+                assert k <= (4 if db else 8) and block <= 1024
+                target = 65536 if ts <= 512 else (262144 if ts >= 65536 else 131072)
+                raw = max(4, target // ts)
+                if T // (4 if db else 8) <= raw <= T:
+                    # unclamped: the largest power of two not above the target
+                    assert c <= raw < 2 * c
+
+
+def test_warp_spec_expected_brute_force():
+    rng = np.random.default_rng(5)
+    for total, ts, T in [(10, 3, 4), (8, 5, 8), (7, 2, 8), (33, 16, 16)]:
+        src = rng.integers(0, 256, total * ts, dtype=np.uint8)
+        before = rng.integers(0, 256, total * ts, dtype=np.uint8)
+        want = before.copy()
+        for t in range((total // T) * T):
+            for b in range(ts):
+                want[t * ts + b] = src[t * ts + b]
+        assert (oracle.warp_spec_expected(src, before, total, ts, T) == want).all()
+
+
+def test_u32_word_checksum():
+    # closed forms
+    for n in (0, 1, 3, 4, 5, 64, 1027):
+        assert oracle.u32_word_checksum(np.ones(n, np.uint8)) == (n // 4) * 0x01010101 + n % 4
+    assert oracle.u32_word_checksum(np.array([0x78, 0x56, 0x34, 0x12], np.uint8)) == 0x12345678
+    # independent little-endian loop
+    rng = np.random.default_rng(9)
+    for n in (1, 7, 64, 255):
+        b = rng.integers(0, 256, n, dtype=np.uint8)
+        ref = sum(int.from_bytes(bytes(b[i:i + 4]), "little") for i in range(0, n - n % 4, 4))
+        ref += sum(int(x) for x in b[n - n % 4:])
+        assert oracle.u32_word_checksum(b) == ref
