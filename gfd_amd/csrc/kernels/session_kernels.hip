@@ -108,7 +108,7 @@ GFD_SG_WARP_SPEC_KERNEL(sg_null_kernel, NullList)
 // ... (list i = entries [i*epl, (i+1)*epl) of d_entries), waits for all
 // num_lists to land, then sets terminate.
 template <typename F>
-__global__ void sg_gpu_submit_kernel(gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq, F fn,
+__global__ __launch_bounds__(3 * 64) void sg_gpu_submit_kernel(gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq, F fn,
                                      const gfd::DeviceSGEntry* d_entries, uint32_t epl, uint32_t num_lists) {
     gfd::sg_warp_spec::_sg_transfer_warp_loop(dq, sq, fn);  // waves 0 and 1 run here; wave 2 returns
     if (gfd::wave::wave_id() != 2) return;

@@ -72,7 +72,7 @@ __device__ __forceinline__ bool _wait_committed(SGTaskQueue* sq, SGDeviceCounter
     const uint64_t t0 = wall_clock64();
     uint32_t grace = 0;
     for (;;) {
-        const uint64_t known = sg::load_dev(&cnt->list_known);
+        const uint64_t known = __hip_atomic_load(&cnt->list_known, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (idx <= known) {
             if (wave::load_system(&mine.sequence) == idx + 1) {
                 if (idx == known) {
@@ -93,18 +93,29 @@ __device__ __forceinline__ bool _wait_committed(SGTaskQueue* sq, SGDeviceCounter
             }
             __builtin_amdgcn_s_sleep(4);
         } else {
-            if (sg::load_dev(&cnt->stop)) return false;
-            __builtin_amdgcn_s_sleep(16);
+            if (__hip_atomic_load(&cnt->stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+            // Back off in proportion to how many commits this wave is still
+            // waiting for: device-scope loads bypass the XCD-local L2, so
+            // hundreds of idle waves polling at full rate would crowd the
+            // fabric the copies use.  Up to ~25 us between polls.
+            const uint64_t dist = idx - known;
+            if (dist < 8) {
+                for (uint64_t i = 0; i < dist; i++) __builtin_amdgcn_s_sleep(16);
+            } else {
+                const uint32_t naps = dist < 64 ? (uint32_t)(dist / 8) : 8u;
+                for (uint32_t i = 0; i < naps; i++) __builtin_amdgcn_s_sleep(127);
+            }
         }
         if (wall_clock64() - t0 > idle_ticks) return false;
     }
 }
 
 template <typename ComputeFn>
-__device__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTaskQueue* sq, ComputeFn compute_fn) {
+__device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTaskQueue* sq, ComputeFn compute_fn) {
     (void)dq;
     __shared__ _SGSlot slots[2];
     __shared__ int terminated;
+    __shared__ wave::BatchLds batch_lds;  // transfer wave's descriptor staging
     const int w = wave::wave_id();
     const int lane = wave::lane_id();
     if (threadIdx.x < 2) {
@@ -120,6 +131,7 @@ __device__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTaskQueue* sq, Com
     if (w == 0) {
         // ---------------- transfer wave
         const uint64_t idle_ticks = _idle_limit_ticks(sq);
+        const int unroll = wave::transfer_unroll(gridDim.x);
         for (uint64_t iter = 0;; iter++) {
             const int s = (int)(iter & 1);
             if (has_compute && !wave::wait_lds_eq(&slots[s].free, 1)) {
@@ -134,7 +146,8 @@ __device__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTaskQueue* sq, Com
             const uint32_t pool_offset = l.pool_offset, count = l.count, list_id = l.list_id, flags = l.flags;
             if (lane == 0) wave::store_system(&l.sequence, 0);  // claimed
 
-            // Copy the list: lane i holds entry b+i's descriptor, the wave walks them.
+            // Copy the list 64 entries at a time: lane i holds entry b+i's
+            // descriptor; the batch moves as one stream of 16-byte vectors.
             uint64_t bytes = 0;
             for (uint32_t b = 0; b < count; b += wave::kWidth) {
                 uint64_t md = 0, ms = 0, mn = 0;
@@ -145,11 +158,7 @@ __device__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTaskQueue* sq, Com
                     mn = e.size;
                 }
                 const uint32_t nb = count - b < (uint32_t)wave::kWidth ? count - b : (uint32_t)wave::kWidth;
-                for (uint32_t j = 0; j < nb; j++) {
-                    const uint64_t n = wave::readlane64(mn, (int)j);
-                    wave::copy<4>(wave::readlane64(md, (int)j), wave::readlane64(ms, (int)j), n);
-                    bytes += n;
-                }
+                bytes += wave::copy_batch(unroll, md, ms, mn, nb, &batch_lds);
             }
             wave::release_agent();  // the list's bytes are visible device-wide
             if (lane == 0) {
@@ -210,12 +219,18 @@ __device__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTaskQueue* sq, Com
     // further waves return to the caller
 }
 
+// Largest workgroup of an SG kernel (1 transfer + up to 3 compute waves).
+// With one wave per SIMD the transfer wave may use up to 512 registers, so
+// its in-flight vectors, their addresses and the entry searches stay in
+// registers.
+constexpr int SG_MAX_BLOCK = 256;
+
 }  // namespace sg_warp_spec
 }  // namespace gfd
 
 // Kernel generation macro (block = 64 * (1 + compute waves) threads).
-#define GFD_SG_WARP_SPEC_KERNEL(kernel_name, ComputeFnType)                             \
-    __global__ void kernel_name(gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq,        \
-                                ComputeFnType compute_fn) {                             \
-        gfd::sg_warp_spec::_sg_transfer_warp_loop(dq, sq, compute_fn);                  \
+#define GFD_SG_WARP_SPEC_KERNEL(kernel_name, ComputeFnType)                                 \
+    __global__ __launch_bounds__(gfd::sg_warp_spec::SG_MAX_BLOCK) void kernel_name(         \
+        gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq, ComputeFnType compute_fn) {         \
+        gfd::sg_warp_spec::_sg_transfer_warp_loop(dq, sq, compute_fn);                      \
     }

@@ -78,7 +78,7 @@ struct _TileSlot {
 };
 
 template <int NSLOTS, typename ComputeFn>
-__device__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, const void* cpu_base, ComputeFn compute_fn) {
+__device__ __forceinline__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, const void* cpu_base, ComputeFn compute_fn) {
     __shared__ _TileSlot slots[NSLOTS];
     const int w = wave::wave_id();
     const int lane = wave::lane_id();
@@ -98,6 +98,7 @@ __device__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, const void* cpu_bas
 
     if (w == 0) {
         // ---------------- transfer wave
+        const int unroll = wave::transfer_unroll(gridDim.x < total_tiles ? gridDim.x : total_tiles);
         bool ok = true;
         for (uint32_t n = 0; ok; n++) {
             const int s = (int)(n % NSLOTS);
@@ -131,8 +132,8 @@ __device__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, const void* cpu_bas
             const uint64_t tok0 = tile * T;
             for (uint32_t k = 0; k < K; k++) {
                 const uint64_t off = (tok0 + (uint64_t)k * C) * token_size;
-                wave::copy<4>((uint64_t)(uintptr_t)gpu_buffer + off, (uint64_t)(uintptr_t)cpu_base + off,
-                              (uint64_t)C * token_size);
+                wave::copy_u(unroll, (uint64_t)(uintptr_t)gpu_buffer + off, (uint64_t)(uintptr_t)cpu_base + off,
+                             (uint64_t)C * token_size);
                 wave::release_agent();
                 if (lane == 0) wave::lds_store(&slots[s].ready, (int)k + 1);
             }
@@ -173,12 +174,12 @@ __device__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, const void* cpu_bas
 }
 
 template <typename ComputeFn>
-__device__ void _warp_spec_tile_loop(TiledQueue* tq, void* gpu_buffer, const void* cpu_base, ComputeFn fn) {
+__device__ __forceinline__ void _warp_spec_tile_loop(TiledQueue* tq, void* gpu_buffer, const void* cpu_base, ComputeFn fn) {
     _tile_loop<1>(tq, gpu_buffer, cpu_base, fn);
 }
 
 template <typename ComputeFn>
-__device__ void _warp_spec_tile_loop_double_buffer(TiledQueue* tq, void* gpu_buffer, const void* cpu_base,
+__device__ __forceinline__ void _warp_spec_tile_loop_double_buffer(TiledQueue* tq, void* gpu_buffer, const void* cpu_base,
                                                    ComputeFn fn) {
     _tile_loop<2>(tq, gpu_buffer, cpu_base, fn);
 }

@@ -30,7 +30,7 @@ struct WarpSpecConfig {
     // optional
     uint32_t tokens_per_tile = 128;
     uint32_t tokens_per_chunk = 0;  // 0 = automatic
-    int num_blocks = 0;             // 0 = one workgroup per CU
+    int num_blocks = 0;             // 0 = one workgroup per tile, at most one per CU
     int numa_node = 0;              // kept for API compatibility
     bool use_copy_engine = true;    // kept for API compatibility (data moves zero-copy)
     bool double_buffer = false;
@@ -125,7 +125,7 @@ private:
 
 struct SGWarpSpecConfig {
     int num_compute_warps = 0;  // compute waves per workgroup (0 -> 1, as in the reference)
-    int num_blocks = 0;         // 0 = one workgroup per CU
+    int num_blocks = 0;         // 0 = min(CU count, 64)
     int numa_node = 0;          // kept for API compatibility
     bool use_copy_engine = true;
     int max_lists = MAX_SG_LISTS;

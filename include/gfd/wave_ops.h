@@ -25,6 +25,16 @@ __device__ __forceinline__ uint64_t readlane64(uint64_t x, int lane) {
 
 __device__ __forceinline__ uint64_t broadcast0(uint64_t x) { return readlane64(x, 0); }
 
+// 16-byte vector as a native clang vector: arrays of these stay in VGPRs at
+// any unroll (arrays of HIP's uint4 wrapper go to scratch from 8 on).
+typedef uint32_t vec4u __attribute__((ext_vector_type(4)));
+// Global-address-space views, so copies compile to global_load/global_store
+// (flat instructions would also wait on the LDS counter).
+typedef __attribute__((address_space(1))) vec4u gvec4u;
+
+__device__ __forceinline__ vec4u gload(uint64_t a) { return *reinterpret_cast<const gvec4u*>(a); }
+__device__ __forceinline__ void gstore(uint64_t a, vec4u v) { *reinterpret_cast<gvec4u*>(a) = v; }
+
 // Copy n bytes s -> d with the whole wave: 16-byte vectors (U in flight per
 // lane) when d and s share their alignment mod 16, bytes otherwise.
 template <int U = 4>
@@ -38,19 +48,21 @@ __device__ __forceinline__ void copy(uint64_t d, uint64_t s, uint64_t n) {
         s += head;
         n -= head;
         const uint64_t nv = n >> 4;
-        const uint4* sv = reinterpret_cast<const uint4*>(s);
-        uint4* dv = reinterpret_cast<uint4*>(d);
+        // Branch-free: a lane past the end works on the last vector instead
+        // (loads it and stores the same bytes back).  A guarded load or store
+        // sits in its own basic block, and the compiler then waits for every
+        // earlier memory operation first, which leaves one in flight.
         for (uint64_t base = 0; base < nv; base += (uint64_t)kWidth * U) {
-            uint4 r[U];
+            vec4u r[U];
 #pragma unroll
             for (int k = 0; k < U; k++) {
                 const uint64_t v = base + (uint64_t)k * kWidth + lane;
-                if (v < nv) r[k] = sv[v];
+                r[k] = gload(s + ((v < nv ? v : nv - 1) << 4));
             }
 #pragma unroll
             for (int k = 0; k < U; k++) {
                 const uint64_t v = base + (uint64_t)k * kWidth + lane;
-                if (v < nv) dv[v] = r[k];
+                gstore(d + ((v < nv ? v : nv - 1) << 4), r[k]);
             }
         }
         const uint64_t tail = n & 15;
@@ -60,6 +72,115 @@ __device__ __forceinline__ void copy(uint64_t d, uint64_t s, uint64_t n) {
         for (uint64_t b = lane; b < n; b += kWidth)
             *reinterpret_cast<uint8_t*>(d + b) = *reinterpret_cast<const uint8_t*>(s + b);
     }
+}
+
+// 16-byte loads in flight per lane of a transfer wave, from the number of
+// transfer waves in the grid: about 1 MiB of host reads outstanding in total
+// (64 lanes x U x 16 B per wave) fills the PCIe link; far more only queues
+// (measured on MI355X: 8 waves reach 48 GB/s at U = 16 but 20 GB/s at
+// U = 4, while 256 waves drop from 55 to 47 GB/s at U = 16).
+__device__ __forceinline__ int transfer_unroll(uint32_t transfer_waves) {
+    return transfer_waves <= 64 ? 16 : (transfer_waves <= 128 ? 8 : 4);
+}
+
+template <int U>
+__device__ __forceinline__ void copy(uint64_t d, uint64_t s, uint64_t n);
+
+// copy() with U chosen at run time (16, 8 or 4).
+__device__ __forceinline__ void copy_u(int u, uint64_t d, uint64_t s, uint64_t n) {
+    if (u >= 16) copy<16>(d, s, n);
+    else if (u >= 8) copy<8>(d, s, n);
+    else copy<4>(d, s, n);
+}
+
+// Per-wave LDS scratch for copy_batch: start vector and addresses of up to 64 entries.
+struct BatchLds {
+    uint32_t start[kWidth + 1];
+    uint64_t src[kWidth];
+    uint64_t dst[kWidth];
+};
+
+// The flat vector stream of copy_batch: vector v of the batch belongs to entry
+// e (v / vpe when every entry has vpe vectors, else the last entry whose
+// start is <= v, found by a fixed 6-step search) at offset v - start[e].
+template <int U, bool kUniform>
+__device__ __forceinline__ void flat_copy(uint32_t total, uint32_t vpe, uint32_t nb, const BatchLds* lds) {
+    const uint32_t lane = (uint32_t)lane_id();
+    for (uint32_t base = 0; base < total; base += (uint32_t)kWidth * U) {
+        vec4u r[U];
+        uint64_t da[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            // Branch-free on a clamped index, as in copy().
+            const uint32_t v0 = base + (uint32_t)k * kWidth + lane;
+            const uint32_t v = v0 < total ? v0 : total - 1;
+            uint32_t e, o;
+            if (kUniform) {
+                e = v / vpe;
+                o = v - e * vpe;
+            } else {
+                e = 0;
+#pragma unroll
+                for (uint32_t step = kWidth / 2; step > 0; step >>= 1)
+                    if (e + step < nb && lds->start[e + step] <= v) e += step;
+                o = v - lds->start[e];
+            }
+            r[k] = gload(lds->src[e] + ((uint64_t)o << 4));
+            da[k] = lds->dst[e] + ((uint64_t)o << 4);
+        }
+#pragma unroll
+        for (int k = 0; k < U; k++) gstore(da[k], r[k]);
+    }
+}
+
+// Copy a batch of nb <= 64 entries, lane j holding entry j's (dst, src, bytes).
+// When every entry is 16-byte aligned on both sides with a size that is a
+// multiple of 16, the batch is copied as one stream of 16-byte vectors across
+// entry boundaries: u loads in flight per lane when all entries have the same
+// size (u = 16, 8 or 4), 4 otherwise.  Other batches go entry by entry.
+// Returns the bytes copied.
+__device__ __forceinline__ uint64_t copy_batch(int u, uint64_t md, uint64_t ms, uint64_t mn, uint32_t nb,
+                                               BatchLds* lds) {
+    const uint32_t lane = (uint32_t)lane_id();
+    const bool mine = lane < nb;
+    const bool aligned = !mine || (((md | ms | mn) & 15) == 0 && (mn >> 4) < (1ull << 26));
+    uint64_t total_bytes = 0;
+    for (uint32_t j = 0; j < nb; j++) total_bytes += readlane64(mn, (int)j);
+    if (__ballot(!aligned) != 0) {
+        for (uint32_t j = 0; j < nb; j++) copy<4>(readlane64(md, (int)j), readlane64(ms, (int)j), readlane64(mn, (int)j));
+        return total_bytes;
+    }
+    // 64 entries of < 2^26 vectors each: the batch's vector index fits 32 bits.
+    const uint32_t vecs = mine ? (uint32_t)(mn >> 4) : 0u;
+    uint32_t incl = vecs;
+#pragma unroll
+    for (int o = 1; o < kWidth; o <<= 1) {
+        const uint32_t t = (uint32_t)__shfl_up((int)incl, o, kWidth);
+        if (lane >= (uint32_t)o) incl += t;
+    }
+    if (mine) {
+        lds->start[lane] = incl - vecs;
+        lds->src[lane] = ms;
+        lds->dst[lane] = md;
+    }
+    const uint32_t total = (uint32_t)(total_bytes >> 4);
+    if (lane == 0) lds->start[nb] = total;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t vpe0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)vecs);
+    if (total > 0) {
+        if (__ballot(mine && vecs != vpe0) == 0) {
+            if (u >= 16) flat_copy<16, true>(total, vpe0, nb, lds);
+            else if (u >= 8) flat_copy<8, true>(total, vpe0, nb, lds);
+            else flat_copy<4, true>(total, vpe0, nb, lds);
+        } else {
+            flat_copy<4, false>(total, 0, nb, lds);
+        }
+    }
+    __builtin_amdgcn_wave_barrier();  // lds reused by the next batch
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    return total_bytes;
 }
 
 // Make this wave's global stores visible device-wide before a flag is raised
