@@ -5,175 +5,114 @@
 // for the same contract (dst[j*T + b] = token_j[b]).
 //
 // Memory-level design
-//   * Each lane moves 16 bytes per load (global_load_dwordx4); a wave covers
-//     1 KiB of one token per instruction, so every PCIe read request is a
-//     full, contiguous cache-line group.
-//   * Each lane keeps U = 4 independent 16-byte loads in flight before it
-//     stores, and the grid is 2 workgroups per CU (512 on MI355X) looping over
-//     the data: 512 x 256 x 4 x 16 B = 8 MiB of host reads can be outstanding,
-//     far above the link's bandwidth-latency product (about 64 GB/s x 2 us).
-//     More concurrency is slower, not faster: with 16 workgroups per CU the
-//     kernel drops from 56 to 52 GB/s, because many more distinct host pages
-//     are in flight at once (measured over 0.5-32 workgroups per CU and
-//     U = 1-16; 2 and 4 are the optimum for 512 B - 64 KiB tokens).
+//   * A wave takes a batch of up to 64 tokens (entries): lane i loads token
+//     i's source address (the KV block / page table entry, normally in HBM)
+//     once, and the batch is then copied as one stream of 16-byte vectors
+//     (global_load_dwordx4 / global_store_dwordx4) across token boundaries,
+//     so a wave covers 1 KiB per instruction and every PCIe read request is
+//     a full, contiguous cache-line group.
+//   * The copy is branch-free: lanes past the end work on the last vector.
+//     A guarded load or store would sit in its own basic block behind a full
+//     wait on every earlier memory operation, leaving one request in flight
+//     per wave.  With straight-line code a lane keeps U loads in flight.
+//   * Grid: a few hundred KiB to 1 MiB of host reads outstanding in total
+//     (waves x 64 lanes x U x 16 B) fills the link; far more only queues.
+//     The measured optimum is set below (kBytesPerWave ...) and can be
+//     overridden with GFD_ZC_WAVES / GFD_ZC_UNROLL.
 //   * Stores are plain 16-byte stores to HBM (coalesced, contiguous).
-//   * Token source addresses come from a per-token table (the KV block/page
-//     table), normally resident in HBM; lanes of one token read the same
-//     8-byte entry, which the L1/L2 broadcast.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
+#include <cstdlib>
+
+#include "gfd/wave_ops.h"
 
 #include "gfd_capi.h"
 
 namespace {
 
 constexpr int kBlock = 256;  // 4 waves
+constexpr int kWavesPerBlock = kBlock / 64;
+// Waves in flight: one per 128 KiB of the job, between 64 and 256, with 4
+// loads in flight per lane (256-1024 KiB of host reads outstanding).
+// Measured on MI355X over 64-2048 waves and U = 4/8/16: 8192 x 4 KiB peaks at
+// 256 waves (56.8 GB/s) and falls to 52 GB/s at 1024-2048; jobs of 1-4 MiB
+// do best at 64 waves; U = 4 is best or within 1% everywhere.
+constexpr uint64_t kBytesPerWave = 128 * 1024;
+constexpr int kMinWaves = 64, kMaxWaves = 256;
+constexpr int kDefaultUnroll = 4;
 
-// Byte-wise fallback for a 16-byte vector whose host source is not 16-byte
-// aligned (never taken for the benchmark layouts, kept for correctness).
-__device__ __forceinline__ uint4 load16_unaligned(const uint8_t* p) {
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        w[i] = (uint32_t)p[4 * i] | ((uint32_t)p[4 * i + 1] << 8) | ((uint32_t)p[4 * i + 2] << 16) |
-               ((uint32_t)p[4 * i + 3] << 24);
-    return make_uint4(w[0], w[1], w[2], w[3]);
-}
+using gfd::wave::BatchLds;
 
-__device__ __forceinline__ uint4 load16(uint64_t addr) {
-    if ((addr & 15) == 0) return *reinterpret_cast<const uint4*>(addr);
-    return load16_unaligned(reinterpret_cast<const uint8_t*>(addr));
-}
-
-// Page-table form: token j lives at src_addrs[j] (host), lands at
-// dst + j * token_size.  token_size is a multiple of 16; the flattened
-// 16-byte vector index v = j * vpt + o is split with a shift when vpt is a
-// power of two.
-template <int U>
-__global__ __launch_bounds__(kBlock) void zc_gather_tokens16(const uint64_t* __restrict__ src_addrs,
-                                                             uint4* __restrict__ dst, uint32_t vpt,
-                                                             int vpt_shift, uint32_t total_vecs) {
-    const uint32_t tid = threadIdx.x;
-    const uint32_t step = gridDim.x * (uint32_t)(kBlock * U);
-    for (uint32_t base = blockIdx.x * (uint32_t)(kBlock * U); base < total_vecs; base += step) {
-        uint4 r[U];
-#pragma unroll
-        for (int k = 0; k < U; k++) {
-            const uint32_t v = base + (uint32_t)k * kBlock + tid;
-            if (v < total_vecs) {
-                uint32_t j, o;
-                if (vpt_shift >= 0) {
-                    j = v >> vpt_shift;
-                    o = v & (vpt - 1);
-                } else {
-                    j = v / vpt;
-                    o = v - j * vpt;
-                }
-                r[k] = load16(src_addrs[j] + (uint64_t)o * 16u);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < U; k++) {
-            const uint32_t v = base + (uint32_t)k * kBlock + tid;
-            if (v < total_vecs) dst[v] = r[k];
-        }
-    }
-}
-
-// Page-table form for token sizes that are not a multiple of 16: byte lanes.
-__global__ __launch_bounds__(kBlock) void zc_gather_tokens1(const uint64_t* __restrict__ src_addrs,
-                                                            uint8_t* __restrict__ dst, uint32_t token_size,
-                                                            uint64_t total_bytes) {
-    const uint64_t step = (uint64_t)gridDim.x * kBlock;
-    for (uint64_t b = (uint64_t)blockIdx.x * kBlock + threadIdx.x; b < total_bytes; b += step) {
-        const uint64_t j = b / token_size;
-        const uint64_t o = b - j * token_size;
-        dst[b] = *reinterpret_cast<const uint8_t*>(src_addrs[j] + o);
-    }
-}
-
-__device__ __forceinline__ uint64_t readlane64(uint64_t x, int lane) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), lane);
-    return ((uint64_t)hi << 32) | lo;
-}
-
-// Copy one entry with the whole wave.
-template <int U>
-__device__ __forceinline__ void wave_copy(uint64_t d, uint64_t s, uint64_t n, uint32_t lane) {
-    if (((d ^ s) & 15) == 0) {
-        // Head bytes up to 16-byte alignment, 16-byte body, tail bytes.
-        uint64_t head = (16 - (d & 15)) & 15;
-        if (head > n) head = n;
-        if (lane < head) *reinterpret_cast<uint8_t*>(d + lane) = *reinterpret_cast<const uint8_t*>(s + lane);
-        d += head;
-        s += head;
-        n -= head;
-        const uint64_t nv = n >> 4;
-        const uint4* sv = reinterpret_cast<const uint4*>(s);
-        uint4* dv = reinterpret_cast<uint4*>(d);
-        for (uint64_t base = 0; base < nv; base += 64u * U) {
-            uint4 r[U];
-#pragma unroll
-            for (int k = 0; k < U; k++) {
-                const uint64_t v = base + (uint64_t)k * 64u + lane;
-                if (v < nv) r[k] = sv[v];
-            }
-#pragma unroll
-            for (int k = 0; k < U; k++) {
-                const uint64_t v = base + (uint64_t)k * 64u + lane;
-                if (v < nv) dv[v] = r[k];
-            }
-        }
-        const uint64_t tail = n & 15;
-        if (lane < tail)
-            *reinterpret_cast<uint8_t*>(d + (nv << 4) + lane) =
-                *reinterpret_cast<const uint8_t*>(s + (nv << 4) + lane);
-    } else {
-        for (uint64_t b = lane; b < n; b += 64)
-            *reinterpret_cast<uint8_t*>(d + b) = *reinterpret_cast<const uint8_t*>(s + b);
-    }
-}
-
-// Generic SG list: any sizes, any (disjoint) destinations.  Each wave takes
-// `per_wave` consecutive entries; lane i loads entry i's 24-byte descriptor
-// once and the wave walks them with readlane (one table round trip per batch).
-template <int U>
-__global__ __launch_bounds__(kBlock) void zc_gather_sg(const gfd_sg_entry* __restrict__ entries, int count,
-                                                       int per_wave) {
-    const uint32_t lane = threadIdx.x & 63;
-    const int wave = (int)((blockIdx.x * kBlock + threadIdx.x) >> 6);
-    const int nwaves = (int)((gridDim.x * kBlock) >> 6);
-    for (int first = wave * per_wave; first < count; first += nwaves * per_wave) {
-        const int n = min(per_wave, count - first);
+// Page-table form: token j of num_tokens lives at src_addrs[j] (host) and
+// lands at dst + j * token_size.  Wave w copies tokens [w*per_wave, ...)
+// strided over the grid, per_wave <= 64 at a time.
+__global__ __launch_bounds__(kBlock) void zc_gather_tokens(const uint64_t* __restrict__ src_addrs, uint64_t dst,
+                                                           uint32_t token_size, uint32_t num_tokens,
+                                                           uint32_t per_wave, int unroll) {
+    __shared__ BatchLds lds[kWavesPerBlock];
+    const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const uint64_t wave = (uint64_t)blockIdx.x * kWavesPerBlock + wid;
+    const uint64_t stride = (uint64_t)gridDim.x * kWavesPerBlock * per_wave;
+    for (uint64_t first = wave * per_wave; first < num_tokens; first += stride) {
+        const uint32_t nb = (uint32_t)min((uint64_t)per_wave, num_tokens - first);
         uint64_t md = 0, ms = 0, mn = 0;
-        if ((int)lane < n) {
+        if (lane < nb) {
+            ms = src_addrs[first + lane];
+            md = dst + (first + lane) * token_size;
+            mn = token_size;
+        }
+        gfd::wave::copy_batch(unroll, md, ms, mn, nb, &lds[wid]);
+    }
+}
+
+// Generic SG list: any sizes, any (disjoint) destinations, same batching.
+__global__ __launch_bounds__(kBlock) void zc_gather_sg(const gfd_sg_entry* __restrict__ entries, uint32_t count,
+                                                       uint32_t per_wave, int unroll) {
+    __shared__ BatchLds lds[kWavesPerBlock];
+    const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const uint64_t wave = (uint64_t)blockIdx.x * kWavesPerBlock + wid;
+    const uint64_t stride = (uint64_t)gridDim.x * kWavesPerBlock * per_wave;
+    for (uint64_t first = wave * per_wave; first < count; first += stride) {
+        const uint32_t nb = (uint32_t)min((uint64_t)per_wave, count - first);
+        uint64_t md = 0, ms = 0, mn = 0;
+        if (lane < nb) {
             const gfd_sg_entry e = entries[first + lane];
             md = e.dst;
             ms = e.src;
             mn = e.size;
         }
-        for (int i = 0; i < n; i++)
-            wave_copy<U>(readlane64(md, i), readlane64(ms, i), readlane64(mn, i), lane);
+        gfd::wave::copy_batch(unroll, md, ms, mn, nb, &lds[wid]);
     }
 }
 
-int g_cu_count = 0;
-
-int cu_count() {
-    if (g_cu_count == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&g_cu_count, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            g_cu_count <= 0)
-            g_cu_count = 256;
-    }
-    return g_cu_count;
+int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : dflt;
 }
 
-constexpr int kUnroll = 4;
-constexpr int kBlocksPerCU = 2;
+// Launch shape for n entries: (blocks, entries per wave, unroll).
+struct Shape {
+    uint32_t blocks, per_wave;
+    int unroll;
+};
+
+Shape shape_for(uint64_t n, uint64_t total_bytes) {
+    // Read per call (a getenv is ~100 ns against a launch of microseconds),
+    // so a process can sweep launch shapes.
+    const int dflt = (int)std::min<uint64_t>(std::max<uint64_t>(total_bytes / kBytesPerWave, kMinWaves), kMaxWaves);
+    const int target = std::max(4, env_int("GFD_ZC_WAVES", dflt));
+    const int unroll_env = env_int("GFD_ZC_UNROLL", kDefaultUnroll);
+    uint64_t per_wave = (n + target - 1) / target;
+    per_wave = std::min<uint64_t>(std::max<uint64_t>(per_wave, 1), 64);
+    const uint64_t waves = (n + per_wave - 1) / per_wave;
+    Shape s;
+    s.per_wave = (uint32_t)per_wave;
+    s.blocks = (uint32_t)((waves + kWavesPerBlock - 1) / kWavesPerBlock);
+    s.unroll = unroll_env >= 16 ? 16 : (unroll_env >= 8 ? 8 : 4);
+    return s;
+}
 
 }  // namespace
 
@@ -182,41 +121,19 @@ extern "C" int gfd_zero_copy_gather_tokens(const uint64_t* src_addrs, void* dst,
     if (num_tokens < 0 || (num_tokens > 0 && (!src_addrs || !dst || token_size == 0)))
         return (int)hipErrorInvalidValue;
     if (num_tokens == 0) return 0;
-    hipStream_t st = (hipStream_t)stream;
-    const uint64_t total = (uint64_t)num_tokens * token_size;
-    const int max_blocks = cu_count() * kBlocksPerCU;
-    if ((token_size & 15) == 0 && ((uintptr_t)dst & 15) == 0) {
-        const uint64_t total_vecs = total >> 4;
-        if (total_vecs >= (1ull << 31)) return (int)hipErrorInvalidValue;  // >= 32 GiB per call
-        const uint32_t vpt = token_size >> 4;
-        const int shift = (vpt & (vpt - 1)) == 0 ? __builtin_ctz(vpt) : -1;
-        uint64_t blocks = (total_vecs + kBlock * kUnroll - 1) / (kBlock * kUnroll);
-        if (blocks > (uint64_t)max_blocks) blocks = max_blocks;
-        hipLaunchKernelGGL(zc_gather_tokens16<kUnroll>, dim3((uint32_t)blocks), dim3(kBlock), 0, st, src_addrs,
-                           (uint4*)dst, vpt, shift, (uint32_t)total_vecs);
-    } else {
-        uint64_t blocks = (total + kBlock - 1) / kBlock;
-        if (blocks > (uint64_t)max_blocks) blocks = max_blocks;
-        hipLaunchKernelGGL(zc_gather_tokens1, dim3((uint32_t)blocks), dim3(kBlock), 0, st, src_addrs,
-                           (uint8_t*)dst, token_size, total);
-    }
+    if ((uint64_t)token_size >= (1ull << 30)) return (int)hipErrorInvalidValue;  // 1 GiB per token at most
+    const Shape s = shape_for((uint64_t)num_tokens, (uint64_t)num_tokens * token_size);
+    hipLaunchKernelGGL(zc_gather_tokens, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, src_addrs,
+                       (uint64_t)(uintptr_t)dst, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll);
     return (int)hipGetLastError();
 }
 
 extern "C" int gfd_zero_copy_gather(const gfd_sg_entry* entries, int count, void* stream) {
     if (count < 0 || (count > 0 && !entries)) return (int)hipErrorInvalidValue;
     if (count == 0) return 0;
-    hipStream_t st = (hipStream_t)stream;
-    // One wave per entry batch, about 4 * 2 waves per CU in flight (the same
-    // concurrency as the page-table kernel); at most 64 entries per batch.
-    const int max_blocks = cu_count() * kBlocksPerCU;
-    const int target_waves = max_blocks * (kBlock / 64);
-    int per_wave = (count + target_waves - 1) / target_waves;
-    if (per_wave < 1) per_wave = 1;
-    if (per_wave > 64) per_wave = 64;
-    const int waves = (count + per_wave - 1) / per_wave;
-    int blocks = (waves + 3) / 4;
-    if (blocks > max_blocks) blocks = max_blocks;
-    hipLaunchKernelGGL(zc_gather_sg<4>, dim3(blocks), dim3(kBlock), 0, st, entries, count, per_wave);
+    // Sizes are in the entry table, not known here: shape for 4 KiB entries.
+    const Shape s = shape_for((uint64_t)count, (uint64_t)count * 4096);
+    hipLaunchKernelGGL(zc_gather_sg, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, entries, (uint32_t)count,
+                       s.per_wave, s.unroll);
     return (int)hipGetLastError();
 }
