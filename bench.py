@@ -28,12 +28,12 @@ import gfd_amd  # noqa: E402
 
 PCIE_GEN5_X16_GBPS = 32.0 * 16 * 128.0 / 130.0 / 8.0  # 63.0 GB/s per direction
 
-# Bytes one zc_gather_tokens16 launch moves at 8192 x 4 KiB, from two
+# Bytes one zc_gather_tokens launch moves at 8192 x 4 KiB, from two
 # rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of `bench.py --only zc,calib`,
 # each scaled by the same counter on a 32 MiB device-to-device copy
-# (FETCH x 1.9986, WRITE x 1.0).  Reads are host-link reads through the L2's
+# (FETCH x 1.9985, WRITE x 1.0).  Reads are host-link reads through the L2's
 # external interface; writes land in HBM.
-ZC_TRAFFIC_8192x4KB = {"read_bytes": 33027 * 1024, "write_bytes": 32768 * 1024}
+ZC_TRAFFIC_8192x4KB = {"read_bytes": 32901 * 1024, "write_bytes": 32768 * 1024}
 METRIC = "scattered H2D GB/s + % of PCIe5 x16 peak at 8192x4KB and 2048x64KB"
 PD = ctypes.POINTER(ctypes.c_double)
 
@@ -256,6 +256,52 @@ def run_moe(oracle, iters, warmup, tokens=4096, experts=64, dim=7168):
     return res
 
 
+def run_sessions(oracle, iters, warmup):
+    """Wave-specialised sessions.  WarpSpecSession on linear tiles (token t at
+    cpu_src + t*T -> gpu_dst + t*T; T = 128 tokens, automatic chunking, no-op
+    consumer), single and double buffered: 8192 x 16 KiB = 128 MiB (the shape
+    of the reference's warp-spec example) and 8192 x 4 KiB.  SGWarpSpecSession
+    (no-op consumer) on 16384 scattered 4 KiB tokens (2x stride, Fisher-Yates
+    order) = 64 MiB in 128 host-submitted lists of 128 entries, timed from
+    the launch until the host sees every list's done marker.  Every output is
+    compared with the source bytes."""
+    out = {}
+    for n, t in ((8192, 16384), (8192, 4096)):
+        host = gfd_amd.HostBuffer(n * t)
+        oracle.fill_tokens(host.array, n, t, t)
+        dst = gfd_amd.DeviceBuffer(n * t)
+        for db in (False, True):
+            dst.fill(0)
+            res, kms = gfd_amd.warp_spec_run(host.ptr, dst.ptr, n, t, 128, 0, db, False, 0, iters=warmup + iters)
+            if not (dst.download() == host.array).all():
+                raise SystemExit("PARITY FAILURE: WarpSpecSession %dx%d db=%d" % (n, t, db))
+            us = kms[warmup:] * 1000.0
+            key = "warp_spec_%dx%dKB%s" % (n, t // 1024, "_db" if db else "")
+            out[key] = {"bytes": n * t, "kernel_us_p50": round(p50(us), 2), "GBps": round(gbps(n * t, p50(us)), 3),
+                        "grid": res["grid"], "block": res["block"], "tokens_per_chunk": res["tokens_per_chunk"],
+                        "chunks_per_tile": res["chunks_per_tile"]}
+            log("  %s: %s" % (key, out[key]))
+        del host, dst
+    n, t, epl = 16384, 4096, 128
+    host = gfd_amd.HostBuffer(n * 2 * t)
+    oracle.fill_tokens(host.array, n, t, 2 * t)
+    perm = oracle.permutation(n)
+    dst = gfd_amd.DeviceBuffer(n * t)
+    dst.fill(0)
+    ent = gfd_amd.device_sg_entries(host.ptr + perm.astype(np.uint64) * np.uint64(2 * t),
+                                    dst.ptr + np.arange(n, dtype=np.uint64) * np.uint64(t), t)
+    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=0, idle_limit_ms=10000)
+    us = sess.bench(ent, epl, warmup=warmup, iters=iters)
+    st = sess.stats()
+    sess.close()
+    if not (dst.download() == oracle.expected_gather(host.array, perm, t, 2 * t)).all():
+        raise SystemExit("PARITY FAILURE: SGWarpSpecSession 16384x4KB")
+    out["sg_16384x4KB_lists128"] = {"bytes": n * t, "us_p50": round(p50(us), 2), "GBps": round(gbps(n * t, p50(us)), 3),
+                                    "grid": st["grid"], "entries_per_list": epl}
+    log("  sg_16384x4KB_lists128: %s" % out["sg_16384x4KB_lists128"])
+    return out
+
+
 class QueueRig:
     def __init__(self, region_bytes):
         self.q = gfd_amd.DescriptorQueue()
@@ -285,7 +331,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=15)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="",
-                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe (calib: add a 32 MiB D2D copy)")
+                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions "
+                         "(calib: add a 32 MiB D2D copy)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this path has no multi-GPU step (each GPU gathers over its own "
@@ -356,6 +403,11 @@ def main():
         del L
     direct.close()
 
+    r_sessions = None
+    if want("sessions"):
+        log("wave-specialised sessions ...")
+        r_sessions = run_sessions(oracle, K, W)
+
     r_moe = None
     if want("moe"):
         log("SG-MoE 4096 x 7168 bf16, top-2 of 64 ...")
@@ -385,7 +437,7 @@ def main():
     roofline = None
     if zc:
         ach = zc["kernel_GBps"]
-        roofline = {"bound": "pcie", "kernel": "zc_gather_tokens16", "achieved": ach,
+        roofline = {"bound": "pcie", "kernel": "zc_gather_tokens", "achieved": ach,
                     "peak": round(PCIE_GEN5_X16_GBPS, 2), "unit": "GB/s",
                     "frac": round(ach / PCIE_GEN5_X16_GBPS, 4),
                     "traffic": ZC_TRAFFIC_8192x4KB["read_bytes"] + ZC_TRAFFIC_8192x4KB["write_bytes"],
@@ -413,6 +465,7 @@ def main():
         "pcie_peak": {"theoretical_GBps": round(PCIE_GEN5_X16_GBPS, 2), "measured_contiguous_GBps": peak},
         "roofline": roofline, "cpu_baseline": cpu,
         "results_8192x4KB": r_main, "results_2048x64KB": r_kv, "results_small": r_small, "results_sg_moe": r_moe,
+        "results_sessions": r_sessions,
         "direct_setup": {k: dinfo[k] for k in ("numa_node", "num_gather_workers", "worker_cpus", "poller_cpu",
                                                "num_ce_channels", "direct_chunk_bytes", "gather_slice_bytes")},
         "host": info,

@@ -151,9 +151,9 @@ int gfd_moe_route(const float* logits, int num_tokens, int num_experts, int* top
  * pinned host memory) -> dst + r*row_bytes (HBM).  out != NULL: producer waves
  * fetch into an LDS ring and consumer waves write the bf16 RMSNorm
  * x / sqrt(mean(x^2) + eps) * weight to out + r*row_bytes; out == NULL: pure
- * transfer.  row_bytes a multiple of 1024, at most 14336.  *error_flag
- * (device int, zeroed by the caller) receives nonzero bits on a bad token id
- * or a stalled hand-off. */
+ * transfer.  row_bytes a multiple of 1024, at most 14336.  num_blocks 0 =
+ * min(CU count, 64) workgroups.  *error_flag (device int, zeroed by the
+ * caller) receives nonzero bits on a bad token id or a stalled hand-off. */
 int gfd_sg_gather_rmsnorm(const void* host_base, uint64_t token_stride, int num_tokens,
                           const int* row_token, int num_rows, uint32_t row_bytes, void* dst, void* out,
                           const uint16_t* weight, float eps, int num_blocks, int* error_flag, void* stream);
