@@ -179,6 +179,69 @@ def run_direct(poller, L, iters, warmup):
     return {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3)}
 
 
+def _busy_union(iv):
+    """Total length of the union of [start, end) intervals."""
+    tot, cur_s, cur_e = 0, None, None
+    for a, b in sorted(iv):
+        if cur_e is None or a > cur_e:
+            if cur_e is not None:
+                tot += cur_e - cur_s
+            cur_s, cur_e = a, b
+        else:
+            cur_e = max(cur_e, b)
+    if cur_e is not None:
+        tot += cur_e - cur_s
+    return tot
+
+
+def sdma_occupancy(copies, t0, t1):
+    """SDMA engine activity inside the window [t0, t1] (ns, HSA system clock):
+    fraction of the window with any engine busy, each engine's busy fraction,
+    the host-link rate while busy, the wait before the first copy starts and
+    the tail after the last copy ends."""
+    c = copies[(copies["start_ns"] >= t0) & (copies["end_ns"] <= t1)]
+    win = max(1, t1 - t0)
+    if len(c) == 0:
+        return None
+    iv = [(int(a), int(b)) for a, b in zip(c["start_ns"], c["end_ns"])]
+    busy = _busy_union(iv)
+    per_engine = {}
+    for e in np.unique(c["engine"]):
+        m = c["engine"] == e
+        per_engine["0x%x" % int(e)] = round(_busy_union([(int(a), int(b)) for a, b in
+                                                         zip(c["start_ns"][m], c["end_ns"][m])]) / win, 4)
+    return {"copies": int(len(c)), "window_us": round(win / 1e3, 2), "busy_frac_any": round(busy / win, 4),
+            "busy_frac_per_engine": per_engine, "link_GBps_while_busy": round(int(c["bytes"].sum()) / busy, 3),
+            "first_copy_start_us": round((int(c["start_ns"].min()) - t0) / 1e3, 2),
+            "tail_after_last_copy_us": round((t1 - int(c["end_ns"].max())) / 1e3, 2)}
+
+
+def direct_timeline(poller, L, calls=20):
+    """SDMA timeline of `calls` submit_direct calls (after the timed loop):
+    median of each per-call figure of sdma_occupancy()."""
+    poller.set_copy_timing(True)
+    windows = []
+    for _ in range(calls):
+        t0 = poller.copy_clock_ns()
+        us = poller.submit_direct(L.entries, L.n)
+        t1 = poller.copy_clock_ns()
+        assert us > 0
+        windows.append((t0, t1))
+    copies = poller.read_copy_times()
+    poller.set_copy_timing(False)
+    L.verify("direct (timed copies)")
+    per = [o for o in (sdma_occupancy(copies[copies["path"] == 1], a, b) for a, b in windows) if o]
+    if not per:
+        return None
+    med = lambda k: round(float(np.median([o[k] for o in per])), 4)
+    engines = sorted(set(k for o in per for k in o["busy_frac_per_engine"]))
+    return {"calls": len(per), "copies_per_call": med("copies"), "window_us": med("window_us"),
+            "busy_frac_any": med("busy_frac_any"), "link_GBps_while_busy": med("link_GBps_while_busy"),
+            "first_copy_start_us": med("first_copy_start_us"), "tail_after_last_copy_us": med("tail_after_last_copy_us"),
+            "busy_frac_per_engine": {e: round(float(np.median([o["busy_frac_per_engine"].get(e, 0.0) for o in per])), 4)
+                                     for e in engines}}
+
+
 def run_memcpy_n(L, iters, warmup):
     t = np.zeros(iters)
     rc = gfd_amd.lib().gfd_bench_memcpy_per_token(L.dst.ptr, L.src_addrs.ctypes.data, L.n, L.t, warmup, iters,
@@ -316,7 +379,23 @@ class QueueRig:
                                            warmup, iters, 10_000_000, t.ctypes.data_as(PD))
         assert rc == 0, gfd_amd.lib().gfd_last_error()
         L.verify("queue")
-        return {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3)}
+        out = {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3),
+               "descriptors_per_s": round(L.n / (p50(t) * 1e-6))}
+        # SDMA timeline over a few more rounds (after the timed loop).
+        self.p.set_copy_timing(True)
+        t2 = np.zeros(5)
+        t0 = self.p.copy_clock_ns()
+        rc = gfd_amd.lib().gfd_bench_queue(self.q.ptr, L.tokens.ptr, L.dst.ptr, L.n, L.t, ctypes.byref(self.base),
+                                           0, 5, 10_000_000, t2.ctypes.data_as(PD))
+        t1 = self.p.copy_clock_ns()
+        copies = self.p.read_copy_times()
+        self.p.set_copy_timing(False)
+        assert rc == 0, gfd_amd.lib().gfd_last_error()
+        occ = sdma_occupancy(copies[copies["path"] == 0], t0, t1)
+        if occ:
+            occ["rounds"] = 5
+        out["sdma"] = occ
+        return out
 
     def close(self):
         self.p.stop()
@@ -397,6 +476,8 @@ def main():
         if want("direct"):
             r["direct"] = run_direct(direct, L, K, W)
             log("  %dx%d direct: %s" % (n, t, r["direct"]))
+            r["direct"]["sdma"] = direct_timeline(direct, L)
+            log("  %dx%d direct SDMA timeline: %s" % (n, t, r["direct"]["sdma"]))
         if want("memcpy"):
             r["memcpy_per_token"] = run_memcpy_n(L, max(5, K // 5), 2)
             log("  %dx%d memcpy(N): %s" % (n, t, r["memcpy_per_token"]))

@@ -88,6 +88,9 @@ MAX_SG_POOL_ENTRIES = 16384
 SG_FLAG_NONE, SG_FLAG_HOST_SUBMITTED = 0, 1
 
 
+COPY_TIME_DTYPE = np.dtype([("seq", np.uint64), ("bytes", np.uint64), ("start_ns", np.uint64), ("end_ns", np.uint64),
+                            ("channel", np.uint32), ("engine", np.uint32), ("path", np.uint32), ("_pad", np.uint32)])
+
 TRACE_DTYPE = np.dtype([("t_ns", np.uint64), ("kind", np.uint32), ("a", np.uint32), ("b", np.uint64)])
 TRACE_KINDS = {1: "batch_first", 2: "flush", 3: "issued", 4: "done", 5: "gap_flush", 6: "direct_begin",
                7: "chunk", 8: "direct_end", 9: "gather_entry", 10: "gather_idle", 11: "gather_published",
@@ -138,6 +141,9 @@ def _declare(L):
         "gfd_poller_get_info": ([vp, ctypes.POINTER(PollerInfo)], c_int),
         "gfd_poller_set_trace": ([vp, c_int], None),
         "gfd_poller_read_trace": ([vp, vp, c_int], c_int),
+        "gfd_poller_set_copy_timing": ([vp, c_int], None),
+        "gfd_poller_read_copy_times": ([vp, vp, c_int], c_int),
+        "gfd_poller_copy_clock_ns": ([vp], c_u64),
         "gfd_poller_set_direct_chunk_bytes": ([vp, c_u64], None),
         "gfd_poller_set_gather_slice_bytes": ([vp, c_u64], None),
         "gfd_host_gather": ([vp, c_int, vp, c_u64, c_u64, c_int, vp], c_int),
@@ -355,6 +361,19 @@ class CpuPollingThread:
         buf = np.zeros(max_events, dtype=TRACE_DTYPE)
         n = lib().gfd_poller_read_trace(self._h, buf.ctypes.data, max_events)
         return buf[:n]
+
+    def set_copy_timing(self, on=True):
+        """Record engine start/end timestamps of every SDMA copy."""
+        lib().gfd_poller_set_copy_timing(self._h, int(bool(on)))
+
+    def read_copy_times(self, max_copies=65536):
+        """Drain the copy timeline: structured array (seq, bytes, start_ns, end_ns, channel, engine, path)."""
+        buf = np.zeros(max_copies, dtype=COPY_TIME_DTYPE)
+        n = lib().gfd_poller_read_copy_times(self._h, buf.ctypes.data, max_copies)
+        return buf[:n]
+
+    def copy_clock_ns(self):
+        return int(lib().gfd_poller_copy_clock_ns(self._h))
 
     def set_direct_chunk_bytes(self, b):
         lib().gfd_poller_set_direct_chunk_bytes(self._h, b)

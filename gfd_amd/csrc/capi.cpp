@@ -188,6 +188,18 @@ int gfd_poller_read_trace(gfd_poller_t p, gfd_trace_event* out, int max) {
     return P(p)->read_trace(reinterpret_cast<gfd::CpuPollingThread::TraceEvent*>(out), max);
 }
 
+void gfd_poller_set_copy_timing(gfd_poller_t p, int on) {
+    if (p) P(p)->set_copy_timing(on != 0);
+}
+
+int gfd_poller_read_copy_times(gfd_poller_t p, gfd_copy_time* out, int max) {
+    static_assert(sizeof(gfd_copy_time) == sizeof(gfd::CpuPollingThread::CopyTiming), "copy time layout");
+    if (!p || !out || max <= 0) return 0;
+    return P(p)->read_copy_times(reinterpret_cast<gfd::CpuPollingThread::CopyTiming*>(out), max);
+}
+
+uint64_t gfd_poller_copy_clock_ns(gfd_poller_t p) { return p ? P(p)->copy_clock_ns() : 0; }
+
 void gfd_poller_set_direct_chunk_bytes(gfd_poller_t p, uint64_t b) {
     if (p) P(p)->set_direct_chunk_bytes(b);
 }

@@ -71,6 +71,18 @@ void CopyEngineManager::shutdown() {
 }
 
 int CopyEngineManager::num_sdma_engines() const { return sdma_ ? sdma_->num_engines() : 0; }
+
+static_assert(sizeof(CopyEngineManager::CopyTime) == sizeof(SdmaQueue::CopyTime), "copy time layout");
+
+void CopyEngineManager::set_copy_timing(bool on) {
+    if (sdma_) sdma_->set_timing(on);
+}
+
+size_t CopyEngineManager::read_copy_times(CopyTime* out, size_t max) {
+    return sdma_ ? sdma_->read_times(reinterpret_cast<SdmaQueue::CopyTime*>(out), max) : 0;
+}
+
+uint64_t CopyEngineManager::copy_clock_ns() const { return sdma_ ? sdma_->now_ns() : 0; }
 uint32_t CopyEngineManager::sdma_engine_mask() const { return sdma_ ? sdma_->engine_mask() : 0; }
 
 Status CopyEngineManager::pin_context() {

@@ -145,6 +145,35 @@ void CpuPollingThread::set_trace(bool on) {
     trace_on_.store(on, std::memory_order_release);
 }
 
+void CpuPollingThread::set_copy_timing(bool on) {
+    if (ce_manager_.is_initialized()) ce_manager_.set_copy_timing(on);
+    if (direct_ce_manager_.is_initialized()) direct_ce_manager_.set_copy_timing(on);
+}
+
+int CpuPollingThread::read_copy_times(CopyTiming* out, int max) {
+    int n = 0;
+    CopyEngineManager* mgrs[2] = {&ce_manager_, &direct_ce_manager_};
+    for (uint32_t path = 0; path < 2 && n < max; path++) {
+        if (!mgrs[path]->is_initialized()) continue;
+        CopyEngineManager::CopyTime buf[256];
+        for (;;) {
+            const size_t want = std::min<size_t>(256, (size_t)(max - n));
+            if (want == 0) break;
+            const size_t got = mgrs[path]->read_copy_times(buf, want);
+            for (size_t i = 0; i < got; i++)
+                out[n++] = CopyTiming{buf[i].seq, buf[i].bytes, buf[i].start_ns, buf[i].end_ns,
+                                      buf[i].channel, buf[i].engine, path, 0};
+            if (got < want) break;
+        }
+    }
+    return n;
+}
+
+uint64_t CpuPollingThread::copy_clock_ns() const {
+    if (direct_ce_manager_.is_initialized()) return direct_ce_manager_.copy_clock_ns();
+    return ce_manager_.copy_clock_ns();
+}
+
 void CpuPollingThread::trace(uint32_t kind, uint32_t a, uint64_t b) {
     if (!trace_on_.load(std::memory_order_relaxed)) return;
     timespec ts;
@@ -202,6 +231,8 @@ bool CpuPollingThread::start_workers() {
     gather_ = new GatherEngine(worker_cpus_);
     if (!slice_bytes_) slice_bytes_ = env_size("GFD_GATHER_SLICE_BYTES", 128 * 1024);
     gather_->set_slice_bytes(slice_bytes_);
+    gather_->set_first_chunk_bytes(env_size("GFD_FIRST_CHUNK_BYTES", 0));
+    gather_->set_chunk_ramp(env_size("GFD_CHUNK_RAMP", 1) != 0);
     GFD_LOG_INFO("gather workers: %d (poller CPU %d, NUMA %d)\n", gather_->num_workers(), poller_cpu_,
                  numa_node_);
     return true;

@@ -223,14 +223,21 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     first_slice_ns_.store(0, std::memory_order_relaxed);
     copiers_.store(0, std::memory_order_relaxed);
 
-    // Chunk edges: a short first chunk gets the first copy going early.
+    // Chunk edges: a short first chunk gets the first copy going early; with
+    // the ramp on, each following chunk doubles until chunk_bytes, so every
+    // chunk is gathered before the copies ahead of it drain and the host
+    // link never waits for the next chunk (the threads gather faster than
+    // the link drains).
     size_t first = first_chunk_bytes_ ? first_chunk_bytes_ : chunk_bytes / 8;
     if (first < 64 * 1024) first = 64 * 1024;
     if (first > chunk_bytes) first = chunk_bytes;
     chunk_end_.clear();
-    for (size_t end = first;; end += chunk_bytes) {
+    size_t size = first;
+    for (size_t end = first;;) {
         chunk_end_.push_back(std::min(end, total));
         if (end >= total) break;
+        size = ramp_ ? std::min(size * 2, chunk_bytes) : chunk_bytes;
+        end += size;
     }
     const int nchunks = (int)chunk_end_.size();
 

@@ -45,6 +45,8 @@ public:
     // Size of the first chunk (0 = chunk_bytes / 8, at least 64 KiB): a short
     // first chunk starts the first copy early.
     void set_first_chunk_bytes(size_t b) { first_chunk_bytes_ = b; }
+    // Chunk sizes double from the first chunk up to chunk_bytes (default on).
+    void set_chunk_ramp(bool on) { ramp_ = on; }
 
     // Wake sleeping workers ahead of a job (they spin again until it comes).
     void prewake();
@@ -112,6 +114,7 @@ private:
 
     size_t slice_bytes_ = 128 * 1024;
     size_t first_chunk_bytes_ = 0;
+    bool ramp_ = true;
     bool caller_copies_ = true;
 };
 

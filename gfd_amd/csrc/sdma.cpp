@@ -123,6 +123,11 @@ int SdmaQueue::init(int device, int channels, int pin_engines) {
         if (st != HSA_STATUS_SUCCESS) return (int)st;
         signals_[i] = h.handle;
     }
+    slot_bytes_.assign(kRing, 0);
+    slot_channel_.assign(kRing, 0);
+    uint64_t freq = 0;
+    if (hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP_FREQUENCY, &freq) == HSA_STATUS_SUCCESS && freq)
+        tick_ns_ = 1e9 / (double)freq;
     next_seq_ = tail_ = 0;
     error_ = 0;
     inited_ = true;
@@ -132,12 +137,48 @@ int SdmaQueue::init(int device, int channels, int pin_engines) {
 
 uint64_t SdmaQueue::retire() {
     while (tail_ < next_seq_) {
-        hsa_signal_value_t v = hsa_signal_load_scacquire(sig(signals_[tail_ % kRing]));
+        const size_t slot = tail_ % kRing;
+        hsa_signal_value_t v = hsa_signal_load_scacquire(sig(signals_[slot]));
         if (v > 0) break;
         if (v < 0) error_ = -1;
+        if (timing_.load(std::memory_order_acquire)) {
+            hsa_amd_profiling_async_copy_time_t t{};
+            if (hsa_amd_profiling_get_async_copy_time(sig(signals_[slot]), &t) == HSA_STATUS_SUCCESS &&
+                t.end >= t.start && t.start != 0) {
+                const uint32_t ch = slot_channel_[slot];
+                CopyTime c{tail_, slot_bytes_[slot], (uint64_t)((double)t.start * tick_ns_),
+                           (uint64_t)((double)t.end * tick_ns_), ch,
+                           pin_ ? engines_[(size_t)ch % engines_.size()] : 0u};
+                std::lock_guard<std::mutex> g(times_mu_);
+                if (times_.size() < (1u << 20)) times_.push_back(c);
+            }
+        }
         tail_++;
     }
     return tail_;
+}
+
+void SdmaQueue::set_timing(bool on) {
+    // Callable from any thread: only the runtime switch and an atomic flag
+    // change.  Copies issued while profiling was off return no timestamps
+    // and are skipped when they retire.
+    if (!inited_ || on == timing_.load(std::memory_order_relaxed)) return;
+    if (hsa_amd_profiling_async_copy_enable(on) == HSA_STATUS_SUCCESS) timing_.store(on, std::memory_order_release);
+}
+
+size_t SdmaQueue::read_times(CopyTime* out, size_t max) {
+    // Only copies already retired by their issuing thread are returned.
+    std::lock_guard<std::mutex> g(times_mu_);
+    const size_t n = times_.size() < max ? times_.size() : max;
+    for (size_t i = 0; i < n; i++) out[i] = times_[i];
+    times_.erase(times_.begin(), times_.begin() + (ptrdiff_t)n);
+    return n;
+}
+
+uint64_t SdmaQueue::now_ns() const {
+    uint64_t ts = 0;
+    hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP, &ts);
+    return (uint64_t)((double)ts * tick_ns_);
 }
 
 int SdmaQueue::wait(uint64_t seq_end) {
@@ -192,6 +233,8 @@ int SdmaQueue::copy(int channel, uint64_t dst, const void* src, size_t bytes, ui
         hsa_signal_store_relaxed(cs, 0);
         return (int)st;
     }
+    slot_bytes_[s % kRing] = bytes;
+    slot_channel_[s % kRing] = (uint32_t)channel;
     next_seq_ = s + 1;
     if (seq) *seq = s;
     return 0;

@@ -15,8 +15,10 @@
 // prefix.  Channels map to SDMA engines reported by
 // hsa_amd_memory_copy_engine_status (channel i -> i-th available engine), or
 // to runtime-chosen engines when engine pinning is off.
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
 #include <vector>
 
 namespace gfd {
@@ -55,6 +57,19 @@ public:
     // Sticky: nonzero once any copy reported failure.
     int error() const { return error_; }
 
+    // Per-copy engine timestamps (hsa_amd_profiling_get_async_copy_time), in
+    // ns of the HSA system clock (now_ns()).  Recorded as copies retire while
+    // timing is on; read_times drains what has been recorded (any thread).
+    // Enabling turns on the runtime's async-copy profiling for the whole
+    // process.
+    struct CopyTime {
+        uint64_t seq, bytes, start_ns, end_ns;
+        uint32_t channel, engine;
+    };
+    void set_timing(bool on);
+    size_t read_times(CopyTime* out, size_t max);
+    uint64_t now_ns() const;
+
     // True if [p, p + n) lies in host memory the runtime has pinned and mapped
     // for the GPU (hipHostMalloc / registered), i.e. a legal SDMA source.
     // Pageable memory is not: the caller must copy it another way.
@@ -77,6 +92,14 @@ private:
     uint64_t tail_ = 0;  // all seq < tail_ complete
     int error_ = 0;
     uintptr_t ok_lo_ = 0, ok_hi_ = 0;  // last pinned range found
+
+    // copy timing
+    std::atomic<bool> timing_{false};
+    double tick_ns_ = 1.0;
+    std::vector<uint64_t> slot_bytes_;
+    std::vector<uint32_t> slot_channel_;
+    std::mutex times_mu_;
+    std::vector<CopyTime> times_;
 };
 
 }  // namespace gfd

@@ -119,6 +119,16 @@ public:
     int num_sdma_engines() const;
     uint32_t sdma_engine_mask() const;
 
+    // Engine timestamps of each copy (SDMA backend only; see SdmaQueue).
+    struct CopyTime {
+        uint64_t seq, bytes, start_ns, end_ns;
+        uint32_t channel, engine;
+    };
+    void set_copy_timing(bool on);
+    size_t read_copy_times(CopyTime* out, size_t max);
+    // Now, on the clock of the copy timestamps (0 without the SDMA backend).
+    uint64_t copy_clock_ns() const;
+
 private:
     Status issue(int ch, DevicePtr dst, const void* src, size_t size);
 

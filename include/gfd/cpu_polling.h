@@ -148,6 +148,16 @@ public:
     void set_trace(bool on);
     // Move up to `max` recorded events (oldest first) into `out`; returns the count.
     int read_trace(TraceEvent* out, int max);
+
+    // SDMA copy timeline: engine start/end of every copy of the Queue path
+    // (path 0) and the Direct path (path 1), on copy_clock_ns()'s clock.
+    struct CopyTiming {
+        uint64_t seq, bytes, start_ns, end_ns;
+        uint32_t channel, engine, path, _pad;
+    };
+    void set_copy_timing(bool on);
+    int read_copy_times(CopyTiming* out, int max);
+    uint64_t copy_clock_ns() const;
     void trace(uint32_t kind, uint32_t a, uint64_t b);
     void trace_at(uint64_t t_ns, uint32_t kind, uint32_t a, uint64_t b);
 

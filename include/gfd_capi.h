@@ -113,6 +113,17 @@ typedef struct gfd_trace_event {
 } gfd_trace_event;
 void gfd_poller_set_trace(gfd_poller_t p, int on);
 int gfd_poller_read_trace(gfd_poller_t p, gfd_trace_event* out, int max);
+/* SDMA copy timeline (no reference counterpart; the reference times only
+ * whole calls): engine start / end of every copy, in ns of the HSA system
+ * clock, path 0 = Queue, 1 = Direct.  Enabling turns on the runtime's
+ * async-copy profiling for the process. */
+typedef struct gfd_copy_time {
+    uint64_t seq, bytes, start_ns, end_ns;
+    uint32_t channel, engine, path, _pad;
+} gfd_copy_time;
+void gfd_poller_set_copy_timing(gfd_poller_t p, int on);
+int gfd_poller_read_copy_times(gfd_poller_t p, gfd_copy_time* out, int max);
+uint64_t gfd_poller_copy_clock_ns(gfd_poller_t p);
 /* Tuning of the pipelined direct path (no reference counterpart). */
 void gfd_poller_set_direct_chunk_bytes(gfd_poller_t p, uint64_t bytes);
 void gfd_poller_set_gather_slice_bytes(gfd_poller_t p, uint64_t bytes);

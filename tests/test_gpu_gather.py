@@ -163,6 +163,31 @@ def test_submit_direct_parity(direct_poller, n, t, chunk):
     direct_poller.set_direct_chunk_bytes(2 << 20)
 
 
+def test_submit_direct_copy_timeline(direct_poller):
+    """The SDMA copy timeline of a Direct call: every copy inside the call's
+    window on the copy clock, bytes summing to the gathered bytes."""
+    log("submit_direct copy timeline")
+    n, t = 8192, 4096
+    L = Layout(n, t)
+    entries = gfd_amd.make_entries(L.src_addrs, L.dst.ptr, t)
+    direct_poller.set_copy_timing(True)
+    try:
+        direct_poller.read_copy_times()  # drop anything recorded before
+        t0 = direct_poller.copy_clock_ns()
+        assert direct_poller.submit_direct(entries, n) > 0
+        t1 = direct_poller.copy_clock_ns()
+        c = direct_poller.read_copy_times()
+    finally:
+        direct_poller.set_copy_timing(False)
+    L.check()
+    c = c[c["path"] == 1]
+    assert len(c) >= 2, "a pipelined 32 MiB gather issues several chunk copies"
+    assert int(c["bytes"].sum()) == n * t
+    assert (c["start_ns"] <= c["end_ns"]).all()
+    assert int(c["start_ns"].min()) >= t0 and int(c["end_ns"].max()) <= t1
+    assert np.all(np.diff(c["seq"].astype(np.int64)) > 0)
+
+
 def test_submit_direct_reference_kat(direct_poller):
     # examples/02_direct_transfer.cu:50-54,117-129: token i = i & 0xFF.
     log("submit_direct KAT")
