@@ -242,6 +242,46 @@ def direct_timeline(poller, L, calls=20):
                                      for e in engines}}
 
 
+def run_direct_scattered(oracle, poller, iters, warmup):
+    """GFD Direct with non-contiguous destinations, 8192 x 4 KiB tokens
+    (scattered sources as in the main layout): 'pages' = a paged KV cache,
+    token j lands in page slot s_j of 16384 (seeded permutation), so every
+    token is its own destination run; 'blocks' = 40 contiguous destination
+    blocks with 12 KiB gaps.  Output checked byte-exact with sentinel gaps."""
+    n, t = 8192, 4096
+    out = {}
+    for name in ("pages", "blocks"):
+        if name == "pages":
+            offs = np.random.default_rng(0x5EED).permutation(2 * n)[:n].astype(np.uint64) * np.uint64(t)
+            region = 2 * n * t
+        else:
+            per = -(-n // 40)
+            offs = np.array([(j // per) * (per * t + 3 * t) + (j % per) * t for j in range(n)], np.uint64)
+            region = 40 * (per * t + 3 * t)
+        L = Layout(oracle, n, t)
+        dst = gfd_amd.DeviceBuffer(region)
+        dst.fill(0xCD)
+        ent = (gfd_amd.SGEntry * n)()
+        a = np.frombuffer(ent, dtype=np.uint64).reshape(n, 3)
+        a[:, 0] = np.uint64(dst.ptr) + offs
+        a[:, 1] = L.src_addrs
+        a[:, 2] = t
+        tt = np.zeros(iters)
+        rc = gfd_amd.lib().gfd_bench_submit_direct(poller._h, ctypes.cast(ent, ctypes.c_void_p), n, warmup, iters,
+                                                   tt.ctypes.data_as(PD))
+        assert rc == 0, gfd_amd.lib().gfd_last_error()
+        expect = np.full(region, 0xCD, np.uint8)
+        toks = L.expected.reshape(n, t)
+        for j in range(n):
+            expect[int(offs[j]):int(offs[j]) + t] = toks[j]
+        if not (dst.download() == expect).all():
+            raise SystemExit("PARITY FAILURE: direct with %s destinations" % name)
+        out[name] = {"us_p50": round(p50(tt), 2), "GBps": round(gbps(n * t, p50(tt)), 3)}
+        log("  8192x4096 direct, scattered destinations (%s): %s" % (name, out[name]))
+        del L, dst
+    return out
+
+
 def run_memcpy_n(L, iters, warmup):
     t = np.zeros(iters)
     rc = gfd_amd.lib().gfd_bench_memcpy_per_token(L.dst.ptr, L.src_addrs.ctypes.data, L.n, L.t, warmup, iters,
@@ -410,7 +450,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=15)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="",
-                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions "
+                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions,scattered "
                          "(calib: add a 32 MiB D2D copy)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -482,6 +522,9 @@ def main():
             r["memcpy_per_token"] = run_memcpy_n(L, max(5, K // 5), 2)
             log("  %dx%d memcpy(N): %s" % (n, t, r["memcpy_per_token"]))
         del L
+    r_scat = None
+    if want("direct") and want("scattered"):
+        r_scat = run_direct_scattered(oracle, direct, K, W)
     direct.close()
 
     r_sessions = None
@@ -547,6 +590,7 @@ def main():
         "roofline": roofline, "cpu_baseline": cpu,
         "results_8192x4KB": r_main, "results_2048x64KB": r_kv, "results_small": r_small, "results_sg_moe": r_moe,
         "results_sessions": r_sessions,
+        "results_direct_scattered_dst_8192x4KB": r_scat,
         "direct_setup": {k: dinfo[k] for k in ("numa_node", "num_gather_workers", "worker_cpus", "poller_cpu",
                                                "num_ce_channels", "direct_chunk_bytes", "gather_slice_bytes")},
         "host": info,

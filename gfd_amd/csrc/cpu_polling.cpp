@@ -33,6 +33,7 @@
 #include <cstdlib>
 #include <vector>
 
+#include "dst_runs.h"
 #include "gather_engine.h"
 #include "gfd/pcie_topology.h"
 #include "gfd/sg_task_queue.h"
@@ -133,6 +134,13 @@ CpuPollingThread::~CpuPollingThread() {
     direct_staging_ = nullptr;
     if (signal_values_) gfd_hip_host_free(signal_values_);
     signal_values_ = nullptr;
+    if (zc_stream_) {
+        gfd_hip_stream_synchronize(zc_stream_);
+        gfd_hip_stream_destroy(zc_stream_);
+        zc_stream_ = nullptr;
+    }
+    if (zc_table_) gfd_hip_host_free(zc_table_);
+    zc_table_ = nullptr;
     ce_manager_.shutdown();
     direct_ce_manager_.shutdown();
 }
@@ -481,17 +489,23 @@ void CpuPollingThread::copy_runs(const SGEntry* e, int count) {
 
 // Gather a dst-contiguous list through the next staging buffer; false if it
 // does not fit (the caller then copies runs directly).
-bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_t total) {
+bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_t total, const DstRun* runs,
+                                              int nruns) {
     if (num_staging_bufs_ == 0 || total > staging_buffer_size_ || !gather_) return false;
     const int cur = staging_cur_;
     const uint64_t t0 = now_us();
     if (ce_manager_.wait_fence(staging_fence_[cur]) != 0) GFD_LOG_ERROR("staging copy reported an error\n");
     const uint64_t t1 = now_us();
     ChunkCtx ctx{this, &ce_manager_, e[0].dst, staging_bufs_[cur], ce_manager_.num_channels(), 0};
+    RunCopyCtx rctx{this, &ce_manager_, staging_bufs_[cur], runs, nruns, 0, ce_manager_.num_channels(), 0, 0};
     {
         std::lock_guard<std::mutex> lock(gather_mutex_);
-        gather_->run(e, count, total, staging_bufs_[cur], direct_chunk_bytes_, issue_chunk, &ctx);
+        if (runs)
+            gather_->run(e, count, total, staging_bufs_[cur], direct_chunk_bytes_, run_copy_chunk, &rctx);
+        else
+            gather_->run(e, count, total, staging_bufs_[cur], direct_chunk_bytes_, issue_chunk, &ctx);
     }
+    if (rctx.err && !ctx.err) ctx.err = rctx.err;
     const uint64_t t2 = now_us();
     staging_fence_[cur] = ce_manager_.fence();
     staging_cur_ = (cur + 1) % num_staging_bufs_;
@@ -504,7 +518,10 @@ bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_
 }
 
 // Route one list: contiguous on both sides -> one copy; dst contiguous ->
-// staged gather; otherwise coalesced runs.
+// staged gather; up to kMaxRunCopies destination runs -> staged gather with
+// one copy per run piece; otherwise one copy per run contiguous on both
+// sides.  (No kernel is launched here: Queue-path consumers spin on the GPU,
+// and a kernel could queue behind them on a shared hardware queue.)
 void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total) {
     const uint64_t t0 = now_us();
     bool dst_contig = true, src_contig = true;
@@ -516,8 +533,12 @@ void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total) {
         SGEntry one{e[0].dst, e[0].src, total};
         ce_manager_.submit_scatter_gather(&one, 1);
         coalesced_entries_.fetch_add(1, std::memory_order_relaxed);
-    } else if (!(dst_contig && gather_through_staging(e, count, total))) {
-        copy_runs(e, count);
+    } else if (dst_contig) {
+        if (!gather_through_staging(e, count, total)) copy_runs(e, count);
+    } else {
+        const int nr = dst_runs(e, count, kMaxRunCopies, queue_runs_);
+        if (!(nr <= kMaxRunCopies && gather_through_staging(e, count, total, queue_runs_.data(), nr)))
+            copy_runs(e, count);
     }
     total_dma_submit_us_.fetch_add(now_us() - t0, std::memory_order_relaxed);
 }

@@ -3,20 +3,23 @@
 // reference: the call blocks until every byte is in HBM and returns the
 // elapsed wall time in microseconds (-1 on error).
 //
-// MI355X design: the destination range is cut into chunks
-// (direct_chunk_bytes, 2 MiB by default).  The gather pool fills the pinned
+// MI355X design: the destination range is cut into chunks (a short first
+// chunk, doubling up to direct_chunk_bytes, 2 MiB by default).  The gather pool fills the pinned
 // direct-staging buffer chunk by chunk, every thread working on the oldest
 // unfinished chunk, and the calling thread starts the SDMA copy of each
 // chunk the moment it is complete, rotating over the copy channels.  Only the
 // first chunk's gather and the last chunk's copy are exposed, instead of one
 // third of the gather as in the reference's fixed 3-chunk pipeline.
+#include <algorithm>
 #include <chrono>
 #include <cstring>
 #include <mutex>
 
+#include "dst_runs.h"
 #include "gather_engine.h"
 #include "gfd/cpu_polling.h"
 #include "gfd/staging_pool.h"
+#include "gfd_capi.h"
 
 namespace gfd {
 
@@ -40,7 +43,84 @@ void direct_chunk(void* p, int chunk, size_t off, size_t len) {
 
 constexpr size_t kContiguousSplitMin = 8u << 20;  // split one contiguous copy above this
 
+void no_chunk(void*, int, size_t, size_t) {}
+
 }  // namespace
+
+void run_copy_chunk(void* p, int chunk, size_t off, size_t len) {
+    RunCopyCtx* c = (RunCopyCtx*)p;
+    const size_t end = off + len;
+    while (c->cursor < c->nruns) {
+        const DstRun& r = c->runs[c->cursor];
+        const size_t a = std::max(off, r.off), b = std::min(end, r.off + r.size);
+        if (b > a) {
+            const int e = c->ce->submit_on_channel(c->next_channel, r.dst + (a - r.off), c->staging + a, b - a);
+            c->next_channel = (c->next_channel + 1) % c->channels;
+            if (e && !c->err) c->err = e;
+        }
+        if (r.off + r.size <= end) c->cursor++;
+        else break;
+    }
+    c->self->trace(CpuPollingThread::TRACE_CHUNK, (uint32_t)chunk, len);
+}
+
+// Destinations scattered over more runs than are worth one SDMA copy each
+// (paged KV caches): the zero-copy kernel writes every entry straight to its
+// destination.  Sources that are pinned host memory are read in place;
+// otherwise the gather pool first packs them into the (pinned) direct staging
+// and the kernel reads from there.  The entry table goes to pinned memory the
+// kernel reads.  Returns 0 or an error code.
+int CpuPollingThread::direct_scattered(const SGEntry* entries, int count, size_t total, bool uniform) {
+    if (zc_table_cap_ < count) {
+        if (zc_table_) gfd_hip_host_free(zc_table_);
+        zc_table_ = nullptr;
+        zc_table_cap_ = 0;
+        const int cap = std::max(count, 4096);
+        void* t = nullptr;
+        if (gfd_hip_host_alloc(&t, (size_t)cap * sizeof(SGEntry), GFD_HOST_DEFAULT) != 0) return -1;
+        zc_table_ = static_cast<SGEntry*>(t);
+        zc_table_cap_ = cap;
+    }
+    // Every destination must lie inside one device allocation (the kernel
+    // writes them directly); ranges are looked up once per allocation.
+    uint64_t dlo = 0, dhi = 0;
+    bool pinned = true, any = false;
+    for (int i = 0; i < count; i++) {
+        if (entries[i].size == 0) continue;
+        any = true;
+        const uint64_t a = entries[i].dst, b = a + entries[i].size;
+        if (a < dlo || b > dhi) {
+            uint64_t base = 0, size = 0;
+            if (!gfd_hip_device_range(a, &base, &size) || b > base + size) {
+                GFD_LOG_ERROR("submit_direct: destination %d is not inside a device allocation\n", i);
+                return -1;
+            }
+            dlo = base;
+            dhi = base + size;
+        }
+        if (pinned && !direct_ce_manager_.host_source_ok(entries[i].src, entries[i].size)) pinned = false;
+    }
+    if (!any) return 0;  // nothing to move
+    if (pinned) {
+        std::memcpy(zc_table_, entries, (size_t)count * sizeof(SGEntry));
+    } else {
+        if (!direct_staging_ || total > direct_staging_size_ || !gather_) return -1;
+        {
+            std::lock_guard<std::mutex> lock(gather_mutex_);
+            gather_->run(entries, count, total, direct_staging_, direct_chunk_bytes_, no_chunk, nullptr,
+                         uniform ? 1 : 0);
+        }
+        size_t off = 0;
+        for (int i = 0; i < count; i++) {
+            zc_table_[i] = SGEntry{entries[i].dst, direct_staging_ + off, entries[i].size};
+            off += entries[i].size;
+        }
+    }
+    if (!zc_stream_ && gfd_hip_stream_create(&zc_stream_) != 0) return -1;
+    int rc = gfd_zero_copy_gather(reinterpret_cast<const gfd_sg_entry*>(zc_table_), count, zc_stream_);
+    if (rc == 0) rc = gfd_hip_stream_synchronize(zc_stream_);
+    return rc;
+}
 
 bool CpuPollingThread::init_direct_ce() {
     if (!use_ce_) return false;
@@ -112,6 +192,21 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
                 off += entries[i].size;
             }
             err = direct_ce_manager_.submit_on_channel(0, entries[0].dst, direct_staging_, total);
+        }
+    } else if (!dst_contig && gather_) {
+        // Destinations in several runs: a packed gather with one copy per run
+        // piece, or the zero-copy kernel when there are many runs.
+        const int nr = dst_runs(entries, count, kMaxRunCopies, direct_runs_);
+        if (nr <= kMaxRunCopies && direct_staging_ && total <= direct_staging_size_) {
+            std::lock_guard<std::mutex> lock(gather_mutex_);
+            RunCopyCtx ctx{this, &direct_ce_manager_, direct_staging_, direct_runs_.data(), nr, 0, nch, 0, 0};
+            gather_->run(entries, count, total, direct_staging_, direct_chunk_bytes_, run_copy_chunk, &ctx,
+                         uniform ? 1 : 0);
+            err = ctx.err;
+        } else if (nr > kMaxRunCopies) {
+            err = direct_scattered(entries, count, total, uniform);
+        } else {
+            err = direct_ce_manager_.submit_scatter_gather(entries, count);
         }
     } else {
         err = direct_ce_manager_.submit_scatter_gather(entries, count);

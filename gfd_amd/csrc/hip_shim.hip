@@ -123,3 +123,21 @@ extern "C" int gfd_hip_pointer_is_device(const void* p) {
     }
     return a.type == hipMemoryTypeDevice ? 1 : 0;
 }
+
+extern "C" int gfd_hip_device_range(uint64_t ptr, uint64_t* base, uint64_t* size) {
+    hipPointerAttribute_t a;
+    if (!ptr || hipPointerGetAttributes(&a, (const void*)(uintptr_t)ptr) != hipSuccess ||
+        a.type != hipMemoryTypeDevice) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    hipDeviceptr_t b = nullptr;
+    size_t n = 0;
+    if (hipMemGetAddressRange(&b, &n, (hipDeviceptr_t)(uintptr_t)ptr) != hipSuccess || !b) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    *base = (uint64_t)(uintptr_t)b;
+    *size = (uint64_t)n;
+    return 1;
+}

@@ -52,6 +52,14 @@ struct SGEntry {
 };
 static_assert(sizeof(SGEntry) == 24, "SGEntry must be 24 bytes");
 
+// One destination-contiguous run of a list packed into staging:
+// staging [off, off + size) lands at dst.
+struct DstRun {
+    DevicePtr dst;
+    size_t off;
+    size_t size;
+};
+
 class SdmaQueue;
 
 class CopyEngineManager {
@@ -118,6 +126,8 @@ public:
     Backend backend() const { return backend_; }
     int num_sdma_engines() const;
     uint32_t sdma_engine_mask() const;
+    // True if [p, p + n) is pinned host memory the GPU can read (SDMA backend).
+    bool host_source_ok(const void* p, size_t n);
 
     // Engine timestamps of each copy (SDMA backend only; see SdmaQueue).
     struct CopyTime {

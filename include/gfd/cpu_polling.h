@@ -184,7 +184,10 @@ private:
     void process_batch_tiled(Descriptor* batch, int count, uint64_t cur_read);
     void process_batch_sg(Descriptor* batch, int count, uint64_t cur_read);
     void submit_list(const SGEntry* e, int count, size_t total);
-    bool gather_through_staging(const SGEntry* e, int count, size_t total);
+    // runs == nullptr: destinations contiguous; else nruns destination runs.
+    bool gather_through_staging(const SGEntry* e, int count, size_t total, const DstRun* runs = nullptr,
+                                int nruns = 0);
+    int direct_scattered(const SGEntry* entries, int count, size_t total, bool uniform);
     void copy_runs(const SGEntry* e, int count);
     void signal_device_u64(uint64_t* dst, uint64_t value, uint64_t after_begin);
     void publish_done(uint64_t value);
@@ -245,6 +248,13 @@ private:
     CompletionSlot pending_;
     std::vector<SGEntry> sg_scratch_;
     std::vector<SGEntry> run_scratch_;
+    std::vector<DstRun> queue_runs_;   // destination runs of a Queue-path list
+    std::vector<DstRun> direct_runs_;  // destination runs of a Direct-path list
+    // Direct path, lists scattered over many destination runs: the entry table
+    // in pinned memory for the zero-copy kernel, and its stream.
+    SGEntry* zc_table_ = nullptr;
+    int zc_table_cap_ = 0;
+    gfd_stream_t zc_stream_ = nullptr;
     std::vector<uint32_t> tile_scratch_;
     size_t slice_bytes_ = 0;
 

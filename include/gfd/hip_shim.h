@@ -64,4 +64,6 @@ int gfd_hip_stream_write_u64(gfd_stream_t s, uint64_t dst, uint64_t value);
 extern "C" {
 // 1 if `p` is device (HBM) memory, 0 if host / unknown.
 int gfd_hip_pointer_is_device(const void* p);
+// 1 and the device allocation [*base, *base + *size) holding ptr, or 0.
+int gfd_hip_device_range(uint64_t ptr, uint64_t* base, uint64_t* size);
 }
