@@ -133,6 +133,44 @@ __device__ __forceinline__ void flat_copy(uint32_t total, uint32_t vpe, uint32_t
     }
 }
 
+// flat_copy() staged through LDS: each lane's 16 bytes go host -> LDS with
+// global_load_lds_dwordx4 (no VGPRs held while the loads are in flight), then
+// LDS -> VGPR -> HBM.  `stage` is this wave's LDS area of U * 64 vectors.
+typedef __attribute__((address_space(1))) const void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
+
+template <int U, bool kUniform>
+__device__ __forceinline__ void flat_copy_lds(uint32_t total, uint32_t vpe, uint32_t nb, const BatchLds* lds,
+                                              vec4u* stage) {
+    const uint32_t lane = (uint32_t)lane_id();
+    for (uint32_t base = 0; base < total; base += (uint32_t)kWidth * U) {
+        uint64_t da[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) {
+            const uint32_t v0 = base + (uint32_t)k * kWidth + lane;
+            const uint32_t v = v0 < total ? v0 : total - 1;
+            uint32_t e, o;
+            if (kUniform) {
+                e = v / vpe;
+                o = v - e * vpe;
+            } else {
+                e = 0;
+#pragma unroll
+                for (uint32_t step = kWidth / 2; step > 0; step >>= 1)
+                    if (e + step < nb && lds->start[e + step] <= v) e += step;
+                o = v - lds->start[e];
+            }
+            // lane l's 16 bytes land at stage[k * 64 + l]
+            __builtin_amdgcn_global_load_lds((gptr_t)(uintptr_t)(lds->src[e] + ((uint64_t)o << 4)),
+                                             (lptr_t)(stage + k * kWidth), 16, 0, 0);
+            da[k] = lds->dst[e] + ((uint64_t)o << 4);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // every load has landed in LDS
+#pragma unroll
+        for (int k = 0; k < U; k++) gstore(da[k], stage[k * kWidth + lane]);
+    }
+}
+
 // Copy a batch of nb <= 64 entries, lane j holding entry j's (dst, src, bytes).
 // When every entry is 16-byte aligned on both sides with a size that is a
 // multiple of 16, the batch is copied as one stream of 16-byte vectors across
@@ -140,7 +178,7 @@ __device__ __forceinline__ void flat_copy(uint32_t total, uint32_t vpe, uint32_t
 // size (u = 16, 8 or 4), 4 otherwise.  Other batches go entry by entry.
 // Returns the bytes copied.
 __device__ __forceinline__ uint64_t copy_batch(int u, uint64_t md, uint64_t ms, uint64_t mn, uint32_t nb,
-                                               BatchLds* lds) {
+                                               BatchLds* lds, vec4u* stage = nullptr) {
     const uint32_t lane = (uint32_t)lane_id();
     const bool mine = lane < nb;
     const bool aligned = !mine || (((md | ms | mn) & 15) == 0 && (mn >> 4) < (1ull << 26));
@@ -170,7 +208,13 @@ __device__ __forceinline__ uint64_t copy_batch(int u, uint64_t md, uint64_t ms, 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const uint32_t vpe0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)vecs);
     if (total > 0) {
-        if (__ballot(mine && vecs != vpe0) == 0) {
+        const bool uniform = __ballot(mine && vecs != vpe0) == 0;
+        if (stage) {  // LDS-staged, `u` vectors per lane (the caller sized stage for it)
+            if (!uniform) flat_copy_lds<4, false>(total, 0, nb, lds, stage);
+            else if (u >= 16) flat_copy_lds<16, true>(total, vpe0, nb, lds, stage);
+            else if (u >= 8) flat_copy_lds<8, true>(total, vpe0, nb, lds, stage);
+            else flat_copy_lds<4, true>(total, vpe0, nb, lds, stage);
+        } else if (uniform) {
             if (u >= 16) flat_copy<16, true>(total, vpe0, nb, lds);
             else if (u >= 8) flat_copy<8, true>(total, vpe0, nb, lds);
             else flat_copy<4, true>(total, vpe0, nb, lds);

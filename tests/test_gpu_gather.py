@@ -65,6 +65,32 @@ def test_zero_copy_tokens_parity(n, t):
     L.check()
 
 
+@pytest.mark.parametrize("n,t,waves,unroll", [(8192, 4096, 0, 4), (2048, 65536, 0, 16), (97, 1000, 0, 8),
+                                              (2048, 512, 64, 8), (300, 48, 4, 16)])
+def test_zero_copy_lds_staged_parity(n, t, waves, unroll, monkeypatch):
+    """The LDS-staged form of the zero-copy kernels (global_load_lds_dwordx4
+    into LDS, then LDS -> HBM), selected per call by GFD_ZC_LDS."""
+    log("zero_copy LDS-staged n=%d t=%d waves=%d U=%d" % (n, t, waves, unroll))
+    monkeypatch.setenv("GFD_ZC_LDS", "1")
+    monkeypatch.setenv("GFD_ZC_UNROLL", str(unroll))
+    if waves:
+        monkeypatch.setenv("GFD_ZC_WAVES", str(waves))
+    L = Layout(n, t)
+    table = gfd_amd.DeviceBuffer(n * 8)
+    table.upload(L.src_addrs)
+    gfd_amd.zero_copy_gather_tokens(table.ptr, L.dst.ptr, t, n)
+    gfd_amd.synchronize()
+    L.check()
+    # the generic SG form, same layout
+    L.reset()
+    entries = gfd_amd.make_entries(L.src_addrs, L.dst.ptr, t)
+    dent = gfd_amd.DeviceBuffer(ctypes.sizeof(entries))
+    dent.upload(np.frombuffer(entries, dtype=np.uint8))
+    gfd_amd.zero_copy_gather(dent.ptr, n)
+    gfd_amd.synchronize()
+    L.check()
+
+
 def test_zero_copy_tokens_coherent_source_and_host_table():
     # Fine-grained source and a page table read from pinned host memory.
     log("zero_copy_tokens coherent")
