@@ -227,16 +227,15 @@ int gfd_host_gather(const gfd_sg_entry* entries, int count, void* out, uint64_t 
     }
     if (count == 0) return 0;
     auto* e = reinterpret_cast<const gfd::SGEntry*>(entries);
-    size_t total = 0;
-    for (int i = 0; i < count; i++) {
-        if (i > 0 && e[i].dst != e[i - 1].dst + e[i - 1].size) {
-            g_last_error = "gfd_host_gather: destinations are not contiguous";
-            return -1;
-        }
-        total += e[i].size;
-    }
     std::vector<int> cpus((size_t)num_workers, -1);
     gfd::GatherEngine engine(cpus);
+    // The same list scan as submit_direct (parallel over the workers for long lists).
+    const gfd::GatherEngine::ListScan sc = engine.scan(e, count);
+    if (!sc.dst_contig) {
+        g_last_error = "gfd_host_gather: destinations are not contiguous";
+        return -1;
+    }
+    const size_t total = sc.total;
     if (slice_bytes) engine.set_slice_bytes(slice_bytes);
     OrderCtx ctx{chunk_order, 0};
     engine.run(e, count, total, (char*)out, chunk_bytes, record_chunk, &ctx);

@@ -147,16 +147,32 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
     if (gather_) gather_->prewake();  // workers wake while the list is inspected
     if (direct_ce_manager_.pin_context() != 0) return -1.0;
 
-    size_t total = 0;
-    for (int i = 0; i < count; i++) total += entries[i].size;
+    // Total bytes and the three list properties the route depends on (split
+    // over the gather workers for long lists).
+    size_t total = entries[0].size;
     bool dst_contig = true, src_contig = true, uniform = true;
-    for (int i = 1; i < count; i++) {
-        dst_contig &= entries[i].dst == entries[i - 1].dst + entries[i - 1].size;
-        src_contig &= (const char*)entries[i].src == (const char*)entries[i - 1].src + entries[i - 1].size;
-        uniform &= entries[i].size == entries[0].size;
+    if (gather_) {
+        std::lock_guard<std::mutex> lock(gather_mutex_);
+        const GatherEngine::ListScan sc = gather_->scan(entries, count);
+        total = sc.total;
+        dst_contig = sc.dst_contig;
+        src_contig = sc.src_contig;
+        uniform = sc.uniform;
+    } else {
+        for (int i = 1; i < count; i++) {
+            const SGEntry& p = entries[i - 1];
+            const SGEntry& e = entries[i];
+            total += e.size;
+            dst_contig &= e.dst == p.dst + p.size;
+            src_contig &= (const char*)e.src == (const char*)p.src + p.size;
+            uniform &= e.size == p.size;
+        }
     }
 
-    trace(TRACE_DIRECT_BEGIN, (uint32_t)count, total);
+    // Stamped with the call's entry time (steady_clock is CLOCK_MONOTONIC, the
+    // trace clock), so the scan above shows up in the timeline.
+    trace_at((uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t0.time_since_epoch()).count(),
+             TRACE_DIRECT_BEGIN, (uint32_t)count, total);
     int err = 0;
     const int nch = direct_ce_manager_.num_channels();
     if (dst_contig && src_contig) {

@@ -100,6 +100,41 @@ def test_host_gather_rejects_scattered_destinations():
         gfd_amd.host_gather(entries, 2, np.zeros(64, np.uint8), num_workers=1)
 
 
+@pytest.mark.parametrize("workers", [0, 3, 7])
+def test_host_gather_long_lists_parallel_scan(workers):
+    """Lists of >= 2048 entries are scanned by the workers in 512-entry parts:
+    parity for uniform and ragged sizes, and a destination break at a part
+    boundary, inside a part and at the last pair is always found."""
+    n, t = 5000, 256
+    region, perm, stride = _layout(n, t)
+    base = 1 << 44
+    srcs = region.ctypes.data + perm.astype(np.uint64) * np.uint64(stride)
+    for rep in range(3):  # back-to-back scan + gather jobs on one engine
+        entries = gfd_amd.make_entries(srcs, base, t)
+        out = np.full(n * t + 64, 0x5A, np.uint8)
+        gfd_amd.host_gather(entries, n, out, chunk_bytes=256 << 10, slice_bytes=16 << 10, num_workers=workers)
+        assert (out[:n * t] == oracle.expected_gather(region, perm, t, stride)).all()
+        assert (out[n * t:] == 0x5A).all()
+    for brk in (512, 1024, 777, n - 1):
+        entries = gfd_amd.make_entries(srcs, base, t)
+        entries[brk].dst = entries[brk].dst + 16
+        with pytest.raises(gfd_amd.GfdError):
+            gfd_amd.host_gather(entries, n, np.zeros(n * t + 64, np.uint8), num_workers=workers)
+    # ragged sizes over several parts
+    rng = np.random.default_rng(3)
+    sizes = rng.integers(1, 600, 3000)
+    src = rng.integers(0, 256, int(sizes.sum()), dtype=np.uint8)
+    offs = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.uint64)
+    e = (gfd_amd.SGEntry * len(sizes))()
+    a = np.frombuffer(e, dtype=np.uint64).reshape(-1, 3)
+    a[:, 0] = np.uint64(base) + offs
+    a[:, 1] = np.uint64(src.ctypes.data) + offs
+    a[:, 2] = sizes
+    out = np.zeros(int(sizes.sum()), np.uint8)
+    gfd_amd.host_gather(e, len(sizes), out, chunk_bytes=100000, slice_bytes=8192, num_workers=workers)
+    assert (out == src).all()
+
+
 def test_host_gather_empty_is_noop():
     out = np.full(16, 3, np.uint8)
     gfd_amd.host_gather((gfd_amd.SGEntry * 1)(), 0, out, num_workers=2)
