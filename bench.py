@@ -128,12 +128,43 @@ def cpu_baseline(oracle, seconds, info):
         pool.close()
         os.sched_setaffinity(0, allowed)
     us = p50(times)
-    return {
+    out = {
         "value": round(gbps(n * t, us), 3), "unit": "GB/s", "cores": workers + 1, "kind": "port",
         "sample": "8192 x 4KiB ParallelGather into pinned staging, %d iterations (%.0f s), P50 %.1f us, "
                   "W=%d workers + caller on CPUs %s, AVX-512=%s" % (
                       len(times), seconds, us, workers, cpus, oracle.has_avx512()),
     }
+    # The CPU-only layout: 256 x 4 KiB from a 2 MiB source into 1 MiB of
+    # staging, with W = 15 workers (the reference's setting; it oversubscribes
+    # a host with fewer than 16 CPUs) and with W = 7.
+    c1 = {}
+    n1 = 256
+    src1 = gfd_amd.HostBuffer(n1 * 2 * t)
+    oracle.fill_tokens(src1.array, n1, t, 2 * t)
+    perm1 = oracle.permutation(n1)
+    stg1 = gfd_amd.HostBuffer(n1 * t)
+    ent1 = oracle.make_entries(src1.ptr, 0, perm1, t, 2 * t)
+    expect1 = oracle.expected_gather(src1.array, perm1, t, 2 * t)
+    for w in (15, 7):
+        wcpus = [allowed[i % len(allowed)] for i in range(w + 1)]  # threads share CPUs when W+1 > CPUs
+        pool = oracle.GatherPool(w, wcpus)
+        try:
+            pool.gather(ent1, n1, stg1.array, 0)
+            if not (stg1.array == expect1).all():
+                raise SystemExit("PARITY FAILURE: CPU baseline 256 x 4KiB")
+            tt = []
+            t_end = time.time() + 1.5
+            while time.time() < t_end:
+                tt.extend(pool.time(ent1, n1, stg1.array, 0, 200).tolist())
+        finally:
+            pool.close()
+            os.sched_setaffinity(0, allowed)
+        c1["W%d" % w] = {"us_p50": round(p50(tt), 2), "GBps": round(gbps(n1 * t, p50(tt)), 3),
+                         "threads": w + 1, "cpus": len(set(wcpus)),
+                         "oversubscribed": w + 1 > len(allowed), "iterations": len(tt)}
+    out["c1_256x4KB"] = c1
+    log("  cpu baseline 256 x 4KiB: %s" % c1)
+    return out
 
 
 def bench_peak(nbytes, iters, warmup):

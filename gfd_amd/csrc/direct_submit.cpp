@@ -143,6 +143,7 @@ bool CpuPollingThread::init_direct_ce() {
 
 double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
     if (!direct_ce_manager_.is_initialized() || count <= 0 || !entries) return -1.0;
+    std::lock_guard<std::mutex> direct_lock(direct_mutex_);
     const auto t0 = std::chrono::steady_clock::now();
     if (gather_) gather_->prewake();  // workers wake while the list is inspected
     if (direct_ce_manager_.pin_context() != 0) return -1.0;

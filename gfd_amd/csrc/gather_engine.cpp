@@ -167,7 +167,7 @@ void GatherEngine::worker_main(int w, int cpu) {
 }
 
 void GatherEngine::prewake() {
-    last_prewake_ns_ = mono_ns();
+    last_prewake_ns_.store(mono_ns(), std::memory_order_relaxed);
     if (sleepers_.load(std::memory_order_seq_cst) > 0) futex_wake_all(&epoch_);
 }
 
@@ -248,7 +248,7 @@ GatherEngine::ListScan GatherEngine::scan(const SGEntry* entries, int count) {
     scan_job_ = true;
     open_.store(true, std::memory_order_seq_cst);
     epoch_.fetch_add(1, std::memory_order_seq_cst);
-    if (sleepers_.load(std::memory_order_seq_cst) > 0 && mono_ns() - last_prewake_ns_ > 200000ull)
+    if (sleepers_.load(std::memory_order_seq_cst) > 0 && mono_ns() - last_prewake_ns_.load(std::memory_order_relaxed) > 200000ull)
         futex_wake_all(&epoch_);
     do_scan_parts();
     while (scan_left_.load(std::memory_order_acquire) != 0) cpu_relax();
@@ -396,7 +396,7 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     // Workers are helpers: the caller can finish the job alone.  If they were
     // woken just before (prewake), do not pay for a second wake syscall here;
     // a worker that fell asleep in between simply sits this job out.
-    if (times_.sleepers > 0 && times_.built - last_prewake_ns_ > 200000ull) futex_wake_all(&epoch_);
+    if (times_.sleepers > 0 && times_.built - last_prewake_ns_.load(std::memory_order_relaxed) > 200000ull) futex_wake_all(&epoch_);
     const int ns = num_slices_;
     times_.published = mono_ns();
     bool counted = false;

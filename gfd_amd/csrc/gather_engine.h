@@ -132,7 +132,7 @@ private:
     alignas(64) std::atomic<int> scan_left_{0};
 
     RunTimes times_{};
-    uint64_t last_prewake_ns_ = 0;
+    std::atomic<uint64_t> last_prewake_ns_{0};  // prewake() may run on another thread
     std::atomic<uint64_t> first_slice_ns_{0};
     std::atomic<int> copiers_{0};
 

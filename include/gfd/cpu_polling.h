@@ -261,6 +261,10 @@ private:
     // Gather workers shared by both paths.
     GatherEngine* gather_ = nullptr;
     std::mutex gather_mutex_;
+    // Held for a whole submit_direct call: concurrent Direct calls on one
+    // poller share the direct staging, run table and zero-copy table, so
+    // they run one after the other.
+    std::mutex direct_mutex_;
     std::vector<int> worker_cpus_;
     int poller_cpu_ = -1;
     bool cpus_chosen_ = false;

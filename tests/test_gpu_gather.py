@@ -214,6 +214,30 @@ def test_submit_direct_copy_timeline(direct_poller):
     assert np.all(np.diff(c["seq"].astype(np.int64)) > 0)
 
 
+def test_submit_direct_concurrent_callers(direct_poller):
+    """Two threads calling submit_direct on one poller at once (the reference
+    documents the call as thread-safe): calls are serialized, both land."""
+    import threading
+    log("submit_direct concurrent callers")
+    La, Lb = Layout(4096, 4096), Layout(2048, 2048)
+    ea = gfd_amd.make_entries(La.src_addrs, La.dst.ptr, La.t)
+    eb = gfd_amd.make_entries(Lb.src_addrs, Lb.dst.ptr, Lb.t)
+    results = []
+
+    def worker(entries, n, reps):
+        for _ in range(reps):
+            results.append(direct_poller.submit_direct(entries, n))
+
+    ts = [threading.Thread(target=worker, args=(ea, La.n, 6)), threading.Thread(target=worker, args=(eb, Lb.n, 6))]
+    for th in ts:
+        th.start()
+    for th in ts:
+        th.join(timeout=60)
+    assert len(results) == 12 and all(r > 0 for r in results)
+    La.check()
+    Lb.check()
+
+
 def test_submit_direct_reference_kat(direct_poller):
     # examples/02_direct_transfer.cu:50-54,117-129: token i = i & 0xFF.
     log("submit_direct KAT")
