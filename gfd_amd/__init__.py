@@ -76,7 +76,8 @@ class SessionResult(ctypes.Structure):
 
     _fields_ = [("units_done", ctypes.c_uint64), ("bytes", ctypes.c_uint64), ("lists_done", ctypes.c_uint64),
                 ("error_bits", ctypes.c_uint64), ("elapsed_ms", ctypes.c_double), ("grid", ctypes.c_int),
-                ("block", ctypes.c_int), ("tokens_per_chunk", ctypes.c_int), ("chunks_per_tile", ctypes.c_int)]
+                ("block", ctypes.c_int), ("tokens_per_chunk", ctypes.c_int), ("chunks_per_tile", ctypes.c_int),
+                ("helper_waves", ctypes.c_int)]
 
     def as_dict(self):
         return {k: getattr(self, k) for k, _ in self._fields_}
@@ -164,9 +165,9 @@ def _declare(L):
         "gfd_bench_submit_direct": ([vp, vp, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_zero_copy_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
         "gfd_bench_queue": ([vp, vp, vp, c_int, c_u32, ctypes.POINTER(c_u64), c_int, c_int, c_u64, pd], c_int),
-        "gfd_warp_spec_run": ([vp, vp, c_u32, c_u32, c_u32, c_u32, c_int, c_int, c_int, vp, c_int, pd,
+        "gfd_warp_spec_run": ([vp, vp, c_u32, c_u32, c_u32, c_u32, c_int, c_int, c_int, c_int, vp, c_int, pd,
                                ctypes.POINTER(SessionResult)], c_int),
-        "gfd_sg_session_create": ([c_int, c_int, c_u32, pvp], c_int),
+        "gfd_sg_session_create": ([c_int, c_int, c_u32, c_int, pvp], c_int),
         "gfd_sg_session_destroy": ([vp], None),
         "gfd_sg_session_submit": ([vp, vp, c_u32, c_u32, c_u32], ctypes.c_int64),
         "gfd_sg_session_launch": ([vp, vp, vp], c_int),
@@ -455,16 +456,20 @@ def sg_gather_rmsnorm(host_base, token_stride, num_tokens, d_row_token, num_rows
 
 
 def warp_spec_run(cpu_src, gpu_dst, total_tokens, token_size, tokens_per_tile=128, tokens_per_chunk=0,
-                  double_buffer=False, per_tile_mode=False, num_blocks=0, token_sums=None, iters=1):
+                  double_buffer=False, per_tile_mode=False, num_blocks=0, token_sums=None, iters=1,
+                  helper_waves=-1):
     """WarpSpecSession (reference include/gfd/warp_spec_session.h:14-132) over
     tokens [0, total_tokens): construct, then `iters` times launch +
     synchronize.  token_sums: device float[total_tokens] for the per-token
-    sum consumer, or None for a no-op consumer.  Returns (result dict, kernel
-    times in ms)."""
+    sum consumer, or None for a no-op consumer.  helper_waves: transfer
+    helper waves per workgroup (negative: about 32 transfer waves per launch,
+    at most 3 helpers; fewer if the workgroup would pass 1024 threads).
+    Returns (result dict, kernel times in ms)."""
     res = SessionResult()
     times = np.zeros(max(iters, 1), dtype=np.float64)
     _check(lib().gfd_warp_spec_run(cpu_src, gpu_dst, total_tokens, token_size, tokens_per_tile, tokens_per_chunk,
-                                   int(bool(double_buffer)), int(bool(per_tile_mode)), num_blocks, token_sums, iters,
+                                   int(bool(double_buffer)), int(bool(per_tile_mode)), num_blocks, helper_waves,
+                                   token_sums, iters,
                                    times.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), ctypes.byref(res)),
            "gfd_warp_spec_run")
     return res.as_dict(), times
@@ -485,9 +490,12 @@ class SGWarpSpecSession:
     """gfd::SGWarpSpecSession (reference include/gfd/warp_spec_session.h:142-258,
     src/sg_warp_spec_session.cpp) with the built-in consumers of the C-ABI."""
 
-    def __init__(self, num_compute_warps=1, num_blocks=0, idle_limit_ms=0):
+    def __init__(self, num_compute_warps=1, num_blocks=0, idle_limit_ms=0, helper_waves=-1):
+        """helper_waves: transfer helper waves per workgroup, 0..3 (negative:
+        about 32 transfer waves per launch, at most 3 helpers)."""
         h = ctypes.c_void_p()
-        _check(lib().gfd_sg_session_create(num_compute_warps, num_blocks, idle_limit_ms, ctypes.byref(h)),
+        _check(lib().gfd_sg_session_create(num_compute_warps, num_blocks, idle_limit_ms, helper_waves,
+                                           ctypes.byref(h)),
                "gfd_sg_session_create")
         self._h = h.value
 

@@ -103,14 +103,15 @@ GFD_WARP_SPEC_KERNEL_DB(ws_null_kernel_db, NullChunk)
 GFD_SG_WARP_SPEC_KERNEL(sg_checksum_kernel, ListChecksum)
 GFD_SG_WARP_SPEC_KERNEL(sg_null_kernel, NullList)
 
-// Transfer (wave 0) + compute (wave 1) + submitter (wave 2) per workgroup, as
-// test/test_sg_gpu_submit.cu:20-213: workgroup b submits lists b, b + grid,
-// ... (list i = entries [i*epl, (i+1)*epl) of d_entries), waits for all
-// num_lists to land, then sets terminate.
+// Transfer (wave 0) + compute (wave 1) + submitter (wave 2) + transfer
+// helpers (waves 3..) per workgroup, as test/test_sg_gpu_submit.cu:20-213:
+// workgroup b submits lists b, b + grid, ... (list i = entries
+// [i*epl, (i+1)*epl) of d_entries), waits for all num_lists to land, then
+// sets terminate.
 template <typename F>
-__global__ __launch_bounds__(3 * 64) void sg_gpu_submit_kernel(gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq, F fn,
+__global__ __launch_bounds__(6 * 64) void sg_gpu_submit_kernel(gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq, F fn,
                                      const gfd::DeviceSGEntry* d_entries, uint32_t epl, uint32_t num_lists) {
-    gfd::sg_warp_spec::_sg_transfer_warp_loop(dq, sq, fn);  // waves 0 and 1 run here; wave 2 returns
+    gfd::sg_warp_spec::_sg_transfer_warp_loop(dq, sq, fn);  // waves 0, 1 and 3.. run here; wave 2 returns
     if (gfd::wave::wave_id() != 2) return;
     gfd::SGDeviceCounters* cnt = gfd::sg_device_counters(sq);
     for (uint32_t l = blockIdx.x; l < num_lists; l += gridDim.x) {
@@ -143,6 +144,7 @@ void fill_ws_result(gfd::WarpSpecSession& s, const gfd::WarpSpecConfig& c, gfd_s
     r->block = (int)p.block;
     r->tokens_per_chunk = (int)c.effective_tokens_per_chunk();
     r->chunks_per_tile = (int)c.chunks_per_tile();
+    r->helper_waves = s.config().helper_waves();
 }
 
 gfd::SGWarpSpecSession* S(gfd_sg_session_t s) { return static_cast<gfd::SGWarpSpecSession*>(s); }
@@ -151,7 +153,7 @@ gfd::SGWarpSpecSession* S(gfd_sg_session_t s) { return static_cast<gfd::SGWarpSp
 
 extern "C" int gfd_warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t total_tokens, uint32_t token_size,
                                  uint32_t tokens_per_tile, uint32_t tokens_per_chunk, int double_buffer,
-                                 int per_tile_mode, int num_blocks, float* token_sums, int iters,
+                                 int per_tile_mode, int num_blocks, int helper_waves, float* token_sums, int iters,
                                  double* kernel_ms, gfd_session_result* res) {
     if (!cpu_src || !gpu_dst || total_tokens == 0 || token_size == 0 || iters < 1 || !res)
         return fail(hipErrorInvalidValue, "gfd_warp_spec_run: invalid argument");
@@ -165,6 +167,7 @@ extern "C" int gfd_warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t to
     c.double_buffer = double_buffer != 0;
     c.per_tile_mode = per_tile_mode != 0;
     c.num_blocks = num_blocks;
+    if (helper_waves >= 0) c.transfer_helper_waves = helper_waves;
     if (c.tokens_per_tile == 0 || c.effective_tokens_per_chunk() == 0 ||
         c.tokens_per_tile % c.effective_tokens_per_chunk() != 0 || c.block_size() > 1024 ||
         c.chunks_per_tile() > (uint32_t)gfd::warp_spec::MAX_CHUNKS_PER_TILE)
@@ -211,13 +214,14 @@ extern "C" int gfd_warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t to
     return rc;
 }
 
-extern "C" int gfd_sg_session_create(int num_compute_warps, int num_blocks, uint32_t idle_limit_ms,
+extern "C" int gfd_sg_session_create(int num_compute_warps, int num_blocks, uint32_t idle_limit_ms, int helper_waves,
                                      gfd_sg_session_t* out) {
     if (!out) return fail(hipErrorInvalidValue, "gfd_sg_session_create: out is NULL");
     gfd::SGWarpSpecConfig c;
     c.num_compute_warps = num_compute_warps;
     c.num_blocks = num_blocks;
     c.idle_limit_ms = idle_limit_ms;
+    if (helper_waves >= 0) c.transfer_helper_waves = helper_waves;
     auto* s = new gfd::SGWarpSpecSession(c);
     if (!s->ok()) {
         delete s;
@@ -256,9 +260,10 @@ extern "C" int gfd_sg_session_launch_gpu_submit(gfd_sg_session_t s, const gfd_de
         entries_per_list > (uint32_t)gfd::MAX_SG_POOL_ENTRIES || num_lists > (uint32_t)gfd::MAX_SG_LISTS)
         return fail(hipErrorInvalidValue, "gfd_sg_session_launch_gpu_submit: invalid argument");
     gfd::SGWarpSpecSession* p = S(s);
-    p->before_launch(stream);
+    const int helpers = p->helper_waves();
+    p->before_launch(stream, helpers);
     const auto* ents = reinterpret_cast<const gfd::DeviceSGEntry*>(d_entries);
-    const dim3 grid((unsigned)p->num_blocks()), block(3 * 64);
+    const dim3 grid((unsigned)p->num_blocks()), block((unsigned)(3 + helpers) * 64);
     if (list_sums)
         hipLaunchKernelGGL(sg_gpu_submit_kernel<ListChecksum>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),
                            p->get_sg_queue(), ListChecksum{list_sums}, ents, entries_per_list, num_lists);
@@ -290,6 +295,8 @@ extern "C" int gfd_sg_session_stats(gfd_sg_session_t s, gfd_session_result* r) {
     r->error_bits = S(s)->error_bits();
     r->elapsed_ms = st.elapsed_ms;
     r->grid = S(s)->num_blocks();
+    r->block = S(s)->block_size();
+    r->helper_waves = S(s)->helper_waves();
     return 0;
 }
 

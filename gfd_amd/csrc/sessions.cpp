@@ -64,6 +64,9 @@ WarpSpecSession::WarpSpecSession(const WarpSpecConfig& config) : config_(config)
     num_blocks_ = config_.num_blocks > 0
                       ? config_.num_blocks
                       : std::max(1, std::min(default_num_blocks(), (int)std::max<uint32_t>(1, config_.total_tiles())));
+    if (config_.transfer_helper_waves < 0)
+        config_.transfer_helper_waves =
+            auto_helper_waves(std::min(num_blocks_, (int)std::max<uint32_t>(1, config_.total_tiles())));
 
     void* q = nullptr;
     if (gfd_hip_host_alloc(&q, sizeof(TiledQueue), GFD_HOST_COHERENT) != 0) {
@@ -158,14 +161,20 @@ WarpSpecSession::Stats WarpSpecSession::get_stats() const {
 // ========================================================== SGWarpSpecSession
 
 SGWarpSpecSession::SGWarpSpecSession(const SGWarpSpecConfig& config) : config_(config) {
-    if (config_.block_size() > 256) {  // SG_MAX_BLOCK of sg_warp_spec.h
-        GFD_LOG_ERROR("SGWarpSpecSession: %d compute waves exceed a 256-thread workgroup\n", config_.num_compute_warps);
+    if (config_.transfer_helper_waves > 3) {  // SG_MAX_HELPERS
+        GFD_LOG_ERROR("SGWarpSpecSession: transfer_helper_waves must be 0..3 (got %d)\n", config_.transfer_helper_waves);
+        return;
+    }
+    if (config_.block_size() > 512) {  // SG_MAX_BLOCK of sg_warp_spec.h
+        GFD_LOG_ERROR("SGWarpSpecSession: %d compute + %d helper waves exceed a 512-thread workgroup\n",
+                      config_.num_compute_warps, config_.transfer_helper_waves);
         return;
     }
     // Default grid: 64 workgroups (8 per XCD).  64 transfer waves with 16
     // loads in flight each keep the PCIe link full; more only add idle
     // pollers (measured: 55 GB/s at 32-64 workgroups, 47-53 at 256).
     num_blocks_ = config_.num_blocks > 0 ? config_.num_blocks : std::min(default_num_blocks(), 64);
+    if (config_.transfer_helper_waves < 0) config_.transfer_helper_waves = auto_helper_waves(num_blocks_);
     void* q = nullptr;
     if (gfd_hip_host_alloc(&q, sizeof(SGTaskQueue), GFD_HOST_COHERENT) != 0) {
         GFD_LOG_ERROR("SGWarpSpecSession: SGTaskQueue allocation failed\n");
@@ -262,7 +271,7 @@ uint64_t SGWarpSpecSession::submit_sg_list(const DeviceSGEntry* entries, uint32_
     return idx;
 }
 
-void SGWarpSpecSession::before_launch(gfd_stream_t stream) {
+void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves) {
     if (running_) synchronize();
     if (!ok_) return;
     __atomic_store_n(&sq_->terminate, 0u, __ATOMIC_RELEASE);
@@ -277,6 +286,7 @@ void SGWarpSpecSession::before_launch(gfd_stream_t stream) {
     c.entries_done = consumed_entries_;
     c.list_known = consumed_lists_;
     c.list_base = consumed_lists_;
+    c.helpers = (uint64_t)(helper_waves < 0 ? config_.transfer_helper_waves : helper_waves);
     gfd_hip_memset_d8((uint64_t)(uintptr_t)sq_->d_list_done, 0, MAX_SG_LISTS * sizeof(uint64_t));
     gfd_hip_memcpy_h2d((uint64_t)(uintptr_t)sg_device_counters(sq_), &c, sizeof(c));
     stream_ = stream;

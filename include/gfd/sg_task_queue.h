@@ -82,7 +82,8 @@ struct SGDeviceCounters {
     uint64_t stop;            // set once `terminate` has been seen: waiting waves exit
     uint64_t list_base;       // first ring index of this launch
     uint64_t bytes_done;      // bytes landed during this launch
-    uint64_t _pad[6];
+    uint64_t helpers;         // transfer helper waves per workgroup (waves 2 .. 1 + helpers)
+    uint64_t _pad[5];
 };
 constexpr int SG_DEVICE_COUNTER_WORDS = (int)(sizeof(SGDeviceCounters) / sizeof(uint64_t));
 
@@ -90,6 +91,7 @@ constexpr int SG_DEVICE_COUNTER_WORDS = (int)(sizeof(SGDeviceCounters) / sizeof(
 constexpr uint64_t SG_ERR_SLOT_WAIT = 1;     // transfer wave: the compute wave never freed an LDS slot
 constexpr uint64_t SG_ERR_COMPUTE_WAIT = 2;  // compute wave: the transfer wave never handed a list over
 constexpr uint64_t SG_ERR_RING_WAIT = 4;     // GPU submitter: a ring slot never became free
+constexpr uint64_t SG_ERR_HELPER_WAIT = 8;   // transfer waves: a copy job's hand-off stalled
 static_assert(sizeof(SGDeviceCounters) == 128, "SGDeviceCounters is two cache lines");
 
 GFD_HD inline SGDeviceCounters* sg_device_counters(const SGTaskQueue* sq) {

@@ -5,15 +5,18 @@
 //   struct MyCompute { __device__ void operator()(gfd::sg_warp_spec::SGListView v) { ... } };
 //   GFD_SG_WARP_SPEC_KERNEL(my_kernel, MyCompute);   // (DescriptorQueue*, SGTaskQueue*, MyCompute)
 //
-// Wave 0 of each workgroup is the transfer wave, wave 1 the compute wave;
-// further waves return from the loop right after its opening barrier, so a
-// kernel may call the loop from every wave and give the others work of its
-// own afterwards (a GPU submitter, for instance).
+// Wave 0 of each workgroup is the transfer wave, wave 1 the compute wave,
+// the last SGDeviceCounters::helpers waves (set by the session per launch)
+// transfer helpers; the waves in between return from the loop right after
+// its opening barrier, so a kernel may call the loop from every wave and give
+// the others work of its own afterwards (a GPU submitter, for instance).
 //
 // The transfer wave claims the next ring index (device-scope atomic on an
 // HBM counter), waits for that list to be committed, copies every entry's
-// bytes from pinned host memory into HBM itself (zero-copy, 16-byte loads
-// over PCIe), marks the list done (d_list_done[list_id] in HBM, the header's
+// bytes from pinned host memory into HBM itself together with the helpers
+// (zero-copy, 16-byte loads over PCIe; the waves claim 64-entry batches of
+// the list from an LDS counter, since one wave alone reaches ~3.3 GB/s and a
+// CU ~13 GB/s), marks the list done (d_list_done[list_id] in HBM, the header's
 // `done` word in host memory) and hands it to the compute wave through one of
 // two LDS slots, so the copy of the next list overlaps the compute of this
 // one.  The reference routes each list through descriptors and the CPU poller
@@ -110,28 +113,86 @@ __device__ __forceinline__ bool _wait_committed(SGTaskQueue* sq, SGDeviceCounter
     }
 }
 
+// Transfer helpers: up to this many further waves copy batches of the
+// transfer wave's current list (SGDeviceCounters::helpers, set per launch).
+constexpr int SG_MAX_HELPERS = 3;
+
+// The list the transfer waves copy together.  The leader (wave 0) publishes
+// it, leader and helpers claim its 64-entry batches, every helper
+// acknowledges it (even with nothing left to claim), and only then does the
+// leader publish the next one, so no helper ever reads a job's fields while
+// they change.
+struct _SGJob {
+    uint32_t pool_offset, count;
+    int seq;           // k + 1 once the k-th job is published; -1: no more jobs
+    int next_batch;    // batches claimed
+    int batches_done;  // batches copied
+    int acks;          // helpers finished with this job
+    unsigned long long bytes;
+};
+
+// Claim and copy batches of the current job (pool_offset, count); adds the
+// batches and bytes copied.  The caller passes the job's fields in registers:
+// wave 0 has them from the list header, a helper read them after every
+// lane's acquire of job->seq.  (Lanes 1..63 of wave 0 must not read them back
+// from LDS: lane 0's plain stores there are not ordered before other lanes'
+// loads, and the compiler does schedule such loads ahead of the stores.)
+__device__ __forceinline__ void _sg_copy_batches(_SGJob* job, const SGTaskQueue* sq, uint32_t pool_offset,
+                                                 uint32_t count, int unroll, wave::BatchLds* lds, int* nbatches_done,
+                                                 uint64_t* bytes) {
+    const int lane = wave::lane_id();
+    const int nbatches = (int)((count + wave::kWidth - 1) / wave::kWidth);
+    for (;;) {
+        int b = 0;
+        if (lane == 0) b = __hip_atomic_fetch_add(&job->next_batch, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        b = __builtin_amdgcn_readfirstlane(b);
+        if (b >= nbatches) break;
+        const uint32_t first = (uint32_t)b * wave::kWidth;
+        uint64_t md = 0, ms = 0, mn = 0;
+        if (first + lane < count) {
+            const DeviceSGEntry e = sq->entries[(pool_offset + first + lane) % MAX_SG_POOL_ENTRIES];
+            md = e.dst_addr;
+            ms = e.src_addr;
+            mn = e.size;
+        }
+        const uint32_t nb = count - first < (uint32_t)wave::kWidth ? count - first : (uint32_t)wave::kWidth;
+        *bytes += wave::copy_batch(unroll, md, ms, mn, nb, lds);
+        (*nbatches_done)++;
+    }
+}
+
 template <typename ComputeFn>
 __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTaskQueue* sq, ComputeFn compute_fn) {
     (void)dq;
     __shared__ _SGSlot slots[2];
     __shared__ int terminated;
-    __shared__ wave::BatchLds batch_lds;  // transfer wave's descriptor staging
+    __shared__ _SGJob job;
+    __shared__ wave::BatchLds batch_lds[1 + SG_MAX_HELPERS];  // per transfer wave
     const int w = wave::wave_id();
     const int lane = wave::lane_id();
     if (threadIdx.x < 2) {
         slots[threadIdx.x].seq = 0;
         slots[threadIdx.x].free = 1;
     }
-    if (threadIdx.x == 0) terminated = 0;
+    if (threadIdx.x == 0) {
+        terminated = 0;
+        job.seq = 0;
+    }
     __syncthreads();
 
     SGDeviceCounters* cnt = sg_device_counters(sq);
-    const bool has_compute = blockDim.x > (unsigned)wave::kWidth;
+    const int nwaves = (int)(blockDim.x / wave::kWidth);
+    const bool has_compute = nwaves > 1;
+    // Helpers are the last `helpers` waves of the workgroup (never wave 0 or 1).
+    int helpers = (int)__hip_atomic_load(&cnt->helpers, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (helpers > SG_MAX_HELPERS) helpers = SG_MAX_HELPERS;
+    if (helpers > nwaves - 2) helpers = nwaves > 2 ? nwaves - 2 : 0;
+    const int first_helper = nwaves - helpers;
+    const int unroll = wave::transfer_unroll(gridDim.x * (1u + (unsigned)helpers));
 
     if (w == 0) {
-        // ---------------- transfer wave
+        // ---------------- transfer wave (leader)
         const uint64_t idle_ticks = _idle_limit_ticks(sq);
-        const int unroll = wave::transfer_unroll(gridDim.x);
         for (uint64_t iter = 0;; iter++) {
             const int s = (int)(iter & 1);
             if (has_compute && !wave::wait_lds_eq(&slots[s].free, 1)) {
@@ -146,21 +207,33 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             const uint32_t pool_offset = l.pool_offset, count = l.count, list_id = l.list_id, flags = l.flags;
             if (lane == 0) wave::store_system(&l.sequence, 0);  // claimed
 
-            // Copy the list 64 entries at a time: lane i holds entry b+i's
-            // descriptor; the batch moves as one stream of 16-byte vectors.
-            uint64_t bytes = 0;
-            for (uint32_t b = 0; b < count; b += wave::kWidth) {
-                uint64_t md = 0, ms = 0, mn = 0;
-                if (b + lane < count) {
-                    const DeviceSGEntry e = sq->entries[(pool_offset + b + lane) % MAX_SG_POOL_ENTRIES];
-                    md = e.dst_addr;
-                    ms = e.src_addr;
-                    mn = e.size;
-                }
-                const uint32_t nb = count - b < (uint32_t)wave::kWidth ? count - b : (uint32_t)wave::kWidth;
-                bytes += wave::copy_batch(unroll, md, ms, mn, nb, &batch_lds);
+            // Publish the copy job, copy batches with the helpers, wait for
+            // every batch and every helper's acknowledgement.
+            if (lane == 0) {
+                job.pool_offset = pool_offset;
+                job.count = count;
+                job.next_batch = 0;
+                job.batches_done = 0;
+                job.acks = 0;
+                job.bytes = 0;
+                wave::lds_store(&job.seq, (int)iter + 1);
             }
-            wave::release_agent();  // the list's bytes are visible device-wide
+            int mine = 0;
+            uint64_t bytes = 0;
+            _sg_copy_batches(&job, sq, pool_offset, count, unroll, &batch_lds[0], &mine, &bytes);
+            const int nbatches = (int)((count + wave::kWidth - 1) / wave::kWidth);
+            if (lane == 0) {
+                __hip_atomic_fetch_add(&job.bytes, (unsigned long long)bytes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                wave::lds_add(&job.batches_done, mine);
+            }
+            if (helpers > 0 &&
+                (!wave::wait_lds_eq(&job.batches_done, nbatches) || !wave::wait_lds_eq(&job.acks, helpers))) {
+                if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_HELPER_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            bytes = __hip_atomic_load(&job.bytes, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            wave::acquire_agent();
+            wave::release_agent();  // the list's bytes (all transfer waves') are visible device-wide
             if (lane == 0) {
                 if (list_id < (uint32_t)MAX_SG_LISTS)
                     __hip_atomic_store(&sq->d_list_done[list_id], 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
@@ -178,7 +251,40 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
                 }
             }
         }
-        if (lane == 0) wave::lds_store(&terminated, 1);
+        if (lane == 0) {
+            wave::lds_store(&job.seq, -1);  // helpers exit
+            wave::lds_store(&terminated, 1);
+        }
+    } else if (helpers > 0 && w >= first_helper) {
+        // ---------------- transfer helper: copies batches of the leader's
+        // jobs; bounded like the compute wave.
+        const uint64_t limit = _idle_limit_ticks(sq) + 100000000ull;
+        for (int want = 1;;) {
+            int seq = 0;
+            const uint64_t t0 = wall_clock64();
+            for (;;) {
+                seq = wave::lds_load(&job.seq);
+                if (seq < 0 || seq >= want) break;
+                if (wall_clock64() - t0 > limit) {
+                    if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_HELPER_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    seq = -1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            if (seq < 0) break;
+            int mine = 0;
+            uint64_t bytes = 0;
+            _sg_copy_batches(&job, sq, job.pool_offset, job.count, unroll, &batch_lds[1 + w - first_helper], &mine,
+                             &bytes);
+            wave::release_agent();  // this wave's stores are visible device-wide before it reports
+            if (lane == 0) {
+                __hip_atomic_fetch_add(&job.bytes, (unsigned long long)bytes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                wave::lds_add(&job.batches_done, mine);
+                wave::lds_add(&job.acks, 1);
+            }
+            want = seq + 1;
+        }
     } else if (w == 1) {
         // ---------------- compute wave: bounded by the transfer wave's idle
         // limit (plus 1 s), the longest the transfer wave can stay silent.
@@ -219,16 +325,14 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
     // further waves return to the caller
 }
 
-// Largest workgroup of an SG kernel (1 transfer + up to 3 compute waves).
-// With one wave per SIMD the transfer wave may use up to 512 registers, so
-// its in-flight vectors, their addresses and the entry searches stay in
-// registers.
-constexpr int SG_MAX_BLOCK = 256;
+// Largest workgroup of an SG kernel: 1 transfer + up to 3 compute + up to
+// 3 helper waves fit in 8 waves (two per SIMD, 256 registers each).
+constexpr int SG_MAX_BLOCK = 512;
 
 }  // namespace sg_warp_spec
 }  // namespace gfd
 
-// Kernel generation macro (block = 64 * (1 + compute waves) threads).
+// Kernel generation macro (block = 64 * (1 + compute + helper waves) threads).
 #define GFD_SG_WARP_SPEC_KERNEL(kernel_name, ComputeFnType)                                 \
     __global__ __launch_bounds__(gfd::sg_warp_spec::SG_MAX_BLOCK) void kernel_name(         \
         gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq, ComputeFnType compute_fn) {         \

@@ -33,7 +33,7 @@ struct TiledQueue {
 struct TileDeviceCounters {
     uint64_t next_tile;
     uint64_t tiles_done;
-    uint64_t error;  // nonzero: a bounded wait gave up
+    uint64_t error;  // nonzero: a bounded wait gave up (bit flags)
     uint64_t _pad[5];
 };
 constexpr int TILE_DEVICE_COUNTER_WORDS = (int)(sizeof(TileDeviceCounters) / sizeof(uint64_t));

@@ -8,13 +8,18 @@
 //
 // Work: tile t = tokens [t*T, (t+1)*T) of a linear token range, cut into K
 // chunks of C tokens.  Wave 0 of a workgroup is the transfer wave: it claims
-// tiles (device-scope atomic on an HBM counter), copies each chunk's bytes
-// straight from pinned host memory to HBM (zero-copy) and raises the chunk
-// count in LDS after a device-scope release.  Compute wave k (1..K) waits for
-// chunk k (LDS acquire + s_sleep), then runs the functor on it.  The
+// tiles (device-scope atomic on an HBM counter) and copies the tile's bytes
+// straight from pinned host memory to HBM (zero-copy).  Waves after the
+// compute waves are transfer helpers: wave 0 and the helpers claim pieces of
+// the tile's chunks from an LDS counter, so one workgroup keeps several
+// waves' loads in flight over PCIe (one wave alone reaches ~3.3 GB/s, a CU
+// ~13 GB/s).  After a device-scope release each piece raises its chunk's
+// count in LDS.  Compute wave k (1..K) waits until every piece of chunk k has
+// landed (LDS acquire + s_sleep), then runs the functor on it.  The
 // double-buffer variant keeps two tile slots with K compute waves each, so the
 // transfer of tile n+1 overlaps the compute of tile n.  Blocks are
-// 64 * (1 + K) (single) or 64 * (1 + 2K) (double) threads, at most 1024.
+// 64 * (1 + K + H) (single) or 64 * (1 + 2K + H) (double) threads, at most
+// 1024, H helpers.
 #include "gfd/tiled_queue.h"
 #include "gfd/wave_ops.h"
 
@@ -25,6 +30,7 @@ constexpr int MAX_CHUNKS_PER_TILE = 16;
 constexpr uint32_t TILE_END = 0xFFFFFFFFu;
 constexpr uint64_t WS_ERR_SLOT_WAIT = 1;
 constexpr uint64_t WS_ERR_CHUNK_WAIT = 2;
+constexpr uint64_t WS_ERR_HELPER_WAIT = 4;  // transfer waves: a tile's hand-off between them stalled
 
 // Read-only view of a chunk whose data is in HBM.
 struct ChunkView {
@@ -73,13 +79,66 @@ __device__ __forceinline__ TileDeviceCounters* tile_counters(TiledQueue* tq) {
 struct _TileSlot {
     uint32_t tile;  // TILE_END: no more tiles
     int seq;        // n + 1 once the n-th tile of this slot is assigned
-    int ready;      // chunks of the current tile already in HBM
     int done;       // compute waves finished with the current tile
+    int chunk_done[MAX_CHUNKS_PER_TILE];  // pieces of chunk k already in HBM
 };
+
+// The tile the transfer waves copy together: wave 0 publishes it, every
+// transfer wave claims its pieces, each helper acknowledges it (even with no
+// piece left to claim) and only then is the next tile published, so no helper
+// reads a job's fields while they change.
+struct _TileJob {
+    uint32_t tile;
+    int slot;
+    int seq;         // n + 1 once the n-th job is published; -1: no more jobs
+    int next_piece;  // pieces claimed
+    int pieces_done;
+    int acks;        // helpers finished with this job
+};
+
+// Pieces per chunk: enough that every transfer wave has one when a tile has
+// fewer chunks than transfer waves, none under 16 KiB.
+__device__ __forceinline__ uint32_t _pieces_per_chunk(uint32_t K, uint32_t transfer_waves, uint64_t chunk_bytes) {
+    uint32_t p = (transfer_waves + K - 1) / K;
+    const uint64_t pmax = chunk_bytes / 16384;
+    if ((uint64_t)p > pmax) p = pmax > 0 ? (uint32_t)pmax : 1u;
+    return p;
+}
+
+// Claim and copy pieces of the current job (tile, slot); returns the pieces
+// copied.  The caller passes the job's fields in registers: wave 0 has them
+// from its own claim, a helper read them after every lane's acquire of
+// job->seq.  (Lanes 1..63 of wave 0 must not read them back from LDS: lane
+// 0's plain stores there are not ordered before other lanes' loads, and the
+// compiler does schedule such loads ahead of the stores.)
+__device__ __forceinline__ int _copy_pieces(_TileJob* job, _TileSlot* slots, uint64_t tile, int slot_idx, uint32_t K,
+                                            uint32_t P, uint64_t chunk_bytes, uint64_t piece_bytes, uint32_t T,
+                                            uint32_t C, uint32_t token_size, void* gpu_buffer, const void* cpu_base,
+                                            int unroll) {
+    const int lane = wave::lane_id();
+    _TileSlot& slot = slots[slot_idx];
+    int mine = 0;
+    for (;;) {
+        int i = 0;
+        if (lane == 0) i = __hip_atomic_fetch_add(&job->next_piece, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        i = __builtin_amdgcn_readfirstlane(i);
+        if ((uint32_t)i >= K * P) break;
+        const uint32_t k = (uint32_t)i / P, j = (uint32_t)i % P;
+        const uint64_t begin = (uint64_t)j * piece_bytes;
+        const uint64_t n = begin < chunk_bytes ? (chunk_bytes - begin < piece_bytes ? chunk_bytes - begin : piece_bytes) : 0;
+        const uint64_t off = (tile * T + (uint64_t)k * C) * token_size + begin;
+        if (n) wave::copy_u(unroll, (uint64_t)(uintptr_t)gpu_buffer + off, (uint64_t)(uintptr_t)cpu_base + off, n);
+        wave::release_agent();  // the piece is visible device-wide before the compute wave hears of it
+        if (lane == 0) wave::lds_add(&slot.chunk_done[k], 1);
+        mine++;
+    }
+    return mine;
+}
 
 template <int NSLOTS, typename ComputeFn>
 __device__ __forceinline__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, const void* cpu_base, ComputeFn compute_fn) {
     __shared__ _TileSlot slots[NSLOTS];
+    __shared__ _TileJob job;
     const int w = wave::wave_id();
     const int lane = wave::lane_id();
     const uint32_t C = tq->scheduler.tokens_per_chunk;
@@ -90,17 +149,25 @@ __device__ __forceinline__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, con
     TileDeviceCounters* cnt = tile_counters(tq);
     if (threadIdx.x < NSLOTS) {
         slots[threadIdx.x].seq = 0;
-        slots[threadIdx.x].ready = 0;
         slots[threadIdx.x].done = (int)K;  // free
         slots[threadIdx.x].tile = 0;
     }
+    if (threadIdx.x == 0) job.seq = 0;
     __syncthreads();
 
+    // Waves after the compute waves are transfer helpers.
+    const int nwaves = (int)(blockDim.x / wave::kWidth);
+    const int first_helper = 1 + NSLOTS * (int)K;
+    const int helpers = nwaves > first_helper ? nwaves - first_helper : 0;
+    const uint64_t chunk_bytes = (uint64_t)C * token_size;
+    const uint32_t P = _pieces_per_chunk(K, 1u + (uint32_t)helpers, chunk_bytes);
+    const uint64_t piece_bytes = ((chunk_bytes + P - 1) / P + 1023) & ~1023ull;
+    const uint32_t active = gridDim.x < total_tiles ? gridDim.x : total_tiles;
+    const int unroll = wave::transfer_unroll(active * (1u + (uint32_t)helpers));
+
     if (w == 0) {
-        // ---------------- transfer wave
-        const int unroll = wave::transfer_unroll(gridDim.x < total_tiles ? gridDim.x : total_tiles);
-        bool ok = true;
-        for (uint32_t n = 0; ok; n++) {
+        // ---------------- transfer wave (leader)
+        for (uint32_t n = 0;; n++) {
             const int s = (int)(n % NSLOTS);
             if (!wave::wait_lds_eq(&slots[s].done, (int)K)) {
                 if (lane == 0) __hip_atomic_fetch_or(&cnt->error, WS_ERR_SLOT_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -112,7 +179,7 @@ __device__ __forceinline__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, con
             const bool last = tile >= total_tiles;
             if (lane == 0) {
                 slots[s].tile = last ? TILE_END : (uint32_t)tile;
-                slots[s].ready = 0;
+                for (uint32_t k = 0; k < K; k++) slots[s].chunk_done[k] = 0;
                 slots[s].done = 0;
                 wave::lds_store(&slots[s].seq, (int)(n / NSLOTS) + 1);
             }
@@ -129,19 +196,54 @@ __device__ __forceinline__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, con
                 }
                 break;
             }
-            const uint64_t tok0 = tile * T;
-            for (uint32_t k = 0; k < K; k++) {
-                const uint64_t off = (tok0 + (uint64_t)k * C) * token_size;
-                wave::copy_u(unroll, (uint64_t)(uintptr_t)gpu_buffer + off, (uint64_t)(uintptr_t)cpu_base + off,
-                             (uint64_t)C * token_size);
-                wave::release_agent();
-                if (lane == 0) wave::lds_store(&slots[s].ready, (int)k + 1);
+            if (lane == 0) {
+                job.tile = (uint32_t)tile;
+                job.slot = s;
+                job.next_piece = 0;
+                job.pieces_done = 0;
+                job.acks = 0;
+                wave::lds_store(&job.seq, (int)n + 1);
+            }
+            const int mine = _copy_pieces(&job, slots, tile, s, K, P, chunk_bytes, piece_bytes, T, C, token_size,
+                                          gpu_buffer, cpu_base, unroll);
+            if (lane == 0) wave::lds_add(&job.pieces_done, mine);
+            if (helpers > 0 &&
+                (!wave::wait_lds_eq(&job.pieces_done, (int)(K * P)) || !wave::wait_lds_eq(&job.acks, helpers))) {
+                if (lane == 0) __hip_atomic_fetch_or(&cnt->error, WS_ERR_HELPER_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
             }
             if (lane == 0) {
                 if (tile < (uint64_t)MAX_TILES)
                     __hip_atomic_store(&tq->d_tile_chunk_done[tile], (uint64_t)T, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_fetch_add(&cnt->tiles_done, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
+        }
+        if (lane == 0) wave::lds_store(&job.seq, -1);  // helpers exit
+    } else if (w >= first_helper) {
+        // ---------------- transfer helper: copies pieces of the leader's tiles
+        for (int want = 1;;) {
+            int seq = 0;
+            bool ok = false;
+            for (uint64_t i = 0; i < wave::kSpinLimit; i++) {
+                seq = wave::lds_load(&job.seq);
+                if (seq < 0 || seq >= want) {
+                    ok = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (!ok) {
+                if (lane == 0) __hip_atomic_fetch_or(&cnt->error, WS_ERR_HELPER_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            if (seq < 0) break;
+            const int mine = _copy_pieces(&job, slots, job.tile, job.slot, K, P, chunk_bytes, piece_bytes, T, C,
+                                          token_size, gpu_buffer, cpu_base, unroll);
+            if (lane == 0) {
+                wave::lds_add(&job.pieces_done, mine);
+                wave::lds_add(&job.acks, 1);
+            }
+            want = seq + 1;
         }
     } else if ((uint32_t)(w - 1) < NSLOTS * K) {
         // ---------------- compute waves: slot g, chunk k
@@ -154,7 +256,7 @@ __device__ __forceinline__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, con
             }
             const uint32_t tile = slots[g].tile;
             if (tile == TILE_END) break;
-            if (!wave::wait_lds_gt(&slots[g].ready, (int)k)) {
+            if (!wave::wait_lds_eq(&slots[g].chunk_done[k], (int)P)) {
                 if (lane == 0) __hip_atomic_fetch_or(&cnt->error, WS_ERR_CHUNK_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }

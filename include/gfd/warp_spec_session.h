@@ -20,6 +20,18 @@
 
 namespace gfd {
 
+// Transfer helper waves per workgroup when the configuration leaves the count
+// to the session (negative): about 32 transfer waves per launch, at most 3
+// helpers.  Measured on MI355X: one wave moves ~3.3 GB/s and one CU ~13 GB/s
+// over PCIe, and 32 waves with 16 loads in flight each fill the link, so
+// small grids (1-8 workgroups) gain up to ~1.6x from helpers while large ones
+// gain nothing.
+inline int auto_helper_waves(int grid) {
+    if (grid <= 0) grid = 1;
+    const int h = (32 + grid - 1) / grid - 1;
+    return h < 0 ? 0 : (h > 3 ? 3 : h);
+}
+
 struct WarpSpecConfig {
     // required
     uint32_t total_tokens = 0;
@@ -35,6 +47,11 @@ struct WarpSpecConfig {
     bool use_copy_engine = true;    // kept for API compatibility (data moves zero-copy)
     bool double_buffer = false;
     bool per_tile_mode = false;     // one chunk per tile
+    // Transfer helper waves per workgroup (this build's addition): they copy
+    // pieces of each tile next to the transfer wave, so one workgroup keeps up
+    // to 4x the loads in flight.  Negative: auto_helper_waves(grid), set by
+    // the session.  Fewer if the workgroup would pass 1024 threads.
+    int transfer_helper_waves = -1;
 
     // Chunk size: about 64 KiB (tokens <= 512 B), 128 KiB, or 256 KiB (tokens
     // >= 64 KiB) per chunk, a power of two, at least 4 tokens, and at most 8
@@ -59,10 +76,16 @@ struct WarpSpecConfig {
     }
     uint32_t total_tiles() const { return tokens_per_tile ? total_tokens / tokens_per_tile : 0; }
     uint32_t chunks_per_tile() const { return tokens_per_tile / effective_tokens_per_chunk(); }
-    // 1 transfer wave + K (or 2K) compute waves of 64 lanes.
+    int helper_waves() const {
+        const int k = (int)chunks_per_tile();
+        const int room = 16 - (double_buffer ? 1 + 2 * k : 1 + k);
+        const int h = transfer_helper_waves > 0 ? transfer_helper_waves : 0;
+        return h < room ? h : (room > 0 ? room : 0);
+    }
+    // 1 transfer wave + K (or 2K) compute waves + helper waves, 64 lanes each.
     int block_size() const {
         const int k = (int)chunks_per_tile();
-        return (double_buffer ? 1 + 2 * k : 1 + k) * 64;
+        return (double_buffer ? 1 + 2 * k : 1 + k) * 64 + helper_waves() * 64;
     }
 };
 
@@ -102,6 +125,8 @@ public:
 
     TiledQueue* get_queue() const { return tq_; }
     CpuPollingThread* get_poller() const { return nullptr; }
+    // The configuration in effect (helper waves resolved).
+    const WarpSpecConfig& config() const { return config_; }
     bool ok() const { return ok_; }
     uint64_t error_bits() const { return error_bits_; }
     uint64_t tiles_done() const { return tiles_done_; }
@@ -131,8 +156,15 @@ struct SGWarpSpecConfig {
     int max_lists = MAX_SG_LISTS;
     int max_entries = MAX_SG_POOL_ENTRIES;
     uint32_t idle_limit_ms = 0;  // transfer waves give up after this long without a list (0 = 30 s)
+    // Transfer helper waves per workgroup (this build's addition, 0..3): they
+    // copy 64-entry batches of each list next to the transfer wave.
+    // Negative: auto_helper_waves(grid), set by the session.
+    int transfer_helper_waves = -1;
 
-    int block_size() const { return (1 + (num_compute_warps > 0 ? num_compute_warps : 1)) * 64; }
+    int block_size() const {
+        const int h = transfer_helper_waves > 0 ? transfer_helper_waves : 0;
+        return (1 + (num_compute_warps > 0 ? num_compute_warps : 1) + h) * 64;
+    }
 };
 
 class SGWarpSpecSession {
@@ -174,9 +206,12 @@ public:
     uint64_t error_bits() const { return error_bits_; }
     uint64_t lists_landed() const { return lists_done_; }  // during the last launch
     int num_blocks() const { return num_blocks_; }
+    int helper_waves() const { return config_.transfer_helper_waves; }
+    int block_size() const { return config_.block_size(); }
 
-    // Internal: called by launch().
-    void before_launch(gfd_stream_t stream);
+    // Internal: called by launch().  helper_waves < 0: the configured count;
+    // kernels whose extra waves have other work (a GPU submitter) pass their own.
+    void before_launch(gfd_stream_t stream, int helper_waves = -1);
 
 private:
     struct Pending {

@@ -228,6 +228,7 @@ typedef struct gfd_session_result {
     uint64_t error_bits;  /* nonzero: a bounded wait inside the kernel gave up */
     double elapsed_ms;    /* launch -> synchronize, host clock */
     int grid, block, tokens_per_chunk, chunks_per_tile;
+    int helper_waves;     /* transfer helper waves per workgroup (this build's addition) */
 } gfd_session_result;
 
 /* WarpSpecSession over tokens [0, total_tokens) of cpu_src (pinned) -> gpu_dst
@@ -236,15 +237,20 @@ typedef struct gfd_session_result {
  * token_sums[t] (test/test_db_small_tiles.cu:18-31); NULL: no-op consumer.
  * kernel_ms[iters] (optional) gets HIP-event times of each launch.
  * Tokens past the last whole tile are not moved (as the reference). */
+/* helper_waves: transfer helper waves per workgroup (negative: about 32
+ * transfer waves per launch, gfd::auto_helper_waves; fewer where the
+ * workgroup would pass 1024 threads). */
 int gfd_warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t total_tokens, uint32_t token_size,
                       uint32_t tokens_per_tile, uint32_t tokens_per_chunk, int double_buffer,
-                      int per_tile_mode, int num_blocks, float* token_sums, int iters,
+                      int per_tile_mode, int num_blocks, int helper_waves, float* token_sums, int iters,
                       double* kernel_ms, gfd_session_result* res);
 
 typedef void* gfd_sg_session_t;
 /* SGWarpSpecSession(SGWarpSpecConfig{num_compute_warps, num_blocks}); idle_limit_ms
- * bounds how long transfer waves wait without a list (0 = 30 s). */
-int gfd_sg_session_create(int num_compute_warps, int num_blocks, uint32_t idle_limit_ms,
+ * bounds how long transfer waves wait without a list (0 = 30 s); helper_waves
+ * = transfer helper waves per workgroup, 0..3 (negative: about 32 transfer
+ * waves per launch, gfd::auto_helper_waves). */
+int gfd_sg_session_create(int num_compute_warps, int num_blocks, uint32_t idle_limit_ms, int helper_waves,
                           gfd_sg_session_t* out);
 void gfd_sg_session_destroy(gfd_sg_session_t s);
 /* submit_sg_list (warp_spec_session.h:170-171): returns the ring index, or -1. */

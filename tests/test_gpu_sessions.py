@@ -30,6 +30,19 @@ def gpu():
     assert gfd_amd.lib().gfd_set_device(0) == 0
 
 
+def auto_helpers(grid):
+    """Default helper count: enough for about 32 transfer waves per launch
+    (ceil(32 / grid) - 1), at most 3."""
+    return max(0, min(3, -(-32 // max(grid, 1)) - 1))
+
+
+def with_helpers(block, helpers):
+    """Workgroup of a session: the reference's block plus this build's
+    transfer helper waves (as many as fit in 1024 threads)."""
+    h = max(0, min(helpers, (1024 - block) // 64))
+    return block + 64 * h, h
+
+
 def random_host(nbytes, seed):
     h = gfd_amd.HostBuffer(nbytes)
     h.array[:] = np.random.default_rng(seed).integers(0, 256, nbytes, dtype=np.uint8)
@@ -63,7 +76,8 @@ def test_warp_spec_db_small_tiles(total, tile, chunk):
     assert (got == want).all(), "first bad token %d" % int(np.argmax(got != want))
     assert (dst.download() == host.array).all()
     c, k, block = oracle.warp_spec_chunking(dim * 4, tile, chunk, True)
-    assert (res["tokens_per_chunk"], res["chunks_per_tile"], res["block"]) == (c, k, block)
+    assert (res["tokens_per_chunk"], res["chunks_per_tile"]) == (c, k)
+    assert (res["block"], res["helper_waves"]) == with_helpers(block, auto_helpers(total // tile))
     assert res["units_done"] == total and res["lists_done"] == total // tile and res["error_bits"] == 0
 
 
@@ -98,8 +112,59 @@ def test_warp_spec_parity(total, ts, tile, chunk, db, per_tile, blocks):
     tiles = total // tile
     assert res["lists_done"] == tiles and res["units_done"] == tiles * tile and res["error_bits"] == 0
     c, k, block = oracle.warp_spec_chunking(ts, tile, chunk, db, per_tile)
-    assert (res["tokens_per_chunk"], res["chunks_per_tile"], res["block"]) == (c, k, block)
+    assert (res["tokens_per_chunk"], res["chunks_per_tile"]) == (c, k)
+    assert (res["block"], res["helper_waves"]) == with_helpers(block, auto_helpers(min(res["grid"], tiles)))
     assert (times > 0).all()
+
+
+HELPER_CASES = [
+    # total tokens, token bytes, tile, chunk, double buffer, per-tile mode
+    (1024, 4096, 128, 0, False, True),     # K = 1: a 512 KiB chunk in pieces
+    (1024, 4096, 128, 64, True, False),    # K = 2 per slot
+    (2048, 1000, 64, 8, False, False),     # K = 8, 8000-byte chunks (one piece each)
+    (600, 20000, 32, 32, False, True),     # 640000-byte chunks, not a multiple of 1 KiB
+]
+
+
+@pytest.mark.parametrize("helpers", [0, 1, 3, 6])
+@pytest.mark.parametrize("blocks", [1, 8])
+@pytest.mark.parametrize("total,ts,tile,chunk,db,per_tile", HELPER_CASES)
+def test_warp_spec_helper_waves(total, ts, tile, chunk, db, per_tile, blocks, helpers):
+    """Transfer helper waves share each tile's pieces with the transfer wave:
+    the landed bytes must not depend on how many there are."""
+    log("warp_spec helpers=%d blocks=%d total=%d ts=%d tile=%d chunk=%d db=%d per_tile=%d" %
+        (helpers, blocks, total, ts, tile, chunk, db, per_tile))
+    host = random_host(total * ts, seed=total + ts + helpers)
+    dst = gfd_amd.DeviceBuffer(total * ts + 4096)
+    dst.fill(SENTINEL)
+    before = dst.download()
+    res, _ = gfd_amd.warp_spec_run(host.ptr, dst.ptr, total, ts, tile, chunk, db, per_tile, blocks, iters=2,
+                                   helper_waves=helpers)
+    want = np.concatenate([oracle.warp_spec_expected(host.array, before[:total * ts], total, ts, tile),
+                           before[total * ts:]])
+    n_bad = int(np.count_nonzero(dst.download() != want))
+    assert n_bad == 0, "%d mismatched bytes" % n_bad
+    _, _, block = oracle.warp_spec_chunking(ts, tile, chunk, db, per_tile)
+    assert (res["block"], res["helper_waves"]) == with_helpers(block, helpers)
+    assert res["lists_done"] == total // tile and res["error_bits"] == 0
+
+
+def test_warp_spec_helper_waves_token_sums():
+    """Compute waves see every piece of their chunk: per-token sums with 3
+    helpers splitting one 256 KiB chunk per tile."""
+    log("warp_spec helpers token sums")
+    total, dim, tile = 2048, 1024, 64
+    host = gfd_amd.HostBuffer(total * dim * 4)
+    host.array.view(np.float32).reshape(total, dim)[:] = (np.arange(total, dtype=np.float32) + 1)[:, None]
+    dst = gfd_amd.DeviceBuffer(total * dim * 4)
+    sums = gfd_amd.DeviceBuffer(total * 4)
+    sums.fill(0)
+    res, _ = gfd_amd.warp_spec_run(host.ptr, dst.ptr, total, dim * 4, tile, 0, False, True, 4, token_sums=sums.ptr,
+                                   helper_waves=3)
+    want = (np.arange(total, dtype=np.float32) + 1) * dim
+    got = sums.download().view(np.float32)
+    assert (got == want).all(), "first bad token %d" % int(np.argmax(got != want))
+    assert res["helper_waves"] == 3 and res["error_bits"] == 0
 
 
 def test_warp_spec_rejects_oversized_block():
@@ -173,10 +238,11 @@ def expected_dst(host, dst_before, dst_ptr, arr):
     return out
 
 
-@pytest.mark.parametrize("blocks,compute", [(1, 1), (8, 1), (0, 1), (0, 3)])
-def test_sg_ragged_lists_checksum(blocks, compute):
-    log("sg ragged blocks=%d compute=%d" % (blocks, compute))
-    rng = np.random.default_rng(100 + blocks * 7 + compute)
+@pytest.mark.parametrize("blocks,compute,helpers", [(1, 1, 3), (8, 1, 3), (0, 1, 3), (0, 3, 3), (1, 1, 0),
+                                                    (1, 1, 1), (8, 1, 2), (8, 3, 0)])
+def test_sg_ragged_lists_checksum(blocks, compute, helpers):
+    log("sg ragged blocks=%d compute=%d helpers=%d" % (blocks, compute, helpers))
+    rng = np.random.default_rng(100 + blocks * 7 + compute + 13 * helpers)
     host = random_host(4 << 20, seed=blocks + 11)
     dst = gfd_amd.DeviceBuffer(48 << 20)
     dst.fill(SENTINEL)
@@ -184,7 +250,8 @@ def test_sg_ragged_lists_checksum(blocks, compute):
     arr, ranges = ragged_lists(rng, host, dst, n_lists=120, max_entries=90, max_size=9000)
     sums = gfd_amd.DeviceBuffer(gfd_amd.MAX_SG_LISTS * 8)
     sums.fill(0)
-    s = gfd_amd.SGWarpSpecSession(num_compute_warps=compute, num_blocks=blocks, idle_limit_ms=5000)
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=compute, num_blocks=blocks, idle_limit_ms=5000,
+                                  helper_waves=helpers)
     for lid, (a, b) in ranges.items():
         s.submit_sg_list(arr[a:b], list_id=lid)
     s.launch(list_sums=sums.ptr)
@@ -197,7 +264,54 @@ def test_sg_ragged_lists_checksum(blocks, compute):
     st = s.stats()
     assert st["units_done"] == len(arr) and st["bytes"] == int(arr["size"].sum()) and st["error_bits"] == 0
     assert st["lists_done"] == len(ranges)
+    assert (st["block"], st["helper_waves"]) == (64 * (1 + compute + helpers), helpers)
     s.close()
+
+
+def test_sg_empty_and_tiny_lists_with_helpers():
+    """Lists with fewer batches than transfer waves (empty, 1 entry, 65
+    entries) keep every helper's acknowledgement in step."""
+    log("sg tiny lists helpers")
+    rng = np.random.default_rng(77)
+    host = random_host(1 << 20, seed=77)
+    dst = gfd_amd.DeviceBuffer(4 << 20)
+    dst.fill(SENTINEL)
+    before = dst.download()
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=2, idle_limit_ms=5000, helper_waves=3)
+    sizes = [0, 1, 65, 0, 2, 130, 64, 1]
+    ents, off = [], 0
+    for lid, k in enumerate(sizes):
+        part = []
+        for _ in range(k):
+            n = int(rng.integers(1, 3000))
+            so = int(rng.integers(0, host.nbytes - n))
+            part.append((host.ptr + so, dst.ptr + off, n))
+            off += n + int(rng.integers(0, 17))
+        arr = entries_array([e[0] for e in part], [e[1] for e in part], [e[2] for e in part]) if part else \
+            np.zeros(0, dtype=gfd_amd.DEVICE_SG_ENTRY_DTYPE)
+        s.submit_sg_list(arr, list_id=lid)
+        ents.append(arr)
+    s.launch()
+    s.synchronize()
+    allents = np.concatenate(ents)
+    assert (dst.download() == expected_dst(host, before, dst.ptr, allents)).all()
+    st = s.stats()
+    assert st["lists_done"] == len(sizes) and st["units_done"] == sum(sizes) and st["error_bits"] == 0
+    s.close()
+
+
+@pytest.mark.parametrize("blocks", [1, 8, 16, 64])
+def test_sg_default_helper_waves(blocks):
+    """Without an explicit count a session adds helpers only to small grids."""
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=blocks, idle_limit_ms=2000)
+    st = s.stats()
+    assert st["helper_waves"] == auto_helpers(blocks) and st["block"] == 64 * (2 + auto_helpers(blocks))
+    s.close()
+
+
+def test_sg_rejects_too_many_helpers():
+    with pytest.raises(gfd_amd.GfdError):
+        gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=1, helper_waves=4)
 
 
 def test_sg_streaming_ring_and_pool_wrap():
@@ -266,12 +380,13 @@ def test_sg_submit_without_kernel_rejects_when_ring_full():
     s.close()
 
 
-@pytest.mark.parametrize("blocks,n_lists,epl,t", [(1, 4, 8, 4096), (8, 64, 32, 2048), (0, 300, 16, 1000)])
-def test_sg_gpu_submit(blocks, n_lists, epl, t):
+@pytest.mark.parametrize("blocks,n_lists,epl,t,helpers", [(1, 4, 8, 4096, 3), (8, 64, 32, 2048, 3),
+                                                         (0, 300, 16, 1000, 3), (8, 64, 32, 2048, 0)])
+def test_sg_gpu_submit(blocks, n_lists, epl, t, helpers):
     """test/test_sg_gpu_submit.cu: a submitter wave per workgroup builds the
     lists on the GPU (entries from a device table), transfer waves land them,
     the compute wave checksums each list."""
-    log("sg gpu submit blocks=%d lists=%d epl=%d t=%d" % (blocks, n_lists, epl, t))
+    log("sg gpu submit blocks=%d lists=%d epl=%d t=%d helpers=%d" % (blocks, n_lists, epl, t, helpers))
     n = n_lists * epl
     host = gfd_amd.HostBuffer(n * t)
     if t % 4 == 0:
@@ -286,7 +401,7 @@ def test_sg_gpu_submit(blocks, n_lists, epl, t):
     d_ent.upload(arr.view(np.uint8))
     sums = gfd_amd.DeviceBuffer(gfd_amd.MAX_SG_LISTS * 8)
     sums.fill(0)
-    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=blocks, idle_limit_ms=5000)
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=blocks, idle_limit_ms=5000, helper_waves=helpers)
     s.launch_gpu_submit(d_ent.ptr, epl, n_lists, list_sums=sums.ptr)
     s.synchronize(extra_gpu_lists=n_lists)
     assert (dst.download() == host.array).all()
