@@ -4,7 +4,8 @@ Workload (one "step"): gather 8192 tokens x 4 KiB (32 MiB) scattered at 2x
 stride in pinned host memory, in a seeded random order, into one contiguous
 HBM buffer.  Also measured in the same run: 2048 x 64 KiB (KV-cache pages),
 2048 x {512 B, 1 KiB, 2 KiB}, the contiguous-copy link peak, per-token
-hipMemcpyAsync, and the CPU ParallelGather restatement on the host cores.
+hipMemcpyAsync, the CPU ParallelGather restatement on the host cores, and the
+reverse path (offload of the same layouts from HBM to pinned host).
 Timing: W warm-up + K timed iterations, P50 (examples/04_benchmark.cu:58-90).
 GB/s = bytes / (us * 1e3).
 
@@ -390,6 +391,50 @@ def run_moe(oracle, iters, warmup, tokens=4096, experts=64, dim=7168):
     return res
 
 
+def run_offload(oracle, iters, warmup):
+    """Offload (HBM -> pinned host, the reverse path): n tokens contiguous in
+    HBM written to the seeded 2x-stride slots of a pinned host region by the
+    zero-copy scatter kernel; checked against the oracle's closed form.  The
+    link reference is one contiguous device->host hipMemcpyAsync of the same
+    bytes."""
+    out = {}
+    for n, t in ((8192, 4096), (2048, 65536)):
+        nbytes, stride = n * t, 2 * t
+        tokens = np.random.default_rng(n + t).integers(0, 256, nbytes, dtype=np.uint8)
+        src = gfd_amd.DeviceBuffer(nbytes)
+        src.upload(tokens)
+        host = gfd_amd.HostBuffer(n * stride)
+        host.array[:] = 0xCD
+        before = host.array.copy()
+        perm = oracle.permutation(n)
+        table = gfd_amd.DeviceBuffer(n * 8)
+        table.upload(np.uint64(host.ptr) + perm.astype(np.uint64) * np.uint64(stride))
+        wall, ev = np.zeros(iters), np.zeros(iters)
+        rc = gfd_amd.lib().gfd_bench_zero_copy_scatter_tokens(table.ptr, src.ptr, t, n, warmup, iters,
+                                                              wall.ctypes.data_as(PD), ev.ctypes.data_as(PD))
+        assert rc == 0, gfd_amd.lib().gfd_last_error()
+        want_region = oracle.expected_scatter(before, tokens, perm, t, stride)
+        assert np.array_equal(host.array, want_region), "offload %dx%d: bytes differ from the oracle" % (n, t)
+        contig = gfd_amd.HostBuffer(nbytes)
+        tc = np.zeros(iters)
+        rc = gfd_amd.lib().gfd_bench_memcpy_contiguous_d2h(contig.ptr, src.ptr, nbytes, 1, warmup, iters,
+                                                           tc.ctypes.data_as(PD))
+        assert rc == 0, gfd_amd.lib().gfd_last_error()
+        d2h = gbps(nbytes, p50(tc))
+        k_gbps = gbps(nbytes, float(ev.mean()))
+        out["%dx%d" % (n, t)] = {
+            "bytes": nbytes, "zero_copy_scatter": {
+                "us_p50": round(p50(wall), 2), "GBps": round(gbps(nbytes, p50(wall)), 3),
+                "kernel_us_mean": round(float(ev.mean()), 2), "kernel_GBps": round(k_gbps, 3),
+                "of_theoretical": round(k_gbps / PCIE_GEN5_X16_GBPS, 4),
+                "of_d2h_contiguous": round(k_gbps / d2h, 4) if d2h else None},
+            "d2h_contiguous_GBps": round(d2h, 3)}
+        log("  offload %dx%d: %s" % (n, t, out["%dx%d" % (n, t)]))
+        for b in (src, host, table, contig):
+            b.free()
+    return out
+
+
 def run_sessions(oracle, iters, warmup):
     """Wave-specialised sessions.  WarpSpecSession on linear tiles (token t at
     cpu_src + t*T -> gpu_dst + t*T; T = 128 tokens, automatic chunking, no-op
@@ -481,7 +526,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=15)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="",
-                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions,scattered "
+                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions,scattered,offload "
                          "(calib: add a 32 MiB D2D copy)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -563,6 +608,11 @@ def main():
         log("wave-specialised sessions ...")
         r_sessions = run_sessions(oracle, K, W)
 
+    r_offload = None
+    if want("offload"):
+        log("offload (HBM -> pinned host) ...")
+        r_offload = run_offload(oracle, K, W)
+
     r_moe = None
     if want("moe"):
         log("SG-MoE 4096 x 7168 bf16, top-2 of 64 ...")
@@ -622,6 +672,7 @@ def main():
         "results_8192x4KB": r_main, "results_2048x64KB": r_kv, "results_small": r_small, "results_sg_moe": r_moe,
         "results_sessions": r_sessions,
         "results_direct_scattered_dst_8192x4KB": r_scat,
+        "results_offload": r_offload,
         "direct_setup": {k: dinfo[k] for k in ("numa_node", "num_gather_workers", "worker_cpus", "poller_cpu",
                                                "num_ce_channels", "direct_chunk_bytes", "gather_slice_bytes")},
         "host": info,

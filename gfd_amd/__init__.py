@@ -147,7 +147,7 @@ def _declare(L):
         "gfd_poller_copy_clock_ns": ([vp], c_u64),
         "gfd_poller_set_direct_chunk_bytes": ([vp, c_u64], None),
         "gfd_poller_set_gather_slice_bytes": ([vp, c_u64], None),
-        "gfd_host_gather": ([vp, c_int, vp, c_u64, c_u64, c_int, vp], c_int),
+        "gfd_host_gather": ([vp, c_int, vp, c_u64, c_u64, c_int, vp, c_int], c_int),
         "gfd_staging_pool_init": ([c_int, c_sz, c_int], c_int),
         "gfd_staging_pool_shutdown": ([], None),
         "gfd_zero_copy_gather_tokens": ([vp, vp, c_u32, c_int, vp], c_int),
@@ -164,6 +164,9 @@ def _declare(L):
         "gfd_bench_sdma_contiguous": ([vp, vp, c_sz, c_int, c_int, c_int, c_int, pd, ctypes.POINTER(c_u32)], c_int),
         "gfd_bench_submit_direct": ([vp, vp, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_zero_copy_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
+        "gfd_zero_copy_scatter_tokens": ([vp, vp, c_u32, c_int, vp], c_int),
+        "gfd_bench_zero_copy_scatter_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
+        "gfd_bench_memcpy_contiguous_d2h": ([vp, vp, ctypes.c_size_t, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_queue": ([vp, vp, vp, c_int, c_u32, ctypes.POINTER(c_u64), c_int, c_int, c_u64, pd], c_int),
         "gfd_warp_spec_run": ([vp, vp, c_u32, c_u32, c_u32, c_u32, c_int, c_int, c_int, c_int, vp, c_int, pd,
                                ctypes.POINTER(SessionResult)], c_int),
@@ -428,16 +431,27 @@ def host_gather(entries, count, out, chunk_bytes=0, slice_bytes=0, num_workers=0
     completion order (see gfd_host_gather in include/gfd_capi.h)."""
     out_ptr = out.ctypes.data if isinstance(out, np.ndarray) else out
     total = sum(int(entries[i].size) for i in range(count)) if count else 0
-    nchunks = (max(1, -(-total // chunk_bytes)) if chunk_bytes else 1) + 1
-    order = np.full(nchunks, -1, dtype=np.int32)
-    _check(lib().gfd_host_gather(ctypes.cast(entries, ctypes.c_void_p), count, out_ptr, chunk_bytes, slice_bytes,
-                                 num_workers, order.ctypes.data), "gfd_host_gather")
-    return order[order >= 0]
+    # Every chunk but the last is at least min(64 KiB, chunk_bytes).
+    cap = total // (min(65536, chunk_bytes) if chunk_bytes else 65536) + 2
+    order = np.full(cap, -1, dtype=np.int32)
+    n = lib().gfd_host_gather(ctypes.cast(entries, ctypes.c_void_p), count, out_ptr, chunk_bytes, slice_bytes,
+                              num_workers, order.ctypes.data, cap)
+    if n < 0:
+        _check(-1, "gfd_host_gather")
+    if n > cap:
+        raise GfdError("gfd_host_gather reported %d chunks, more than the %d it may" % (n, cap))
+    return order[:n]
 
 
 def zero_copy_gather_tokens(src_addrs_ptr, dst_ptr, token_size, num_tokens, stream=None):
     _check(lib().gfd_zero_copy_gather_tokens(src_addrs_ptr, dst_ptr, token_size, num_tokens, stream),
            "gfd_zero_copy_gather_tokens")
+
+
+def zero_copy_scatter_tokens(dst_addrs_ptr, src_ptr, token_size, num_tokens, stream=None):
+    """Offload (reverse path): dst_addrs[j] (pinned host) <- src + j*token_size (HBM)."""
+    _check(lib().gfd_zero_copy_scatter_tokens(dst_addrs_ptr, src_ptr, token_size, num_tokens, stream),
+           "gfd_zero_copy_scatter_tokens")
 
 
 def zero_copy_gather(entries_ptr, count, stream=None):

@@ -40,6 +40,36 @@ double elapsed_us(std::chrono::steady_clock::time_point a, std::chrono::steady_c
     return std::chrono::duration<double, std::micro>(b - a).count();
 }
 
+
+// Time `launch(stream)` warmup + iters times: wall clock launch -> sync and
+// HIP events around the launch on its stream.
+template <typename Launch>
+int bench_kernel(Launch launch, int warmup, int iters, double* wall_us, double* event_us, const char* what) {
+    gfd_stream_t s = nullptr;
+    gfd_event_t a = nullptr, b = nullptr;
+    int rc = gfd_hip_stream_create(&s);
+    if (!rc) rc = gfd_hip_event_create(&a, 1);
+    if (!rc) rc = gfd_hip_event_create(&b, 1);
+    for (int it = -warmup; it < iters && !rc; it++) {
+        auto t0 = std::chrono::steady_clock::now();
+        rc = gfd_hip_event_record(a, s);
+        if (!rc) rc = launch(s);
+        if (!rc) rc = gfd_hip_event_record(b, s);
+        if (!rc) rc = gfd_hip_stream_synchronize(s);
+        auto t1 = std::chrono::steady_clock::now();
+        float ms = 0;
+        if (!rc) rc = gfd_hip_event_elapsed_ms(&ms, a, b);
+        if (it >= 0 && !rc) {
+            wall_us[it] = elapsed_us(t0, t1);
+            if (event_us) event_us[it] = ms * 1000.0;
+        }
+    }
+    if (a) gfd_hip_event_destroy(a);
+    if (b) gfd_hip_event_destroy(b);
+    if (s) gfd_hip_stream_destroy(s);
+    return rc ? fail(rc, what) : 0;
+}
+
 }  // namespace
 
 void gfd_internal_set_error(const char* what) { g_last_error = what ? what : ""; }
@@ -210,18 +240,20 @@ void gfd_poller_set_gather_slice_bytes(gfd_poller_t p, uint64_t b) {
 namespace {
 struct OrderCtx {
     int* order;
+    int cap;
     int n;
 };
 void record_chunk(void* p, int chunk, size_t, size_t) {
     OrderCtx* c = (OrderCtx*)p;
-    if (c->order) c->order[c->n] = chunk;
+    if (c->order && c->n < c->cap) c->order[c->n] = chunk;
     c->n++;
 }
 }  // namespace
 
 int gfd_host_gather(const gfd_sg_entry* entries, int count, void* out, uint64_t chunk_bytes,
-                    uint64_t slice_bytes, int num_workers, int* chunk_order) {
-    if (count < 0 || (count > 0 && (!entries || !out)) || num_workers < 0 || num_workers > 64) {
+                    uint64_t slice_bytes, int num_workers, int* chunk_order, int chunk_order_cap) {
+    if (count < 0 || (count > 0 && (!entries || !out)) || num_workers < 0 || num_workers > 64 ||
+        chunk_order_cap < 0) {
         g_last_error = "gfd_host_gather: invalid argument";
         return -1;
     }
@@ -237,9 +269,9 @@ int gfd_host_gather(const gfd_sg_entry* entries, int count, void* out, uint64_t 
     }
     const size_t total = sc.total;
     if (slice_bytes) engine.set_slice_bytes(slice_bytes);
-    OrderCtx ctx{chunk_order, 0};
+    OrderCtx ctx{chunk_order, chunk_order ? chunk_order_cap : 0, 0};
     engine.run(e, count, total, (char*)out, chunk_bytes, record_chunk, &ctx);
-    return 0;
+    return ctx.n;
 }
 
 int gfd_staging_pool_init(int num_gpus, size_t buf_size, int numa_node) {
@@ -349,32 +381,40 @@ int gfd_bench_submit_direct(gfd_poller_t p, const gfd_sg_entry* entries, int cou
     return 0;
 }
 
-int gfd_bench_zero_copy_tokens(const uint64_t* src_addrs, void* dst, uint32_t T, int n, int warmup, int iters,
-                               double* wall_us, double* event_us) {
-    gfd_stream_t s = nullptr;
-    gfd_event_t a = nullptr, b = nullptr;
-    CAPI_CHECK(gfd_hip_stream_create(&s), "hipStreamCreate");
-    CAPI_CHECK(gfd_hip_event_create(&a, 1), "hipEventCreate");
-    CAPI_CHECK(gfd_hip_event_create(&b, 1), "hipEventCreate");
+int gfd_bench_zero_copy_scatter_tokens(const uint64_t* dst_addrs, const void* src, uint32_t T, int n, int warmup,
+                                       int iters, double* wall_us, double* event_us) {
+    return bench_kernel([&](gfd_stream_t s) { return gfd_zero_copy_scatter_tokens(dst_addrs, src, T, n, s); },
+                        warmup, iters, wall_us, event_us, "zero-copy scatter");
+}
+
+int gfd_bench_memcpy_contiguous_d2h(void* dst, const void* src, size_t bytes, int ns, int warmup, int iters,
+                                    double* times_us) {
+    if (ns < 1) ns = 1;
+    if (ns > 8) ns = 8;
+    gfd_stream_t st[8] = {};
+    for (int i = 0; i < ns; i++) CAPI_CHECK(gfd_hip_stream_create(&st[i]), "hipStreamCreate");
+    const size_t per = ((bytes + ns - 1) / ns + 4095) & ~(size_t)4095;
     int rc = 0;
     for (int it = -warmup; it < iters && !rc; it++) {
         auto t0 = std::chrono::steady_clock::now();
-        rc = gfd_hip_event_record(a, s);
-        if (!rc) rc = gfd_zero_copy_gather_tokens(src_addrs, dst, T, n, s);
-        if (!rc) rc = gfd_hip_event_record(b, s);
-        if (!rc) rc = gfd_hip_stream_synchronize(s);
-        auto t1 = std::chrono::steady_clock::now();
-        float ms = 0;
-        if (!rc) rc = gfd_hip_event_elapsed_ms(&ms, a, b);
-        if (it >= 0 && !rc) {
-            wall_us[it] = elapsed_us(t0, t1);
-            if (event_us) event_us[it] = ms * 1000.0;
+        for (int i = 0; i < ns && !rc; i++) {
+            const size_t off = (size_t)i * per;
+            if (off >= bytes) break;
+            const size_t len = std::min(per, bytes - off);
+            rc = gfd_hip_memcpy_d2h_async((char*)dst + off, (uint64_t)(uintptr_t)src + off, len, st[i]);
         }
+        for (int i = 0; i < ns && !rc; i++) rc = gfd_hip_stream_synchronize(st[i]);
+        auto t1 = std::chrono::steady_clock::now();
+        if (it >= 0) times_us[it] = elapsed_us(t0, t1);
     }
-    gfd_hip_event_destroy(a);
-    gfd_hip_event_destroy(b);
-    gfd_hip_stream_destroy(s);
-    return rc ? fail(rc, "zero-copy gather") : 0;
+    for (int i = 0; i < ns; i++) gfd_hip_stream_destroy(st[i]);
+    return rc ? fail(rc, "contiguous D2H copy") : 0;
+}
+
+int gfd_bench_zero_copy_tokens(const uint64_t* src_addrs, void* dst, uint32_t T, int n, int warmup, int iters,
+                               double* wall_us, double* event_us) {
+    return bench_kernel([&](gfd_stream_t s) { return gfd_zero_copy_gather_tokens(src_addrs, dst, T, n, s); },
+                        warmup, iters, wall_us, event_us, "zero-copy gather");
 }
 
 int gfd_bench_queue(void* queue, const void* tokens, void* gpu_dst, int n, uint32_t T, uint64_t* base_slot,

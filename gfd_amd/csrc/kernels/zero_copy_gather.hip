@@ -18,7 +18,9 @@
 //   * Grid: a few hundred KiB to 1 MiB of host reads outstanding in total
 //     (waves x 64 lanes x U x 16 B) fills the link; far more only queues.
 //     The measured optimum is set below (kBytesPerWave ...) and can be
-//     overridden with GFD_ZC_WAVES / GFD_ZC_UNROLL.
+//     overridden with GFD_ZC_WAVES / GFD_ZC_UNROLL (GFD_ZCS_WAVES /
+//     GFD_ZCS_UNROLL for the offload kernel, whose posted writes need fewer
+//     waves).
 //   * Stores are plain 16-byte stores to HBM (coalesced, contiguous).
 //   * Staging: in registers by default.  GFD_ZC_LDS=1 selects the form that
 //     stages through LDS (global_load_lds_dwordx4 host -> LDS, then LDS ->
@@ -47,6 +49,13 @@ constexpr uint64_t kBytesPerWave = 128 * 1024;
 constexpr int kMinWaves = 64, kMaxWaves = 256;
 constexpr int kDefaultUnroll = 4;
 constexpr int kDefaultLds = 0;
+// Offload (HBM -> host): the stores are posted PCIe writes, so few waves fill
+// the link.  Measured on MI355X over 16-512 waves and U = 4/8/16: 8192 x 4 KiB
+// is flat at 54.8-54.9 GB/s from 16 to 128 waves and 54.5 at 256-512;
+// 2048 x 64 KiB peaks at 64 waves (55.5 GB/s).  One wave per 512 KiB, 16-64.
+constexpr uint64_t kScatterBytesPerWave = 512 * 1024;
+constexpr int kScatterMinWaves = 16, kScatterMaxWaves = 64;
+constexpr int kScatterUnroll = 8;
 
 using gfd::wave::BatchLds;
 
@@ -71,6 +80,32 @@ __global__ __launch_bounds__(kBlock) void zc_gather_tokens(const uint64_t* __res
         if (lane < nb) {
             ms = src_addrs[first + lane];
             md = dst + (first + lane) * token_size;
+            mn = token_size;
+        }
+        gfd::wave::copy_batch(unroll, md, ms, mn, nb, &lds[wid], kLds ? stage[wid] : nullptr);
+    }
+}
+
+// Reverse direction (KV-page offload): token j of num_tokens is read from HBM
+// at src + j * token_size and stored to dst_addrs[j] in pinned host memory.
+// HBM loads return in ~1-2 us, and the 16-byte stores become posted PCIe
+// writes, so each wave moves its batch as one vector stream, exactly as the
+// gather does.
+template <bool kLds>
+__global__ __launch_bounds__(kBlock) void zc_scatter_tokens(const uint64_t* __restrict__ dst_addrs, uint64_t src,
+                                                            uint32_t token_size, uint32_t num_tokens,
+                                                            uint32_t per_wave, int unroll) {
+    __shared__ BatchLds lds[kWavesPerBlock];
+    __shared__ gfd::wave::vec4u stage[kLds ? kWavesPerBlock : 1][kLds ? kStageVecs : 1];
+    const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const uint64_t wave = (uint64_t)blockIdx.x * kWavesPerBlock + wid;
+    const uint64_t stride = (uint64_t)gridDim.x * kWavesPerBlock * per_wave;
+    for (uint64_t first = wave * per_wave; first < num_tokens; first += stride) {
+        const uint32_t nb = (uint32_t)min((uint64_t)per_wave, num_tokens - first);
+        uint64_t md = 0, ms = 0, mn = 0;
+        if (lane < nb) {
+            md = dst_addrs[first + lane];
+            ms = src + (first + lane) * token_size;
             mn = token_size;
         }
         gfd::wave::copy_batch(unroll, md, ms, mn, nb, &lds[wid], kLds ? stage[wid] : nullptr);
@@ -111,12 +146,24 @@ struct Shape {
     bool lds;  // stage through LDS
 };
 
-Shape shape_for(uint64_t n, uint64_t total_bytes) {
+struct ShapeDefaults {
+    uint64_t bytes_per_wave;
+    int min_waves, max_waves, unroll;
+    const char* waves_env;
+    const char* unroll_env;
+};
+constexpr ShapeDefaults kGatherShape{kBytesPerWave, kMinWaves, kMaxWaves, kDefaultUnroll, "GFD_ZC_WAVES",
+                                     "GFD_ZC_UNROLL"};
+constexpr ShapeDefaults kScatterShape{kScatterBytesPerWave, kScatterMinWaves, kScatterMaxWaves, kScatterUnroll,
+                                      "GFD_ZCS_WAVES", "GFD_ZCS_UNROLL"};
+
+Shape shape_for(uint64_t n, uint64_t total_bytes, const ShapeDefaults& d = kGatherShape) {
     // Read per call (a getenv is ~100 ns against a launch of microseconds),
     // so a process can sweep launch shapes.
-    const int dflt = (int)std::min<uint64_t>(std::max<uint64_t>(total_bytes / kBytesPerWave, kMinWaves), kMaxWaves);
-    const int target = std::max(4, env_int("GFD_ZC_WAVES", dflt));
-    const int unroll_env = env_int("GFD_ZC_UNROLL", kDefaultUnroll);
+    const int dflt = (int)std::min<uint64_t>(
+        std::max<uint64_t>(total_bytes / d.bytes_per_wave, (uint64_t)d.min_waves), (uint64_t)d.max_waves);
+    const int target = std::max(4, env_int(d.waves_env, dflt));
+    const int unroll_env = env_int(d.unroll_env, d.unroll);
     uint64_t per_wave = (n + target - 1) / target;
     per_wave = std::min<uint64_t>(std::max<uint64_t>(per_wave, 1), 64);
     const uint64_t waves = (n + per_wave - 1) / per_wave;
@@ -143,6 +190,22 @@ extern "C" int gfd_zero_copy_gather_tokens(const uint64_t* src_addrs, void* dst,
     else
         hipLaunchKernelGGL(zc_gather_tokens<false>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, src_addrs,
                            (uint64_t)(uintptr_t)dst, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll);
+    return (int)hipGetLastError();
+}
+
+extern "C" int gfd_zero_copy_scatter_tokens(const uint64_t* dst_addrs, const void* src, uint32_t token_size,
+                                            int num_tokens, void* stream) {
+    if (num_tokens < 0 || (num_tokens > 0 && (!dst_addrs || !src || token_size == 0)))
+        return (int)hipErrorInvalidValue;
+    if (num_tokens == 0) return 0;
+    if ((uint64_t)token_size >= (1ull << 30)) return (int)hipErrorInvalidValue;  // 1 GiB per token at most
+    const Shape s = shape_for((uint64_t)num_tokens, (uint64_t)num_tokens * token_size, kScatterShape);
+    if (s.lds)
+        hipLaunchKernelGGL(zc_scatter_tokens<true>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, dst_addrs,
+                           (uint64_t)(uintptr_t)src, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll);
+    else
+        hipLaunchKernelGGL(zc_scatter_tokens<false>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, dst_addrs,
+                           (uint64_t)(uintptr_t)src, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll);
     return (int)hipGetLastError();
 }
 

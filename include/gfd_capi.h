@@ -130,12 +130,14 @@ void gfd_poller_set_gather_slice_bytes(gfd_poller_t p, uint64_t bytes);
 
 /* Host-only gather (no GPU): the staging step of the pipelined direct path.
  * Entries must have contiguous destinations; entry i lands at
- * out + (entries[i].dst - entries[0].dst).  chunk_order (optional, capacity
- * ceil(total/chunk_bytes) + 1: the first chunk is shorter) receives the chunk
- * indices in the order they were reported complete.  num_workers threads plus the caller.  (Reference
+ * out + (entries[i].dst - entries[0].dst).  chunk_order (optional) receives
+ * the chunk indices in the order they were reported complete, at most
+ * chunk_order_cap of them (every chunk but the last is at least
+ * min(64 KiB, chunk_bytes) bytes, which bounds the count).  num_workers threads plus the caller.
+ * Returns the number of chunks, or -1 on an invalid argument.  (Reference
  * counterpart: CpuPollingThread::parallel_gather, src/parallel_gather.cpp:74.) */
 int gfd_host_gather(const gfd_sg_entry* entries, int count, void* out, uint64_t chunk_bytes,
-                    uint64_t slice_bytes, int num_workers, int* chunk_order);
+                    uint64_t slice_bytes, int num_workers, int* chunk_order, int chunk_order_cap);
 
 /* ---- StagingPool (reference include/gfd/staging_pool.h:50,176) ---- */
 int gfd_staging_pool_init(int num_gpus, size_t buf_size, int numa_node);
@@ -147,8 +149,16 @@ void gfd_staging_pool_shutdown(void);
  * src_addrs: device-readable table (HBM or pinned host); tokens in pinned host memory. */
 int gfd_zero_copy_gather_tokens(const uint64_t* src_addrs, void* dst, uint32_t token_size,
                                 int num_tokens, void* stream);
-/* Arbitrary SG list (device-readable array of entries, disjoint destinations). */
+/* Arbitrary SG list (device-readable array of entries, disjoint destinations).
+ * Direction-agnostic: sources and destinations may each be HBM or pinned host
+ * memory (H2D gather, D2H offload, D2D). */
 int gfd_zero_copy_gather(const gfd_sg_entry* entries, int count, void* stream);
+/* Reverse path, no reference counterpart (the reference lists D2H as future
+ * work, docs/Architecture.md:642,993): offload of KV pages from HBM to host.
+ * dst_addrs[j] (pinned host) <- src + j*token_size (HBM), j < num_tokens.
+ * dst_addrs: device-readable table (HBM or pinned host). */
+int gfd_zero_copy_scatter_tokens(const uint64_t* dst_addrs, const void* src, uint32_t token_size,
+                                 int num_tokens, void* stream);
 
 /* ---- MoE-routed SG gather with a wave-specialised consumer (the SG
  * warp-specialised path, reference include/gfd/sg_warp_spec.cuh and
@@ -200,6 +210,14 @@ int gfd_bench_submit_direct(gfd_poller_t p, const gfd_sg_entry* entries, int cou
 int gfd_bench_zero_copy_tokens(const uint64_t* src_addrs, void* dst, uint32_t token_size,
                                int num_tokens, int warmup, int iters, double* wall_us,
                                double* event_us);
+/* The same for the offload kernel (gfd_zero_copy_scatter_tokens). */
+int gfd_bench_zero_copy_scatter_tokens(const uint64_t* dst_addrs, const void* src, uint32_t token_size,
+                                       int num_tokens, int warmup, int iters, double* wall_us,
+                                       double* event_us);
+/* hipMemcpyAsync device->host of one contiguous range over num_streams
+ * streams (the D2H link-rate reference). */
+int gfd_bench_memcpy_contiguous_d2h(void* dst, const void* src, size_t bytes, int num_streams,
+                                    int warmup, int iters, double* times_us);
 /* Queue mode: submit kernel + wait kernel, wall time launch->device sync. */
 int gfd_bench_queue(void* queue, const void* tokens, void* gpu_dst, int num_tokens,
                     uint32_t token_size, uint64_t* base_slot, int warmup, int iters,

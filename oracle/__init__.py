@@ -18,6 +18,9 @@ Pins (tests/test_oracle.py):
   * moe_routing — brute-force top-2 on tiny inputs, tie rule checked on a
     planted tie, list sizes summing to 2*tokens, stability (token order).
   * rmsnorm — closed forms (constant rows, unit weights) and scale invariance.
+  * expected_scatter (offload, no reference counterpart) — byte equality with
+    a naive per-byte loop on tiny inputs; it inverts expected_gather on the
+    tokens' bytes; bytes no token covers keep their value.
   * warp_spec_chunking — the chunk sizes the reference's heuristic gives for
     its documented targets, plus the invariants (power of two, K <= 8, tile
     divisible); warp_spec_expected — brute-force copy on tiny inputs;
@@ -64,6 +67,7 @@ def lib():
     L.oracle_fill_tokens.argtypes = [vp, sz, sz, sz, u64, ctypes.c_uint8]
     L.oracle_permutation.argtypes = [vp, sz, u64]
     L.oracle_expected_gather.argtypes = [vp, vp, vp, sz, sz, sz]
+    L.oracle_expected_scatter.argtypes = [vp, vp, vp, sz, sz, sz]
     L.oracle_gather_entries.argtypes = [vp, vp, ctypes.c_int, u64]
     L.oracle_fnv1a64.argtypes = [vp, sz]
     L.oracle_fnv1a64.restype = u64
@@ -105,6 +109,21 @@ def expected_gather(region, perm, token_size, stride):
     out = np.empty(n * token_size, dtype=np.uint8)
     perm = np.ascontiguousarray(perm, dtype=np.uint32)
     lib().oracle_expected_gather(_ptr(out), _ptr(region), _ptr(perm), n, token_size, stride)
+    return out
+
+
+def expected_scatter(region_before, tokens, perm, token_size, stride):
+    """Host region after an offload: token j of ``tokens`` (contiguous, j*T)
+    lands at perm[j]*stride; every other byte keeps its value.  No reference
+    counterpart (the reference is H2D only)."""
+    out = np.array(region_before, dtype=np.uint8, copy=True)
+    perm = np.ascontiguousarray(perm, dtype=np.uint32)
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint8)
+    n = len(perm)
+    assert tokens.nbytes >= n * token_size
+    if n:
+        assert out.nbytes >= int(perm.max()) * stride + token_size
+    lib().oracle_expected_scatter(_ptr(out), _ptr(tokens), _ptr(perm), n, token_size, stride)
     return out
 
 

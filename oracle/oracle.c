@@ -22,6 +22,8 @@
  *       store fence (src/parallel_gather.cpp:10-27).  It is the CPU baseline
  *       ("kind": "port") and a second, independently written gather that the
  *       closed form is checked against.
+ *   oracle_expected_scatter — the offload (HBM -> host) closed form, the
+ *       inverse of oracle_expected_gather; no reference counterpart.
  *   oracle_fnv1a64 — FNV-1a 64-bit hash used by the golden fixtures.
  */
 #define _GNU_SOURCE
@@ -129,6 +131,19 @@ ORACLE_API void oracle_gather_entries(uint8_t* out, const oracle_sg_entry* e, in
         uint8_t* d = out + (e[i].dst - min_dst);
         for (size_t b = 0; b < e[i].size; b++) d[b] = s[b];
     }
+}
+
+/*
+ * Offload (reverse path, no reference counterpart: the reference lists D2H
+ * as future work, docs/Architecture.md:642,993): token j of a contiguous
+ * device range, tokens + j*token_size, lands at region + perm[j]*stride.
+ * Bytes of `region` no token covers keep their value.  It is the inverse of
+ * oracle_expected_gather on the tokens' bytes.
+ */
+ORACLE_API void oracle_expected_scatter(uint8_t* region, const uint8_t* tokens, const uint32_t* perm,
+                                        size_t n, size_t token_size, size_t stride) {
+    for (size_t j = 0; j < n; j++)
+        memcpy(region + (size_t)perm[j] * stride, tokens + j * token_size, token_size);
 }
 
 ORACLE_API uint64_t oracle_fnv1a64(const uint8_t* p, size_t n) {

@@ -71,6 +71,38 @@ def test_host_gather_matches_oracle(workers, n, t, chunk, slice_):
     assert order.tolist() == list(range(len(order)))  # chunks reported in order
 
 
+def _ramp_chunks(total, chunk):
+    """Chunk count of the gather engine's ramp: a first chunk of chunk/8
+    (at least 64 KiB, at most chunk), then doubling up to chunk."""
+    first = max(chunk // 8, 64 << 10)
+    first = min(first, chunk)
+    n, end, size = 1, first, first
+    while end < total:
+        size = min(size * 2, chunk)
+        end += size
+        n += 1
+    return n
+
+
+def test_host_gather_reports_every_ramp_chunk_within_capacity():
+    """The ramp gives more chunks than ceil(total / chunk) + 1: 4 MiB in
+    2 MiB chunks is 256 K + 512 K + 1 M + 2 M + 256 K = 5 chunks.  All are
+    reported, and a caller array shorter than that is never written past."""
+    n, t = 1024, 4096
+    region, perm, stride = _layout(n, t)
+    entries = gfd_amd.make_entries(region.ctypes.data + perm.astype(np.uint64) * np.uint64(stride), 1 << 44, t)
+    out = np.zeros(n * t, np.uint8)
+    order = gfd_amd.host_gather(entries, n, out, chunk_bytes=2 << 20, num_workers=2)
+    assert len(order) == _ramp_chunks(n * t, 2 << 20) == 5
+    assert order.tolist() == list(range(5))
+    guard = np.full(8, -7, dtype=np.int32)  # room for 2, then guard words
+    got = gfd_amd.lib().gfd_host_gather(ctypes.cast(entries, ctypes.c_void_p), n, out.ctypes.data, 2 << 20, 0, 2,
+                                        guard.ctypes.data, 2)
+    assert got == 5
+    assert guard[:2].tolist() == [0, 1] and (guard[2:] == -7).all()
+    assert (out == oracle.expected_gather(region, perm, t, stride)).all()
+
+
 def test_host_gather_mixed_sizes():
     rng = np.random.default_rng(7)
     sizes = rng.integers(1, 9000, 300)

@@ -92,6 +92,44 @@ def test_expected_gather_matches_naive(n, t):
     assert (oracle.expected_gather(region, perm, t, stride) == naive_gather(region, perm, t, stride)).all()
 
 
+def naive_scatter(region, tokens, perm, t, stride):
+    out = bytearray(region.tobytes())
+    for j, p in enumerate(perm):
+        for b in range(t):
+            out[int(p) * stride + b] = int(tokens[j * t + b])
+    return np.frombuffer(bytes(out), np.uint8)
+
+
+@pytest.mark.parametrize("n,t,stride", [(1, 16, 16), (5, 7, 9), (33, 100, 200), (64, 64, 128)])
+def test_expected_scatter_matches_naive(n, t, stride):
+    rng = np.random.default_rng(n * 7 + t)
+    region = rng.integers(0, 256, n * stride + 5, dtype=np.uint8)
+    tokens = rng.integers(0, 256, n * t, dtype=np.uint8)
+    perm = oracle.permutation(n)
+    got = oracle.expected_scatter(region, tokens, perm, t, stride)
+    assert (got == naive_scatter(region, tokens, perm, t, stride)).all()
+
+
+@pytest.mark.parametrize("n,t", [(3, 1), (100, 48), (512, 4096)])
+def test_expected_scatter_inverts_gather(n, t):
+    """Offload then gather with the same order returns the tokens; bytes no
+    token covers (the 2x-stride gaps) keep the sentinel."""
+    rng = np.random.default_rng(n + t)
+    stride = 2 * t
+    tokens = rng.integers(0, 256, n * t, dtype=np.uint8)
+    perm = oracle.permutation(n)
+    region = np.full(n * stride, 0xCD, np.uint8)
+    out = oracle.expected_scatter(region, tokens, perm, t, stride)
+    assert (oracle.expected_gather(out, perm, t, stride) == tokens).all()
+    assert (out.reshape(n, 2, t)[:, 1, :] == 0xCD).all()
+    # The inverse order in place of the order (a transposed index) is caught
+    # whenever the order is not its own inverse.
+    inv = np.argsort(perm).astype(np.uint32)
+    if not (inv == perm).all():
+        wrong = oracle.expected_scatter(region, tokens, inv, t, stride)
+        assert not (oracle.expected_gather(wrong, perm, t, stride) == tokens).all()
+
+
 def test_gather_entries_closed_form_with_gaps():
     rng = np.random.default_rng(1)
     src = rng.integers(0, 256, 50000, dtype=np.uint8)
