@@ -399,6 +399,9 @@ void CpuPollingThread::polling_loop() {
                 trace(TRACE_BATCH_FIRST, (uint32_t)(read % QUEUE_SIZE), read);
             }
             do {
+                // The ring lines were last written by the GPU, so each is a
+                // cache miss: fetch a few descriptors ahead of the reads.
+                _mm_prefetch((const char*)&queue_->entries[(read + 16) % QUEUE_SIZE], _MM_HINT_T0);
                 take(d);
                 read++;
                 if (n == 1) threshold = batch[0].size <= 2048 ? BATCH_THRESHOLD_SMALL : BATCH_THRESHOLD;
@@ -489,6 +492,16 @@ void CpuPollingThread::copy_runs(const SGEntry* e, int count) {
 
 // Gather a dst-contiguous list through the next staging buffer; false if it
 // does not fit (the caller then copies runs directly).
+void CpuPollingThread::trace_gather_run() {
+    if (!gather_ || !trace_on_.load(std::memory_order_relaxed)) return;
+    const GatherEngine::RunTimes rt = gather_->last_run();
+    trace_at(rt.entry, TRACE_GATHER_ENTRY, 0, 0);
+    trace_at(rt.idle, TRACE_GATHER_IDLE, 0, 0);
+    trace_at(rt.built, TRACE_GATHER_BUILT, 0, 0);
+    trace_at(rt.published, TRACE_GATHER_PUBLISHED, (uint32_t)rt.sleepers, 0);
+    trace_at(rt.first_slice, TRACE_GATHER_FIRST_SLICE, (uint32_t)rt.copiers, 0);
+}
+
 bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_t total, const DstRun* runs,
                                               int nruns) {
     if (num_staging_bufs_ == 0 || total > staging_buffer_size_ || !gather_) return false;
@@ -504,6 +517,7 @@ bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_
             gather_->run(e, count, total, staging_bufs_[cur], direct_chunk_bytes_, run_copy_chunk, &rctx);
         else
             gather_->run(e, count, total, staging_bufs_[cur], direct_chunk_bytes_, issue_chunk, &ctx);
+        trace_gather_run();
     }
     if (rctx.err && !ctx.err) ctx.err = rctx.err;
     const uint64_t t2 = now_us();

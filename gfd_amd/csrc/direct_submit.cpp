@@ -194,14 +194,7 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
             gather_->run(entries, count, total, direct_staging_, direct_chunk_bytes_, direct_chunk, &ctx,
                          uniform ? 1 : 0);
             err = ctx.err;
-            if (trace_on_.load(std::memory_order_relaxed)) {
-                const GatherEngine::RunTimes rt = gather_->last_run();
-                trace_at(rt.entry, TRACE_GATHER_ENTRY, 0, 0);
-                trace_at(rt.idle, TRACE_GATHER_IDLE, 0, 0);
-                trace_at(rt.built, TRACE_GATHER_BUILT, 0, 0);
-                trace_at(rt.published, TRACE_GATHER_PUBLISHED, (uint32_t)rt.sleepers, 0);
-                trace_at(rt.first_slice, TRACE_GATHER_FIRST_SLICE, (uint32_t)rt.copiers, 0);
-            }
+            trace_gather_run();
         } else {
             size_t off = 0;
             for (int i = 0; i < count; i++) {

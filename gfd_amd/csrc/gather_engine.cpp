@@ -325,7 +325,13 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
         for (int i = 1; i < count && uniform; i++) uniform = entries[i].size == esz;
     }
     uniform = uniform && esz > 0;
-    const size_t first_slice = std::max<size_t>(16 * 1024, std::min(slice_bytes_, chunk_end_[0] / 16));
+    // Slices: about two per thread for the whole job, between 16 KiB and
+    // slice_bytes_.  A small job (a 0.5 MiB queue batch) cut into 128 KiB
+    // slices leaves a whole chunk to one thread while the others idle.
+    const size_t threads = (size_t)num_workers() + 1;
+    const size_t job_slice = std::max<size_t>(
+        16 * 1024, std::min(slice_bytes_, ((total / (2 * threads)) + 4095) & ~(size_t)4095));
+    const size_t first_slice = std::max<size_t>(16 * 1024, std::min(job_slice, chunk_end_[0] / 16));
     slices_.clear();
     int e = 0;
     size_t eo = 0;
@@ -335,7 +341,7 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     size_t q_sb = 0, r_sb = 0, cur_sb = 0;
     for (int c = 0; c < nchunks; c++) {
         const size_t cend = chunk_end_[c];
-        const size_t sb = c == 0 ? first_slice : slice_bytes_;
+        const size_t sb = c == 0 ? first_slice : job_slice;
         while (pos < cend) {
             const size_t len = std::min(sb, cend - pos);
             if (uniform) {

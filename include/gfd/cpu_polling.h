@@ -160,6 +160,7 @@ public:
     uint64_t copy_clock_ns() const;
     void trace(uint32_t kind, uint32_t a, uint64_t b);
     void trace_at(uint64_t t_ns, uint32_t kind, uint32_t a, uint64_t b);
+    void trace_gather_run();  // the last gather job's phases (when tracing)
 
     // Host-side effects applied once a batch's copies have completed.
     struct CompletionSlot {
