@@ -100,10 +100,15 @@ int gfd_memcpy_d2h(void* dst, const void* src, size_t n) {
 }
 int gfd_memcpy_d2d(void* dst, const void* src, size_t n) {
     CAPI_CHECK(gfd_hip_memcpy_d2d((uint64_t)(uintptr_t)dst, (uint64_t)(uintptr_t)src, n), "hipMemcpy D2D");
+    CAPI_CHECK(gfd_hip_device_synchronize(), "hipDeviceSynchronize");  // device-to-device copies may return early
     return 0;
 }
 int gfd_memset_device(void* dst, int value, size_t n) {
+    // hipMemset of device memory may return before the fill has run (as
+    // cudaMemset may); SDMA copies issued next by submit_direct are not
+    // ordered after it, so wait.
     CAPI_CHECK(gfd_hip_memset_d8((uint64_t)(uintptr_t)dst, value, n), "hipMemset");
+    CAPI_CHECK(gfd_hip_device_synchronize(), "hipDeviceSynchronize");
     return 0;
 }
 int gfd_stream_create(void** s) { CAPI_CHECK(gfd_hip_stream_create(s), "hipStreamCreate"); return 0; }

@@ -264,6 +264,26 @@ GatherEngine::ListScan GatherEngine::scan(const SGEntry* entries, int count) {
     return r;
 }
 
+int GatherEngine::chunk_of(int s) const {
+    if (!lazy_) return slices_[s].chunk;
+    int lo = 0, hi = (int)chunk_first_.size() - 1;  // chunk_first_ is strictly increasing
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (chunk_first_[mid] <= s) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+GatherEngine::Slice GatherEngine::slice_at(int s) const {
+    if (!lazy_) return slices_[s];
+    const int c = chunk_of(s);
+    const size_t sb = chunk_slice_[c];
+    const size_t pos = (c ? chunk_end_[c - 1] : 0) + (size_t)(s - chunk_first_[c]) * sb;
+    const size_t len = std::min(sb, chunk_end_[c] - pos);
+    return Slice{(int)(pos / esz_), pos % esz_, pos, len, c};
+}
+
 // Claim and copy slices until none are left.  Returns after the last claim.
 void GatherEngine::do_slices() {
     const int ns = num_slices_;
@@ -271,10 +291,11 @@ void GatherEngine::do_slices() {
     for (;;) {
         const int s = next_slice_.fetch_add(1, std::memory_order_relaxed);
         if (s >= ns) break;
-        copy_slice(slices_[s]);
+        const Slice sl = slice_at(s);
+        copy_slice(sl);
         store_fence();
         note_slice(counted);
-        remaining_[slices_[s].chunk].fetch_sub(1, std::memory_order_release);
+        remaining_[sl.chunk].fetch_sub(1, std::memory_order_release);
     }
 }
 
@@ -332,32 +353,38 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     const size_t job_slice = std::max<size_t>(
         16 * 1024, std::min(slice_bytes_, ((total / (2 * threads)) + 4095) & ~(size_t)4095));
     const size_t first_slice = std::max<size_t>(16 * 1024, std::min(job_slice, chunk_end_[0] / 16));
-    slices_.clear();
-    int e = 0;
-    size_t eo = 0;
-    size_t pos = 0;
-    // Uniform sizes: (entry, offset) advance by whole slices without dividing
-    // per slice (two 64-bit divisions per slice cost ~4 us for 32 MiB).
-    size_t q_sb = 0, r_sb = 0, cur_sb = 0;
-    for (int c = 0; c < nchunks; c++) {
-        const size_t cend = chunk_end_[c];
-        const size_t sb = c == 0 ? first_slice : job_slice;
-        while (pos < cend) {
-            const size_t len = std::min(sb, cend - pos);
-            if (uniform) {
-                slices_.push_back(Slice{e, eo, pos, len, c});
-                if (len != cur_sb) {
-                    cur_sb = len;
-                    q_sb = len / esz;
-                    r_sb = len % esz;
-                }
-                e += (int)q_sb;
-                eo += r_sb;
-                if (eo >= esz) {
-                    eo -= esz;
-                    e++;
-                }
-            } else {
+    if (remaining_cap_ < nchunks) {
+        remaining_.reset(new std::atomic<int>[nchunks]);
+        remaining_cap_ = nchunks;
+    }
+    lazy_ = uniform;
+    int nslices = 0;
+    if (uniform) {
+        // Slice s of chunk c starts (s - chunk_first_[c]) slices into it.
+        esz_ = esz;
+        chunk_first_.resize(nchunks);
+        chunk_slice_.resize(nchunks);
+        size_t start = 0;
+        for (int c = 0; c < nchunks; c++) {
+            const size_t sb = c == 0 ? first_slice : job_slice;
+            const int k = (int)((chunk_end_[c] - start + sb - 1) / sb);
+            chunk_first_[c] = nslices;
+            chunk_slice_[c] = sb;
+            remaining_[c].store(k, std::memory_order_relaxed);
+            nslices += k;
+            start = chunk_end_[c];
+        }
+    } else {
+        slices_.clear();
+        int e = 0;
+        size_t eo = 0;
+        size_t pos = 0;
+        for (int c = 0; c < nchunks; c++) {
+            const size_t cend = chunk_end_[c];
+            const size_t sb = c == 0 ? first_slice : job_slice;
+            int k = 0;
+            while (pos < cend) {
+                const size_t len = std::min(sb, cend - pos);
                 while (e < count && eo == entries[e].size) {  // skip spent / empty entries
                     e++;
                     eo = 0;
@@ -375,21 +402,18 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
                         eo = 0;
                     }
                 }
+                pos += len;
+                k++;
             }
-            pos += len;
+            remaining_[c].store(k, std::memory_order_relaxed);
         }
+        nslices = (int)slices_.size();
     }
-    if (remaining_cap_ < nchunks) {
-        remaining_.reset(new std::atomic<int>[nchunks]);
-        remaining_cap_ = nchunks;
-    }
-    for (int c = 0; c < nchunks; c++) remaining_[c].store(0, std::memory_order_relaxed);
-    for (const Slice& s : slices_) remaining_[s.chunk].fetch_add(1, std::memory_order_relaxed);
 
     entries_ = entries;
     count_ = count;
     staging_ = staging;
-    num_slices_ = (int)slices_.size();
+    num_slices_ = nslices;
     next_slice_.store(0, std::memory_order_relaxed);
     scan_job_ = false;
 
@@ -420,13 +444,14 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
         // the hand-off of this one by that long.  With no such slice left it
         // spins until the workers finish the chunk.
         const int peek = next_slice_.load(std::memory_order_relaxed);
-        if (caller_copy && (nw == 0 || (peek < ns && slices_[peek].chunk <= ready))) {
+        if (caller_copy && (nw == 0 || (peek < ns && chunk_of(peek) <= ready))) {
             const int s = next_slice_.fetch_add(1, std::memory_order_relaxed);
             if (s < ns) {
-                copy_slice(slices_[s]);
+                const Slice sl = slice_at(s);
+                copy_slice(sl);
                 store_fence();
                 note_slice(counted);
-                remaining_[slices_[s].chunk].fetch_sub(1, std::memory_order_release);
+                remaining_[sl.chunk].fetch_sub(1, std::memory_order_release);
                 continue;
             }
         }

@@ -70,6 +70,9 @@ int gfd_host_alloc(void** p, size_t bytes, unsigned flags);
 int gfd_host_free(void* p);
 int gfd_device_alloc(void** p, size_t bytes);           /* cudaMalloc */
 int gfd_device_free(void* p);
+/* Blocking helpers: each returns once the operation is complete on the
+ * device, so copies issued afterwards on other engines (SDMA, other streams)
+ * cannot be overtaken by it. */
 int gfd_memcpy_h2d(void* dst, const void* src, size_t n);
 int gfd_memcpy_d2h(void* dst, const void* src, size_t n);
 int gfd_memcpy_d2d(void* dst, const void* src, size_t n);
