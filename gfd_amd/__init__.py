@@ -165,6 +165,7 @@ def _declare(L):
         "gfd_bench_submit_direct": ([vp, vp, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_zero_copy_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
         "gfd_zero_copy_scatter_tokens": ([vp, vp, c_u32, c_int, vp], c_int),
+        "gfd_plan_expert_entries": ([vp, c_int, c_int, vp, c_u64, vp, c_u32, vp, vp, vp], c_int),
         "gfd_bench_zero_copy_scatter_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
         "gfd_bench_memcpy_contiguous_d2h": ([vp, vp, ctypes.c_size_t, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_queue": ([vp, vp, vp, c_int, c_u32, ctypes.POINTER(c_u64), c_int, c_int, c_u64, pd], c_int),
@@ -446,6 +447,15 @@ def host_gather(entries, count, out, chunk_bytes=0, slice_bytes=0, num_workers=0
 def zero_copy_gather_tokens(src_addrs_ptr, dst_ptr, token_size, num_tokens, stream=None):
     _check(lib().gfd_zero_copy_gather_tokens(src_addrs_ptr, dst_ptr, token_size, num_tokens, stream),
            "gfd_zero_copy_gather_tokens")
+
+
+def plan_expert_entries(routing_ptr, num_tokens, expert, cpu_base, stride, gpu_dst, token_size, entries_ptr,
+                        count_ptr, stream=None):
+    """GPU-built SG list (examples/03_gpu_planned_transfer.cu): the tokens
+    routed to `expert`, in token order, as gfd_sg_entry records written to
+    entries_ptr (pinned host or HBM); the match count goes to count_ptr."""
+    _check(lib().gfd_plan_expert_entries(routing_ptr, num_tokens, expert, cpu_base, stride, gpu_dst, token_size,
+                                         entries_ptr, count_ptr, stream), "gfd_plan_expert_entries")
 
 
 def zero_copy_scatter_tokens(dst_addrs_ptr, src_ptr, token_size, num_tokens, stream=None):

@@ -156,6 +156,15 @@ int gfd_zero_copy_gather_tokens(const uint64_t* src_addrs, void* dst, uint32_t t
  * Direction-agnostic: sources and destinations may each be HBM or pinned host
  * memory (H2D gather, D2H offload, D2D). */
 int gfd_zero_copy_gather(const gfd_sg_entry* entries, int count, void* stream);
+/* GPU-built SG list for submit_direct (the pattern of examples/03_gpu_planned_transfer.cu:32-66,
+ * plan_compact_kernel + plan_build_sg_kernel): the tokens t with routing[t] == expert, in token
+ * order, become entries[k] = {gpu_dst + k*token_size, cpu_base + t*stride, token_size}, and
+ * *count = their number.  routing: device-readable int[num_tokens]; entries and count may be
+ * pinned host memory (the list is then ready for submit_direct once the stream is synchronised)
+ * or HBM.  entries must hold every match.  Stable order, unlike the reference's atomicAdd slots. */
+int gfd_plan_expert_entries(const int* routing, int num_tokens, int expert, const void* cpu_base,
+                            uint64_t stride, void* gpu_dst, uint32_t token_size, gfd_sg_entry* entries,
+                            int* count, void* stream);
 /* Reverse path, no reference counterpart (the reference lists D2H as future
  * work, docs/Architecture.md:642,993): offload of KV pages from HBM to host.
  * dst_addrs[j] (pinned host) <- src + j*token_size (HBM), j < num_tokens.
