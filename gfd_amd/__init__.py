@@ -166,6 +166,7 @@ def _declare(L):
         "gfd_bench_zero_copy_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
         "gfd_zero_copy_scatter_tokens": ([vp, vp, c_u32, c_int, vp], c_int),
         "gfd_plan_expert_entries": ([vp, c_int, c_int, vp, c_u64, vp, c_u32, vp, vp, vp], c_int),
+        "gfd_queue_fused_checksums": ([vp, vp, vp, c_int, c_u32, c_u64, c_u64, vp, vp, vp], c_int),
         "gfd_bench_zero_copy_scatter_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
         "gfd_bench_memcpy_contiguous_d2h": ([vp, vp, ctypes.c_size_t, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_queue": ([vp, vp, vp, c_int, c_u32, ctypes.POINTER(c_u64), c_int, c_int, c_u64, pd], c_int),

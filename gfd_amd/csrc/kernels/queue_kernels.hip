@@ -29,6 +29,59 @@ __global__ void queue_wait_kernel(gfd::DescriptorQueue* queue, uint64_t expected
     }
 }
 
+// Fused request + wait + consume in one launch (the reference's
+// examples/01_basic_transfer.cu:27-85 fused_prefetch_and_compute_kernel):
+// every lane writes and commits its token's descriptor; lane 0 of each
+// workgroup waits (bounded) until the poller has landed all of them; then the
+// workgroup's waves read their tokens from HBM and write each token's u32-word
+// checksum (an integer sum, so the result is exact).  Every workgroup of the
+// launch must be resident at once (it waits for descriptors the others
+// write): num_tokens <= QUEUE_SIZE keeps the grid at 64 workgroups.
+__global__ __launch_bounds__(256) void queue_fused_checksum_kernel(gfd::DescriptorQueue* queue,
+                                                                   const gfd::TokenInfo* __restrict__ tokens,
+                                                                   void* gpu_dst, int num_tokens, uint32_t token_size,
+                                                                   uint64_t base_slot, uint64_t max_ticks,
+                                                                   unsigned long long* __restrict__ sums,
+                                                                   int* status) {
+    __shared__ int landed;
+    const int tid = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    const bool active = tid < num_tokens;
+    if (active)
+        gfd::device::write_descriptor(queue, base_slot, tid, tokens[tid].cpu_addr, gpu_dst, token_size, num_tokens);
+    gfd::device::fence_and_commit(queue, base_slot, tid, active);
+    if (threadIdx.x == 0)
+        landed = gfd::device::wait_for_completion(queue, base_slot + (uint64_t)num_tokens, max_ticks) ? 1 : 0;
+    __syncthreads();
+    if (!landed) {
+        if (threadIdx.x == 0) __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        return;
+    }
+    // The copy engines wrote the tokens: every lane acquires before reading.
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+    const int lane = (int)(threadIdx.x & 63), wave = (int)(threadIdx.x >> 6), nwaves = (int)(blockDim.x >> 6);
+    const int first = (int)(blockIdx.x * blockDim.x), last = min(num_tokens, first + (int)blockDim.x);
+    const uint32_t nw = token_size / 4;
+    for (int j = first + wave; j < last; j += nwaves) {
+        const uint8_t* p = (const uint8_t*)gpu_dst + (uint64_t)j * token_size;
+        unsigned long long acc = 0;
+        if (((uintptr_t)p & 3) == 0) {
+            const uint32_t* w = (const uint32_t*)p;
+            for (uint32_t k = (uint32_t)lane; k < nw; k += 64) acc += w[k];
+        } else {
+            for (uint32_t k = (uint32_t)lane; k < nw; k += 64)
+                acc += (uint32_t)p[4 * k] | ((uint32_t)p[4 * k + 1] << 8) | ((uint32_t)p[4 * k + 2] << 16) |
+                       ((uint32_t)p[4 * k + 3] << 24);
+        }
+        for (uint32_t b = nw * 4 + (uint32_t)lane; b < token_size; b += 64) acc += p[b];
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)acc, o, 64);
+            const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(acc >> 32), o, 64);
+            acc += ((unsigned long long)hi << 32) | lo;
+        }
+        if (lane == 0) sums[j] = acc;
+    }
+}
+
 }  // namespace
 
 extern "C" int gfd_queue_alloc(void** queue) {
@@ -58,6 +111,23 @@ extern "C" int gfd_queue_submit_tokens(void* queue, const void* tokens, void* gp
     const int blocks = (num_tokens + threads - 1) / threads;
     hipLaunchKernelGGL(queue_submit_tokens_kernel, dim3(blocks), dim3(threads), 0, (hipStream_t)stream, q,
                        (const gfd::TokenInfo*)tokens, gpu_dst, num_tokens, token_size, base_slot);
+    return (int)hipGetLastError();
+}
+
+extern "C" int gfd_queue_fused_checksums(void* queue, const void* tokens, void* gpu_dst, int num_tokens,
+                                         uint32_t token_size, uint64_t base_slot, uint64_t timeout_us,
+                                         unsigned long long* sums, int* status, void* stream) {
+    if (!queue || !status || !sums || num_tokens <= 0 || !tokens || !gpu_dst || token_size == 0)
+        return (int)hipErrorInvalidValue;
+    auto* q = (gfd::DescriptorQueue*)queue;
+    const uint64_t read = __atomic_load_n(&q->read_idx, __ATOMIC_ACQUIRE);
+    if (num_tokens > gfd::QUEUE_SIZE || base_slot < read || base_slot + (uint64_t)num_tokens - read > (uint64_t)gfd::QUEUE_SIZE)
+        return (int)hipErrorInvalidValue;
+    const uint64_t ticks = timeout_us * (gfd::device::kWallClockHz / 1000000ull);
+    const int threads = 256;
+    const int blocks = (num_tokens + threads - 1) / threads;
+    hipLaunchKernelGGL(queue_fused_checksum_kernel, dim3(blocks), dim3(threads), 0, (hipStream_t)stream, q,
+                       (const gfd::TokenInfo*)tokens, gpu_dst, num_tokens, token_size, base_slot, ticks, sums, status);
     return (int)hipGetLastError();
 }
 

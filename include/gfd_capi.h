@@ -205,6 +205,14 @@ int gfd_queue_submit_tokens(void* queue, const void* tokens, void* gpu_dst, int 
  * host-visible int) receives 0 on completion, 1 on timeout. */
 int gfd_queue_wait(void* queue, uint64_t expected_done, uint64_t timeout_us, int* status,
                    void* stream);
+/* fused_prefetch_and_compute_kernel (examples/01_basic_transfer.cu:27-85) in one launch:
+ * descriptors as gfd_queue_submit_tokens, then each workgroup waits (bounded by timeout_us)
+ * until the poller has landed all num_tokens, then writes sums[j] = the u32-word checksum of
+ * token j as landed in HBM (little-endian words, a trailing partial word byte by byte).
+ * *status (set to 0 by the caller) becomes 1 if a wait timed out.  num_tokens <= QUEUE_SIZE. */
+int gfd_queue_fused_checksums(void* queue, const void* tokens, void* gpu_dst, int num_tokens,
+                              uint32_t token_size, uint64_t base_slot, uint64_t timeout_us,
+                              unsigned long long* sums, int* status, void* stream);
 
 /* ---- measurement helpers (examples/04_benchmark.cu:92-115 and the peak
  * reference copy); fill times_us[iters] with wall times ---- */

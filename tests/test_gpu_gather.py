@@ -326,3 +326,48 @@ def test_queue_mode_parity(n, t):
         p.stop()
         p.close()
         q.free()
+
+
+@pytest.mark.parametrize("n,t", [(1024, 4096), (3000, 1000), (1, 4096), (16384, 512)])
+def test_queue_fused_request_wait_consume(n, t):
+    """examples/01_basic_transfer.cu fused kernel: one launch writes the
+    descriptors, waits in-kernel for the poller, then reads the landed tokens
+    (u32-word checksum per token, exact).  1024 x 4 KiB uses the example's
+    floats t*1000+d (:138-142); two rounds move the ring's base slot."""
+    log("queue fused n=%d t=%d" % (n, t))
+    L = Layout(n, t)
+    if (n, t) == (1024, 4096):
+        vals = L.host.array.reshape(n, 2, t)[:, 0, :].view(np.float32)
+        vals[:] = (np.arange(n, dtype=np.float32)[:, None] * 1000 + np.arange(t // 4, dtype=np.float32)[None, :])
+        L.expected = oracle.expected_gather(L.host.array, L.perm, t, L.stride)
+    want = [oracle.u32_word_checksum(L.expected[j * t:(j + 1) * t]) for j in range(n)]
+    q = gfd_amd.DescriptorQueue()
+    p = gfd_amd.CpuPollingThread(q, L.dst.ptr, L.host.ptr, L.host.nbytes, numa_node=-1)
+    try:
+        assert p.init_copy_engine()
+        p.start()
+        tokens = np.zeros((n, 2), np.uint64)
+        tokens[:, 0] = L.src_addrs
+        tokens[:, 1] = np.arange(n, dtype=np.uint64)
+        dtok = gfd_amd.DeviceBuffer(tokens.nbytes)
+        dtok.upload(tokens)
+        sums = gfd_amd.DeviceBuffer(n * 8)
+        status = gfd_amd.HostBuffer(64)
+        for rep in range(2):
+            sums.fill(0)
+            status.array.view(np.int32)[0] = 0
+            rc = gfd_amd.lib().gfd_queue_fused_checksums(q.ptr, dtok.ptr, L.dst.ptr, n, t, rep * n, 10_000_000,
+                                                         sums.ptr, status.ptr, None)
+            assert rc == 0, gfd_amd.lib().gfd_last_error()
+            gfd_amd.synchronize()
+            assert int(status.array.view(np.int32)[0]) == 0, "an in-kernel wait timed out"
+            L.check()
+            got = sums.download().view(np.uint64)
+            bad = [j for j in range(n) if int(got[j]) != want[j]]
+            assert not bad, "token %d checksum %d != %d" % (bad[0], int(got[bad[0]]), want[bad[0]])
+            L.reset()
+        assert q.done_idx == 2 * n
+    finally:
+        p.stop()
+        p.close()
+        q.free()
