@@ -167,6 +167,10 @@ def _declare(L):
         "gfd_zero_copy_scatter_tokens": ([vp, vp, c_u32, c_int, vp], c_int),
         "gfd_plan_expert_entries": ([vp, c_int, c_int, vp, c_u64, vp, c_u32, vp, vp, vp], c_int),
         "gfd_queue_fused_checksums": ([vp, vp, vp, c_int, c_u32, c_u64, c_u64, vp, vp, vp], c_int),
+        "gfd_tiled_queue_alloc": ([pvp, c_u32, c_u32, c_u32, c_u32, c_int], c_int),
+        "gfd_tiled_queue_free": ([vp], c_int),
+        "gfd_tiled_queue_reset": ([vp], c_int),
+        "gfd_tiled_poller_run": ([vp, vp, vp, c_int, c_u64, vp, vp, vp], c_int),
         "gfd_bench_zero_copy_scatter_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
         "gfd_bench_memcpy_contiguous_d2h": ([vp, vp, ctypes.c_size_t, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_queue": ([vp, vp, vp, c_int, c_u32, ctypes.POINTER(c_u64), c_int, c_int, c_u64, pd], c_int),
@@ -397,6 +401,53 @@ class CpuPollingThread:
             self.close()
         except Exception:
             pass
+
+
+class TiledQueue:
+    """gfd::TiledQueue (reference include/gfd/tiled_queue.h:8-43) in
+    fine-grained host memory; ``ptr`` also serves as its DescriptorQueue."""
+
+    def __init__(self, total_tiles, tokens_per_tile, tokens_per_chunk, token_size, device_signals=True):
+        p = ctypes.c_void_p()
+        _check(lib().gfd_tiled_queue_alloc(ctypes.byref(p), total_tiles, tokens_per_tile, tokens_per_chunk,
+                                           token_size, int(bool(device_signals))), "gfd_tiled_queue_alloc")
+        self.ptr = p.value
+        self.total_tiles = total_tiles
+        # TiledQueue: base (QUEUE_SIZE descriptors + 3 indices, 64-aligned),
+        # TileScheduler (64 B), tile_chunk_done[MAX_TILES], d_tile_chunk_done.
+        base_bytes = (QUEUE_SIZE * 64 + 3 * 8 + 63) // 64 * 64
+        self._idx = np.ctypeslib.as_array((ctypes.c_uint64 * 3).from_address(self.ptr + QUEUE_SIZE * 64))
+        self._done = np.ctypeslib.as_array((ctypes.c_uint64 * MAX_TILES).from_address(self.ptr + base_bytes + 64))
+        self._dptr = (ctypes.c_uint64 * 1).from_address(self.ptr + base_bytes + 64 + MAX_TILES * 8)
+
+    def reset(self):
+        _check(lib().gfd_tiled_queue_reset(self.ptr), "gfd_tiled_queue_reset")
+
+    @property
+    def done_idx(self):
+        return int(self._idx[2])
+
+    def tile_progress(self):
+        """Per-tile cumulative landed-token counts (HBM words when allocated there)."""
+        n = self.total_tiles
+        if self._dptr[0]:
+            out = np.zeros(n, np.uint64)
+            _check(lib().gfd_memcpy_d2h(out.ctypes.data, self._dptr[0], n * 8), "gfd_memcpy_d2h")
+            return out
+        return self._done[:n].copy()
+
+    def free(self):
+        if self.ptr:
+            self._idx = self._done = self._dptr = None
+            lib().gfd_tiled_queue_free(self.ptr)
+            self.ptr = None
+
+
+def tiled_poller_run(tq, cpu_base, gpu_base, sums_ptr, status_ptr, whole_tile=False, timeout_us=10_000_000,
+                     stream=None):
+    """Kernel-driven tiled mode (see gfd_tiled_poller_run in include/gfd_capi.h)."""
+    _check(lib().gfd_tiled_poller_run(tq.ptr, cpu_base, gpu_base, int(bool(whole_tile)), timeout_us, sums_ptr,
+                                      status_ptr, stream), "gfd_tiled_poller_run")
 
 
 class DescriptorQueue:

@@ -171,19 +171,23 @@ Status CopyEngineManager::submit_scatter_gather(const SGEntry* entries, int coun
 }
 
 Status CopyEngineManager::submit_after(DevicePtr dst, const void* src, size_t size, uint64_t after_begin,
-                                       uint64_t after_end) {
+                                       uint64_t after_end, uint64_t also_after) {
     if (!initialized_) return GFD_SUCCESS;
     if (backend_ == BACKEND_SDMA) {
         uint64_t deps[16];
         int nd = 0;
         const uint64_t tail = sdma_->retire();
         if (after_begin < tail) after_begin = tail;
-        if (after_end - after_begin > 16) {
+        const bool extra = also_after != kNoFence && also_after >= tail &&
+                           (also_after < after_begin || also_after >= after_end);
+        const uint64_t room = extra ? 15 : 16;
+        if (after_end > after_begin && after_end - after_begin > room) {
             // Too many to chain on the engine: wait for the older ones here.
-            if (sdma_->wait(after_end - 16) != 0) return -1;
-            after_begin = after_end - 16;
+            if (sdma_->wait(after_end - room) != 0) return -1;
+            after_begin = after_end - room;
         }
         for (uint64_t f = after_begin; f < after_end; f++) deps[nd++] = f;
+        if (extra) deps[nd++] = also_after;
         int st = sdma_->copy(last_channel_, dst, src, size, nullptr, deps, nd);
         if (st) return st;
     } else {

@@ -582,9 +582,15 @@ void CpuPollingThread::signal_device_u64(uint64_t* dst, uint64_t value, uint64_t
     ce_manager_.wait_fence(signal_fence_[slot]);  // previous use of this value slot has finished
     signal_values_[slot] = value;
     const uint64_t end = ce_manager_.fence();
+    // Chained after the previous flag write as well as after its own batch's
+    // copies: two progress writes to one tile issued back to back could
+    // otherwise land out of order on different engines and leave the older,
+    // smaller count in place.
     if (ce_manager_.submit_after((DevicePtr)(uintptr_t)dst, &signal_values_[slot], sizeof(uint64_t), after_begin,
-                                 end) != 0)
+                                 end, last_signal_copy_) != 0)
         GFD_LOG_ERROR("flag write submission failed\n");
+    else
+        last_signal_copy_ = end;  // the copy just issued got fence number `end`
     signal_fence_[slot] = ce_manager_.fence();
 }
 

@@ -92,10 +92,12 @@ public:
     Status submit_on_channel(int channel, DevicePtr dst, const void* src, size_t size);
 
     // Enqueue a small copy that starts only after the copies with fence
-    // numbers in [after_begin, after_end) have finished (ordered on the copy
-    // engines, no host wait).  Used for completion flags in HBM.
+    // numbers in [after_begin, after_end) have finished, and after copy
+    // `also_after` if given (ordered on the copy engines, no host wait).
+    // Used for completion flags in HBM.
+    static constexpr uint64_t kNoFence = ~0ull;
     Status submit_after(DevicePtr dst, const void* src, size_t size, uint64_t after_begin,
-                        uint64_t after_end);
+                        uint64_t after_end, uint64_t also_after = kNoFence);
 
     // Fences: every copy gets the next fence number.  fence() is the number the
     // next copy will get; fence_done(f) is true once every copy below f has

@@ -238,6 +238,9 @@ private:
     uint64_t* signal_values_ = nullptr;
     uint64_t signal_fence_[SIGNAL_SLOTS] = {};
     int signal_next_ = 0;
+    // Fence number of the last flag write into HBM: each one is ordered after
+    // the previous, so a progress word's final value is its latest.
+    uint64_t last_signal_copy_ = CopyEngineManager::kNoFence;
     int list_done_on_device_ = -1;  // -1 unknown, 0 host memory, 1 HBM
     int tile_done_on_device_ = -1;
 

@@ -205,6 +205,23 @@ int gfd_queue_submit_tokens(void* queue, const void* tokens, void* gpu_dst, int 
  * host-visible int) receives 0 on completion, 1 on timeout. */
 int gfd_queue_wait(void* queue, uint64_t expected_done, uint64_t timeout_us, int* status,
                    void* stream);
+/* ---- the poller's tiled mode (TiledQueue, include/gfd/tiled_queue.h; reference
+ * include/gfd/tiled_queue.h:8-43) driven by a kernel through include/gfd/device_primitives.h ---- */
+/* TiledQueue in fine-grained host memory with its scheduler fields set; device_signals != 0
+ * also allocates d_tile_chunk_done[MAX_TILES] in HBM (the poller then signals there with
+ * copy-engine writes; otherwise it writes tile_chunk_done in host memory). */
+int gfd_tiled_queue_alloc(void** tq, uint32_t total_tiles, uint32_t tokens_per_tile,
+                          uint32_t tokens_per_chunk, uint32_t token_size, int device_signals);
+int gfd_tiled_queue_free(void* tq);
+/* Ring indices, sequences, progress words and next_tile back to zero (poller stopped). */
+int gfd_tiled_queue_reset(void* tq);
+/* baseline_kernel of examples/07_warp_spec_simple.cu:88-134: one workgroup per tile submits
+ * its tokens (token g: cpu_base + g*T -> gpu_base + g*T) chunk by chunk (whole_tile: in one
+ * go) and waits (bounded by timeout_us) for the tile's progress word; then sums[g] = the
+ * u32-word checksum of token g as landed.  *status (0 from the caller) becomes 1 on a
+ * timeout.  The whole launch must fit the ring (total_tiles * tokens_per_tile slots). */
+int gfd_tiled_poller_run(void* tq, const void* cpu_base, void* gpu_base, int whole_tile,
+                         uint64_t timeout_us, unsigned long long* sums, int* status, void* stream);
 /* fused_prefetch_and_compute_kernel (examples/01_basic_transfer.cu:27-85) in one launch:
  * descriptors as gfd_queue_submit_tokens, then each workgroup waits (bounded by timeout_us)
  * until the poller has landed all num_tokens, then writes sums[j] = the u32-word checksum of
