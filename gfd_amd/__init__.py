@@ -171,6 +171,10 @@ def _declare(L):
         "gfd_tiled_queue_free": ([vp], c_int),
         "gfd_tiled_queue_reset": ([vp], c_int),
         "gfd_tiled_poller_run": ([vp, vp, vp, c_int, c_u64, vp, vp, vp], c_int),
+        "gfd_sg_task_queue_alloc": ([pvp, c_int], c_int),
+        "gfd_sg_task_queue_free": ([vp], c_int),
+        "gfd_sg_task_queue_reset": ([vp], c_int),
+        "gfd_sg_poller_run": ([vp, vp, vp, vp, c_int, c_u32, c_u64, vp, vp, vp], c_int),
         "gfd_bench_zero_copy_scatter_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
         "gfd_bench_memcpy_contiguous_d2h": ([vp, vp, ctypes.c_size_t, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_queue": ([vp, vp, vp, c_int, c_u32, ctypes.POINTER(c_u64), c_int, c_int, c_u64, pd], c_int),
@@ -448,6 +452,31 @@ def tiled_poller_run(tq, cpu_base, gpu_base, sums_ptr, status_ptr, whole_tile=Fa
     """Kernel-driven tiled mode (see gfd_tiled_poller_run in include/gfd_capi.h)."""
     _check(lib().gfd_tiled_poller_run(tq.ptr, cpu_base, gpu_base, int(bool(whole_tile)), timeout_us, sums_ptr,
                                       status_ptr, stream), "gfd_tiled_poller_run")
+
+
+class SGTaskQueue:
+    """gfd::SGTaskQueue for the poller's SG mode (set_sg_task_queue), with its
+    d_list_done flags in HBM (device_flags) or fine-grained host memory."""
+
+    def __init__(self, device_flags=True):
+        p = ctypes.c_void_p()
+        _check(lib().gfd_sg_task_queue_alloc(ctypes.byref(p), int(bool(device_flags))), "gfd_sg_task_queue_alloc")
+        self.ptr = p.value
+
+    def reset(self):
+        _check(lib().gfd_sg_task_queue_reset(self.ptr), "gfd_sg_task_queue_reset")
+
+    def free(self):
+        if self.ptr:
+            lib().gfd_sg_task_queue_free(self.ptr)
+            self.ptr = None
+
+
+def sg_poller_run(queue, sg_queue, d_entries_ptr, d_offsets_ptr, num_lists, total_entries, sums_ptr, status_ptr,
+                  timeout_us=10_000_000, stream=None):
+    """Kernel-driven SG mode (see gfd_sg_poller_run in include/gfd_capi.h)."""
+    _check(lib().gfd_sg_poller_run(queue.ptr, sg_queue.ptr, d_entries_ptr, d_offsets_ptr, num_lists, total_entries,
+                                   timeout_us, sums_ptr, status_ptr, stream), "gfd_sg_poller_run")
 
 
 class DescriptorQueue:

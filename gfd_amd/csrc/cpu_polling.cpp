@@ -458,6 +458,14 @@ void CpuPollingThread::flush_batch(Descriptor* batch, int& count, uint32_t& or_f
     }
     if (sg_queue_ && (or_flags & FLAG_LAST_IN_TILE)) {
         process_batch_sg(batch, count, cur_read);
+    } else if (sg_queue_) {
+        // No list ends here: the batch's last list continues in a later batch.
+        const uint64_t f0 = ce_manager_.fence();
+        process_batch(batch, count);
+        if (!sg_open_) {
+            sg_open_ = true;
+            sg_open_begin_ = f0;
+        }
     } else if (tiled_queue_) {
         process_batch_tiled(batch, count, cur_read);
     } else {
@@ -637,6 +645,10 @@ void CpuPollingThread::process_batch_sg(Descriptor* batch, int count, uint64_t c
             j++;
         }
         const uint64_t f0 = ce_manager_.fence();
+        // The batch's first run may finish a list opened in earlier batches:
+        // its flag then waits for those batches' copies too.
+        const bool continues = i == 0 && sg_open_;
+        const uint64_t begin = continues ? sg_open_begin_ : f0;
         submit_list(list.data(), (int)list.size(), total);
         total_bytes_copied_.fetch_add(total, std::memory_order_relaxed);
         descriptors_processed_.fetch_add(j - i, std::memory_order_relaxed);
@@ -644,11 +656,18 @@ void CpuPollingThread::process_batch_sg(Descriptor* batch, int count, uint64_t c
         const bool list_end = (batch[j - 1].flags & FLAG_LAST_IN_TILE) != 0;
         if (list_end && sg_queue_->d_list_done && list_id < (uint32_t)MAX_SG_LISTS) {
             if (list_done_on_device_)
-                signal_device_u64(sg_queue_->d_list_done + list_id, 1, f0);
+                signal_device_u64(sg_queue_->d_list_done + list_id, 1, begin);
             else
                 pending_.host_lists.push_back(list_id);
         }
-        if (list_end) pending_.lists_done++;
+        if (list_end) {
+            pending_.lists_done++;
+            sg_open_ = false;
+        } else {
+            // Only the batch's last run can leave its list open.
+            if (!continues) sg_open_begin_ = f0;
+            sg_open_ = true;
+        }
         i = j;
     }
 }

@@ -242,6 +242,10 @@ private:
     // the previous, so a progress word's final value is its latest.
     uint64_t last_signal_copy_ = CopyEngineManager::kNoFence;
     int list_done_on_device_ = -1;  // -1 unknown, 0 host memory, 1 HBM
+    // SG mode: a list whose entries span several batches is "open" from its
+    // first batch; its HBM flag waits for every copy since sg_open_begin_.
+    bool sg_open_ = false;
+    uint64_t sg_open_begin_ = 0;
     int tile_done_on_device_ = -1;
 
     // Tiled / SG completion bookkeeping.

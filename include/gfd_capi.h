@@ -336,6 +336,26 @@ void* gfd_sg_session_queue(gfd_sg_session_t s); /* get_sg_queue(): the SGTaskQue
 int gfd_bench_sg_session(gfd_sg_session_t s, const gfd_device_sg_entry* entries, uint32_t count,
                          uint32_t entries_per_list, int warmup, int iters, double* times_us);
 
+/* ---- the poller's SG mode (set_sg_task_queue; reference src/batch_processor.cpp:307-446)
+ * driven by a kernel with the reference's SG transfer-warp protocol
+ * (include/gfd/sg_warp_spec.cuh:95-262) ---- */
+/* SGTaskQueue in fine-grained host memory; d_list_done (MAX_SG_LISTS flags + device counters)
+ * in HBM when device_flags != 0 (the poller writes the flags with copy-engine writes after
+ * each list's copies), else in fine-grained host memory (host stores at completion). */
+int gfd_sg_task_queue_alloc(void** sg_queue, int device_flags);
+int gfd_sg_task_queue_free(void* sg_queue);
+int gfd_sg_task_queue_reset(void* sg_queue);  /* flags and lists_completed back to zero */
+/* Workgroup l posts list l = d_entries[d_list_offsets[l] .. d_list_offsets[l+1]) as descriptors
+ * (user_data = l << 32 | i, FLAG_LAST_IN_TILE on the last entry) into `queue`, waits (bounded
+ * by timeout_us) for d_list_done[l], then adds the u32-word checksum of every landed entry to
+ * list_sums[l] (zeroed by the caller).  *status (0 from the caller) becomes 1 on a timeout.
+ * num_lists <= MAX_SG_LISTS; total_entries (the sum of the list sizes) must fit the ring.
+ * Currently switched off (returns hipErrorNotSupported): its first GPU run aborted and the
+ * cause is not yet known. */
+int gfd_sg_poller_run(void* queue, void* sg_queue, const gfd_device_sg_entry* d_entries,
+                      const uint32_t* d_list_offsets, int num_lists, uint32_t total_entries,
+                      uint64_t timeout_us, unsigned long long* list_sums, int* status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
