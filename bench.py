@@ -481,6 +481,52 @@ def run_sessions(oracle, iters, warmup):
     return out
 
 
+def run_helper_waves(oracle, iters, warmup):
+    """Transfer helper waves at small grids (1, 4 and 8 workgroups, the block
+    counts the reference's own tests use): WarpSpecSession 8192 x 16 KiB and
+    SGWarpSpecSession 16384 x 4 KiB scattered in lists of 512, each without
+    helpers and with 3.  Outputs are compared with the source bytes."""
+    out = {}
+    n, t = 8192, 16384
+    host = gfd_amd.HostBuffer(n * t)
+    oracle.fill_tokens(host.array, n, t, t)
+    dst = gfd_amd.DeviceBuffer(n * t)
+    for blocks in (1, 4, 8):
+        for h in (0, 3):
+            dst.fill(0)
+            res, kms = gfd_amd.warp_spec_run(host.ptr, dst.ptr, n, t, 128, 0, False, False, blocks,
+                                             iters=warmup + iters, helper_waves=h)
+            if not (dst.download() == host.array).all():
+                raise SystemExit("PARITY FAILURE: WarpSpecSession blocks=%d helpers=%d" % (blocks, h))
+            us = kms[warmup:] * 1000.0
+            key = "warp_spec_%dx%dKB_blocks%d_helpers%d" % (n, t // 1024, blocks, h)
+            out[key] = {"kernel_us_p50": round(p50(us), 2), "GBps": round(gbps(n * t, p50(us)), 3),
+                        "block": res["block"]}
+            log("  %s: %s" % (key, out[key]))
+    del host, dst
+    n, t, epl = 16384, 4096, 512
+    host = gfd_amd.HostBuffer(n * 2 * t)
+    oracle.fill_tokens(host.array, n, t, 2 * t)
+    perm = oracle.permutation(n)
+    dst = gfd_amd.DeviceBuffer(n * t)
+    ent = gfd_amd.device_sg_entries(host.ptr + perm.astype(np.uint64) * np.uint64(2 * t),
+                                    dst.ptr + np.arange(n, dtype=np.uint64) * np.uint64(t), t)
+    want = oracle.expected_gather(host.array, perm, t, 2 * t)
+    for blocks in (1, 4, 8):
+        for h in (0, 3):
+            dst.fill(0)
+            sess = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=blocks, idle_limit_ms=10000,
+                                            helper_waves=h)
+            us = sess.bench(ent, epl, warmup=max(1, warmup // 5), iters=max(3, iters // 5))
+            sess.close()
+            if not (dst.download() == want).all():
+                raise SystemExit("PARITY FAILURE: SGWarpSpecSession blocks=%d helpers=%d" % (blocks, h))
+            key = "sg_16384x4KB_lists512_blocks%d_helpers%d" % (blocks, h)
+            out[key] = {"us_p50": round(p50(us), 2), "GBps": round(gbps(n * t, p50(us)), 3)}
+            log("  %s: %s" % (key, out[key]))
+    return out
+
+
 class QueueRig:
     def __init__(self, region_bytes):
         self.q = gfd_amd.DescriptorQueue()
@@ -526,7 +572,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=15)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="",
-                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions,scattered,offload "
+                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions,scattered,offload,"
+                         "helpers (helpers is not in the default run) "
                          "(calib: add a 32 MiB D2D copy)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -608,6 +655,11 @@ def main():
         log("wave-specialised sessions ...")
         r_sessions = run_sessions(oracle, K, W)
 
+    r_helpers = None
+    if "helpers" in only:
+        log("transfer helper waves at 1/4/8 workgroups ...")
+        r_helpers = run_helper_waves(oracle, K, W)
+
     r_offload = None
     if want("offload"):
         log("offload (HBM -> pinned host) ...")
@@ -673,6 +725,7 @@ def main():
         "results_sessions": r_sessions,
         "results_direct_scattered_dst_8192x4KB": r_scat,
         "results_offload": r_offload,
+        "results_helper_waves": r_helpers,
         "direct_setup": {k: dinfo[k] for k in ("numa_node", "num_gather_workers", "worker_cpus", "poller_cpu",
                                                "num_ce_channels", "direct_chunk_bytes", "gather_slice_bytes")},
         "host": info,
