@@ -125,6 +125,7 @@ int SdmaQueue::init(int device, int channels, int pin_engines) {
     }
     slot_bytes_.assign(kRing, 0);
     slot_channel_.assign(kRing, 0);
+    waiter_.assign(kRing, 0);
     uint64_t freq = 0;
     if (hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP_FREQUENCY, &freq) == HSA_STATUS_SUCCESS && freq)
         tick_ns_ = 1e9 / (double)freq;
@@ -214,12 +215,24 @@ int SdmaQueue::copy(int channel, uint64_t dst, const void* src, size_t bytes, ui
         if (wait(next_seq_ - kRing + 1) != 0) return -1;
     }
     const uint64_t s = next_seq_;
+    // A copy that depends on this slot's previous occupant may not have
+    // polled its signal yet (it can sit behind other copies on its engine).
+    // Resetting the signal now would make it wait for this new copy instead,
+    // which may be queued behind it on the same engine: wait for it first.
+    // It can finish: its dependency, the previous occupant, has completed.
+    const uint64_t w = waiter_[s % kRing];
+    if (w > tail_ && wait(w) != 0) return -1;
+    waiter_[s % kRing] = 0;
     hsa_signal_t cs = sig(signals_[s % kRing]);
     hsa_signal_store_relaxed(cs, 1);
     hsa_signal_t dep_sigs[16];
+    size_t dep_slots[16];
     uint32_t nd = 0;
     for (int i = 0; i < ndeps && nd < 16; i++)
-        if (deps[i] >= tail_ && deps[i] < s) dep_sigs[nd++] = sig(signals_[deps[i] % kRing]);
+        if (deps[i] >= tail_ && deps[i] < s) {
+            dep_slots[nd] = deps[i] % kRing;
+            dep_sigs[nd++] = sig(signals_[deps[i] % kRing]);
+        }
     hsa_agent_t gpu{gpu_agent_}, cpu{cpu_agent_};
     hsa_status_t st;
     if (pin_) {
@@ -233,6 +246,7 @@ int SdmaQueue::copy(int channel, uint64_t dst, const void* src, size_t bytes, ui
         hsa_signal_store_relaxed(cs, 0);
         return (int)st;
     }
+    for (uint32_t i = 0; i < nd; i++) waiter_[dep_slots[i]] = s + 1;
     slot_bytes_[s % kRing] = bytes;
     slot_channel_[s % kRing] = (uint32_t)channel;
     next_seq_ = s + 1;

@@ -88,6 +88,12 @@ private:
     uint32_t engine_mask_ = 0;
     std::vector<uint32_t> engines_;
     std::vector<uint64_t> signals_;  // ring of hsa_signal_t handles
+    // Per ring slot: 1 + the sequence number of the newest copy that waits on
+    // the slot's current signal (0 = none).  An engine evaluates a dependency
+    // when the dependent copy reaches the head of its ring, by polling the
+    // signal's value at that moment, so a slot is not handed to a new copy
+    // until every copy that depends on its previous occupant has finished.
+    std::vector<uint64_t> waiter_;
     uint64_t next_seq_ = 0;
     uint64_t tail_ = 0;  // all seq < tail_ complete
     int error_ = 0;

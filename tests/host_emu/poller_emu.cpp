@@ -1,0 +1,370 @@
+// Runs the product poller (CpuPollingThread with its SDMA copy queue) on the
+// host against the emulated runtime of emu.h, driven by threads that follow
+// the device protocols of the kernels in gfd_amd/csrc/kernels:
+//
+//   sg <case> <rounds> <seed>
+//       SG mode (set_sg_task_queue; src/batch_processor.cpp:307-446 of the
+//       reference): one producer per list claims ring slots, writes the
+//       list's descriptors tagged list_id << 32 | i with FLAG_LAST_IN_TILE on
+//       the last, commits them, waits for d_list_done[list_id] and then
+//       checksums what landed (sg_poller_kernel's protocol).  Cases:
+//       split_small_tokens, ragged, host_flags, one_entry_lists.
+//   queue <n> <token_bytes> <scattered 0|1> <rounds> <seed>
+//       Queue mode (src/cpu_polling.cpp:337-490, examples/04_benchmark.cu:
+//       31-54 of the reference): producers of 256 descriptors each, the last
+//       flagged FLAG_LAST_IN_BATCH, then a wait for done_idx.
+//   sdma_slot_reuse
+//       SdmaQueue alone: a signal slot comes round again while a copy that
+//       depends on its previous occupant is still queued (see the function).
+//
+// Every landed byte is compared with the expected image (the entries applied
+// by plain memcpy), and list checksums exactly.  Exit status: 0 pass,
+// 2 a wait timed out, 3 mismatch, 4 setup failure, 86 the emulated copy
+// engines stalled on each other.
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "gfd/cpu_polling.h"
+#include "gfd/descriptor_queue.h"
+#include "gfd/hip_shim.h"
+#include "gfd/sg_task_queue.h"
+#include "sdma.h"
+
+using namespace gfd;
+
+namespace {
+
+constexpr uint8_t kSentinel = 0xCD;
+constexpr double kWaitSeconds = 20.0;
+
+struct Rng {
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed ? seed : 0x9E3779B97F4A7C15ull) {}
+    uint64_t next() {
+        s ^= s << 13;
+        s ^= s >> 7;
+        s ^= s << 17;
+        return s;
+    }
+    uint64_t below(uint64_t n) { return next() % n; }
+};
+
+struct Entry {
+    uint64_t src, dst;
+    uint32_t size;
+};
+
+void* host_alloc(size_t n) {
+    void* p = nullptr;
+    if (gfd_hip_host_alloc(&p, n, GFD_HOST_COHERENT) != 0) {
+        std::fprintf(stderr, "host alloc failed\n");
+        std::exit(4);
+    }
+    return p;
+}
+
+void* dev_alloc(size_t n) {
+    void* p = nullptr;
+    if (gfd_hip_malloc(&p, n) != 0) {
+        std::fprintf(stderr, "device alloc failed\n");
+        std::exit(4);
+    }
+    return p;
+}
+
+double seconds_since(std::chrono::steady_clock::time_point t0) {
+    return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+}
+
+uint64_t word_checksum(const uint8_t* p, uint32_t n) {
+    uint64_t acc = 0;
+    const uint32_t nw = n / 4;
+    for (uint32_t k = 0; k < nw; k++) {
+        uint32_t w;
+        std::memcpy(&w, p + 4 * k, 4);
+        acc += w;
+    }
+    for (uint32_t b = nw * 4; b < n; b++) acc += p[b];
+    return acc;
+}
+
+// Claim `count` consecutive ring slots and commit descriptors for them; lanes
+// of a wave commit in no fixed order, so each group of 64 is committed in a
+// shuffled order.
+uint64_t post(DescriptorQueue* q, const Entry* e, uint32_t count, uint64_t tag_hi, uint32_t last_flag, Rng& rng) {
+    const uint64_t base = __atomic_fetch_add(&q->write_idx, (uint64_t)count, __ATOMIC_RELAXED);
+    uint32_t order[64];
+    for (uint32_t g = 0; g < count; g += 64) {
+        const uint32_t n = std::min<uint32_t>(64, count - g);
+        for (uint32_t k = 0; k < n; k++) order[k] = k;
+        for (uint32_t k = n; k > 1; k--) std::swap(order[k - 1], order[rng.below(k)]);
+        for (uint32_t k = 0; k < n; k++) {
+            const uint32_t i = g + order[k];
+            Descriptor* d = &q->entries[(base + i) % QUEUE_SIZE];
+            d->src_addr = e[i].src;
+            d->dst_addr = e[i].dst;
+            d->size = e[i].size;
+            d->flags = i == count - 1 ? last_flag : FLAG_NONE;
+            d->user_data = (tag_hi << 32) | i;
+            __atomic_store_n(&d->sequence, base + i + 1, __ATOMIC_RELEASE);
+        }
+    }
+    return base;
+}
+
+bool wait_u64(volatile uint64_t* p, uint64_t at_least) {
+    const auto t0 = std::chrono::steady_clock::now();
+    while (__atomic_load_n(p, __ATOMIC_ACQUIRE) < at_least) {
+        if (seconds_since(t0) > kWaitSeconds) return false;
+        std::this_thread::yield();
+    }
+    return true;
+}
+
+int check_image(const uint8_t* got, const std::vector<uint8_t>& want, const char* what, int rnd) {
+    size_t bad = 0, first = 0;
+    for (size_t i = 0; i < want.size(); i++)
+        if (got[i] != want[i]) {
+            if (!bad) first = i;
+            bad++;
+        }
+    if (bad) {
+        std::printf("%s round %d: %zu mismatched bytes (first at %zu)\n", what, rnd, bad, first);
+        return 3;
+    }
+    return 0;
+}
+
+int run_sg(const std::string& kase, int rounds, uint64_t seed) {
+    Rng rng(seed);
+    const size_t host_bytes = 8u << 20, dst_bytes = 96u << 20;
+    auto* host = (uint8_t*)host_alloc(host_bytes);
+    for (size_t i = 0; i < host_bytes; i++) host[i] = (uint8_t)rng.next();
+    auto* dst = (uint8_t*)dev_alloc(dst_bytes);
+
+    std::vector<uint32_t> sizes;
+    uint32_t lo = 1024, hi = 1024;
+    if (kase == "split_small_tokens") {
+        sizes = {1500, 700, 2500, 1, 3000};
+    } else if (kase == "ragged" || kase == "host_flags") {
+        for (int l = 0; l < 40; l++) sizes.push_back(1 + (uint32_t)rng.below(199));
+        lo = 1;
+        hi = 8999;
+    } else if (kase == "one_entry_lists") {
+        sizes.assign(300, 1);
+        lo = hi = 4096;
+    } else {
+        std::fprintf(stderr, "unknown case %s\n", kase.c_str());
+        return 4;
+    }
+    std::vector<Entry> ent;
+    std::vector<uint32_t> offs{0};
+    size_t off = 0;
+    for (uint32_t k : sizes) {
+        for (uint32_t i = 0; i < k; i++) {
+            const uint32_t n = lo + (uint32_t)rng.below(hi - lo + 1);
+            const uint64_t so = rng.below(host_bytes - n);
+            ent.push_back(Entry{(uint64_t)(uintptr_t)host + so, (uint64_t)(uintptr_t)dst + off, n});
+            off += n + rng.below(33);
+        }
+        offs.push_back((uint32_t)ent.size());
+    }
+    if (off > dst_bytes) return 4;
+    std::vector<uint64_t> want_sums(sizes.size(), 0);
+    std::vector<uint8_t> want(off, kSentinel);
+    for (size_t l = 0; l < sizes.size(); l++)
+        for (uint32_t i = offs[l]; i < offs[l + 1]; i++) {
+            const Entry& e = ent[i];
+            want_sums[l] += word_checksum((const uint8_t*)(uintptr_t)e.src, e.size);
+            std::memcpy(&want[e.dst - (uint64_t)(uintptr_t)dst], (const void*)(uintptr_t)e.src, e.size);
+        }
+
+    auto* q = (DescriptorQueue*)host_alloc(sizeof(DescriptorQueue));
+    auto* sq = (SGTaskQueue*)host_alloc(sizeof(SGTaskQueue));
+    const size_t flag_words = MAX_SG_LISTS + SG_DEVICE_COUNTER_WORDS;
+    const bool device_flags = kase != "host_flags";
+    sq->d_list_done = (uint64_t*)(device_flags ? dev_alloc(flag_words * 8) : host_alloc(flag_words * 8));
+
+    int rc = 0;
+    {
+        CpuPollingThread p(q, dst, host, host_bytes, true, -1);
+        p.set_sg_task_queue(sq);
+        if (!p.init_copy_engine()) return 4;
+        p.start();
+        for (int rnd = 0; rnd < rounds && rc == 0; rnd++) {
+            std::printf("sg %s round %d: %zu lists, %zu entries\n", kase.c_str(), rnd, sizes.size(), ent.size());
+            std::fflush(stdout);
+            std::memset(dst, kSentinel, off);
+            std::memset(sq->d_list_done, 0, flag_words * 8);
+            sq->lists_completed = 0;
+            std::vector<uint64_t> sums(sizes.size(), 0);
+            std::atomic<int> timed_out{-1};
+            std::vector<std::thread> wg;
+            for (size_t l = 0; l < sizes.size(); l++)
+                wg.emplace_back([&, l] {
+                    Rng lr(seed * 1000003u + l * 7919u + (uint64_t)rnd);
+                    const uint32_t count = offs[l + 1] - offs[l];
+                    if (count == 0) return;
+                    post(q, &ent[offs[l]], count, l, FLAG_LAST_IN_TILE, lr);
+                    if (!wait_u64(&sq->d_list_done[l], 1)) {
+                        timed_out = (int)l;
+                        return;
+                    }
+                    uint64_t acc = 0;
+                    for (uint32_t i = offs[l]; i < offs[l + 1]; i++)
+                        acc += word_checksum((const uint8_t*)(uintptr_t)ent[i].dst, ent[i].size);
+                    sums[l] = acc;
+                });
+            for (auto& t : wg) t.join();
+            if (timed_out >= 0) {
+                std::printf("sg %s round %d: list %d wait timed out\n", kase.c_str(), rnd, timed_out.load());
+                rc = 2;
+                break;
+            }
+            rc = check_image(dst, want, "sg", rnd);
+            for (size_t l = 0; l < sizes.size() && rc == 0; l++)
+                if (sums[l] != want_sums[l]) {
+                    std::printf("sg %s round %d: list %zu checksum\n", kase.c_str(), rnd, l);
+                    rc = 3;
+                }
+        }
+        p.stop();
+    }
+    if (rc == 0 && q->done_idx != (uint64_t)rounds * ent.size()) {
+        std::printf("done_idx %llu, want %llu\n", (unsigned long long)q->done_idx,
+                    (unsigned long long)rounds * ent.size());
+        rc = 3;
+    }
+    if (rc == 0) std::printf("sg %s: pass\n", kase.c_str());
+    gfd_hip_free(device_flags ? (void*)sq->d_list_done : nullptr);
+    if (!device_flags) gfd_hip_host_free(sq->d_list_done);
+    gfd_hip_host_free(sq);
+    gfd_hip_host_free(q);
+    gfd_hip_free(dst);
+    gfd_hip_host_free(host);
+    return rc;
+}
+
+int run_queue(uint32_t n, uint32_t t, bool scattered, int rounds, uint64_t seed) {
+    Rng rng(seed);
+    const size_t host_bytes = (size_t)n * 2 * t;
+    auto* host = (uint8_t*)host_alloc(host_bytes);
+    for (size_t i = 0; i < host_bytes; i++) host[i] = (uint8_t)rng.next();
+    std::vector<uint32_t> perm(n);
+    for (uint32_t i = 0; i < n; i++) perm[i] = i;
+    for (uint32_t i = n; i > 1; i--) std::swap(perm[i - 1], perm[rng.below(i)]);
+    std::vector<Entry> ent(n);
+    size_t off = 0;
+    auto* dst = (uint8_t*)dev_alloc((size_t)n * (t + 32) + 64);
+    for (uint32_t j = 0; j < n; j++) {
+        ent[j] = Entry{(uint64_t)(uintptr_t)host + (uint64_t)perm[j] * 2 * t, (uint64_t)(uintptr_t)dst + off, t};
+        off += t + (scattered ? rng.below(33) : 0);
+    }
+    std::vector<uint8_t> want(off, kSentinel);
+    for (const Entry& e : ent)
+        std::memcpy(&want[e.dst - (uint64_t)(uintptr_t)dst], (const void*)(uintptr_t)e.src, e.size);
+    auto* q = (DescriptorQueue*)host_alloc(sizeof(DescriptorQueue));
+    int rc = 0;
+    {
+        CpuPollingThread p(q, dst, host, host_bytes, true, -1);
+        if (!p.init_copy_engine()) return 4;
+        p.start();
+        for (int rnd = 0; rnd < rounds && rc == 0; rnd++) {
+            std::printf("queue %ux%u scattered=%d round %d\n", n, t, (int)scattered, rnd);
+            std::fflush(stdout);
+            std::memset(dst, kSentinel, off);
+            const uint64_t start = q->write_idx;
+            std::vector<std::thread> wg;
+            for (uint32_t b = 0; b < n; b += 256)
+                wg.emplace_back([&, b] {
+                    Rng lr(seed + b + (uint64_t)rnd * 65537u);
+                    const uint32_t c = std::min<uint32_t>(256, n - b);
+                    post(q, &ent[b], c, 0, b + c == n ? FLAG_LAST_IN_BATCH : FLAG_NONE, lr);
+                });
+            for (auto& th : wg) th.join();
+            if (!wait_u64(&q->done_idx, start + n)) {
+                std::printf("queue round %d: done_idx wait timed out\n", rnd);
+                rc = 2;
+                break;
+            }
+            rc = check_image(dst, want, "queue", rnd);
+        }
+        p.stop();
+    }
+    if (rc == 0) std::printf("queue %ux%u scattered=%d: pass\n", n, t, (int)scattered);
+    gfd_hip_host_free(q);
+    gfd_hip_free(dst);
+    gfd_hip_host_free(host);
+    return rc;
+}
+
+// SdmaQueue completion-signal slot reuse.  Copy X (engine 0) depends on copy
+// d (engine 1) but sits behind a long copy on its engine; the issuer then
+// runs through the whole signal ring so that d's slot comes round again,
+// with the new occupant placed on engine 0 behind X.  If the slot were
+// reused before X had polled it, X would wait for a copy queued behind
+// itself.  Expected: every copy lands and the queue drains.
+int run_sdma_slot_reuse() {
+    SdmaQueue q;
+    if (q.init(0, 2, 1) != 0 || q.num_engines() < 2) return 4;
+    const size_t big = 64u << 20, small = 256;
+    constexpr int kSlots = 1024;  // SdmaQueue's signal ring
+    auto* src = (uint8_t*)host_alloc(big);
+    auto* dst = (uint8_t*)dev_alloc(big + (kSlots + 8) * small);
+    for (size_t i = 0; i < big; i++) src[i] = (uint8_t)(i * 131 + 7);
+    uint8_t* dst_small = dst + big;
+    auto small_copy = [&](int ch, uint64_t k, const uint64_t* deps, int nd) {
+        return q.copy(ch, (uint64_t)(uintptr_t)(dst_small + k * small), src + (k % 1000) * small, small, nullptr,
+                      deps, nd);
+    };
+    std::printf("sdma slot reuse: ring %d, long copy %zu MiB\n", kSlots, big >> 20);
+    int st = small_copy(1, 0, nullptr, 0);                                       // seq 0
+    if (!st) st = small_copy(1, 1, nullptr, 0);                                  // seq 1 = d
+    if (!st) st = q.copy(0, (uint64_t)(uintptr_t)dst, src, big, nullptr, nullptr, 0);  // seq 2, long
+    const uint64_t d = 1;
+    if (!st) st = small_copy(0, 3, &d, 1);                                       // seq 3 = X, after d
+    for (uint64_t k = 4; !st && k < (uint64_t)kSlots + 1; k++) st = small_copy(1, k, nullptr, 0);
+    if (!st) st = small_copy(0, kSlots + 1, nullptr, 0);  // takes d's slot, on X's engine
+    if (st) {
+        std::printf("sdma slot reuse: copy failed (%d)\n", st);
+        return 4;
+    }
+    if (q.wait_all() != 0) return 3;
+    for (size_t i = 0; i < big; i++)
+        if (dst[i] != src[i]) {
+            std::printf("sdma slot reuse: long copy mismatch at %zu\n", i);
+            return 3;
+        }
+    for (uint64_t k = 0; k <= (uint64_t)kSlots + 1; k++)
+        if (k != 2 && std::memcmp(dst_small + k * small, src + (k % 1000) * small, small) != 0) {
+            std::printf("sdma slot reuse: copy %llu mismatch\n", (unsigned long long)k);
+            return 3;
+        }
+    std::printf("sdma slot reuse: pass\n");
+    gfd_hip_free(dst);
+    gfd_hip_host_free(src);
+    return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    setvbuf(stdout, nullptr, _IOLBF, 0);
+    if (argc >= 2 && std::string(argv[1]) == "sdma_slot_reuse") return run_sdma_slot_reuse();
+    if (argc >= 5 && std::string(argv[1]) == "sg")
+        return run_sg(argv[2], std::atoi(argv[3]), std::strtoull(argv[4], nullptr, 0));
+    if (argc >= 7 && std::string(argv[1]) == "queue")
+        return run_queue((uint32_t)std::atoi(argv[2]), (uint32_t)std::atoi(argv[3]), std::atoi(argv[4]) != 0,
+                         std::atoi(argv[5]), std::strtoull(argv[6], nullptr, 0));
+    std::fprintf(stderr,
+                 "usage: poller_emu sg <case> <rounds> <seed>\n"
+                 "       poller_emu queue <n> <token_bytes> <scattered> <rounds> <seed>\n");
+    return 4;
+}
