@@ -344,7 +344,9 @@ class CpuPollingThread:
         lib().gfd_poller_set_tiled_queue(self._h, getattr(tq, "ptr", tq))
 
     def set_sg_task_queue(self, sq):
-        lib().gfd_poller_set_sg_task_queue(self._h, getattr(sq, "ptr", sq))
+        """Switched off: CpuPollingThread::start() refuses an SG task queue (an
+        SG-mode run aborted the process on MI355X and the cause is not found)."""
+        raise RuntimeError("the poller's SG task-queue mode is switched off in this build")
 
     def start(self):
         lib().gfd_poller_start(self._h)
@@ -462,9 +464,28 @@ class SGTaskQueue:
         p = ctypes.c_void_p()
         _check(lib().gfd_sg_task_queue_alloc(ctypes.byref(p), int(bool(device_flags))), "gfd_sg_task_queue_alloc")
         self.ptr = p.value
+        self.device_flags = bool(device_flags)
+
+    # Field offsets in gfd::SGTaskQueue (static_asserts in sg_poller_kernels.hip).
+    _LISTS_COMPLETED = 409856
+    _D_LIST_DONE = 409872
 
     def reset(self):
         _check(lib().gfd_sg_task_queue_reset(self.ptr), "gfd_sg_task_queue_reset")
+
+    @property
+    def lists_completed(self):
+        return int(ctypes.c_uint64.from_address(self.ptr + self._LISTS_COMPLETED).value)
+
+    def list_done(self, n):
+        """d_list_done[0:n] (read from HBM or host memory, wherever it lives)."""
+        p = int(ctypes.c_uint64.from_address(self.ptr + self._D_LIST_DONE).value)
+        out = np.zeros(n, np.uint64)
+        if self.device_flags:
+            _check(lib().gfd_memcpy_d2h(out.ctypes.data, p, n * 8), "gfd_memcpy_d2h")
+        else:
+            out[:] = np.ctypeslib.as_array((ctypes.c_uint64 * n).from_address(p))
+        return out
 
     def free(self):
         if self.ptr:

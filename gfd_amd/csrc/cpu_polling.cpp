@@ -305,6 +305,17 @@ void CpuPollingThread::start() {
         GFD_LOG_ERROR("start(): init_copy_engine() has not succeeded\n");
         return;
     }
+#ifndef GFD_HOST_EMULATION
+    // Switched off: with an SG task queue set, the process aborted on MI355X
+    // ("stack smashing detected" on a non-Python thread) in both runs made,
+    // one with lists posted by a kernel and one by a CPU producer, and the
+    // cause has not been found.  The host emulation build keeps the mode so
+    // that its logic stays tested.
+    if (sg_queue_) {
+        GFD_LOG_ERROR("start(): SG task-queue mode is switched off in this build\n");
+        return;
+    }
+#endif
     running_.store(true, std::memory_order_release);
     thread_ = std::thread(&CpuPollingThread::polling_loop, this);
 }

@@ -8,12 +8,17 @@
 // allocates an SGTaskQueue whose d_list_done the poller signals.
 #include <hip/hip_runtime.h>
 
+#include <cstddef>
 #include <cstring>
 
 #include "gfd/device.h"
 #include "gfd/sg_task_queue.h"
 #include "gfd/tiled_queue.h"
 #include "gfd_capi.h"
+
+// Offsets the Python binding reads (gfd_amd.SGTaskQueue).
+static_assert(offsetof(gfd::SGTaskQueue, lists_completed) == 409856, "SGTaskQueue layout");
+static_assert(offsetof(gfd::SGTaskQueue, d_list_done) == 409872, "SGTaskQueue layout");
 
 namespace {
 

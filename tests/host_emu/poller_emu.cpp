@@ -8,7 +8,7 @@
 //       list's descriptors tagged list_id << 32 | i with FLAG_LAST_IN_TILE on
 //       the last, commits them, waits for d_list_done[list_id] and then
 //       checksums what landed (sg_poller_kernel's protocol).  Cases:
-//       split_small_tokens, ragged, host_flags, one_entry_lists.
+//       split_small_tokens, ragged, host_flags, one_entry_lists, pages.
 //   queue <n> <token_bytes> <scattered 0|1> <rounds> <seed>
 //       Queue mode (src/cpu_polling.cpp:337-490, examples/04_benchmark.cu:
 //       31-54 of the reference): producers of 256 descriptors each, the last
@@ -160,16 +160,38 @@ int run_sg(const std::string& kase, int rounds, uint64_t seed) {
     } else if (kase == "one_entry_lists") {
         sizes.assign(300, 1);
         lo = hi = 4096;
+    } else if (kase == "pages") {
+        // Page-aligned 4 KiB entries into page slots scattered over twice the
+        // region, posted by one producer in list order; two lists are longer
+        // than the 4096-entry batch threshold.
+        sizes = {5000, 300, 1, 4500, 64};
+        lo = hi = 4096;
     } else {
         std::fprintf(stderr, "unknown case %s\n", kase.c_str());
         return 4;
     }
+    const bool pages = kase == "pages";
     std::vector<Entry> ent;
     std::vector<uint32_t> offs{0};
     size_t off = 0;
+    std::vector<uint64_t> slot;
+    if (pages) {
+        size_t total = 0;
+        for (uint32_t k : sizes) total += k;
+        slot.resize(2 * total);
+        for (size_t i = 0; i < slot.size(); i++) slot[i] = i;
+        for (size_t i = slot.size(); i > 1; i--) std::swap(slot[i - 1], slot[rng.below(i)]);
+        off = 2 * total * 4096;
+    }
     for (uint32_t k : sizes) {
         for (uint32_t i = 0; i < k; i++) {
             const uint32_t n = lo + (uint32_t)rng.below(hi - lo + 1);
+            if (pages) {
+                const uint64_t so = rng.below(host_bytes / 4096) * 4096;
+                const uint64_t dofs = slot[ent.size()] * 4096;
+                ent.push_back(Entry{(uint64_t)(uintptr_t)host + so, (uint64_t)(uintptr_t)dst + dofs, n});
+                continue;
+            }
             const uint64_t so = rng.below(host_bytes - n);
             ent.push_back(Entry{(uint64_t)(uintptr_t)host + so, (uint64_t)(uintptr_t)dst + off, n});
             off += n + rng.below(33);
@@ -207,12 +229,17 @@ int run_sg(const std::string& kase, int rounds, uint64_t seed) {
             std::vector<uint64_t> sums(sizes.size(), 0);
             std::atomic<int> timed_out{-1};
             std::vector<std::thread> wg;
+            if (pages) {
+                Rng lr(seed + (uint64_t)rnd);
+                for (size_t l = 0; l < sizes.size(); l++)
+                    post(q, &ent[offs[l]], offs[l + 1] - offs[l], l, FLAG_LAST_IN_TILE, lr);
+            }
             for (size_t l = 0; l < sizes.size(); l++)
                 wg.emplace_back([&, l] {
                     Rng lr(seed * 1000003u + l * 7919u + (uint64_t)rnd);
                     const uint32_t count = offs[l + 1] - offs[l];
                     if (count == 0) return;
-                    post(q, &ent[offs[l]], count, l, FLAG_LAST_IN_TILE, lr);
+                    if (!pages) post(q, &ent[offs[l]], count, l, FLAG_LAST_IN_TILE, lr);
                     if (!wait_u64(&sq->d_list_done[l], 1)) {
                         timed_out = (int)l;
                         return;

@@ -9,8 +9,10 @@ Host threads follow the kernels' device protocols:
 - SG mode (reference src/batch_processor.cpp:307-446, include/gfd/
   sg_warp_spec.cuh:95-262): lists tagged list_id << 32 | i, FLAG_LAST_IN_TILE
   on the last entry, a wait on d_list_done[list_id], then a checksum of what
-  landed.  The same four cases as the GPU test of the kernel-driven mode,
-  including lists split over several batches.
+  landed.  The four cases of the GPU test of the kernel-driven mode
+  (including lists split over several batches) and the page-scattered lists
+  of the CPU-producer GPU test.  The product library switches this mode off;
+  the emulation build (GFD_HOST_EMULATION) keeps it so its logic stays tested.
 - Queue mode (reference src/cpu_polling.cpp:337-490): contiguous and
   scattered destinations, then a wait on done_idx.
 - SdmaQueue signal-slot reuse: a copy that depends on a slot's previous
@@ -51,7 +53,7 @@ def test_sdma_signal_slot_reuse_waits_for_pending_dependents(poller_emu):
     run(poller_emu, ["sdma_slot_reuse"])
 
 
-@pytest.mark.parametrize("case", ["split_small_tokens", "ragged", "host_flags", "one_entry_lists"])
+@pytest.mark.parametrize("case", ["split_small_tokens", "ragged", "host_flags", "one_entry_lists", "pages"])
 def test_sg_mode_lists(poller_emu, case):
     run(poller_emu, ["sg", case, 2, 1])
 
