@@ -13,6 +13,8 @@
 //       Queue mode (src/cpu_polling.cpp:337-490, examples/04_benchmark.cu:
 //       31-54 of the reference): producers of 256 descriptors each, the last
 //       flagged FLAG_LAST_IN_BATCH, then a wait for done_idx.
+//   ragged <direct|queue> <n> <runs> <rounds> <seed>
+//       Ragged entries over a few destination runs, at every alignment.
 //   sdma_slot_reuse
 //       SdmaQueue alone: a signal slot comes round again while a copy that
 //       depends on its previous occupant is still queued (see the function).
@@ -332,6 +334,82 @@ int run_queue(uint32_t n, uint32_t t, bool scattered, int rounds, uint64_t seed)
     return rc;
 }
 
+// Ragged entries (1..8999 bytes, random pinned sources) whose destinations
+// follow the list order, cut into `nruns` runs by odd-length gaps.  Direct:
+// one submit_direct call (runs <= 64 take the staged routes); Queue: one
+// producer posts the list, last entry FLAG_LAST_IN_BATCH, then a wait on
+// done_idx.
+int run_ragged(const std::string& path, uint32_t n, uint32_t nruns, int rounds, uint64_t seed) {
+    Rng rng(seed);
+    std::vector<uint32_t> sizes(n);
+    size_t total = 0;
+    for (auto& s : sizes) {
+        s = 1 + (uint32_t)rng.below(8999);
+        total += s;
+    }
+    const size_t host_bytes = 2 * total + 64;
+    auto* host = (uint8_t*)host_alloc(host_bytes);
+    for (size_t i = 0; i < host_bytes; i++) host[i] = (uint8_t)rng.next();
+    std::vector<uint8_t> cut(n, 0);
+    for (uint32_t k = 1; k < nruns && k < n; k++) {
+        uint32_t c;
+        do c = 1 + (uint32_t)rng.below(n - 1);
+        while (cut[c]);
+        cut[c] = 1;
+    }
+    std::vector<Entry> ent(n);
+    size_t off = 0;
+    auto* dst = (uint8_t*)dev_alloc(total + (size_t)nruns * 4200 + 4096);
+    for (uint32_t i = 0; i < n; i++) {
+        if (cut[i]) off += 2 * rng.below(2048) + 1;
+        ent[i] = Entry{(uint64_t)(uintptr_t)host + rng.below(host_bytes - sizes[i]), (uint64_t)(uintptr_t)dst + off,
+                       sizes[i]};
+        off += sizes[i];
+    }
+    std::vector<uint8_t> want(off + 4096, kSentinel);
+    for (const Entry& e : ent)
+        std::memcpy(&want[e.dst - (uint64_t)(uintptr_t)dst], (const void*)(uintptr_t)e.src, e.size);
+    int rc = 0;
+    if (path == "direct") {
+        CpuPollingThread p(nullptr, nullptr, nullptr, 64u << 20, true, -1);
+        if (!p.init_direct_ce()) return 4;
+        std::vector<SGEntry> sg(n);
+        for (uint32_t i = 0; i < n; i++) sg[i] = SGEntry{ent[i].dst, (const void*)(uintptr_t)ent[i].src, ent[i].size};
+        for (int rnd = 0; rnd < rounds && rc == 0; rnd++) {
+            std::printf("ragged direct %u entries, %u runs, call %d\n", n, nruns, rnd);
+            std::memset(dst, kSentinel, want.size());
+            if (p.submit_direct(sg.data(), (int)n) < 0) return 3;
+            rc = check_image(dst, want, "ragged direct", rnd);
+        }
+    } else {
+        auto* q = (DescriptorQueue*)host_alloc(sizeof(DescriptorQueue));
+        {
+            CpuPollingThread p(q, dst, host, host_bytes, true, -1);
+            if (!p.init_copy_engine()) return 4;
+            p.start();
+            for (int rnd = 0; rnd < rounds && rc == 0; rnd++) {
+                std::printf("ragged queue %u entries, %u runs, round %d\n", n, nruns, rnd);
+                std::memset(dst, kSentinel, want.size());
+                const uint64_t start = q->write_idx;
+                Rng lr(seed + (uint64_t)rnd);
+                post(q, ent.data(), n, 0, FLAG_LAST_IN_BATCH, lr);
+                if (!wait_u64(&q->done_idx, start + n)) {
+                    std::printf("ragged queue round %d: done_idx wait timed out\n", rnd);
+                    rc = 2;
+                    break;
+                }
+                rc = check_image(dst, want, "ragged queue", rnd);
+            }
+            p.stop();
+        }
+        gfd_hip_host_free(q);
+    }
+    if (rc == 0) std::printf("ragged %s %u runs: pass\n", path.c_str(), nruns);
+    gfd_hip_free(dst);
+    gfd_hip_host_free(host);
+    return rc;
+}
+
 // SdmaQueue completion-signal slot reuse.  Copy X (engine 0) depends on copy
 // d (engine 1) but sits behind a long copy on its engine; the issuer then
 // runs through the whole signal ring so that d's slot comes round again,
@@ -385,6 +463,9 @@ int run_sdma_slot_reuse() {
 int main(int argc, char** argv) {
     setvbuf(stdout, nullptr, _IOLBF, 0);
     if (argc >= 2 && std::string(argv[1]) == "sdma_slot_reuse") return run_sdma_slot_reuse();
+    if (argc >= 7 && std::string(argv[1]) == "ragged")
+        return run_ragged(argv[2], (uint32_t)std::atoi(argv[3]), (uint32_t)std::atoi(argv[4]), std::atoi(argv[5]),
+                          std::strtoull(argv[6], nullptr, 0));
     if (argc >= 5 && std::string(argv[1]) == "sg")
         return run_sg(argv[2], std::atoi(argv[3]), std::strtoull(argv[4], nullptr, 0));
     if (argc >= 7 && std::string(argv[1]) == "queue")

@@ -67,3 +67,11 @@ def test_sg_mode_split_lists_slow_engines(poller_emu):
                                            (1, 4096, 0)])
 def test_queue_mode(poller_emu, n, t, scattered):
     run(poller_emu, ["queue", n, t, scattered, 2, 3])
+
+
+@pytest.mark.parametrize("path,nruns", [("direct", 1), ("direct", 8), ("direct", 40), ("queue", 1), ("queue", 8),
+                                        ("queue", 100)])
+def test_ragged_entries_over_destination_runs(poller_emu, path, nruns):
+    # Entries of 1..8999 bytes at every alignment: staged gathers with one
+    # copy per chunk or per run piece, and per-run copies.
+    run(poller_emu, ["ragged", path, 700, nruns, 2, 3])
