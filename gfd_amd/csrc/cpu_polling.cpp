@@ -411,8 +411,9 @@ void CpuPollingThread::polling_loop() {
             }
             do {
                 // The ring lines were last written by the GPU, so each is a
-                // cache miss: fetch a few descriptors ahead of the reads.
-                _mm_prefetch((const char*)&queue_->entries[(read + 16) % QUEUE_SIZE], _MM_HINT_T0);
+                // cache miss: fetch 32 descriptors ahead of the reads (16 and
+                // 64 measured equal or slower at 8192 x 4 KiB and 2048 x 512 B).
+                _mm_prefetch((const char*)&queue_->entries[(read + 32) % QUEUE_SIZE], _MM_HINT_T0);
                 take(d);
                 read++;
                 if (n == 1) threshold = batch[0].size <= 2048 ? BATCH_THRESHOLD_SMALL : BATCH_THRESHOLD;
