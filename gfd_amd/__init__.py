@@ -184,6 +184,7 @@ def _declare(L):
         "gfd_sg_session_destroy": ([vp], None),
         "gfd_sg_session_submit": ([vp, vp, c_u32, c_u32, c_u32], ctypes.c_int64),
         "gfd_sg_session_launch": ([vp, vp, vp], c_int),
+        "gfd_sg_session_launch_l2norm": ([vp, vp, c_u32, vp], c_int),
         "gfd_sg_session_launch_gpu_submit": ([vp, vp, c_u32, c_u32, vp, vp], c_int),
         "gfd_sg_session_synchronize": ([vp, c_u64], c_int),
         "gfd_sg_session_reset": ([vp], c_int),
@@ -636,6 +637,10 @@ class SGWarpSpecSession:
 
     def launch(self, list_sums=None, stream=None):
         _check(lib().gfd_sg_session_launch(self._h, list_sums, stream), "gfd_sg_session_launch")
+
+    def launch_l2norm(self, out, out_len, stream=None):
+        """Launch with the per-entry fp32 L2-norm consumer (out: device float[out_len])."""
+        _check(lib().gfd_sg_session_launch_l2norm(self._h, out, out_len, stream), "gfd_sg_session_launch_l2norm")
 
     def launch_gpu_submit(self, d_entries, entries_per_list, num_lists, list_sums=None, stream=None):
         _check(lib().gfd_sg_session_launch_gpu_submit(self._h, d_entries, entries_per_list, num_lists, list_sums,

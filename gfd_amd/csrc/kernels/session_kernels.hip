@@ -96,12 +96,36 @@ struct NullList {
     __device__ void operator()(SGListView) const {}
 };
 
+// Per entry, the L2 norm of its landed bytes read as fp32, stored at
+// out[list_id * count + i] (the MoE consumer of examples/09_sg_warp_spec.cu:
+// 44-65).  The wave sums the squares lane-parallel, then across lanes.
+// Entries whose destination is not 4-byte aligned, or whose slot lies past
+// out_len, are skipped.
+struct EntryL2Norm {
+    float* out;
+    uint32_t out_len;
+    __device__ void operator()(SGListView v) const {
+        for (uint32_t e = 0; e < v.count; e++) {
+            const gfd::DeviceSGEntry d = v.get_entry(e);
+            const uint64_t slot = (uint64_t)v.list_id * v.count + e;
+            if ((d.dst_addr & 3) != 0 || slot >= out_len) continue;
+            const float* x = reinterpret_cast<const float*>(d.dst_addr);
+            const uint32_t nf = d.size / 4;
+            float acc = 0.f;
+            for (uint32_t k = (uint32_t)v.lane_id; k < nf; k += 64) acc = fmaf(x[k], x[k], acc);
+            for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+            if (v.lane_id == 0) out[slot] = sqrtf(acc);
+        }
+    }
+};
+
 GFD_WARP_SPEC_KERNEL(ws_token_sum_kernel, TokenSum)
 GFD_WARP_SPEC_KERNEL_DB(ws_token_sum_kernel_db, TokenSum)
 GFD_WARP_SPEC_KERNEL(ws_null_kernel, NullChunk)
 GFD_WARP_SPEC_KERNEL_DB(ws_null_kernel_db, NullChunk)
 GFD_SG_WARP_SPEC_KERNEL(sg_checksum_kernel, ListChecksum)
 GFD_SG_WARP_SPEC_KERNEL(sg_null_kernel, NullList)
+GFD_SG_WARP_SPEC_KERNEL(sg_l2norm_kernel, EntryL2Norm)
 
 // Transfer (wave 0) + compute (wave 1) + submitter (wave 2) + transfer
 // helpers (waves 3..) per workgroup, as test/test_sg_gpu_submit.cu:20-213:
@@ -251,6 +275,13 @@ extern "C" int gfd_sg_session_launch(gfd_sg_session_t s, unsigned long long* lis
     else S(s)->launch(sg_null_kernel, NullList{}, stream);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail(e, "gfd_sg_session_launch: launch failed");
+}
+
+extern "C" int gfd_sg_session_launch_l2norm(gfd_sg_session_t s, float* out, uint32_t out_len, void* stream) {
+    if (!s || !out) return fail(hipErrorInvalidValue, "gfd_sg_session_launch_l2norm: NULL argument");
+    S(s)->launch(sg_l2norm_kernel, EntryL2Norm{out, out_len}, stream);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail(e, "gfd_sg_session_launch_l2norm: launch failed");
 }
 
 extern "C" int gfd_sg_session_launch_gpu_submit(gfd_sg_session_t s, const gfd_device_sg_entry* d_entries,

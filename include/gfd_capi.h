@@ -316,6 +316,11 @@ int64_t gfd_sg_session_submit(gfd_sg_session_t s, const gfd_device_sg_entry* ent
  * (a trailing partial word adds its bytes); list_sums == NULL: no-op consumer
  * (test/test_sg_e2e.cu:10-17). */
 int gfd_sg_session_launch(gfd_sg_session_t s, unsigned long long* list_sums, void* stream);
+/* launch with the MoE consumer of examples/09_sg_warp_spec.cu:44-65: for entry i
+ * of list list_id, out[list_id * count + i] = L2 norm of the landed bytes read
+ * as fp32 (device float[out_len]; entries with an unaligned destination or a
+ * slot past out_len are skipped). */
+int gfd_sg_session_launch_l2norm(gfd_sg_session_t s, float* out, uint32_t out_len, void* stream);
 /* Kernel with a submitter wave per workgroup (test/test_sg_gpu_submit.cu:20-213):
  * list i = entries [i*entries_per_list, (i+1)*entries_per_list) of d_entries
  * (device array), list_id i; the submitters set terminate once all landed. */
