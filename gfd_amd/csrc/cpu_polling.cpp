@@ -557,12 +557,16 @@ bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_
 // sides.  (No kernel is launched here: Queue-path consumers spin on the GPU,
 // and a kernel could queue behind them on a shared hardware queue.)
 void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total) {
-    const uint64_t t0 = now_us();
     bool dst_contig = true, src_contig = true;
     for (int i = 1; i < count && (dst_contig || src_contig); i++) {
         if (e[i].dst != e[i - 1].dst + e[i - 1].size) dst_contig = false;
         if ((const char*)e[i].src != (const char*)e[i - 1].src + e[i - 1].size) src_contig = false;
     }
+    submit_list(e, count, total, dst_contig, src_contig);
+}
+
+void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total, bool dst_contig, bool src_contig) {
+    const uint64_t t0 = now_us();
     if (count == 1 || (dst_contig && src_contig)) {
         SGEntry one{e[0].dst, e[0].src, total};
         ce_manager_.submit_scatter_gather(&one, 1);
@@ -577,20 +581,33 @@ void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total) {
     total_dma_submit_us_.fetch_add(now_us() - t0, std::memory_order_relaxed);
 }
 
+// The previous batch's gather workers still hold this array's lines in their
+// caches: plain stores would take each line back one by one (12.6 us for
+// 4096 entries against 5 us unshared).  Streaming stores skip those reads,
+// and the route's contiguity tests are made here from the poller's own copy.
 bool CpuPollingThread::process_batch(Descriptor* batch, int count) {
     std::vector<SGEntry>& sg = sg_scratch_;
     sg.resize(count);
     size_t total = 0;
+    bool dst_contig = true, src_contig = true;
+    uint64_t dst_end = batch[0].dst_addr, src_end = batch[0].src_addr;
     for (int i = 0; i < count; i++) {
-        sg[i].dst = batch[i].dst_addr;
-        sg[i].src = (const void*)(uintptr_t)batch[i].src_addr;
-        sg[i].size = batch[i].size;
-        total += batch[i].size;
+        const uint64_t d = batch[i].dst_addr, s = batch[i].src_addr, n = batch[i].size;
+        dst_contig &= d == dst_end;
+        src_contig &= s == src_end;
+        dst_end = d + n;
+        src_end = s + n;
+        total += n;
+        long long* out = reinterpret_cast<long long*>(&sg[i]);
+        _mm_stream_si64(out, (long long)d);
+        _mm_stream_si64(out + 1, (long long)s);
+        _mm_stream_si64(out + 2, (long long)n);
     }
+    _mm_sfence();
     total_bytes_copied_.fetch_add(total, std::memory_order_relaxed);
     descriptors_processed_.fetch_add(count, std::memory_order_relaxed);
     batches_submitted_.fetch_add(1, std::memory_order_relaxed);
-    submit_list(sg.data(), count, total);
+    submit_list(sg.data(), count, total, dst_contig, src_contig);
     return true;
 }
 

@@ -185,6 +185,7 @@ private:
     void process_batch_tiled(Descriptor* batch, int count, uint64_t cur_read);
     void process_batch_sg(Descriptor* batch, int count, uint64_t cur_read);
     void submit_list(const SGEntry* e, int count, size_t total);
+    void submit_list(const SGEntry* e, int count, size_t total, bool dst_contig, bool src_contig);
     // runs == nullptr: destinations contiguous; else nruns destination runs.
     bool gather_through_staging(const SGEntry* e, int count, size_t total, const DstRun* runs = nullptr,
                                 int nruns = 0);
