@@ -74,6 +74,8 @@ public:
     double submit_direct(const SGEntry* entries, int count);
 
     void set_tiled_queue(TiledQueue* tq) { tiled_queue_ = tq; }
+    // SG mode is switched off in the product library: start() logs an error
+    // and does not start while an SG task queue is set.
     void set_sg_task_queue(SGTaskQueue* sq) { sg_queue_ = sq; }
 
     void start();

@@ -98,7 +98,7 @@ int gfd_poller_init_direct_ce(gfd_poller_t p);                       /* init_dir
  * the data is in HBM; returns elapsed microseconds, or -1 on error. */
 double gfd_poller_submit_direct(gfd_poller_t p, const gfd_sg_entry* entries, int count);
 void gfd_poller_set_tiled_queue(gfd_poller_t p, void* tiled_queue);  /* set_tiled_queue (:48) */
-void gfd_poller_set_sg_task_queue(gfd_poller_t p, void* sg_queue);   /* set_sg_task_queue (:53) */
+void gfd_poller_set_sg_task_queue(gfd_poller_t p, void* sg_queue);   /* set_sg_task_queue (:53); SG mode is switched off: start() then refuses */
 void gfd_poller_start(gfd_poller_t p);                               /* start (:56) */
 void gfd_poller_stop(gfd_poller_t p);                                /* stop (:57) */
 int gfd_poller_get_stats(gfd_poller_t p, gfd_poller_stats* out);     /* get_* (:60-71) */
@@ -343,7 +343,10 @@ int gfd_bench_sg_session(gfd_sg_session_t s, const gfd_device_sg_entry* entries,
 
 /* ---- the poller's SG mode (set_sg_task_queue; reference src/batch_processor.cpp:307-446)
  * driven by a kernel with the reference's SG transfer-warp protocol
- * (include/gfd/sg_warp_spec.cuh:95-262) ---- */
+ * (include/gfd/sg_warp_spec.cuh:95-262).  Switched off in this library:
+ * gfd_poller_start refuses a poller with an SG task queue set, because runs of
+ * the mode aborted the process on MI355X and the cause is not found.  GPU-built
+ * SG lists run through the gfd_sg_session_* entry points instead. ---- */
 /* SGTaskQueue in fine-grained host memory; d_list_done (MAX_SG_LISTS flags + device counters)
  * in HBM when device_flags != 0 (the poller writes the flags with copy-engine writes after
  * each list's copies), else in fine-grained host memory (host stores at completion). */
