@@ -13,6 +13,8 @@
 //       Queue mode (src/cpu_polling.cpp:337-490, examples/04_benchmark.cu:
 //       31-54 of the reference): producers of 256 descriptors each, the last
 //       flagged FLAG_LAST_IN_BATCH, then a wait for done_idx.
+//   tiled <tiles> <T> <C> <token_bytes> <whole 0|1> <hbm 0|1> <rounds> <seed>
+//       Tiled mode, per-tile cumulative progress words.
 //   ragged <direct|queue> <n> <runs> <rounds> <seed>
 //       Ragged entries over a few destination runs, at every alignment.
 //   sdma_slot_reuse
@@ -37,6 +39,7 @@
 #include "gfd/descriptor_queue.h"
 #include "gfd/hip_shim.h"
 #include "gfd/sg_task_queue.h"
+#include "gfd/tiled_queue.h"
 #include "sdma.h"
 
 using namespace gfd;
@@ -410,6 +413,111 @@ int run_ragged(const std::string& path, uint32_t n, uint32_t nruns, int rounds, 
     return rc;
 }
 
+// Tiled mode (set_tiled_queue; src/batch_processor.cpp:69-298 of the
+// reference), driven as tiled_poller_kernel drives it: one producer per tile
+// claims slots chunk by chunk (or the whole tile at once), writes descriptors
+// tagged tile << 32 | token with FLAG_LAST_IN_TILE on each chunk's last entry
+// and FLAG_LAST_CHUNK_IN_TILE on the tile's last, commits them and waits for
+// the tile's cumulative progress word (in HBM or host memory).
+int run_tiled(uint32_t tiles, uint32_t T, uint32_t C, uint32_t ts, bool whole, bool dev, int rounds, uint64_t seed) {
+    if (tiles == 0 || tiles > (uint32_t)MAX_TILES || C == 0 || T % C != 0 || (uint64_t)tiles * T > QUEUE_SIZE) return 4;
+    Rng rng(seed);
+    const uint32_t K = T / C;
+    const size_t n = (size_t)tiles * T, bytes = n * ts;
+    auto* host = (uint8_t*)host_alloc(bytes);
+    for (size_t i = 0; i < bytes; i++) host[i] = (uint8_t)rng.next();
+    auto* dst = (uint8_t*)dev_alloc(bytes + 4096);
+    std::vector<uint8_t> want(bytes + 4096, kSentinel);
+    std::memcpy(want.data(), host, bytes);
+    auto* tq = (TiledQueue*)host_alloc(sizeof(TiledQueue));
+    tq->scheduler.total_tiles = tiles;
+    tq->scheduler.tokens_per_tile = T;
+    tq->scheduler.tokens_per_chunk = C;
+    tq->scheduler.chunks_per_tile = K;
+    tq->scheduler.token_size = ts;
+    const size_t dev_words = MAX_TILES + TILE_DEVICE_COUNTER_WORDS;
+    if (dev) tq->d_tile_chunk_done = (uint64_t*)dev_alloc(dev_words * 8);
+    volatile uint64_t* progress = dev ? tq->d_tile_chunk_done : tq->tile_chunk_done;
+    int rc = 0;
+    {
+        CpuPollingThread p(&tq->base, dst, host, bytes, true, -1);
+        p.set_tiled_queue(tq);
+        if (!p.init_copy_engine()) return 4;
+        for (int rnd = 0; rnd < rounds && rc == 0; rnd++) {
+            std::printf("tiled %u tiles T=%u C=%u ts=%u whole=%d dev=%d round %d\n", tiles, T, C, ts, (int)whole,
+                        (int)dev, rnd);
+            p.stop();
+            std::memset((void*)&tq->base, 0, sizeof(tq->base));
+            std::memset((void*)tq->tile_chunk_done, 0, sizeof(tq->tile_chunk_done));
+            if (dev) std::memset(tq->d_tile_chunk_done, 0, dev_words * 8);
+            p.reset_stats();
+            std::memset(dst, kSentinel, want.size());
+            p.start();
+            std::atomic<int> timed_out{-1};
+            std::vector<std::thread> wg;
+            for (uint32_t tile = 0; tile < tiles; tile++)
+                wg.emplace_back([&, tile] {
+                    Rng lr(seed * 7919u + tile + 131u * (uint64_t)rnd);
+                    const uint32_t steps = whole ? 1 : K, per = whole ? T : C;
+                    for (uint32_t k = 0; k < steps; k++) {
+                        std::vector<Entry> e(per);
+                        std::vector<uint32_t> fl(per), tok(per);
+                        for (uint32_t i = 0; i < per; i++) {
+                            const uint32_t in_tile = k * per + i, g = tile * T + in_tile;
+                            e[i] = Entry{(uint64_t)(uintptr_t)host + (uint64_t)g * ts,
+                                         (uint64_t)(uintptr_t)dst + (uint64_t)g * ts, ts};
+                            fl[i] = (in_tile % C) == C - 1 ? FLAG_LAST_IN_TILE : FLAG_NONE;
+                            if (in_tile == T - 1) fl[i] |= FLAG_LAST_CHUNK_IN_TILE;
+                            tok[i] = g;
+                        }
+                        const uint64_t base = __atomic_fetch_add(&tq->base.write_idx, (uint64_t)per, __ATOMIC_RELAXED);
+                        for (uint32_t i = 0; i < per; i++) {
+                            Descriptor* d = &tq->base.entries[(base + i) % QUEUE_SIZE];
+                            d->src_addr = e[i].src;
+                            d->dst_addr = e[i].dst;
+                            d->size = e[i].size;
+                            d->flags = fl[i];
+                            d->user_data = ((uint64_t)tile << 32) | tok[i];
+                        }
+                        uint32_t order[64];
+                        for (uint32_t g0 = 0; g0 < per; g0 += 64) {
+                            const uint32_t m = std::min<uint32_t>(64, per - g0);
+                            for (uint32_t q = 0; q < m; q++) order[q] = q;
+                            for (uint32_t q = m; q > 1; q--) std::swap(order[q - 1], order[lr.below(q)]);
+                            for (uint32_t q = 0; q < m; q++)
+                                __atomic_store_n(&tq->base.entries[(base + g0 + order[q]) % QUEUE_SIZE].sequence,
+                                                 base + g0 + order[q] + 1, __ATOMIC_RELEASE);
+                        }
+                        if (!wait_u64(&progress[tile], (uint64_t)(k + 1) * per)) {
+                            timed_out = (int)tile;
+                            return;
+                        }
+                    }
+                });
+            for (auto& t : wg) t.join();
+            if (timed_out >= 0) {
+                std::printf("tiled round %d: tile %d wait timed out\n", rnd, timed_out.load());
+                rc = 2;
+                break;
+            }
+            rc = check_image(dst, want, "tiled", rnd);
+            for (uint32_t tile = 0; tile < tiles && rc == 0; tile++)
+                if (progress[tile] != T) {
+                    std::printf("tiled round %d: tile %u progress %llu\n", rnd, tile,
+                                (unsigned long long)progress[tile]);
+                    rc = 3;
+                }
+        }
+        p.stop();
+    }
+    if (rc == 0) std::printf("tiled: pass\n");
+    if (dev) gfd_hip_free(tq->d_tile_chunk_done);
+    gfd_hip_host_free(tq);
+    gfd_hip_free(dst);
+    gfd_hip_host_free(host);
+    return rc;
+}
+
 // SdmaQueue completion-signal slot reuse.  Copy X (engine 0) depends on copy
 // d (engine 1) but sits behind a long copy on its engine; the issuer then
 // runs through the whole signal ring so that d's slot comes round again,
@@ -463,6 +571,10 @@ int run_sdma_slot_reuse() {
 int main(int argc, char** argv) {
     setvbuf(stdout, nullptr, _IOLBF, 0);
     if (argc >= 2 && std::string(argv[1]) == "sdma_slot_reuse") return run_sdma_slot_reuse();
+    if (argc >= 10 && std::string(argv[1]) == "tiled")
+        return run_tiled((uint32_t)std::atoi(argv[2]), (uint32_t)std::atoi(argv[3]), (uint32_t)std::atoi(argv[4]),
+                         (uint32_t)std::atoi(argv[5]), std::atoi(argv[6]) != 0, std::atoi(argv[7]) != 0,
+                         std::atoi(argv[8]), std::strtoull(argv[9], nullptr, 0));
     if (argc >= 7 && std::string(argv[1]) == "ragged")
         return run_ragged(argv[2], (uint32_t)std::atoi(argv[3]), (uint32_t)std::atoi(argv[4]), std::atoi(argv[5]),
                           std::strtoull(argv[6], nullptr, 0));

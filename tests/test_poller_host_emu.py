@@ -75,3 +75,20 @@ def test_ragged_entries_over_destination_runs(poller_emu, path, nruns):
     # Entries of 1..8999 bytes at every alignment: staged gathers with one
     # copy per chunk or per run piece, and per-run copies.
     run(poller_emu, ["ragged", path, 700, nruns, 2, 3])
+
+
+@pytest.mark.parametrize("tiles,T,C,ts,whole,hbm", [(8, 128, 32, 4096, 0, 1), (8, 128, 32, 4096, 1, 1),
+                                                    (16, 64, 64, 1000, 0, 1), (4, 256, 16, 2048, 0, 0),
+                                                    (100, 32, 8, 512, 0, 1)])
+def test_tiled_mode(poller_emu, tiles, T, C, ts, whole, hbm):
+    # Tiled mode (reference src/batch_processor.cpp:69-298): per-tile
+    # cumulative progress words after each chunk's copies, in HBM (8-byte
+    # copies chained behind the data and the previous progress write) or in
+    # host memory; the shapes of the GPU test of the kernel-driven mode.
+    run(poller_emu, ["tiled", tiles, T, C, ts, whole, hbm, 2, 3])
+
+
+def test_tiled_mode_whole_tiles_slow_engines(poller_emu):
+    # Four batches of one tile in flight together on slow engines: each
+    # progress write must land after the previous one.
+    run(poller_emu, ["tiled", 8, 128, 32, 4096, 1, 1, 2, 5], env={"GFD_EMU_COPY_NS": "3000"})
