@@ -42,6 +42,8 @@ def run(binary, args, env=None):
     e = dict(os.environ)
     e.update(env or {})
     e.setdefault("GFD_EMU_STALL_MS", "3000")
+    # Also catch writes through pointers into stack frames that have returned.
+    e.setdefault("ASAN_OPTIONS", "detect_stack_use_after_return=1")
     p = subprocess.run([binary] + [str(a) for a in args], capture_output=True, text=True, timeout=120, env=e)
     out = p.stdout + p.stderr
     assert p.returncode == 0, "poller_emu %s exited %d:\n%s" % (" ".join(map(str, args)), p.returncode, out[-3000:])
