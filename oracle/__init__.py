@@ -1,8 +1,8 @@
 """CPU oracle for the scattered host-to-device gather path.
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
-``bench.py``'s ``cpu_baseline`` leg import this package, and only as the
-checker (or, for the CPU baseline, as the thing timed on the host cores).
+``bench.py``'s ``cpu_baseline`` leg import this package, and only to verify
+results (or, for the CPU baseline, as the thing timed on the host cores).
 The product path (``gfd_amd``) never imports it.
 
 What each function restates is cited in ``oracle/oracle.c`` and below.

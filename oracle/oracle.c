@@ -1,7 +1,7 @@
 /*
  * oracle.c — CPU oracle for the scattered host-to-device gather path.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker: only tests/,
+ * TEST INFRASTRUCTURE ONLY.  This file verifies results: only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.  The
  * product library (gfd_amd/libgfd_amd.so) never links or calls it.
  *
