@@ -347,7 +347,7 @@ class CpuPollingThread:
     def set_sg_task_queue(self, sq):
         """Switched off: CpuPollingThread::start() refuses an SG task queue (an
         SG-mode run aborted the process on MI355X and the cause is not found)."""
-        raise RuntimeError("the poller's SG task-queue mode is switched off in this build")
+        raise RuntimeError("the poller's SG task-queue mode is switched off in this library")
 
     def start(self):
         lib().gfd_poller_start(self._h)

@@ -312,7 +312,7 @@ void CpuPollingThread::start() {
     // cause has not been found.  The host emulation build keeps the mode so
     // that its logic stays tested.
     if (sg_queue_) {
-        GFD_LOG_ERROR("start(): SG task-queue mode is switched off in this build\n");
+        GFD_LOG_ERROR("start(): SG task-queue mode is switched off in this library\n");
         return;
     }
 #endif

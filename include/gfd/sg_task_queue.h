@@ -53,7 +53,7 @@ struct SGTaskQueue {
 
     alignas(64) volatile uint64_t lists_completed;
     volatile uint32_t terminate;
-    // The reference's padding word after `terminate`.  This build reads it as
+    // The reference's padding word after `terminate`.  This library reads it as
     // the transfer waves' idle limit in milliseconds (0 = 30 s): a wave that
     // sees no committed list for that long gives up instead of spinning
     // forever when the host never sets `terminate`.

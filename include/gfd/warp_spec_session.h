@@ -47,7 +47,7 @@ struct WarpSpecConfig {
     bool use_copy_engine = true;    // kept for API compatibility (data moves zero-copy)
     bool double_buffer = false;
     bool per_tile_mode = false;     // one chunk per tile
-    // Transfer helper waves per workgroup (this build's addition): they copy
+    // Transfer helper waves per workgroup (an addition to the reference's API): they copy
     // pieces of each tile next to the transfer wave, so one workgroup keeps up
     // to 4x the loads in flight.  Negative: auto_helper_waves(grid), set by
     // the session.  Fewer if the workgroup would pass 1024 threads.
@@ -156,7 +156,7 @@ struct SGWarpSpecConfig {
     int max_lists = MAX_SG_LISTS;
     int max_entries = MAX_SG_POOL_ENTRIES;
     uint32_t idle_limit_ms = 0;  // transfer waves give up after this long without a list (0 = 30 s)
-    // Transfer helper waves per workgroup (this build's addition, 0..3): they
+    // Transfer helper waves per workgroup (an addition to the reference's API, 0..3): they
     // copy 64-entry batches of each list next to the transfer wave.
     // Negative: auto_helper_waves(grid), set by the session.
     int transfer_helper_waves = -1;

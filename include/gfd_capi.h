@@ -283,7 +283,7 @@ typedef struct gfd_session_result {
     uint64_t error_bits;  /* nonzero: a bounded wait inside the kernel gave up */
     double elapsed_ms;    /* launch -> synchronize, host clock */
     int grid, block, tokens_per_chunk, chunks_per_tile;
-    int helper_waves;     /* transfer helper waves per workgroup (this build's addition) */
+    int helper_waves;     /* transfer helper waves per workgroup (an addition to the reference's API) */
 } gfd_session_result;
 
 /* WarpSpecSession over tokens [0, total_tokens) of cpu_src (pinned) -> gpu_dst

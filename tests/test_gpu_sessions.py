@@ -37,7 +37,7 @@ def auto_helpers(grid):
 
 
 def with_helpers(block, helpers):
-    """Workgroup of a session: the reference's block plus this build's
+    """Workgroup of a session: the reference's block plus this library's
     transfer helper waves (as many as fit in 1024 threads)."""
     h = max(0, min(helpers, (1024 - block) // 64))
     return block + 64 * h, h
