@@ -196,3 +196,10 @@ def test_host_gather_with_sleeping_workers():
     env = dict(os.environ, GFD_GATHER_SPIN_US="0", PYTHONPATH=ROOT)
     r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stderr
+
+
+def test_poller_sg_mode_is_refused_in_the_binding():
+    # The poller's SG task-queue mode is switched off in this library (two
+    # MI355X runs aborted, cause not found); the binding says so at once.
+    with pytest.raises(RuntimeError, match="switched off"):
+        gfd_amd.CpuPollingThread.set_sg_task_queue(object(), None)
