@@ -527,6 +527,146 @@ def run_helper_waves(oracle, iters, warmup):
     return out
 
 
+TRACE_NAMES = {1: "batch_first_read", 2: "flush", 3: "copies_issued", 4: "done_published", 5: "gap_flush",
+               7: "chunk_copy_issued", 9: "gather_entry", 10: "gather_idle", 11: "gather_published",
+               12: "gather_first_slice", 13: "gather_built"}
+
+
+def _phase_medians(rows):
+    """rows: list of {phase: us}; median per phase over the rows that have it."""
+    keys = []
+    for r in rows:
+        for k in r:
+            if k not in keys:
+                keys.append(k)
+    out = {}
+    for k in keys:
+        v = [r[k] for r in rows if k in r]
+        out[k] = round(float(np.median(v)), 2)
+    return dict(sorted(out.items(), key=lambda kv: kv[1]))
+
+
+def _call_phases(tr, cp, t0, t1):
+    """Phase times (us after t0) of one call from the poller trace `tr` and
+    the SDMA copy timeline `cp`, both on CLOCK_MONOTONIC ns."""
+    ph = {}
+    for ev in tr[(tr["t_ns"] >= t0) & (tr["t_ns"] <= t1)]:
+        name = TRACE_NAMES.get(int(ev["kind"]))
+        if name is None:
+            continue
+        us = (int(ev["t_ns"]) - t0) / 1e3
+        if name + "_first" not in ph:
+            ph[name + "_first"] = us
+        ph[name + "_last"] = us
+    c = cp[(cp["start_ns"] >= t0) & (cp["end_ns"] <= t1)]
+    if len(c):
+        ph["sdma_first_start"] = (int(c["start_ns"].min()) - t0) / 1e3
+        ph["sdma_last_end"] = (int(c["end_ns"].max()) - t0) / 1e3
+        ph["sdma_copies"] = float(len(c))
+    ph["return"] = (t1 - t0) / 1e3
+    return ph
+
+
+def run_timeline(oracle, calls=30):
+    """Where the time of one call goes, for GFD Direct and GFD Queue at
+    2048 x {512, 1024, 2048} B and 8192 x 4 KiB: the poller's trace events
+    and the SDMA copy timeline of `calls` back-to-back calls, as the median
+    time of each phase after the call starts (us).  Direct: from entry into
+    submit_direct to its return.  Queue: from the host's launch of the
+    submit kernel to the return of the stream synchronisation after the wait
+    kernel.  Every call's output is compared with the oracle."""
+    L_ = gfd_amd.lib()
+    out = {"calls": calls}
+    shapes = [(2048, 512), (2048, 1024), (2048, 2048), (8192, 4096)]
+    direct = gfd_amd.CpuPollingThread(None, None, None, 8192 * 4096 * 2, numa_node=-1)
+    assert direct.init_direct_ce(), "init_direct_ce failed"
+    for n, t in shapes:
+        L = Layout(oracle, n, t)
+        for _ in range(10):
+            assert direct.submit_direct(L.entries, L.n) > 0
+        direct.set_trace(True)
+        direct.set_copy_timing(True)
+        direct.read_trace()
+        direct.read_copy_times()
+        win = []
+        for _ in range(calls):
+            a = time.monotonic_ns()
+            assert direct.submit_direct(L.entries, L.n) > 0
+            win.append((a, time.monotonic_ns()))
+        tr, cp = direct.read_trace(), direct.read_copy_times()
+        direct.set_trace(False)
+        direct.set_copy_timing(False)
+        L.verify("direct (timeline)")
+        rows = []
+        for a, b in win:
+            begin = tr[(tr["kind"] == 6) & (tr["t_ns"] >= a) & (tr["t_ns"] <= b)]
+            t0 = int(begin["t_ns"][0]) if len(begin) else a
+            rows.append(_call_phases(tr, cp[cp["path"] == 1], t0, b))
+        out["direct_%dx%d" % (n, t)] = _phase_medians(rows)
+        log("  timeline direct %dx%d: %s" % (n, t, out["direct_%dx%d" % (n, t)]))
+        del L
+    direct.close()
+
+    q = gfd_amd.DescriptorQueue()
+    p = gfd_amd.CpuPollingThread(q, None, None, 8192 * 4096 * 2, numa_node=-1)
+    assert p.init_copy_engine(), "queue poller init failed"
+    p.start()
+    st = ctypes.c_void_p()
+    L_.gfd_stream_create(ctypes.byref(st))
+    status = gfd_amd.HostBuffer(64, gfd_amd.HOST_COHERENT)
+    base = 0
+    try:
+        for n, t in shapes:
+            L = Layout(oracle, n, t)
+            rows = []
+            for i in range(10 + calls):
+                if i == 10:
+                    p.set_trace(True)
+                    p.set_copy_timing(True)
+                    p.read_trace()
+                    p.read_copy_times()
+                status.array.view(np.int32)[0] = -1
+                a = time.monotonic_ns()
+                assert L_.gfd_queue_submit_tokens(q.ptr, L.tokens.ptr, L.dst.ptr, n, t, base, st) == 0
+                base += n
+                assert L_.gfd_queue_wait(q.ptr, base, 10_000_000, status.ptr, st) == 0
+                assert L_.gfd_stream_synchronize(st) == 0
+                b = time.monotonic_ns()
+                assert int(status.array.view(np.int32)[0]) == 0, "queue wait timed out"
+                if i >= 10:
+                    rows.append((a, b))
+            tr, cp = p.read_trace(), p.read_copy_times()
+            p.set_trace(False)
+            p.set_copy_timing(False)
+            L.verify("queue (timeline)")
+            out["queue_%dx%d" % (n, t)] = _phase_medians([_call_phases(tr, cp[cp["path"] == 0], a, b)
+                                                          for a, b in rows])
+            log("  timeline queue %dx%d: %s" % (n, t, out["queue_%dx%d" % (n, t)]))
+            del L
+    finally:
+        L_.gfd_stream_destroy(st)
+        p.stop()
+        p.close()
+        q.free()
+    return out
+
+
+def first_call_latency(oracle):
+    """A fresh poller's first submit_direct (256 x 4 KiB scattered, 1 MiB),
+    then its second: the one-off set-up cost a caller pays on first use."""
+    L = Layout(oracle, 256, 4096)
+    t_init = time.monotonic_ns()
+    p = gfd_amd.CpuPollingThread(None, None, None, L.n * L.stride, numa_node=-1)
+    assert p.init_direct_ce(), "init_direct_ce failed"
+    init_us = (time.monotonic_ns() - t_init) / 1e3
+    first = p.submit_direct(L.entries, L.n)
+    second = p.submit_direct(L.entries, L.n)
+    p.close()
+    L.verify("direct (first call)")
+    return {"init_direct_ce_us": round(init_us, 1), "first_call_us": round(first, 2),
+            "second_call_us": round(second, 2)}
+
+
 class QueueRig:
     def __init__(self, region_bytes):
         self.q = gfd_amd.DescriptorQueue()
@@ -573,7 +713,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="",
                     help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions,scattered,offload,"
-                         "helpers (helpers is not in the default run) "
+                         "firstcall,helpers,timeline (helpers and timeline are not in the default run) "
                          "(calib: add a 32 MiB D2D copy)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -655,6 +795,16 @@ def main():
         log("wave-specialised sessions ...")
         r_sessions = run_sessions(oracle, K, W)
 
+    r_timeline = None
+    if "timeline" in only:
+        log("per-call timelines (Direct, Queue) ...")
+        r_timeline = run_timeline(oracle)
+
+    r_first = None
+    if want("firstcall"):
+        r_first = first_call_latency(oracle)
+        log("first submit_direct of a fresh poller: %s" % r_first)
+
     r_helpers = None
     if "helpers" in only:
         log("transfer helper waves at 1/4/8 workgroups ...")
@@ -726,6 +876,8 @@ def main():
         "results_direct_scattered_dst_8192x4KB": r_scat,
         "results_offload": r_offload,
         "results_helper_waves": r_helpers,
+        "results_timeline": r_timeline,
+        "first_call_direct_256x4KB": r_first,
         "direct_setup": {k: dinfo[k] for k in ("numa_node", "num_gather_workers", "worker_cpus", "poller_cpu",
                                                "num_ce_channels", "direct_chunk_bytes", "gather_slice_bytes")},
         "host": info,

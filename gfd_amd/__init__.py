@@ -58,6 +58,7 @@ class PollerInfo(ctypes.Structure):
         ("poller_cpu", ctypes.c_int), ("worker_cpus", ctypes.c_int * 16), ("num_ce_channels", ctypes.c_int),
         ("num_staging_buffers", ctypes.c_int), ("staging_buffer_size", ctypes.c_uint64),
         ("direct_chunk_bytes", ctypes.c_uint64), ("gather_slice_bytes", ctypes.c_uint64),
+        ("staging_pool_set", ctypes.c_int), ("running", ctypes.c_int),
     ]
 
 
@@ -134,9 +135,10 @@ def _declare(L):
         "gfd_poller_init_direct_ce": ([vp], c_int),
         "gfd_poller_submit_direct": ([vp, vp, c_int], c_dbl),
         "gfd_poller_set_tiled_queue": ([vp, vp], None),
-        "gfd_poller_set_sg_task_queue": ([vp, vp], None),
-        "gfd_poller_start": ([vp], None),
+        "gfd_poller_set_sg_task_queue": ([vp, vp], c_int),
+        "gfd_poller_start": ([vp], c_int),
         "gfd_poller_stop": ([vp], None),
+        "gfd_poller_is_running": ([vp], c_int),
         "gfd_poller_get_stats": ([vp, ctypes.POINTER(PollerStats)], c_int),
         "gfd_poller_reset_stats": ([vp], None),
         "gfd_poller_get_info": ([vp, ctypes.POINTER(PollerInfo)], c_int),
@@ -159,6 +161,7 @@ def _declare(L):
         "gfd_queue_free": ([vp], c_int),
         "gfd_queue_submit_tokens": ([vp, vp, vp, c_int, c_u32, c_u64, vp], c_int),
         "gfd_queue_wait": ([vp, c_u64, c_u64, vp, vp], c_int),
+        "gfd_queue_submit_tokens_safe": ([vp, vp, vp, c_int, c_u32, c_u64, c_u64, vp, vp, vp], c_int),
         "gfd_bench_memcpy_per_token": ([vp, vp, c_int, c_u32, c_int, c_int, pd], c_int),
         "gfd_bench_memcpy_contiguous": ([vp, vp, c_sz, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_sdma_contiguous": ([vp, vp, c_sz, c_int, c_int, c_int, c_int, pd, ctypes.POINTER(c_u32)], c_int),
@@ -346,11 +349,18 @@ class CpuPollingThread:
 
     def set_sg_task_queue(self, sq):
         """Switched off: CpuPollingThread::start() refuses an SG task queue (an
-        SG-mode run aborted the process on MI355X and the cause is not found)."""
-        raise RuntimeError("the poller's SG task-queue mode is switched off in this library")
+        SG-mode run aborted the process on MI355X and the cause is not found).
+        The C-ABI records the queue and reports GFD_ERR_NOT_SUPPORTED."""
+        rc = lib().gfd_poller_set_sg_task_queue(self._h, getattr(sq, "ptr", sq))
+        if rc != 0:
+            raise RuntimeError(lib().gfd_last_error().decode())
 
     def start(self):
-        lib().gfd_poller_start(self._h)
+        """Start the polling thread; raises GfdError if it did not start."""
+        _check(lib().gfd_poller_start(self._h), "CpuPollingThread.start")
+
+    def is_running(self):
+        return bool(lib().gfd_poller_is_running(self._h))
 
     def stop(self):
         lib().gfd_poller_stop(self._h)

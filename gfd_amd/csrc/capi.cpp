@@ -166,15 +166,25 @@ double gfd_poller_submit_direct(gfd_poller_t p, const gfd_sg_entry* entries, int
 void gfd_poller_set_tiled_queue(gfd_poller_t p, void* tq) {
     if (p) P(p)->set_tiled_queue((gfd::TiledQueue*)tq);
 }
-void gfd_poller_set_sg_task_queue(gfd_poller_t p, void* sq) {
-    if (p) P(p)->set_sg_task_queue((gfd::SGTaskQueue*)sq);
+int gfd_poller_set_sg_task_queue(gfd_poller_t p, void* sq) {
+    if (!p) return fail(1, "null poller");
+    P(p)->set_sg_task_queue((gfd::SGTaskQueue*)sq);
+    if (!sq) return 0;
+    g_last_error = "the poller's SG task-queue mode is switched off in this library: start() will refuse to run";
+    return GFD_ERR_NOT_SUPPORTED;
 }
-void gfd_poller_start(gfd_poller_t p) {
-    if (p) P(p)->start();
+int gfd_poller_start(gfd_poller_t p) {
+    if (!p) return fail(1, "null poller");
+    P(p)->start();
+    if (P(p)->is_running()) return 0;
+    g_last_error = "start(): the polling thread did not start (no descriptor queue, init_copy_engine() not done, "
+                   "or an SG task queue is set)";
+    return -1;
 }
 void gfd_poller_stop(gfd_poller_t p) {
     if (p) P(p)->stop();
 }
+int gfd_poller_is_running(gfd_poller_t p) { return p && P(p)->is_running() ? 1 : 0; }
 
 int gfd_poller_get_stats(gfd_poller_t p, gfd_poller_stats* out) {
     if (!p || !out) return -1;
@@ -210,6 +220,8 @@ int gfd_poller_get_info(gfd_poller_t p, gfd_poller_info* out) {
     out->staging_buffer_size = t->staging_buffer_size();
     out->direct_chunk_bytes = t->direct_chunk_bytes();
     out->gather_slice_bytes = t->gather_slice_bytes();
+    out->staging_pool_set = t->staging_pool_set();
+    out->running = t->is_running() ? 1 : 0;
     return 0;
 }
 

@@ -21,6 +21,36 @@ __global__ __launch_bounds__(256) void queue_submit_tokens_kernel(gfd::Descripto
                                   token_size, num_tokens);
 }
 
+// Backpressure form (the reference's write_descriptor_safe, device.cuh:120-152,
+// with the caller's retry it asks for): lane j writes descriptor j at slot
+// base_slot + j only once the poller has consumed that slot, retrying with
+// s_sleep; the wait is bounded by max_ticks (then *status = 1 and the lane
+// gives up).  Launches may hold more descriptors than QUEUE_SIZE: lanes of a
+// later lap wait for the earlier lap's slots, which lower-numbered
+// workgroups (dispatched first, never waiting themselves) have committed.
+// full_count (HBM, optional) counts lanes that found their slot occupied.
+__global__ __launch_bounds__(256) void queue_submit_safe_kernel(gfd::DescriptorQueue* queue,
+                                                                const gfd::TokenInfo* __restrict__ tokens,
+                                                                void* gpu_dst, int num_tokens, uint32_t token_size,
+                                                                uint64_t base_slot, uint64_t max_ticks, int* status,
+                                                                unsigned int* full_count) {
+    const int tid = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (tid >= num_tokens) return;
+    const uint64_t src = tokens[tid].cpu_addr;
+    const uint64_t t0 = wall_clock64();
+    bool waited = false;
+    while (!gfd::device::write_descriptor_safe(queue, base_slot, tid, src, gpu_dst, token_size, num_tokens)) {
+        waited = true;
+        if (wall_clock64() - t0 > max_ticks) {
+            __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(8);
+    }
+    gfd::device::commit_slot(queue, base_slot + (uint64_t)tid);
+    if (waited && full_count) atomicAdd(full_count, 1u);
+}
+
 __global__ void queue_wait_kernel(gfd::DescriptorQueue* queue, uint64_t expected_done, uint64_t max_ticks,
                                   int* status) {
     if (threadIdx.x == 0 && blockIdx.x == 0) {
@@ -111,6 +141,23 @@ extern "C" int gfd_queue_submit_tokens(void* queue, const void* tokens, void* gp
     const int blocks = (num_tokens + threads - 1) / threads;
     hipLaunchKernelGGL(queue_submit_tokens_kernel, dim3(blocks), dim3(threads), 0, (hipStream_t)stream, q,
                        (const gfd::TokenInfo*)tokens, gpu_dst, num_tokens, token_size, base_slot);
+    return (int)hipGetLastError();
+}
+
+extern "C" int gfd_queue_submit_tokens_safe(void* queue, const void* tokens, void* gpu_dst, int num_tokens,
+                                            uint32_t token_size, uint64_t base_slot, uint64_t timeout_us, int* status,
+                                            unsigned int* full_count, void* stream) {
+    if (!queue || !status || num_tokens < 0 || (num_tokens > 0 && (!tokens || !gpu_dst || token_size == 0)))
+        return (int)hipErrorInvalidValue;
+    if (num_tokens == 0) return 0;
+    auto* q = (gfd::DescriptorQueue*)queue;
+    if (base_slot < __atomic_load_n(&q->read_idx, __ATOMIC_ACQUIRE)) return (int)hipErrorInvalidValue;
+    const uint64_t ticks = timeout_us * (gfd::device::kWallClockHz / 1000000ull);
+    const int threads = 256;
+    const int blocks = (num_tokens + threads - 1) / threads;
+    hipLaunchKernelGGL(queue_submit_safe_kernel, dim3(blocks), dim3(threads), 0, (hipStream_t)stream, q,
+                       (const gfd::TokenInfo*)tokens, gpu_dst, num_tokens, token_size, base_slot, ticks, status,
+                       full_count);
     return (int)hipGetLastError();
 }
 

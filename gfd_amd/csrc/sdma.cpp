@@ -200,6 +200,10 @@ bool SdmaQueue::host_source_ok(const void* p, size_t n) {
     if (hsa_amd_pointer_info(const_cast<void*>(p), &info, nullptr, nullptr, nullptr) != HSA_STATUS_SUCCESS)
         return false;
     if (info.type != HSA_EXT_POINTER_TYPE_HSA && info.type != HSA_EXT_POINTER_TYPE_LOCKED) return false;
+    // Registered (locked) memory can be mapped for the GPU at another address
+    // than the host's.  Copies and kernels here are given host addresses, so
+    // such a range is not a legal source: the caller then copies it another way.
+    if (info.type == HSA_EXT_POINTER_TYPE_LOCKED && info.agentBaseAddress != info.hostBaseAddress) return false;
     const uintptr_t base = (uintptr_t)info.hostBaseAddress;
     if (!base || lo < base || hi > base + info.sizeInBytes) return false;
     ok_lo_ = base;

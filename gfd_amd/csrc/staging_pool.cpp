@@ -12,6 +12,7 @@
 
 #include "gfd/hip_shim.h"
 #include "gfd/log.h"
+#include "gfd/pcie_topology.h"
 
 namespace gfd {
 
@@ -71,17 +72,16 @@ bool StagingPool::init(int num_gpus, size_t buf_size, int numa_node) {
     for (int s = 0; s < num_sets_; s++) {
         BufferSet& set = sets_[s];
         set.buf_size = buf_size;
-        set.numa_node = numa_node;
+        set.numa_node = numa_node >= 0 ? numa_node : discover_gpu_topology(s).numa_node;
         set.in_use = false;
+        set.hugepage = false;
         bool ok = true;
         for (int b = 0; b < BUFS_PER_SET; b++) {
-            bool hp = false;
-            set.bufs[b] = alloc_pinned(buf_size, numa_node, &hp);
+            set.bufs[b] = alloc_pinned(buf_size, set.numa_node, nullptr);
             if (!set.bufs[b]) {
                 ok = false;
                 break;
             }
-            set.hugepage = hp;
         }
         if (ok) {
             ok_sets++;
@@ -94,22 +94,28 @@ bool StagingPool::init(int num_gpus, size_t buf_size, int numa_node) {
         }
     }
     initialized_ = true;
-    GFD_LOG_INFO("StagingPool: %d set(s) x %d x %zu bytes, NUMA %d\n", ok_sets, BUFS_PER_SET,
-                 buf_size, numa_node);
+    GFD_LOG_INFO("StagingPool: %d set(s) x %d x %zu bytes, NUMA %d%s\n", ok_sets, BUFS_PER_SET, buf_size,
+                 numa_node, numa_node < 0 ? " (per GPU)" : "");
     return ok_sets > 0;
 }
 
+int StagingPool::choose_set(const BufferSet* sets, int n, size_t required_size, int numa_node) {
+    int other = -1;
+    for (int s = 0; s < n; s++) {
+        const BufferSet& b = sets[s];
+        if (b.in_use || b.buf_size < required_size || !b.bufs[0]) continue;
+        if (numa_node < 0 || b.numa_node == numa_node) return s;
+        if (other < 0) other = s;
+    }
+    return other;
+}
+
 int StagingPool::acquire_buffers(size_t required_size, int numa_node) {
-    (void)numa_node;
     std::lock_guard<std::mutex> lock(mutex_);
     if (!initialized_) return -1;
-    for (int s = 0; s < num_sets_; s++) {
-        if (!sets_[s].in_use && sets_[s].buf_size >= required_size && sets_[s].bufs[0]) {
-            sets_[s].in_use = true;
-            return s;
-        }
-    }
-    return -1;
+    const int s = choose_set(sets_, num_sets_, required_size, numa_node);
+    if (s >= 0) sets_[s].in_use = true;
+    return s;
 }
 
 void StagingPool::get_buffers(int set_idx, char* out_bufs[BUFS_PER_SET], size_t& out_size,

@@ -75,11 +75,14 @@ public:
 
     void set_tiled_queue(TiledQueue* tq) { tiled_queue_ = tq; }
     // SG mode is switched off in the product library: start() logs an error
-    // and does not start while an SG task queue is set.
+    // and does not start while an SG task queue is set (is_running() then
+    // stays false).
     void set_sg_task_queue(SGTaskQueue* sq) { sg_queue_ = sq; }
 
     void start();
     void stop();
+    // True between a start() that launched the polling thread and stop().
+    bool is_running() const { return running_.load(std::memory_order_acquire); }
 
     uint64_t get_descriptors_processed() const { return descriptors_processed_.load(std::memory_order_relaxed); }
     uint64_t get_batches_submitted() const { return batches_submitted_.load(std::memory_order_relaxed); }
@@ -123,6 +126,8 @@ public:
     size_t gather_slice_bytes() const { return slice_bytes_; }
     size_t staging_buffer_size() const { return staging_buffer_size_; }
     int num_staging_buffers() const { return num_staging_bufs_; }
+    // StagingPool set the Queue-path staging came from (-1: self-allocated).
+    int staging_pool_set() const { return staging_pool_set_; }
 
     // Timeline trace (off by default; GFD_TRACE=1 or set_trace(true)).
     // Timestamps are CLOCK_MONOTONIC nanoseconds.

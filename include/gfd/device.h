@@ -71,13 +71,21 @@ __device__ __forceinline__ void write_and_commit(DescriptorQueue* queue, uint64_
     }
 }
 
-// Write only if the slot has been consumed (sequence == 0); false if the ring
-// is full at this slot.
+// Write only if the ring has room at this slot; false if it is full there (the
+// caller retries).  Room means the slot's previous use, slot - QUEUE_SIZE, has
+// been consumed: the poller's read_idx has passed it (the poller zeroes a
+// slot's sequence before it publishes read_idx past the slot).  The reference
+// tests sequence == 0 instead (device.cuh:129-152), which cannot tell a
+// consumed slot from one whose previous use has not been written yet: when
+// one launch spans more than QUEUE_SIZE slots, a writer of the later lap can
+// run first, overwrite the slot, and the poller then waits forever for the
+// earlier descriptor.
 __device__ __forceinline__ bool write_descriptor_safe(DescriptorQueue* queue, uint64_t base_slot, int token_idx,
                                                       uint64_t src_addr, void* gpu_dst, uint32_t token_size,
                                                       int num_tokens, uint64_t user_data = 0) {
     const uint64_t slot = base_slot + (uint64_t)token_idx;
-    if (load_acquire_system(&queue->entries[slot % QUEUE_SIZE].sequence) != 0) return false;
+    if (slot >= (uint64_t)QUEUE_SIZE && load_acquire_system(&queue->read_idx) <= slot - (uint64_t)QUEUE_SIZE)
+        return false;
     write_descriptor(queue, base_slot, token_idx, src_addr, gpu_dst, token_size, num_tokens, user_data);
     return true;
 }

@@ -1,14 +1,17 @@
 #pragma once
 // StagingPool: process-wide pre-allocated pinned staging buffers, one set of
 // BUFS_PER_SET buffers per GPU poller (include/gfd/staging_pool.h:29-189 of
-// the reference).
+// the reference).  Lifecycle as in the reference: init() once, each poller's
+// init_copy_engine() acquires a set (falling back to allocating its own when
+// none fits), the poller's destructor releases it, shutdown() at the end.
 //
-// MI355X allocation order: hipHostMalloc with the NUMA-user flag while the
-// allocating thread's memory policy is bound to the GPU-local node (pages land
-// on that node and are pinned by the driver), then madvise(MADV_HUGEPAGE);
-// if that fails, a plain hipHostMalloc.  Registering an existing mmap'd
-// hugetlb region (the reference's first choice) is not used: registering
-// already-mapped memory is not supported on the target systems.
+// MI355X allocation: hipHostMalloc with the NUMA-user flag while the
+// allocating thread's memory policy is bound to the set's node, so the pages
+// land on that node and are pinned by the driver; if that fails, a plain
+// hipHostMalloc.  The driver picks the page size of pinned allocations, so
+// `hugepage` is always false.  The reference's first choice, registering an
+// mmap'd hugetlb region, is not used: registering memory that is already
+// mapped is refused on the target systems.
 #include <cstddef>
 #include <mutex>
 
@@ -23,18 +26,22 @@ public:
     struct BufferSet {
         char* bufs[BUFS_PER_SET] = {};
         size_t buf_size = 0;
-        bool hugepage = false;  // true when THP was requested and granted for every buffer
+        bool hugepage = false;  // always false here (see above)
         bool in_use = false;
-        int numa_node = 0;
+        int numa_node = 0;      // node the buffers are bound to (-1: none)
     };
 
     static StagingPool& instance();
 
-    // Allocate `num_gpus` sets of BUFS_PER_SET buffers of `buf_size` bytes on
-    // `numa_node` (-1: no binding).  Returns true if at least one set exists.
+    // Allocate `num_gpus` sets of BUFS_PER_SET buffers of `buf_size` bytes.
+    // numa_node >= 0: every set on that node (the reference's behaviour);
+    // -1: set g on the node of GPU g (sysfs), unbound where none is reported.
+    // Returns true if at least one set exists.
     bool init(int num_gpus, size_t buf_size, int numa_node = 0);
 
-    // Claim a free set whose buffers hold >= required_size; -1 if none.
+    // Claim a free set whose buffers hold >= required_size, preferring one on
+    // `numa_node` (any node when -1); another node's set only when no set on
+    // it is free.  -1 if none fits (the caller then allocates its own).
     int acquire_buffers(size_t required_size, int numa_node = 0);
     void get_buffers(int set_idx, char* out_bufs[BUFS_PER_SET], size_t& out_size,
                      bool& out_hugepage);
@@ -45,9 +52,15 @@ public:
     void shutdown();
 
     // Pinned allocation helper shared with the poller's self-allocation path.
-    // Returns nullptr on failure; *hugepage tells whether THP was applied.
+    // Returns nullptr on failure; *hugepage (optional) is set to false.
     static char* alloc_pinned(size_t bytes, int numa_node, bool* hugepage);
     static void free_pinned(char* p);
+
+    // The selection rule of acquire_buffers over `n` sets (no locking): a
+    // free, large enough set on `numa_node` first, else any free, large enough
+    // set; -1 if none.
+    static int choose_set(const BufferSet* sets, int n, size_t required_size, int numa_node);
+    int num_sets() const { return num_sets_; }
 
 private:
     StagingPool() = default;

@@ -54,8 +54,12 @@ typedef struct gfd_poller_info {
     uint64_t staging_buffer_size;
     uint64_t direct_chunk_bytes;
     uint64_t gather_slice_bytes;
+    int staging_pool_set;   /* StagingPool set of the Queue staging, -1 = self-allocated */
+    int running;            /* polling thread running */
 } gfd_poller_info;
 
+/* Returned by entry points whose mode this library switches off. */
+#define GFD_ERR_NOT_SUPPORTED 801
 const char* gfd_version(void);
 const char* gfd_last_error(void);
 
@@ -98,9 +102,15 @@ int gfd_poller_init_direct_ce(gfd_poller_t p);                       /* init_dir
  * the data is in HBM; returns elapsed microseconds, or -1 on error. */
 double gfd_poller_submit_direct(gfd_poller_t p, const gfd_sg_entry* entries, int count);
 void gfd_poller_set_tiled_queue(gfd_poller_t p, void* tiled_queue);  /* set_tiled_queue (:48) */
-void gfd_poller_set_sg_task_queue(gfd_poller_t p, void* sg_queue);   /* set_sg_task_queue (:53); SG mode is switched off: start() then refuses */
-void gfd_poller_start(gfd_poller_t p);                               /* start (:56) */
+/* set_sg_task_queue (:53).  The poller's SG task-queue mode is switched off in
+ * this library: the queue is recorded (start() then refuses to run) and the
+ * call returns GFD_ERR_NOT_SUPPORTED with gfd_last_error() saying so. */
+int gfd_poller_set_sg_task_queue(gfd_poller_t p, void* sg_queue);
+/* start (:56).  0 once the polling thread runs; nonzero (and gfd_last_error())
+ * if it did not start: no queue, init_copy_engine not done, or SG mode. */
+int gfd_poller_start(gfd_poller_t p);
 void gfd_poller_stop(gfd_poller_t p);                                /* stop (:57) */
+int gfd_poller_is_running(gfd_poller_t p);                           /* 1 while the polling thread runs */
 int gfd_poller_get_stats(gfd_poller_t p, gfd_poller_stats* out);     /* get_* (:60-71) */
 void gfd_poller_reset_stats(gfd_poller_t p);                         /* reset_stats (:73) */
 int gfd_poller_get_info(gfd_poller_t p, gfd_poller_info* out);
@@ -200,6 +210,13 @@ int gfd_queue_free(void* queue);
  * at slot base_slot + j, one wave64 lane per descriptor. */
 int gfd_queue_submit_tokens(void* queue, const void* tokens, void* gpu_dst, int num_tokens,
                             uint32_t token_size, uint64_t base_slot, void* stream);
+/* The same descriptors written with write_descriptor_safe (include/gfd/device.cuh:120-152):
+ * each lane writes its slot only once the poller has consumed it, retrying (bounded by
+ * timeout_us; then *status = 1).  num_tokens may exceed QUEUE_SIZE: later laps wait for the
+ * ring.  full_count (HBM, optional) receives the number of lanes that found their slot full. */
+int gfd_queue_submit_tokens_safe(void* queue, const void* tokens, void* gpu_dst, int num_tokens,
+                                 uint32_t token_size, uint64_t base_slot, uint64_t timeout_us, int* status,
+                                 unsigned int* full_count, void* stream);
 /* bench_gfd_wait_kernel (examples/04_benchmark.cu:49-54) with a bound: spins
  * until done_idx >= expected_done or timeout_us elapses; *status (device or
  * host-visible int) receives 0 on completion, 1 on timeout. */

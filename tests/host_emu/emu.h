@@ -20,13 +20,20 @@
 
 namespace emu {
 
-enum class Kind { Pinned, Device };
+// Locked: host memory registered with the runtime (hipHostRegister-style),
+// which the runtime reports as HSA_EXT_POINTER_TYPE_LOCKED with a GPU-side
+// address of its own.
+enum class Kind { Pinned, Device, Locked };
 
 // Registry of live allocations made through the emulated shim.
 void note_alloc(void* p, size_t n, Kind k);
+// A locked range whose GPU-side base address is agent_base.
+void note_locked(void* p, size_t n, uintptr_t agent_base);
 void note_free(void* p);
 // True and the allocation holding [p, p + n) if it is registered as `k`.
 bool find_alloc(const void* p, size_t n, Kind k, uintptr_t* base, size_t* size);
+// GPU-side base of the locked range starting at `base`.
+uintptr_t locked_agent_base(uintptr_t base);
 
 // Engine stall watchdog: an engine that has polled one dependency for longer
 // than this (GFD_EMU_STALL_MS, default 5000) prints what it waits on and ends

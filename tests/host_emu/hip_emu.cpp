@@ -17,6 +17,7 @@ namespace {
 struct Alloc {
     size_t size;
     Kind kind;
+    uintptr_t agent_base;
 };
 
 std::mutex& reg_mu() {
@@ -33,7 +34,18 @@ std::map<uintptr_t, Alloc>& reg() {
 
 void note_alloc(void* p, size_t n, Kind k) {
     std::lock_guard<std::mutex> g(reg_mu());
-    reg()[(uintptr_t)p] = Alloc{n, k};
+    reg()[(uintptr_t)p] = Alloc{n, k, (uintptr_t)p};
+}
+
+void note_locked(void* p, size_t n, uintptr_t agent_base) {
+    std::lock_guard<std::mutex> g(reg_mu());
+    reg()[(uintptr_t)p] = Alloc{n, Kind::Locked, agent_base};
+}
+
+uintptr_t locked_agent_base(uintptr_t base) {
+    std::lock_guard<std::mutex> g(reg_mu());
+    auto it = reg().find(base);
+    return it == reg().end() ? 0 : it->second.agent_base;
 }
 
 void note_free(void* p) {

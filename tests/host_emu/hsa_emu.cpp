@@ -298,6 +298,11 @@ hsa_status_t HSA_API hsa_amd_pointer_info(const void* ptr, hsa_amd_pointer_info_
         info->hostBaseAddress = (void*)base;
         info->agentBaseAddress = (void*)base;
         info->sizeInBytes = size;
+    } else if (emu::find_alloc(ptr, 1, emu::Kind::Locked, &base, &size)) {
+        info->type = HSA_EXT_POINTER_TYPE_LOCKED;
+        info->hostBaseAddress = (void*)base;
+        info->agentBaseAddress = (void*)emu::locked_agent_base(base);
+        info->sizeInBytes = size;
     } else if (emu::find_alloc(ptr, 1, emu::Kind::Device, &base, &size)) {
         info->type = HSA_EXT_POINTER_TYPE_HSA;
         info->hostBaseAddress = nullptr;

@@ -20,6 +20,11 @@
 //   sdma_slot_reuse
 //       SdmaQueue alone: a signal slot comes round again while a copy that
 //       depends on its previous occupant is still queued (see the function).
+//   staging_pool <rounds> <seed>
+//       StagingPool selection, acquire / release / too small, and Queue
+//       pollers on pool sets and on their own staging.
+//   locked_source
+//       SdmaQueue::host_source_ok on registered host memory.
 //
 // Every landed byte is compared with the expected image (the entries applied
 // by plain memcpy), and list checksums exactly.  Exit status: 0 pass,
@@ -37,8 +42,10 @@
 
 #include "gfd/cpu_polling.h"
 #include "gfd/descriptor_queue.h"
+#include "emu.h"
 #include "gfd/hip_shim.h"
 #include "gfd/sg_task_queue.h"
+#include "gfd/staging_pool.h"
 #include "gfd/tiled_queue.h"
 #include "sdma.h"
 
@@ -284,6 +291,29 @@ int run_sg(const std::string& kase, int rounds, uint64_t seed) {
     return rc;
 }
 
+// One Queue round on a started poller: producers of 256 descriptors each,
+// the last flagged FLAG_LAST_IN_BATCH, then a wait for done_idx and a check
+// of every byte of the destination region.
+int queue_round(DescriptorQueue* q, const std::vector<Entry>& ent, uint8_t* dst, const std::vector<uint8_t>& want,
+                uint64_t seed, int rnd, const char* what) {
+    const uint32_t n = (uint32_t)ent.size();
+    std::memset(dst, kSentinel, want.size());
+    const uint64_t start = q->write_idx;
+    std::vector<std::thread> wg;
+    for (uint32_t b = 0; b < n; b += 256)
+        wg.emplace_back([&, b] {
+            Rng lr(seed + b + (uint64_t)rnd * 65537u);
+            const uint32_t c = std::min<uint32_t>(256, n - b);
+            post(q, &ent[b], c, 0, b + c == n ? FLAG_LAST_IN_BATCH : FLAG_NONE, lr);
+        });
+    for (auto& th : wg) th.join();
+    if (!wait_u64(&q->done_idx, start + n)) {
+        std::printf("%s round %d: done_idx wait timed out\n", what, rnd);
+        return 2;
+    }
+    return check_image(dst, want, what, rnd);
+}
+
 int run_queue(uint32_t n, uint32_t t, bool scattered, int rounds, uint64_t seed) {
     Rng rng(seed);
     const size_t host_bytes = (size_t)n * 2 * t;
@@ -311,22 +341,7 @@ int run_queue(uint32_t n, uint32_t t, bool scattered, int rounds, uint64_t seed)
         for (int rnd = 0; rnd < rounds && rc == 0; rnd++) {
             std::printf("queue %ux%u scattered=%d round %d\n", n, t, (int)scattered, rnd);
             std::fflush(stdout);
-            std::memset(dst, kSentinel, off);
-            const uint64_t start = q->write_idx;
-            std::vector<std::thread> wg;
-            for (uint32_t b = 0; b < n; b += 256)
-                wg.emplace_back([&, b] {
-                    Rng lr(seed + b + (uint64_t)rnd * 65537u);
-                    const uint32_t c = std::min<uint32_t>(256, n - b);
-                    post(q, &ent[b], c, 0, b + c == n ? FLAG_LAST_IN_BATCH : FLAG_NONE, lr);
-                });
-            for (auto& th : wg) th.join();
-            if (!wait_u64(&q->done_idx, start + n)) {
-                std::printf("queue round %d: done_idx wait timed out\n", rnd);
-                rc = 2;
-                break;
-            }
-            rc = check_image(dst, want, "queue", rnd);
+            rc = queue_round(q, ent, dst, want, seed, rnd, "queue");
         }
         p.stop();
     }
@@ -568,9 +583,143 @@ int run_sdma_slot_reuse() {
 
 }  // namespace
 
+// StagingPool (reference include/gfd/staging_pool.h:50-176 and the pool
+// branch of src/cpu_polling.cpp:160-245): the selection rule, acquire /
+// release / too small, then Queue pollers that take pool sets while sets are
+// free and fit, and allocate their own staging otherwise (a region larger
+// than the pool's buffers, or every set taken).  Each poller moves a Queue
+// round checked byte for byte; once the pollers are gone every set is free.
+int run_staging_pool(int rounds, uint64_t seed) {
+    int rc = 0;
+    auto expect = [&](bool ok, const char* what) {
+        if (!ok && rc == 0) {
+            std::printf("staging pool: %s\n", what);
+            rc = 3;
+        }
+    };
+    StagingPool& pool = StagingPool::instance();
+    expect(!pool.is_initialized() && pool.acquire_buffers(1, -1) == -1, "acquire before init must fail");
+
+    // Selection rule on a table of three sets (buffers are never touched).
+    static char dummy[1];
+    StagingPool::BufferSet t[3];
+    for (auto& b : t) b.bufs[0] = dummy;
+    t[0].buf_size = 100, t[0].numa_node = 0;
+    t[1].buf_size = 100, t[1].numa_node = 1;
+    t[2].buf_size = 50, t[2].numa_node = 1;
+    expect(StagingPool::choose_set(t, 3, 100, 1) == 1, "set on the requested node first");
+    expect(StagingPool::choose_set(t, 3, 100, 0) == 0, "node 0");
+    expect(StagingPool::choose_set(t, 3, 100, -1) == 0, "any node: first free set");
+    expect(StagingPool::choose_set(t, 3, 50, 1) == 1, "the first fitting set on the node");
+    t[1].in_use = true;
+    expect(StagingPool::choose_set(t, 3, 100, 1) == 0, "another node's set when none on the node is free");
+    expect(StagingPool::choose_set(t, 3, 60, 1) == 0, "a set too small is skipped");
+    expect(StagingPool::choose_set(t, 3, 101, -1) == -1, "nothing fits");
+
+    const uint32_t n = 512, T = 4096;
+    const size_t region = (size_t)n * 2 * T;  // the pollers' total_cpu_size
+    expect(pool.init(2, region, -1), "init");
+    expect(pool.num_sets() == 2, "two sets");
+    expect(pool.acquire_buffers(region + 1, -1) == -1, "a request larger than the buffers gets -1");
+    const int a = pool.acquire_buffers(region, -1), b = pool.acquire_buffers(region, 0);
+    expect(a >= 0 && b >= 0 && a != b, "two sets acquired");
+    expect(pool.acquire_buffers(region, -1) == -1, "all sets in use");
+    char* bufs[StagingPool::BUFS_PER_SET] = {};
+    size_t sz = 0;
+    bool hp = true;
+    pool.get_buffers(a, bufs, sz, hp);
+    expect(sz == region && !hp, "buffer size and hugepage flag");
+    for (int i = 0; i < StagingPool::BUFS_PER_SET; i++) {
+        expect(bufs[i] != nullptr, "buffer allocated");
+        for (int j = 0; j < i; j++) expect(bufs[i] != bufs[j], "distinct buffers");
+    }
+    pool.release_buffers(a);
+    pool.release_buffers(b);
+    if (rc) return rc;
+
+    Rng rng(seed);
+    auto* host = (uint8_t*)host_alloc(region);
+    for (size_t i = 0; i < region; i++) host[i] = (uint8_t)rng.next();
+    std::vector<uint32_t> perm(n);
+    for (uint32_t i = 0; i < n; i++) perm[i] = i;
+    for (uint32_t i = n; i > 1; i--) std::swap(perm[i - 1], perm[rng.below(i)]);
+    auto* dst = (uint8_t*)dev_alloc((size_t)n * T);
+    std::vector<Entry> ent(n);
+    for (uint32_t j = 0; j < n; j++)
+        ent[j] = Entry{(uint64_t)(uintptr_t)host + (uint64_t)perm[j] * 2 * T, (uint64_t)(uintptr_t)dst + (uint64_t)j * T, T};
+    std::vector<uint8_t> want((size_t)n * T);
+    for (uint32_t j = 0; j < n; j++) std::memcpy(&want[(size_t)j * T], (const void*)(uintptr_t)ent[j].src, T);
+
+    // Pollers in creation order: A and B fit the pool and take its two sets,
+    // C's region is larger than the pool's buffers, D finds every set taken.
+    const size_t totals[4] = {region, region, 2 * region, region};
+    const bool pooled[4] = {true, true, false, false};
+    std::vector<DescriptorQueue*> qs;
+    std::vector<CpuPollingThread*> ps;
+    for (int k = 0; k < 4 && rc == 0; k++) {
+        qs.push_back((DescriptorQueue*)host_alloc(sizeof(DescriptorQueue)));
+        std::memset(qs.back(), 0, sizeof(DescriptorQueue));
+        ps.push_back(new CpuPollingThread(qs.back(), dst, host, totals[k], true, -1));
+        if (!ps.back()->init_copy_engine()) {
+            rc = 4;
+            break;
+        }
+        expect((ps.back()->staging_pool_set() >= 0) == pooled[k], "pool set taken exactly when one fits and is free");
+        expect(ps.back()->num_staging_buffers() == 5 && ps.back()->staging_buffer_size() == totals[k],
+               "five staging buffers of the poller's region size");
+        ps.back()->start();
+        for (int rnd = 0; rnd < rounds && rc == 0; rnd++) {
+            std::printf("staging pool: poller %d (%s) round %d\n", k, pooled[k] ? "pool set" : "own staging", rnd);
+            std::fflush(stdout);
+            rc = queue_round(qs.back(), ent, dst, want, seed + (uint64_t)k, rnd, "staging pool");
+        }
+    }
+    for (auto* p : ps) delete p;  // stops each poller and releases its set
+    for (auto* q : qs) gfd_hip_host_free(q);
+    if (rc == 0) {
+        const int x = pool.acquire_buffers(region, -1), y = pool.acquire_buffers(region, -1);
+        expect(x >= 0 && y >= 0 && x != y, "both sets free again after the pollers are gone");
+        pool.release_buffers(x);
+        pool.release_buffers(y);
+        pool.shutdown();
+        expect(!pool.is_initialized() && pool.acquire_buffers(1, -1) == -1, "shut down");
+    }
+    gfd_hip_free(dst);
+    gfd_hip_host_free(host);
+    if (rc == 0) std::printf("staging pool: pass\n");
+    return rc;
+}
+
+// SdmaQueue::host_source_ok on host memory registered with the runtime: a
+// legal SDMA source (and zero-copy kernel source) only when the GPU sees it
+// at its host address.
+int run_locked_source() {
+    int dev = 0;
+    SdmaQueue q;
+    if (q.init(dev, 2, 1) != 0) return 4;
+    std::vector<uint8_t> same(1 << 16), moved(1 << 16);
+    emu::note_locked(same.data(), same.size(), (uintptr_t)same.data());
+    emu::note_locked(moved.data(), moved.size(), (uintptr_t)moved.data() + (1ull << 40));
+    const bool ok_same = q.host_source_ok(same.data() + 100, 4096);
+    const bool ok_moved = q.host_source_ok(moved.data() + 100, 4096);
+    const bool ok_outside = q.host_source_ok(same.data() + same.size() - 10, 4096);
+    emu::note_free(same.data());
+    emu::note_free(moved.data());
+    if (!ok_same || ok_moved || ok_outside) {
+        std::printf("locked source: same-address %d (want 1), other-address %d (want 0), overrun %d (want 0)\n",
+                    (int)ok_same, (int)ok_moved, (int)ok_outside);
+        return 3;
+    }
+    std::printf("locked source: pass\n");
+    return 0;
+}
+
 int main(int argc, char** argv) {
     setvbuf(stdout, nullptr, _IOLBF, 0);
     if (argc >= 2 && std::string(argv[1]) == "sdma_slot_reuse") return run_sdma_slot_reuse();
+    if (argc >= 2 && std::string(argv[1]) == "locked_source") return run_locked_source();
+    if (argc >= 4 && std::string(argv[1]) == "staging_pool")
+        return run_staging_pool(std::atoi(argv[2]), std::strtoull(argv[3], nullptr, 0));
     if (argc >= 10 && std::string(argv[1]) == "tiled")
         return run_tiled((uint32_t)std::atoi(argv[2]), (uint32_t)std::atoi(argv[3]), (uint32_t)std::atoi(argv[4]),
                          (uint32_t)std::atoi(argv[5]), std::atoi(argv[6]) != 0, std::atoi(argv[7]) != 0,

@@ -52,7 +52,7 @@ def _layout(n, t, stride=None):
     return region, perm, stride
 
 
-@pytest.mark.parametrize("workers", [0, 1, 2, 7])
+@pytest.mark.parametrize("workers", [0, 1, 2, 7, 15])
 @pytest.mark.parametrize("n,t,chunk,slice_", [
     (256, 4096, 64 << 10, 16 << 10),     # the 256 x 4 KB CPU layout
     (256, 4096, 1 << 20, 128 << 10),     # one chunk
@@ -200,6 +200,28 @@ def test_host_gather_with_sleeping_workers():
 
 def test_poller_sg_mode_is_refused_in_the_binding():
     # The poller's SG task-queue mode is switched off in this library (two
-    # MI355X runs aborted, cause not found); the binding says so at once.
-    with pytest.raises(RuntimeError, match="switched off"):
-        gfd_amd.CpuPollingThread.set_sg_task_queue(object(), None)
+    # MI355X runs aborted, cause not found).  A C caller learns it from the
+    # return codes: set_sg_task_queue reports GFD_ERR_NOT_SUPPORTED, start()
+    # a nonzero status, and the thread is not running.  No GPU call is made:
+    # the poller is created but never initialised.
+    L = gfd_amd.lib()
+    h = L.gfd_poller_create(None, None, None, 1 << 20, 1, -1, 0, 0, -1, 0)
+    assert h
+    try:
+        assert L.gfd_poller_set_sg_task_queue(h, ctypes.c_void_p(0x1000)) == 801
+        assert b"switched off" in L.gfd_last_error()
+        assert L.gfd_poller_start(h) != 0
+        assert b"did not start" in L.gfd_last_error()
+        assert L.gfd_poller_is_running(h) == 0
+        assert L.gfd_poller_set_sg_task_queue(h, None) == 0  # clearing it is allowed
+    finally:
+        L.gfd_poller_destroy(h)
+    p = gfd_amd.CpuPollingThread(None, None, None, 1 << 20, numa_node=-1)
+    try:
+        with pytest.raises(RuntimeError, match="switched off"):
+            p.set_sg_task_queue(ctypes.c_void_p(0x1000))
+        with pytest.raises(gfd_amd.GfdError, match="did not start"):
+            p.start()
+        assert not p.is_running()
+    finally:
+        p.close()

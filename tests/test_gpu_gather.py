@@ -296,7 +296,8 @@ def test_memcpy_per_token_baseline_parity():
 
 # ------------------------------------------------------------- GFD Queue
 
-@pytest.mark.parametrize("n,t", [(2048, 512), (2048, 2048), (8192, 4096), (1, 4096), (300, 1000)])
+@pytest.mark.parametrize("n,t", [(2048, 512), (2048, 1024), (2048, 2048), (8192, 4096), (2048, 65536), (1, 4096),
+                                 (300, 1000)])
 def test_queue_mode_parity(n, t):
     log("queue n=%d t=%d" % (n, t))
     L = Layout(n, t)
@@ -322,6 +323,111 @@ def test_queue_mode_parity(n, t):
         assert q.done_idx == base.value and q.read_idx == base.value
         s = p.stats()
         assert s["descriptors_processed"] == 2 * n
+    finally:
+        p.stop()
+        p.close()
+        q.free()
+
+
+def _queue_rounds(q, p, L, rounds, base):
+    n, t = L.n, L.t
+    tokens = np.zeros((n, 2), np.uint64)
+    tokens[:, 0] = L.src_addrs
+    tokens[:, 1] = np.arange(n, dtype=np.uint64)
+    dtok = gfd_amd.DeviceBuffer(tokens.nbytes)
+    dtok.upload(tokens)
+    b = ctypes.c_uint64(base)
+    times = np.zeros(1)
+    for _ in range(rounds):
+        rc = gfd_amd.lib().gfd_bench_queue(q.ptr, dtok.ptr, L.dst.ptr, n, t, ctypes.byref(b), 0, 1, 10_000_000,
+                                           times.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+        assert rc == 0, gfd_amd.lib().gfd_last_error()
+        L.check()
+        L.reset()
+    return b.value
+
+
+def test_queue_parity_on_staging_pool_sets():
+    """StagingPool (reference include/gfd/staging_pool.h:50-176 and the pool
+    branch of src/cpu_polling.cpp:160-245): with a pool of one set sized to
+    the region, the first Queue poller takes the set, a second finds it taken
+    and allocates its own staging, and once the first is destroyed a third
+    takes the set again.  Each moves two rounds of 2048 x 4 KiB, byte-exact."""
+    n, t = 2048, 4096
+    log("queue on StagingPool sets n=%d t=%d" % (n, t))
+    L = Layout(n, t)
+    region = L.host.nbytes
+    assert gfd_amd.StagingPool.init(1, region, -1)
+    qs, ps = [], []
+    try:
+        for k, want_set in enumerate((0, -1)):
+            qs.append(gfd_amd.DescriptorQueue())
+            ps.append(gfd_amd.CpuPollingThread(qs[-1], L.dst.ptr, L.host.ptr, region, numa_node=-1))
+            assert ps[-1].init_copy_engine()
+            info = ps[-1].info()
+            assert info["staging_pool_set"] == want_set, info
+            assert info["num_staging_buffers"] == 5 and info["staging_buffer_size"] == region
+            ps[-1].start()
+            assert _queue_rounds(qs[-1], ps[-1], L, 2, 0) == 2 * n
+        ps[0].stop()
+        ps[0].close()  # releases set 0
+        ps[0] = gfd_amd.CpuPollingThread(qs[0], L.dst.ptr, L.host.ptr, region, numa_node=-1)
+        assert ps[0].init_copy_engine()
+        assert ps[0].info()["staging_pool_set"] == 0, "the released set is taken again"
+        ps[0].start()
+        assert _queue_rounds(qs[0], ps[0], L, 2, 2 * n) == 4 * n
+    finally:
+        for p in ps:
+            p.stop()
+            p.close()
+        for q in qs:
+            q.free()
+        gfd_amd.StagingPool.shutdown()
+
+
+def test_queue_write_descriptor_safe_through_a_full_ring():
+    """write_descriptor_safe (reference include/gfd/device.cuh:120-152) with
+    the caller's retry: 3 x QUEUE_SIZE + 100 descriptors of 512 B in one
+    launch, so lanes of later laps find their slot still occupied and wait
+    for the poller to consume it.  Every byte lands (oracle), done_idx and
+    read_idx reach the end, and the ring was full for some lanes.  (With the
+    reference's sequence == 0 test a later-lap lane can overwrite a slot
+    whose earlier descriptor is not written yet, and the ring stalls; the
+    room test here is the poller's read_idx.)"""
+    n, t = 3 * gfd_amd.QUEUE_SIZE + 100, 512
+    log("queue write_descriptor_safe n=%d t=%d" % (n, t))
+    L = Layout(n, t)
+    q = gfd_amd.DescriptorQueue()
+    p = gfd_amd.CpuPollingThread(q, L.dst.ptr, L.host.ptr, L.host.nbytes, numa_node=-1)
+    try:
+        assert p.init_copy_engine()
+        p.start()
+        tokens = np.zeros((n, 2), np.uint64)
+        tokens[:, 0] = L.src_addrs
+        tokens[:, 1] = np.arange(n, dtype=np.uint64)
+        dtok = gfd_amd.DeviceBuffer(tokens.nbytes)
+        dtok.upload(tokens)
+        status = gfd_amd.HostBuffer(64, gfd_amd.HOST_COHERENT)
+        full = gfd_amd.DeviceBuffer(4)
+        for rep in range(2):
+            full.fill(0)
+            status.array.view(np.int32)[:2] = 0
+            base = rep * n
+            rc = gfd_amd.lib().gfd_queue_submit_tokens_safe(q.ptr, dtok.ptr, L.dst.ptr, n, t, base, 10_000_000,
+                                                            status.ptr, full.ptr, None)
+            assert rc == 0, gfd_amd.lib().gfd_last_error()
+            rc = gfd_amd.lib().gfd_queue_wait(q.ptr, base + n, 10_000_000, status.ptr + 4, None)
+            assert rc == 0, gfd_amd.lib().gfd_last_error()
+            gfd_amd.synchronize()
+            st = status.array.view(np.int32)[:2]
+            assert int(st[0]) == 0, "a lane gave up waiting for its slot (round %d)" % rep
+            assert int(st[1]) == 0, "done_idx wait timed out (round %d)" % rep
+            L.check()
+            L.reset()
+            hits = int(full.download().view(np.uint32)[0])
+            log("  round %d: %d lanes found their slot full" % (rep, hits))
+            assert hits > 0, "the ring never filled"
+        assert q.done_idx == 2 * n and q.read_idx == 2 * n
     finally:
         p.stop()
         p.close()

@@ -17,6 +17,10 @@ Host threads follow the kernels' device protocols:
   scattered destinations, then a wait on done_idx.
 - SdmaQueue signal-slot reuse: a copy that depends on a slot's previous
   occupant must have polled it before the slot is handed on.
+- StagingPool sets taken and released by Queue pollers, with the fallback to
+  the poller's own staging.
+- Registered host memory mapped at another GPU address is refused as a
+  copy source.
 Every landed byte is compared with the expected image, list checksums exactly.
 """
 import os
@@ -94,3 +98,21 @@ def test_tiled_mode_whole_tiles_slow_engines(poller_emu):
     # Four batches of one tile in flight together on slow engines: each
     # progress write must land after the previous one.
     run(poller_emu, ["tiled", 8, 128, 32, 4096, 1, 1, 2, 5], env={"GFD_EMU_COPY_NS": "3000"})
+
+
+def test_staging_pool_sets_and_fallback(poller_emu):
+    # StagingPool (reference include/gfd/staging_pool.h:50-176): the set
+    # selection rule (the requested NUMA node first, then any node), acquire /
+    # release / a request larger than the buffers (-1), then four Queue
+    # pollers: two take the pool's two sets, one whose region is larger than
+    # the buffers and one that finds every set taken allocate their own
+    # staging (src/cpu_polling.cpp:160-245).  Every poller's rounds are
+    # checked byte for byte, and both sets are free once the pollers are gone.
+    run(poller_emu, ["staging_pool", 2, 5])
+
+
+def test_registered_host_memory_at_another_gpu_address_is_not_a_copy_source(poller_emu):
+    # Host memory the runtime reports as locked (registered) with a GPU-side
+    # address different from its host address cannot be handed to SDMA copies
+    # or the zero-copy kernel by its host address; at the same address it can.
+    run(poller_emu, ["locked_source"])
