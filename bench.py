@@ -36,6 +36,7 @@ PCIE_GEN5_X16_GBPS = 32.0 * 16 * 128.0 / 130.0 / 8.0  # 63.0 GB/s per direction
 # external interface; writes land in HBM.
 ZC_TRAFFIC_8192x4KB = {"read_bytes": 32901 * 1024, "write_bytes": 32768 * 1024}
 METRIC = "scattered H2D GB/s + % of PCIe5 x16 peak at 8192x4KB and 2048x64KB"
+DIRECT_ZC_MAX = 8 << 20  # submit_direct's default zero-copy route limit (bytes)
 PD = ctypes.POINTER(ctypes.c_double)
 
 
@@ -191,24 +192,46 @@ def bench_peak(nbytes, iters, warmup):
 
 
 def run_zero_copy(L, iters, warmup):
+    """Zero-copy tokens kernel.  us_p50: launch call until the host sees the
+    grid's completion word (the library's own wait); wall_sync_us_p50: launch
+    until hipStreamSynchronize returns; kernel_*: HIP events on the stream."""
     wall = np.zeros(iters)
     ev = np.zeros(iters)
     rc = gfd_amd.lib().gfd_bench_zero_copy_tokens(L.table.ptr, L.dst.ptr, L.t, L.n, warmup, iters,
                                                   wall.ctypes.data_as(PD), ev.ctypes.data_as(PD))
     assert rc == 0, gfd_amd.lib().gfd_last_error()
     L.verify("zero-copy")
-    return {"us_p50": round(p50(wall), 2), "GBps": round(gbps(L.bytes, p50(wall)), 3),
+    sig = np.zeros(iters)
+    rc = gfd_amd.lib().gfd_bench_zero_copy_tokens_signal(L.table.ptr, L.dst.ptr, L.t, L.n, warmup, iters,
+                                                         sig.ctypes.data_as(PD))
+    assert rc == 0, gfd_amd.lib().gfd_last_error()
+    L.verify("zero-copy (signalled)")
+    return {"us_p50": round(p50(sig), 2), "GBps": round(gbps(L.bytes, p50(sig)), 3),
+            "wall_sync_us_p50": round(p50(wall), 2),
             "kernel_us_mean": round(float(ev.mean()), 2), "kernel_us_p50": round(p50(ev), 2),
-            "kernel_GBps": round(gbps(L.bytes, float(ev.mean())), 3)}
+            "kernel_GBps": round(gbps(L.bytes, float(ev.mean())), 3),
+            "wall_over_kernel": round(p50(sig) / float(ev.mean()), 4)}
 
 
 def run_direct(poller, L, iters, warmup):
+    """submit_direct as configured (lists up to 8 MiB on the zero-copy route);
+    for those, also the staged SDMA route alone (staged_sdma)."""
     t = np.zeros(iters)
     rc = gfd_amd.lib().gfd_bench_submit_direct(poller._h, ctypes.cast(L.entries, ctypes.c_void_p), L.n, warmup,
                                                iters, t.ctypes.data_as(PD))
     assert rc == 0, gfd_amd.lib().gfd_last_error()
     L.verify("direct")
-    return {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3)}
+    out = {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3),
+           "route": "zero-copy kernel" if L.bytes <= DIRECT_ZC_MAX else "staged SDMA"}
+    if L.bytes <= DIRECT_ZC_MAX:
+        poller.set_direct_zero_copy_max_bytes(0)
+        rc = gfd_amd.lib().gfd_bench_submit_direct(poller._h, ctypes.cast(L.entries, ctypes.c_void_p), L.n, warmup,
+                                                   iters, t.ctypes.data_as(PD))
+        poller.set_direct_zero_copy_max_bytes(DIRECT_ZC_MAX)
+        assert rc == 0, gfd_amd.lib().gfd_last_error()
+        L.verify("direct (staged SDMA)")
+        out["staged_sdma"] = {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3)}
+    return out
 
 
 def _busy_union(iv):

@@ -148,6 +148,11 @@ def _declare(L):
         "gfd_poller_read_copy_times": ([vp, vp, c_int], c_int),
         "gfd_poller_copy_clock_ns": ([vp], c_u64),
         "gfd_poller_set_direct_chunk_bytes": ([vp, c_u64], None),
+        "gfd_poller_set_direct_zero_copy_max_bytes": ([vp, c_u64], None),
+        "gfd_bench_zero_copy_tokens_signal": ([vp, vp, c_u32, c_int, c_int, c_int, pd], c_int),
+        "gfd_zero_copy_gather_tokens_signal": ([vp, vp, c_u32, c_int, vp, vp, c_u64, vp], c_int),
+        "gfd_zero_copy_scatter_tokens_signal": ([vp, vp, c_u32, c_int, vp, vp, c_u64, vp], c_int),
+        "gfd_zero_copy_gather_signal": ([vp, c_int, vp, vp, c_u64, vp], c_int),
         "gfd_poller_set_gather_slice_bytes": ([vp, c_u64], None),
         "gfd_host_gather": ([vp, c_int, vp, c_u64, c_u64, c_int, vp, c_int], c_int),
         "gfd_staging_pool_init": ([c_int, c_sz, c_int], c_int),
@@ -404,6 +409,11 @@ class CpuPollingThread:
 
     def set_direct_chunk_bytes(self, b):
         lib().gfd_poller_set_direct_chunk_bytes(self._h, b)
+
+    def set_direct_zero_copy_max_bytes(self, b):
+        """Lists up to b bytes (destination-contiguous, pinned sources) use the
+        zero-copy kernel; 0 = always the staged SDMA route."""
+        lib().gfd_poller_set_direct_zero_copy_max_bytes(self._h, b)
 
     def set_gather_slice_bytes(self, b):
         lib().gfd_poller_set_gather_slice_bytes(self._h, b)

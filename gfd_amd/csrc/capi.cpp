@@ -247,6 +247,9 @@ int gfd_poller_read_copy_times(gfd_poller_t p, gfd_copy_time* out, int max) {
 
 uint64_t gfd_poller_copy_clock_ns(gfd_poller_t p) { return p ? P(p)->copy_clock_ns() : 0; }
 
+void gfd_poller_set_direct_zero_copy_max_bytes(gfd_poller_t p, uint64_t b) {
+    if (p) P(p)->set_direct_zero_copy_max_bytes(b);
+}
 void gfd_poller_set_direct_chunk_bytes(gfd_poller_t p, uint64_t b) {
     if (p) P(p)->set_direct_chunk_bytes(b);
 }
@@ -426,6 +429,40 @@ int gfd_bench_memcpy_contiguous_d2h(void* dst, const void* src, size_t bytes, in
     }
     for (int i = 0; i < ns; i++) gfd_hip_stream_destroy(st[i]);
     return rc ? fail(rc, "contiguous D2H copy") : 0;
+}
+
+int gfd_bench_zero_copy_tokens_signal(const uint64_t* src_addrs, void* dst, uint32_t T, int n, int warmup,
+                                      int iters, double* wall_us) {
+    gfd_stream_t s = nullptr;
+    void* counter = nullptr;
+    uint64_t* word = nullptr;
+    int rc = gfd_hip_stream_create(&s);
+    if (!rc) rc = gfd_hip_malloc(&counter, 256);
+    if (!rc) rc = gfd_hip_memset_d8((uint64_t)(uintptr_t)counter, 0, 256);
+    if (!rc) rc = gfd_hip_device_synchronize();
+    if (!rc) rc = gfd_hip_host_alloc((void**)&word, 64, GFD_HOST_COHERENT);
+    if (!rc) *word = 0;
+    for (int it = -warmup; it < iters && !rc; it++) {
+        const uint64_t gen = (uint64_t)(it + warmup + 1);
+        auto t0 = std::chrono::steady_clock::now();
+        rc = gfd_zero_copy_gather_tokens_signal(src_addrs, dst, T, n, (unsigned int*)counter, word, gen, s);
+        while (!rc && __atomic_load_n(word, __ATOMIC_ACQUIRE) != gen) {
+            if (elapsed_us(t0, std::chrono::steady_clock::now()) > 10e6) {
+                rc = gfd_hip_stream_synchronize(s);
+                if (!rc && __atomic_load_n(word, __ATOMIC_ACQUIRE) != gen) rc = -1;
+                break;
+            }
+        }
+        auto t1 = std::chrono::steady_clock::now();
+        if (it >= 0 && !rc) wall_us[it] = elapsed_us(t0, t1);
+    }
+    if (s) {
+        gfd_hip_stream_synchronize(s);
+        gfd_hip_stream_destroy(s);
+    }
+    if (counter) gfd_hip_free(counter);
+    if (word) gfd_hip_host_free(word);
+    return rc ? fail(rc, "zero-copy gather (signalled)") : 0;
 }
 
 int gfd_bench_zero_copy_tokens(const uint64_t* src_addrs, void* dst, uint32_t T, int n, int warmup, int iters,

@@ -85,6 +85,10 @@ size_t CopyEngineManager::read_copy_times(CopyTime* out, size_t max) {
 uint64_t CopyEngineManager::copy_clock_ns() const { return sdma_ ? sdma_->now_ns() : 0; }
 
 bool CopyEngineManager::host_source_ok(const void* p, size_t n) { return sdma_ && sdma_->host_source_ok(p, n); }
+void CopyEngineManager::last_pinned_range(uintptr_t* lo, uintptr_t* hi) const {
+    *lo = *hi = 0;
+    if (sdma_) sdma_->last_pinned_range(lo, hi);
+}
 uint32_t CopyEngineManager::sdma_engine_mask() const { return sdma_ ? sdma_->engine_mask() : 0; }
 
 Status CopyEngineManager::pin_context() {

@@ -110,6 +110,7 @@ CpuPollingThread::CpuPollingThread(DescriptorQueue* queue, void* gpu_base, void*
       exclusive_core_count_(exclusive_core_count) {
     gfd_hip_get_device(&device_);
     direct_chunk_bytes_ = env_size("GFD_DIRECT_CHUNK_BYTES", direct_chunk_bytes_);
+    direct_zc_max_bytes_ = env_size("GFD_DIRECT_ZC_MAX_BYTES", direct_zc_max_bytes_);
     fifo_ = new CompletionFifo();
     if (env_size("GFD_TRACE", 0)) set_trace(true);
 }
@@ -141,6 +142,12 @@ CpuPollingThread::~CpuPollingThread() {
     }
     if (zc_table_) gfd_hip_host_free(zc_table_);
     zc_table_ = nullptr;
+    if (zc_src_table_) gfd_hip_host_free(zc_src_table_);
+    zc_src_table_ = nullptr;
+    if (zc_done_) gfd_hip_host_free(zc_done_);
+    zc_done_ = nullptr;
+    if (zc_counter_) gfd_hip_free(zc_counter_);
+    zc_counter_ = nullptr;
     ce_manager_.shutdown();
     direct_ce_manager_.shutdown();
 }
@@ -523,7 +530,7 @@ void CpuPollingThread::trace_gather_run() {
 }
 
 bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_t total, const DstRun* runs,
-                                              int nruns) {
+                                              int nruns, int uniform_hint) {
     if (num_staging_bufs_ == 0 || total > staging_buffer_size_ || !gather_) return false;
     const int cur = staging_cur_;
     const uint64_t t0 = now_us();
@@ -534,9 +541,10 @@ bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_
     {
         std::lock_guard<std::mutex> lock(gather_mutex_);
         if (runs)
-            gather_->run(e, count, total, staging_bufs_[cur], direct_chunk_bytes_, run_copy_chunk, &rctx);
+            gather_->run(e, count, total, staging_bufs_[cur], direct_chunk_bytes_, run_copy_chunk, &rctx,
+                         uniform_hint);
         else
-            gather_->run(e, count, total, staging_bufs_[cur], direct_chunk_bytes_, issue_chunk, &ctx);
+            gather_->run(e, count, total, staging_bufs_[cur], direct_chunk_bytes_, issue_chunk, &ctx, uniform_hint);
         trace_gather_run();
     }
     if (rctx.err && !ctx.err) ctx.err = rctx.err;
@@ -557,25 +565,28 @@ bool CpuPollingThread::gather_through_staging(const SGEntry* e, int count, size_
 // sides.  (No kernel is launched here: Queue-path consumers spin on the GPU,
 // and a kernel could queue behind them on a shared hardware queue.)
 void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total) {
-    bool dst_contig = true, src_contig = true;
-    for (int i = 1; i < count && (dst_contig || src_contig); i++) {
-        if (e[i].dst != e[i - 1].dst + e[i - 1].size) dst_contig = false;
-        if ((const char*)e[i].src != (const char*)e[i - 1].src + e[i - 1].size) src_contig = false;
+    bool dst_contig = true, src_contig = true, uniform = true;
+    for (int i = 1; i < count; i++) {
+        dst_contig &= e[i].dst == e[i - 1].dst + e[i - 1].size;
+        src_contig &= (const char*)e[i].src == (const char*)e[i - 1].src + e[i - 1].size;
+        uniform &= e[i].size == e[0].size;
     }
-    submit_list(e, count, total, dst_contig, src_contig);
+    submit_list(e, count, total, dst_contig, src_contig, uniform);
 }
 
-void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total, bool dst_contig, bool src_contig) {
+void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total, bool dst_contig, bool src_contig,
+                                   bool uniform) {
     const uint64_t t0 = now_us();
     if (count == 1 || (dst_contig && src_contig)) {
         SGEntry one{e[0].dst, e[0].src, total};
         ce_manager_.submit_scatter_gather(&one, 1);
         coalesced_entries_.fetch_add(1, std::memory_order_relaxed);
     } else if (dst_contig) {
-        if (!gather_through_staging(e, count, total)) copy_runs(e, count);
+        if (!gather_through_staging(e, count, total, nullptr, 0, uniform ? 1 : 0)) copy_runs(e, count);
     } else {
         const int nr = dst_runs(e, count, kMaxRunCopies, queue_runs_);
-        if (!(nr <= kMaxRunCopies && gather_through_staging(e, count, total, queue_runs_.data(), nr)))
+        if (!(nr <= kMaxRunCopies &&
+              gather_through_staging(e, count, total, queue_runs_.data(), nr, uniform ? 1 : 0)))
             copy_runs(e, count);
     }
     total_dma_submit_us_.fetch_add(now_us() - t0, std::memory_order_relaxed);
@@ -589,12 +600,14 @@ bool CpuPollingThread::process_batch(Descriptor* batch, int count) {
     std::vector<SGEntry>& sg = sg_scratch_;
     sg.resize(count);
     size_t total = 0;
-    bool dst_contig = true, src_contig = true;
+    bool dst_contig = true, src_contig = true, uniform = true;
     uint64_t dst_end = batch[0].dst_addr, src_end = batch[0].src_addr;
+    const uint64_t size0 = batch[0].size;
     for (int i = 0; i < count; i++) {
         const uint64_t d = batch[i].dst_addr, s = batch[i].src_addr, n = batch[i].size;
         dst_contig &= d == dst_end;
         src_contig &= s == src_end;
+        uniform &= n == size0;
         dst_end = d + n;
         src_end = s + n;
         total += n;
@@ -607,7 +620,9 @@ bool CpuPollingThread::process_batch(Descriptor* batch, int count) {
     total_bytes_copied_.fetch_add(total, std::memory_order_relaxed);
     descriptors_processed_.fetch_add(count, std::memory_order_relaxed);
     batches_submitted_.fetch_add(1, std::memory_order_relaxed);
-    submit_list(sg.data(), count, total, dst_contig, src_contig);
+    // The workers gather from this array: telling run() the list is uniform
+    // spares it a pass over entries just written with streaming stores.
+    submit_list(sg.data(), count, total, dst_contig, src_contig, uniform);
     return true;
 }
 

@@ -12,6 +12,9 @@
 // third of the gather as in the reference's fixed 3-chunk pipeline.
 #include <algorithm>
 #include <chrono>
+#include <climits>
+#include <cstdlib>
+#include <immintrin.h>
 #include <cstring>
 #include <mutex>
 
@@ -42,6 +45,7 @@ void direct_chunk(void* p, int chunk, size_t off, size_t len) {
 }
 
 constexpr size_t kContiguousSplitMin = 8u << 20;  // split one contiguous copy above this
+constexpr int kZcNotTaken = INT_MIN;               // direct_zero_copy: the list does not qualify
 
 void no_chunk(void*, int, size_t, size_t) {}
 
@@ -62,6 +66,122 @@ void run_copy_chunk(void* p, int chunk, size_t off, size_t len) {
         else break;
     }
     c->self->trace(CpuPollingThread::TRACE_CHUNK, (uint32_t)chunk, len);
+}
+
+// Zero-copy completion state: the HBM wave counter and the host word the
+// grid's last wave raises (allocated once per poller).
+bool CpuPollingThread::zc_ready() {
+    if (zc_done_ && zc_counter_ && zc_stream_) return true;
+    if (!zc_stream_ && gfd_hip_stream_create(&zc_stream_) != 0) return false;
+    if (!zc_done_) {
+        void* h = nullptr;
+        if (gfd_hip_host_alloc(&h, 64, GFD_HOST_COHERENT) != 0) return false;
+        std::memset(h, 0, 64);
+        zc_done_ = static_cast<uint64_t*>(h);
+    }
+    if (!zc_counter_) {
+        void* d = nullptr;
+        if (gfd_hip_malloc(&d, 256) != 0) return false;
+        if (gfd_hip_memset_d8((uint64_t)(uintptr_t)d, 0, 256) != 0 || gfd_hip_device_synchronize() != 0) {
+            gfd_hip_free(d);
+            return false;
+        }
+        zc_counter_ = static_cast<unsigned int*>(d);
+    }
+    return true;
+}
+
+// Wait until the grid launched with generation `gen` has raised the host
+// word (every byte it wrote is then in HBM).  Bounded: after
+// GFD_DIRECT_TIMEOUT_MS (10 s) the stream is synchronised to surface the
+// error and -1 (or the stream's error) is returned.
+int CpuPollingThread::zc_wait(uint64_t gen) {
+    static const uint64_t limit_us = (uint64_t)std::max(1ll, std::atoll(std::getenv("GFD_DIRECT_TIMEOUT_MS") ? std::getenv("GFD_DIRECT_TIMEOUT_MS") : "10000")) * 1000ull;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (unsigned i = 1;; i++) {
+        if (__atomic_load_n(zc_done_, __ATOMIC_ACQUIRE) == gen) return 0;
+        _mm_pause();
+        if ((i & 4095) == 0 &&
+            (uint64_t)std::chrono::duration_cast<std::chrono::microseconds>(std::chrono::steady_clock::now() - t0)
+                    .count() > limit_us) {
+            const int rc = gfd_hip_stream_synchronize(zc_stream_);
+            if (__atomic_load_n(zc_done_, __ATOMIC_ACQUIRE) == gen) return rc;
+            GFD_LOG_ERROR("zero-copy gather did not signal completion (stream status %d)\n", rc);
+            return rc ? rc : -1;
+        }
+    }
+}
+
+// Every source lies in pinned host memory the GPU reads at its host address.
+// Checked against the last pinned range found, entry by entry; with
+// fill_src_table the sources are also written to zc_src_table_ (uniform lists).
+bool CpuPollingThread::zc_sources_pinned(const SGEntry* entries, int count, bool fill_src_table) {
+    if (fill_src_table && zc_src_cap_ < count) {
+        if (zc_src_table_) gfd_hip_host_free(zc_src_table_);
+        zc_src_table_ = nullptr;
+        zc_src_cap_ = 0;
+        const int cap = std::max(count, 4096);
+        void* t = nullptr;
+        if (gfd_hip_host_alloc(&t, (size_t)cap * sizeof(uint64_t), GFD_HOST_DEFAULT) != 0) return false;
+        zc_src_table_ = static_cast<uint64_t*>(t);
+        zc_src_cap_ = cap;
+    }
+    uintptr_t lo = 1, hi = 0;  // empty range: the first entry looks it up
+    for (int i = 0; i < count; i++) {
+        const uintptr_t a = (uintptr_t)entries[i].src, b = a + entries[i].size;
+        if (a < lo || b > hi) {
+            if (!direct_ce_manager_.host_source_ok(entries[i].src, entries[i].size)) return false;
+            direct_ce_manager_.last_pinned_range(&lo, &hi);
+            if (a < lo || b > hi) lo = a, hi = b;
+        }
+        if (fill_src_table) zc_src_table_[i] = (uint64_t)a;
+    }
+    return true;
+}
+
+// [lo, hi) lies inside one device allocation.
+bool CpuPollingThread::zc_dst_in_device(uint64_t lo, uint64_t hi) {
+    if (lo >= zc_dst_lo_ && hi <= zc_dst_hi_) return true;
+    uint64_t base = 0, size = 0;
+    if (!gfd_hip_device_range(lo, &base, &size) || hi > base + size) return false;
+    zc_dst_lo_ = base;
+    zc_dst_hi_ = base + size;
+    return true;
+}
+
+// Small destination-contiguous list with pinned sources: the zero-copy
+// kernel reads the tokens over PCIe and writes them to HBM; its last wave
+// raises zc_done_.  Uniform lists pass only their source addresses (8 bytes
+// per token); others pass the whole entry table.  Returns 0, kZcNotTaken
+// when the list does not qualify (the caller then takes the staged route), or
+// an error.
+int CpuPollingThread::direct_zero_copy(const SGEntry* entries, int count, size_t total, bool uniform) {
+    if (!zc_ready()) return kZcNotTaken;
+    if (!zc_dst_in_device(entries[0].dst, entries[0].dst + total)) return kZcNotTaken;
+    if (!zc_sources_pinned(entries, count, uniform)) return kZcNotTaken;
+    const uint64_t gen = ++zc_gen_;
+    int rc;
+    if (uniform) {
+        rc = gfd_zero_copy_gather_tokens_signal(zc_src_table_, (void*)(uintptr_t)entries[0].dst,
+                                                (uint32_t)entries[0].size, count, zc_counter_, zc_done_, gen,
+                                                zc_stream_);
+    } else {
+        if (zc_table_cap_ < count) {
+            if (zc_table_) gfd_hip_host_free(zc_table_);
+            zc_table_ = nullptr;
+            zc_table_cap_ = 0;
+            const int cap = std::max(count, 4096);
+            void* t = nullptr;
+            if (gfd_hip_host_alloc(&t, (size_t)cap * sizeof(SGEntry), GFD_HOST_DEFAULT) != 0) return -1;
+            zc_table_ = static_cast<SGEntry*>(t);
+            zc_table_cap_ = cap;
+        }
+        std::memcpy(zc_table_, entries, (size_t)count * sizeof(SGEntry));
+        rc = gfd_zero_copy_gather_signal(reinterpret_cast<const gfd_sg_entry*>(zc_table_), count, zc_counter_,
+                                         zc_done_, gen, zc_stream_);
+    }
+    if (rc != 0) return rc;
+    return zc_wait(gen);
 }
 
 // Destinations scattered over more runs than are worth one SDMA copy each
@@ -116,9 +236,11 @@ int CpuPollingThread::direct_scattered(const SGEntry* entries, int count, size_t
             off += entries[i].size;
         }
     }
-    if (!zc_stream_ && gfd_hip_stream_create(&zc_stream_) != 0) return -1;
-    int rc = gfd_zero_copy_gather(reinterpret_cast<const gfd_sg_entry*>(zc_table_), count, zc_stream_);
-    if (rc == 0) rc = gfd_hip_stream_synchronize(zc_stream_);
+    if (!zc_ready()) return -1;
+    const uint64_t gen = ++zc_gen_;
+    int rc = gfd_zero_copy_gather_signal(reinterpret_cast<const gfd_sg_entry*>(zc_table_), count, zc_counter_,
+                                         zc_done_, gen, zc_stream_);
+    if (rc == 0) rc = zc_wait(gen);
     return rc;
 }
 
@@ -187,7 +309,11 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
             err = direct_ce_manager_.submit_on_channel(c, entries[0].dst + off,
                                                        (const char*)entries[0].src + off, len);
         }
+    } else if (dst_contig && total <= direct_zc_max_bytes_ && count > 1 &&
+               (err = direct_zero_copy(entries, count, total, uniform)) != kZcNotTaken) {
+        // done by the zero-copy kernel (err 0) or failed
     } else if (dst_contig && direct_staging_ && total <= direct_staging_size_) {
+        err = 0;
         std::lock_guard<std::mutex> lock(gather_mutex_);
         if (gather_) {
             DirectCtx ctx{this, &direct_ce_manager_, entries[0].dst, direct_staging_, nch, 0};

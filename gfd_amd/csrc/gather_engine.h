@@ -53,13 +53,16 @@ public:
 
     // Properties of a list the Direct path chooses its route by, computed by
     // the workers and the caller in parallel (a cold 8192-entry list costs
-    // the caller alone 10-30 us of DRAM reads).  Lists under 2048 entries are
-    // scanned by the caller.
+    // the caller alone 10-30 us of DRAM reads).  Lists of up to
+    // kCallerScanMax entries are scanned by the caller alone: handing them to
+    // the workers costs ~1.8 us, and the zero-copy route reads them again on
+    // the caller right after.
     struct ListScan {
         size_t total;
         bool dst_contig, src_contig, uniform;
     };
     ListScan scan(const SGEntry* entries, int count);
+    static constexpr int kCallerScanMax = 4096;
 
     // CLOCK_MONOTONIC ns of the last run(): entry, after the wait for the
     // previous job's workers, job published, first slice finished (by any
@@ -146,6 +149,9 @@ private:
     std::atomic<uint64_t> first_slice_ns_{0};
     std::atomic<int> copiers_{0};
 
+    // Source bytes of a slice prefetched ahead of the copy (GFD_GATHER_PREFETCH_BYTES;
+    // 0 = only the first line of the token four entries ahead).
+    size_t prefetch_bytes_ = 6144;
     size_t slice_bytes_ = 128 * 1024;
     size_t first_chunk_bytes_ = 0;
     bool ramp_ = true;

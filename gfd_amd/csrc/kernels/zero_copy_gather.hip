@@ -58,6 +58,7 @@ constexpr int kScatterMinWaves = 16, kScatterMaxWaves = 64;
 constexpr int kScatterUnroll = 8;
 
 using gfd::wave::BatchLds;
+using gfd::wave::GridDone;
 
 // LDS staging area per wave for the staged variant: up to 16 vectors per lane.
 constexpr int kStageVecs = 16 * 64;
@@ -68,7 +69,7 @@ constexpr int kStageVecs = 16 * 64;
 template <bool kLds>
 __global__ __launch_bounds__(kBlock) void zc_gather_tokens(const uint64_t* __restrict__ src_addrs, uint64_t dst,
                                                            uint32_t token_size, uint32_t num_tokens,
-                                                           uint32_t per_wave, int unroll) {
+                                                           uint32_t per_wave, int unroll, GridDone done) {
     __shared__ BatchLds lds[kWavesPerBlock];
     __shared__ gfd::wave::vec4u stage[kLds ? kWavesPerBlock : 1][kLds ? kStageVecs : 1];
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -84,6 +85,7 @@ __global__ __launch_bounds__(kBlock) void zc_gather_tokens(const uint64_t* __res
         }
         gfd::wave::copy_batch(unroll, md, ms, mn, nb, &lds[wid], kLds ? stage[wid] : nullptr);
     }
+    gfd::wave::signal_grid_done(done, gridDim.x * kWavesPerBlock);
 }
 
 // Reverse direction (KV-page offload): token j of num_tokens is read from HBM
@@ -94,7 +96,7 @@ __global__ __launch_bounds__(kBlock) void zc_gather_tokens(const uint64_t* __res
 template <bool kLds>
 __global__ __launch_bounds__(kBlock) void zc_scatter_tokens(const uint64_t* __restrict__ dst_addrs, uint64_t src,
                                                             uint32_t token_size, uint32_t num_tokens,
-                                                            uint32_t per_wave, int unroll) {
+                                                            uint32_t per_wave, int unroll, GridDone done) {
     __shared__ BatchLds lds[kWavesPerBlock];
     __shared__ gfd::wave::vec4u stage[kLds ? kWavesPerBlock : 1][kLds ? kStageVecs : 1];
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -110,12 +112,13 @@ __global__ __launch_bounds__(kBlock) void zc_scatter_tokens(const uint64_t* __re
         }
         gfd::wave::copy_batch(unroll, md, ms, mn, nb, &lds[wid], kLds ? stage[wid] : nullptr);
     }
+    gfd::wave::signal_grid_done(done, gridDim.x * kWavesPerBlock);
 }
 
 // Generic SG list: any sizes, any (disjoint) destinations, same batching.
 template <bool kLds>
 __global__ __launch_bounds__(kBlock) void zc_gather_sg(const gfd_sg_entry* __restrict__ entries, uint32_t count,
-                                                       uint32_t per_wave, int unroll) {
+                                                       uint32_t per_wave, int unroll, GridDone done) {
     __shared__ BatchLds lds[kWavesPerBlock];
     __shared__ gfd::wave::vec4u stage[kLds ? kWavesPerBlock : 1][kLds ? kStageVecs : 1];
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -132,6 +135,7 @@ __global__ __launch_bounds__(kBlock) void zc_gather_sg(const gfd_sg_entry* __res
         }
         gfd::wave::copy_batch(unroll, md, ms, mn, nb, &lds[wid], kLds ? stage[wid] : nullptr);
     }
+    gfd::wave::signal_grid_done(done, gridDim.x * kWavesPerBlock);
 }
 
 int env_int(const char* name, int dflt) {
@@ -175,10 +179,9 @@ Shape shape_for(uint64_t n, uint64_t total_bytes, const ShapeDefaults& d = kGath
     return s;
 }
 
-}  // namespace
-
-extern "C" int gfd_zero_copy_gather_tokens(const uint64_t* src_addrs, void* dst, uint32_t token_size,
-                                           int num_tokens, void* stream) {
+// Launchers; `done` is {nullptr, nullptr, 0} for stream-ordered completion.
+int launch_gather_tokens(const uint64_t* src_addrs, void* dst, uint32_t token_size, int num_tokens, void* stream,
+                         GridDone done) {
     if (num_tokens < 0 || (num_tokens > 0 && (!src_addrs || !dst || token_size == 0)))
         return (int)hipErrorInvalidValue;
     if (num_tokens == 0) return 0;
@@ -186,15 +189,15 @@ extern "C" int gfd_zero_copy_gather_tokens(const uint64_t* src_addrs, void* dst,
     const Shape s = shape_for((uint64_t)num_tokens, (uint64_t)num_tokens * token_size);
     if (s.lds)
         hipLaunchKernelGGL(zc_gather_tokens<true>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, src_addrs,
-                           (uint64_t)(uintptr_t)dst, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll);
+                           (uint64_t)(uintptr_t)dst, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll, done);
     else
         hipLaunchKernelGGL(zc_gather_tokens<false>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, src_addrs,
-                           (uint64_t)(uintptr_t)dst, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll);
+                           (uint64_t)(uintptr_t)dst, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll, done);
     return (int)hipGetLastError();
 }
 
-extern "C" int gfd_zero_copy_scatter_tokens(const uint64_t* dst_addrs, const void* src, uint32_t token_size,
-                                            int num_tokens, void* stream) {
+int launch_scatter_tokens(const uint64_t* dst_addrs, const void* src, uint32_t token_size, int num_tokens,
+                          void* stream, GridDone done) {
     if (num_tokens < 0 || (num_tokens > 0 && (!dst_addrs || !src || token_size == 0)))
         return (int)hipErrorInvalidValue;
     if (num_tokens == 0) return 0;
@@ -202,23 +205,63 @@ extern "C" int gfd_zero_copy_scatter_tokens(const uint64_t* dst_addrs, const voi
     const Shape s = shape_for((uint64_t)num_tokens, (uint64_t)num_tokens * token_size, kScatterShape);
     if (s.lds)
         hipLaunchKernelGGL(zc_scatter_tokens<true>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, dst_addrs,
-                           (uint64_t)(uintptr_t)src, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll);
+                           (uint64_t)(uintptr_t)src, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll, done);
     else
         hipLaunchKernelGGL(zc_scatter_tokens<false>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, dst_addrs,
-                           (uint64_t)(uintptr_t)src, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll);
+                           (uint64_t)(uintptr_t)src, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll, done);
     return (int)hipGetLastError();
 }
 
-extern "C" int gfd_zero_copy_gather(const gfd_sg_entry* entries, int count, void* stream) {
+int launch_gather_sg(const gfd_sg_entry* entries, int count, void* stream, GridDone done) {
     if (count < 0 || (count > 0 && !entries)) return (int)hipErrorInvalidValue;
     if (count == 0) return 0;
     // Sizes are in the entry table, not known here: shape for 4 KiB entries.
     const Shape s = shape_for((uint64_t)count, (uint64_t)count * 4096);
     if (s.lds)
         hipLaunchKernelGGL(zc_gather_sg<true>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, entries,
-                           (uint32_t)count, s.per_wave, s.unroll);
+                           (uint32_t)count, s.per_wave, s.unroll, done);
     else
         hipLaunchKernelGGL(zc_gather_sg<false>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, entries,
-                           (uint32_t)count, s.per_wave, s.unroll);
+                           (uint32_t)count, s.per_wave, s.unroll, done);
     return (int)hipGetLastError();
+}
+
+GridDone grid_done(unsigned int* counter, uint64_t* host_word, uint64_t value) { return GridDone{counter, host_word, value}; }
+
+}  // namespace
+
+extern "C" int gfd_zero_copy_gather_tokens(const uint64_t* src_addrs, void* dst, uint32_t token_size,
+                                           int num_tokens, void* stream) {
+    return launch_gather_tokens(src_addrs, dst, token_size, num_tokens, stream, GridDone{nullptr, nullptr, 0});
+}
+
+extern "C" int gfd_zero_copy_scatter_tokens(const uint64_t* dst_addrs, const void* src, uint32_t token_size,
+                                            int num_tokens, void* stream) {
+    return launch_scatter_tokens(dst_addrs, src, token_size, num_tokens, stream, GridDone{nullptr, nullptr, 0});
+}
+
+extern "C" int gfd_zero_copy_gather(const gfd_sg_entry* entries, int count, void* stream) {
+    return launch_gather_sg(entries, count, stream, GridDone{nullptr, nullptr, 0});
+}
+
+extern "C" int gfd_zero_copy_gather_tokens_signal(const uint64_t* src_addrs, void* dst, uint32_t token_size,
+                                                  int num_tokens, unsigned int* done_counter, uint64_t* done_word,
+                                                  uint64_t done_value, void* stream) {
+    if (!done_counter || !done_word) return (int)hipErrorInvalidValue;
+    return launch_gather_tokens(src_addrs, dst, token_size, num_tokens, stream,
+                                grid_done(done_counter, done_word, done_value));
+}
+
+extern "C" int gfd_zero_copy_scatter_tokens_signal(const uint64_t* dst_addrs, const void* src, uint32_t token_size,
+                                                   int num_tokens, unsigned int* done_counter, uint64_t* done_word,
+                                                   uint64_t done_value, void* stream) {
+    if (!done_counter || !done_word) return (int)hipErrorInvalidValue;
+    return launch_scatter_tokens(dst_addrs, src, token_size, num_tokens, stream,
+                                 grid_done(done_counter, done_word, done_value));
+}
+
+extern "C" int gfd_zero_copy_gather_signal(const gfd_sg_entry* entries, int count, unsigned int* done_counter,
+                                           uint64_t* done_word, uint64_t done_value, void* stream) {
+    if (!done_counter || !done_word) return (int)hipErrorInvalidValue;
+    return launch_gather_sg(entries, count, stream, grid_done(done_counter, done_word, done_value));
 }

@@ -74,6 +74,11 @@ public:
     // for the GPU (hipHostMalloc / registered), i.e. a legal SDMA source.
     // Pageable memory is not: the caller must copy it another way.
     bool host_source_ok(const void* p, size_t n);
+    // Bounds of the pinned allocation the last successful host_source_ok found.
+    void last_pinned_range(uintptr_t* lo, uintptr_t* hi) const {
+        *lo = ok_lo_;
+        *hi = ok_hi_;
+    }
 
 private:
     struct Slot;

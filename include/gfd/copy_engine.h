@@ -130,6 +130,9 @@ public:
     uint32_t sdma_engine_mask() const;
     // True if [p, p + n) is pinned host memory the GPU can read (SDMA backend).
     bool host_source_ok(const void* p, size_t n);
+    // Bounds of the pinned allocation the last successful host_source_ok found
+    // (both 0 without the SDMA backend).
+    void last_pinned_range(uintptr_t* lo, uintptr_t* hi) const;
 
     // Engine timestamps of each copy (SDMA backend only; see SdmaQueue).
     struct CopyTime {

@@ -118,6 +118,12 @@ public:
     int numa_node() const { return numa_node_; }
     int device() const { return device_; }
     const CopyEngineManager& get_direct_ce_manager() const { return direct_ce_manager_; }
+    // Destination-contiguous lists of at most this many bytes whose sources
+    // are pinned host memory go through the zero-copy gather kernel instead
+    // of the staged SDMA copies (0 = never; GFD_DIRECT_ZC_MAX_BYTES).  Below
+    // a few MiB the copy engines' fixed start-up latency dominates.
+    void set_direct_zero_copy_max_bytes(size_t b) { direct_zc_max_bytes_ = b; }
+    size_t direct_zero_copy_max_bytes() const { return direct_zc_max_bytes_; }
     // Chunk size of the pipelined gather (payload bytes per copy).
     void set_direct_chunk_bytes(size_t b) { direct_chunk_bytes_ = b ? b : 1; }
     size_t direct_chunk_bytes() const { return direct_chunk_bytes_; }
@@ -192,11 +198,17 @@ private:
     void process_batch_tiled(Descriptor* batch, int count, uint64_t cur_read);
     void process_batch_sg(Descriptor* batch, int count, uint64_t cur_read);
     void submit_list(const SGEntry* e, int count, size_t total);
-    void submit_list(const SGEntry* e, int count, size_t total, bool dst_contig, bool src_contig);
+    void submit_list(const SGEntry* e, int count, size_t total, bool dst_contig, bool src_contig, bool uniform);
     // runs == nullptr: destinations contiguous; else nruns destination runs.
+    // uniform_hint as for GatherEngine::run.
     bool gather_through_staging(const SGEntry* e, int count, size_t total, const DstRun* runs = nullptr,
-                                int nruns = 0);
+                                int nruns = 0, int uniform_hint = -1);
     int direct_scattered(const SGEntry* entries, int count, size_t total, bool uniform);
+    int direct_zero_copy(const SGEntry* entries, int count, size_t total, bool uniform);
+    bool zc_sources_pinned(const SGEntry* entries, int count, bool fill_src_table);
+    bool zc_dst_in_device(uint64_t lo, uint64_t hi);
+    bool zc_ready();
+    int zc_wait(uint64_t gen);
     void copy_runs(const SGEntry* e, int count);
     void signal_device_u64(uint64_t* dst, uint64_t value, uint64_t after_begin);
     void publish_done(uint64_t value);
@@ -271,6 +283,17 @@ private:
     SGEntry* zc_table_ = nullptr;
     int zc_table_cap_ = 0;
     gfd_stream_t zc_stream_ = nullptr;
+    // Completion of the zero-copy kernels, signalled by the grid's last wave:
+    // a wave counter in HBM and the generation word it writes to host memory.
+    unsigned int* zc_counter_ = nullptr;
+    uint64_t* zc_done_ = nullptr;
+    uint64_t zc_gen_ = 0;
+    // Small destination-contiguous lists: source addresses (uniform sizes) in
+    // pinned memory for the zero-copy tokens kernel.
+    uint64_t* zc_src_table_ = nullptr;
+    int zc_src_cap_ = 0;
+    size_t direct_zc_max_bytes_ = 8u << 20;
+    uint64_t zc_dst_lo_ = 0, zc_dst_hi_ = 0;  // last device allocation found for a destination
     std::vector<uint32_t> tile_scratch_;
     size_t slice_bytes_ = 0;
 

@@ -275,5 +275,31 @@ __device__ __forceinline__ uint32_t load_system32(const volatile uint32_t* p) {
     return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+// Completion of a whole grid signalled to the host without a stream
+// synchronisation.  Every wave of the grid calls it once after its last
+// store: the wave releases its stores at agent scope and counts itself in
+// `counter` (HBM, 0 before the launch); the last wave of `total_waves`
+// acquires them, puts the counter back to 0 for the next launch, and stores
+// `value` to `host_word` (pinned host memory) with a system-scope release, so
+// every byte the grid wrote is visible to any agent once the host reads
+// `value` there.  A null host_word disables it.
+struct GridDone {
+    unsigned int* counter;
+    uint64_t* host_word;
+    uint64_t value;
+};
+
+__device__ __forceinline__ void signal_grid_done(const GridDone& g, uint32_t total_waves) {
+    if (!g.host_word) return;
+    release_agent();
+    if (lane_id() == 0) {
+        const unsigned int prev = __hip_atomic_fetch_add(g.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev + 1 == total_waves) {
+            __hip_atomic_store(g.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(g.host_word, g.value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+}
+
 }  // namespace wave
 }  // namespace gfd

@@ -139,6 +139,9 @@ int gfd_poller_read_copy_times(gfd_poller_t p, gfd_copy_time* out, int max);
 uint64_t gfd_poller_copy_clock_ns(gfd_poller_t p);
 /* Tuning of the pipelined direct path (no reference counterpart). */
 void gfd_poller_set_direct_chunk_bytes(gfd_poller_t p, uint64_t bytes);
+/* Destination-contiguous lists of at most `bytes` with pinned sources go
+ * through the zero-copy kernel (0 = never). */
+void gfd_poller_set_direct_zero_copy_max_bytes(gfd_poller_t p, uint64_t bytes);
 void gfd_poller_set_gather_slice_bytes(gfd_poller_t p, uint64_t bytes);
 
 /* Host-only gather (no GPU): the staging step of the pipelined direct path.
@@ -166,6 +169,21 @@ int gfd_zero_copy_gather_tokens(const uint64_t* src_addrs, void* dst, uint32_t t
  * Direction-agnostic: sources and destinations may each be HBM or pinned host
  * memory (H2D gather, D2H offload, D2D). */
 int gfd_zero_copy_gather(const gfd_sg_entry* entries, int count, void* stream);
+/* The same three kernels with completion signalled to the host instead of by
+ * the stream (no reference counterpart; the reference waits on stream events):
+ * when every byte has landed (and is visible to any agent), the grid's last
+ * wave stores done_value to *done_word (pinned host memory, ideally coherent),
+ * which the caller polls.  done_counter: one unsigned int in HBM, 0 before the
+ * first launch; the kernel leaves it 0 again.  Launches that share a counter
+ * must be ordered (one stream).  The stream still orders the launch as usual. */
+int gfd_zero_copy_gather_tokens_signal(const uint64_t* src_addrs, void* dst, uint32_t token_size,
+                                       int num_tokens, unsigned int* done_counter, uint64_t* done_word,
+                                       uint64_t done_value, void* stream);
+int gfd_zero_copy_scatter_tokens_signal(const uint64_t* dst_addrs, const void* src, uint32_t token_size,
+                                        int num_tokens, unsigned int* done_counter, uint64_t* done_word,
+                                        uint64_t done_value, void* stream);
+int gfd_zero_copy_gather_signal(const gfd_sg_entry* entries, int count, unsigned int* done_counter,
+                                uint64_t* done_word, uint64_t done_value, void* stream);
 /* GPU-built SG list for submit_direct (the pattern of examples/03_gpu_planned_transfer.cu:32-66,
  * plan_compact_kernel + plan_build_sg_kernel): the tokens t with routing[t] == expert, in token
  * order, become entries[k] = {gpu_dst + k*token_size, cpu_base + t*stride, token_size}, and
@@ -260,6 +278,10 @@ int gfd_bench_sdma_contiguous(void* dst, const void* src, size_t bytes, int chan
                               int warmup, int iters, double* times_us, uint32_t* engine_mask);
 int gfd_bench_submit_direct(gfd_poller_t p, const gfd_sg_entry* entries, int count, int warmup,
                             int iters, double* times_us);
+/* Zero-copy tokens kernel with its completion signalled to a host word:
+ * wall time from the launch call until the host sees the word. */
+int gfd_bench_zero_copy_tokens_signal(const uint64_t* src_addrs, void* dst, uint32_t token_size,
+                                      int num_tokens, int warmup, int iters, double* wall_us);
 /* Zero-copy tokens kernel: wall time launch->sync and HIP-event kernel time. */
 int gfd_bench_zero_copy_tokens(const uint64_t* src_addrs, void* dst, uint32_t token_size,
                                int num_tokens, int warmup, int iters, double* wall_us,

@@ -196,4 +196,29 @@ int gfd_hip_device_range(uint64_t ptr, uint64_t* base, uint64_t* size) {
 // The Direct path's zero-copy route is a GPU kernel: not emulated.
 int gfd_zero_copy_gather(const gfd_sg_entry*, int, void*) { return 801; }
 
+// The zero-copy kernels with host-word completion, run on the calling thread:
+// every entry is copied, then the counter is left at 0 and done_value is
+// stored with release ordering, as the grid's last wave does.
+int gfd_zero_copy_gather_tokens_signal(const uint64_t* src_addrs, void* dst, uint32_t token_size, int num_tokens,
+                                       unsigned int* done_counter, uint64_t* done_word, uint64_t done_value,
+                                       void*) {
+    if (!done_counter || !done_word || num_tokens < 0 || (num_tokens > 0 && (!src_addrs || !dst || !token_size)))
+        return 1;
+    for (int j = 0; j < num_tokens; j++)
+        std::memcpy((char*)dst + (size_t)j * token_size, (const void*)(uintptr_t)src_addrs[j], token_size);
+    __atomic_store_n(done_counter, 0u, __ATOMIC_RELAXED);
+    __atomic_store_n(done_word, done_value, __ATOMIC_RELEASE);
+    return 0;
+}
+
+int gfd_zero_copy_gather_signal(const gfd_sg_entry* entries, int count, unsigned int* done_counter,
+                                uint64_t* done_word, uint64_t done_value, void*) {
+    if (!done_counter || !done_word || count < 0 || (count > 0 && !entries)) return 1;
+    for (int i = 0; i < count; i++)
+        std::memcpy((void*)(uintptr_t)entries[i].dst, (const void*)(uintptr_t)entries[i].src, entries[i].size);
+    __atomic_store_n(done_counter, 0u, __ATOMIC_RELAXED);
+    __atomic_store_n(done_word, done_value, __ATOMIC_RELEASE);
+    return 0;
+}
+
 }  // extern "C"

@@ -175,18 +175,48 @@ DIRECT_CASES = [(256, 4096, 2 << 20), (8192, 4096, 2 << 20), (8192, 4096, 256 <<
                 (40, 4096, 2 << 20)]
 
 
+@pytest.mark.parametrize("route", ["default", "staged"])
 @pytest.mark.parametrize("n,t,chunk", DIRECT_CASES)
-def test_submit_direct_parity(direct_poller, n, t, chunk):
-    log("submit_direct n=%d t=%d chunk=%d" % (n, t, chunk))
+def test_submit_direct_parity(direct_poller, n, t, chunk, route):
+    """Both Direct routes for destination-contiguous lists: by default lists
+    up to 8 MiB with pinned sources go through the zero-copy kernel (larger
+    ones through staged SDMA copies); 'staged' forces the staged SDMA route
+    at every size."""
+    log("submit_direct n=%d t=%d chunk=%d route=%s" % (n, t, chunk, route))
     L = Layout(n, t)
     direct_poller.set_direct_chunk_bytes(chunk)
+    if route == "staged":
+        direct_poller.set_direct_zero_copy_max_bytes(0)
     entries = gfd_amd.make_entries(L.src_addrs, L.dst.ptr, t)
+    try:
+        for rep in range(2):
+            us = direct_poller.submit_direct(entries, n)
+            assert us > 0
+            L.check()
+            L.reset()
+    finally:
+        direct_poller.set_direct_chunk_bytes(2 << 20)
+        direct_poller.set_direct_zero_copy_max_bytes(8 << 20)
+
+
+@pytest.mark.parametrize("n,t", [(2048, 512), (300, 1000)])
+def test_submit_direct_small_list_from_pageable_sources(direct_poller, n, t):
+    """Sources in pageable (not pinned) memory cannot be read by the GPU: a
+    small list must take the staged route (gather into pinned staging, then
+    SDMA) and still land byte-exact."""
+    log("submit_direct pageable sources n=%d t=%d" % (n, t))
+    region = np.empty(n * 2 * t, np.uint8)
+    oracle.fill_tokens(region, n, t, 2 * t)
+    perm = oracle.permutation(n)
+    dst = gfd_amd.DeviceBuffer(n * t + TAIL)
+    dst.fill(SENTINEL)
+    entries = gfd_amd.make_entries(region.ctypes.data + perm.astype(np.uint64) * np.uint64(2 * t), dst.ptr, t)
     for rep in range(2):
-        us = direct_poller.submit_direct(entries, n)
-        assert us > 0
-        L.check()
-        L.reset()
-    direct_poller.set_direct_chunk_bytes(2 << 20)
+        assert direct_poller.submit_direct(entries, n) > 0
+        got = dst.download()
+        assert (got[:n * t] == oracle.expected_gather(region, perm, t, 2 * t)).all()
+        assert (got[n * t:] == SENTINEL).all()
+        dst.fill(SENTINEL)
 
 
 def test_submit_direct_copy_timeline(direct_poller):
