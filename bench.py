@@ -408,6 +408,41 @@ def run_moe(oracle, iters, warmup, tokens=4096, experts=64, dim=7168):
             if not np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-6):
                 raise SystemExit("PARITY FAILURE: MoE RMSNorm outside bf16 tolerance")
         res[name] = {"us_p50": round(p50(t), 2), "GBps": round(gbps(n * row_bytes, p50(t)), 3)}
+    # The same workload through SGWarpSpecSession: GPU submitter waves build
+    # lists of <= 32 rows from the routing output, the session's transfer
+    # waves copy them, its compute wave runs the RMSNorm.  Timed with HIP
+    # events around launch_moe on the stream (the session's per-launch set-up
+    # included); the kernel ends itself once every list has landed.
+    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=0, idle_limit_ms=10000)
+    try:
+        for name, with_norm in (("session_transfer_only", False), ("session_overlapped_rmsnorm", True)):
+            t = []
+            for i in range(-warmup, iters):
+                sess.reset()
+                L.gfd_event_record(ea, st)
+                sess.launch_moe(host.ptr, stride, tokens, d_off.ptr, d_rows.ptr, experts, n, row_bytes, d_dst.ptr,
+                                d_out.ptr if with_norm else None, d_w.ptr, 1e-6, 32, st)
+                L.gfd_event_record(eb, st)
+                L.gfd_event_synchronize(eb)
+                sess.synchronize(0)
+                ms = ctypes.c_float(0)
+                L.gfd_event_elapsed_ms(ctypes.byref(ms), ea, eb)
+                if i >= 0:
+                    t.append(ms.value * 1000.0)
+            stt = sess.stats()
+            if stt["lists_done"] < experts or stt["units_done"] != n:
+                raise SystemExit("MoE session: %s" % stt)
+            if not (d_dst.download().view(np.uint16).reshape(n, dim) == expect).all():
+                raise SystemExit("PARITY FAILURE: MoE session rows (%s)" % name)
+            if with_norm:
+                ref = oracle.rmsnorm_rows(oracle.bf16_to_f32(expect), oracle.bf16_to_f32(weight), 1e-6)
+                got = oracle.bf16_to_f32(d_out.download().view(np.uint16).reshape(n, dim))
+                if not np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-6):
+                    raise SystemExit("PARITY FAILURE: MoE session RMSNorm outside bf16 tolerance")
+            res[name] = {"us_p50": round(p50(t), 2), "GBps": round(gbps(n * row_bytes, p50(t)), 3),
+                         "lists": stt["lists_done"], "grid": stt["grid"], "rows_per_list": 32}
+    finally:
+        sess.close()
     L.gfd_event_destroy(ea)
     L.gfd_event_destroy(eb)
     L.gfd_stream_destroy(st)

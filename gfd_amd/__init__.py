@@ -195,6 +195,8 @@ def _declare(L):
         "gfd_sg_session_launch_l2norm": ([vp, vp, c_u32, vp], c_int),
         "gfd_sg_session_launch_gpu_submit": ([vp, vp, c_u32, c_u32, vp, vp], c_int),
         "gfd_sg_session_synchronize": ([vp, c_u64], c_int),
+        "gfd_sg_session_launch_moe": ([vp, vp, c_u64, c_int, vp, vp, c_int, c_int, c_u32, c_u32, vp, vp, vp,
+                                       ctypes.c_float, vp], c_int),
         "gfd_sg_session_reset": ([vp], c_int),
         "gfd_sg_session_stats": ([vp, ctypes.POINTER(SessionResult)], c_int),
         "gfd_sg_session_queue": ([vp], vp),
@@ -665,6 +667,14 @@ class SGWarpSpecSession:
     def launch_gpu_submit(self, d_entries, entries_per_list, num_lists, list_sums=None, stream=None):
         _check(lib().gfd_sg_session_launch_gpu_submit(self._h, d_entries, entries_per_list, num_lists, list_sums,
                                                       stream), "gfd_sg_session_launch_gpu_submit")
+
+    def launch_moe(self, host_base, token_stride, num_tokens, d_offsets, d_row_token, num_experts, num_rows,
+                   row_bytes, d_dst, d_out=None, d_weight=None, eps=1e-6, rows_per_list=32, stream=None):
+        """The MoE-routed gather with GPU-built lists (gfd_sg_session_launch_moe);
+        the kernel ends itself once every list has landed."""
+        _check(lib().gfd_sg_session_launch_moe(self._h, host_base, token_stride, num_tokens, d_offsets, d_row_token,
+                                               num_experts, num_rows, row_bytes, rows_per_list, d_dst, d_out,
+                                               d_weight, eps, stream), "SGWarpSpecSession.launch_moe")
 
     def synchronize(self, extra_gpu_lists=0):
         _check(lib().gfd_sg_session_synchronize(self._h, extra_gpu_lists), "gfd_sg_session_synchronize")

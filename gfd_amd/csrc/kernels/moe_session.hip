@@ -1,0 +1,208 @@
+// The MoE-routed gather (top-2 of 64 experts, 14 KiB bf16 rows) through
+// SGWarpSpecSession, as the reference runs its SG MoE example: per-expert
+// (src, dst, size) lists are built on the GPU by submitter waves and posted
+// with the sg:: primitives (the pattern of examples/09_sg_warp_spec.cu:78-294
+// and test/test_sg_gpu_submit.cu:20-213), the session's transfer waves copy
+// each list from pinned host memory to HBM (include/gfd/sg_warp_spec.h), and
+// the compute wave runs the consumer on every landed list: a per-row bf16
+// RMSNorm, or nothing (pure transfer).
+//
+// Lists: expert e's rows [offsets[e], offsets[e+1]) in the expert-major order
+// of gfd_moe_route, cut into lists of at most rows_per_list (<= 64) rows, so
+// a workgroup gets several lists and the RMSNorm of one overlaps the copy of
+// the next.  List ids run 0 .. total-1 over experts in order (lists past
+// MAX_SG_LISTS reuse ring slots once landed; ids from MAX_SG_LISTS on have no
+// d_list_done word, which the kernel does not need).  Entry k of the
+// list for rows [r, r + n): src = host_base + row_token[r + k] * token_stride,
+// dst = dst + (r + k) * row_bytes, size = row_bytes, tag = r + k (the row).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "bf16_ops.h"
+#include "capi_error.h"
+#include "gfd/sg_device_primitives.h"
+#include "gfd/sg_warp_spec.h"
+#include "gfd/warp_spec_session.h"
+#include "gfd_capi.h"
+
+namespace {
+
+using gfd::sg_warp_spec::SGListView;
+
+// y = x / sqrt(mean(x^2) + eps) * w per landed row, fp32 arithmetic, bf16
+// round-to-nearest-even out, to out + row * row_bytes (the entry's tag is the
+// row).  V = row_bytes / 1 KiB vectors per lane, a template parameter so each
+// lane issues its V loads of a row (and of the weights) back to back.
+template <int V>
+__device__ __forceinline__ void rmsnorm_row(uint64_t src, uint64_t o, const uint16_t* weight, float eps,
+                                            uint32_t lane) {
+    using gfd::wave::vec4u;
+    vec4u x[V];
+#pragma unroll
+    for (int k = 0; k < V; k++) x[k] = gfd::wave::gload(src + (uint64_t)(k * 64 + lane) * 16);
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < V; k++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float a = gfd::bf16::lo(x[k][j]), b = gfd::bf16::hi(x[k][j]);
+            ss += a * a + b * b;
+        }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    const float scale = 1.0f / sqrtf(ss / (float)(V * 512) + eps);
+#pragma unroll
+    for (int k = 0; k < V; k++) {
+        const uint64_t off = (uint64_t)(k * 64 + lane) * 16;
+        const vec4u w = gfd::wave::gload((uint64_t)(uintptr_t)weight + off);
+        vec4u y;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float l = gfd::bf16::lo(x[k][j]) * scale * gfd::bf16::lo(w[j]);
+            const float h = gfd::bf16::hi(x[k][j]) * scale * gfd::bf16::hi(w[j]);
+            y[j] = gfd::bf16::from_f32(l) | (gfd::bf16::from_f32(h) << 16);
+        }
+        gfd::wave::gstore(o + off, y);
+    }
+}
+
+struct RowRMSNorm {
+    uint8_t* out;
+    const uint16_t* weight;
+    float eps;
+    __device__ void operator()(SGListView v) const {
+        const uint32_t lane = (uint32_t)v.lane_id;
+        for (uint32_t e = 0; e < v.count; e++) {
+            const gfd::DeviceSGEntry d = v.get_entry(e);
+            const uint64_t o = (uint64_t)(uintptr_t)out + (uint64_t)d.tag * d.size;
+            switch (d.size) {  // skipped rows (size 0) and other sizes do nothing
+#define GFD_RMS_CASE(v) \
+    case v * 1024: rmsnorm_row<v>(d.dst_addr, o, weight, eps, lane); break;
+                GFD_RMS_CASE(1) GFD_RMS_CASE(2) GFD_RMS_CASE(3) GFD_RMS_CASE(4) GFD_RMS_CASE(5) GFD_RMS_CASE(6)
+                GFD_RMS_CASE(7) GFD_RMS_CASE(8) GFD_RMS_CASE(9) GFD_RMS_CASE(10) GFD_RMS_CASE(11) GFD_RMS_CASE(12)
+                GFD_RMS_CASE(13) GFD_RMS_CASE(14)
+#undef GFD_RMS_CASE
+                default: break;
+            }
+        }
+    }
+};
+
+struct NoCompute {
+    __device__ void operator()(SGListView) const {}
+};
+
+struct MoeLists {
+    uint64_t host_base, token_stride, dst;
+    const int* offsets;
+    const int* row_token;
+    int num_experts, num_tokens, num_rows;
+    uint32_t row_bytes, rows_per_list;
+};
+
+// Submitter wave: posts this workgroup's share of the lists (list L goes to
+// workgroup L mod grid); workgroup 0 then waits for every list to land and
+// terminates the transfer waves.  Routing entries out of range are reported
+// (SG_ERR_BAD_ROW) and become empty entries: nothing outside the host buffer
+// is ever read.
+__device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
+    using namespace gfd;
+    const int lane = wave::lane_id();
+    SGDeviceCounters* cnt = sg_device_counters(sq);
+    // Lists per expert (one lane per expert, at most 64 experts) and their
+    // exclusive prefix: the first list id of each expert.
+    int a = 0, b = 0, nl = 0;
+    if (lane < m.num_experts) {
+        a = m.offsets[lane];
+        b = m.offsets[lane + 1];
+        if (a < 0 || b < a || b > m.num_rows) {
+            __hip_atomic_fetch_or(&cnt->error, SG_ERR_BAD_ROW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            a = b = 0;
+        }
+        nl = (int)(((uint32_t)(b - a) + m.rows_per_list - 1) / m.rows_per_list);
+    }
+    int incl = nl;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += t;
+    }
+    const int excl = incl - nl;
+    const uint32_t total = (uint32_t)__shfl(incl, 63, 64);
+    for (uint32_t L = blockIdx.x; L < total; L += gridDim.x) {
+        // The expert of list L: the highest expert whose first list id is <= L.
+        const uint64_t mask = __ballot(lane < m.num_experts && (uint32_t)excl <= L);
+        const int e = 63 - __builtin_clzll(mask);
+        const int ea = __shfl(a, e, 64), eb = __shfl(b, e, 64), efirst = __shfl(excl, e, 64);
+        const uint32_t r0 = (uint32_t)ea + (L - (uint32_t)efirst) * m.rows_per_list;
+        const uint32_t n = min(m.rows_per_list, (uint32_t)eb - r0);
+        if (!sg::sg_wait_entry_space(sq, n) || !sg::sg_wait_list_space(sq)) {
+            if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_RING_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        const uint64_t pool = sg::sg_alloc_entries(sq, n);
+        if ((uint32_t)lane < n) {
+            const uint32_t r = r0 + (uint32_t)lane;
+            const int tok = m.row_token[r];
+            DeviceSGEntry& d = sq->entries[(pool + (uint32_t)lane) % MAX_SG_POOL_ENTRIES];
+            d.dst_addr = m.dst + (uint64_t)r * m.row_bytes;
+            d.tag = r;
+            if (tok >= 0 && tok < m.num_tokens) {
+                d.src_addr = m.host_base + (uint64_t)tok * m.token_stride;
+                d.size = m.row_bytes;
+            } else {
+                __hip_atomic_fetch_or(&cnt->error, SG_ERR_BAD_ROW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                d.src_addr = m.host_base;
+                d.size = 0;
+            }
+        }
+        const uint64_t slot = sg::sg_alloc_list(sq);
+        if (!sg::sg_commit_list(sq, slot, (uint32_t)(pool % MAX_SG_POOL_ENTRIES), n, L, SG_FLAG_NONE)) break;
+    }
+    if (blockIdx.x == 0) {
+        if (!sg::sg_wait_list_done(sq, total) && lane == 0)
+            __hip_atomic_fetch_or(&cnt->error, SG_ERR_LIST_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sg::sg_terminate(sq);
+    }
+}
+
+// Wave 0 transfer, wave 1 compute, wave 2 submitter, waves 3.. transfer helpers.
+template <typename F>
+__global__ __launch_bounds__(6 * 64) void sg_moe_kernel(gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq, F fn,
+                                                        MoeLists m) {
+    gfd::sg_warp_spec::_sg_transfer_warp_loop(dq, sq, fn);  // waves 0, 1 and 3.. run here; wave 2 returns
+    if (gfd::wave::wave_id() == 2) moe_submit(sq, m);
+}
+
+int fail(int code, const char* what) {
+    gfd_internal_set_error(what);
+    return code ? code : (int)hipErrorInvalidValue;
+}
+
+}  // namespace
+
+extern "C" int gfd_sg_session_launch_moe(gfd_sg_session_t s, const void* host_base, uint64_t token_stride,
+                                         int num_tokens, const int* offsets, const int* row_token, int num_experts,
+                                         int num_rows, uint32_t row_bytes, uint32_t rows_per_list, void* dst,
+                                         void* out, const uint16_t* weight, float eps, void* stream) {
+    if (!s || !host_base || !offsets || !row_token || !dst || num_tokens <= 0 || num_experts < 1 ||
+        num_experts > 64 || num_rows < 0 || num_rows > gfd::MAX_SG_POOL_ENTRIES || row_bytes == 0 ||
+        rows_per_list == 0 || rows_per_list > 64 ||
+        (out && (!weight || row_bytes % 1024 != 0 || row_bytes > 14 * 1024)))
+        return fail(hipErrorInvalidValue, "gfd_sg_session_launch_moe: invalid argument");
+    auto* p = static_cast<gfd::SGWarpSpecSession*>(s);
+    const int helpers = p->helper_waves();
+    p->before_launch(stream, helpers);
+    const MoeLists m{(uint64_t)(uintptr_t)host_base, token_stride, (uint64_t)(uintptr_t)dst, offsets, row_token,
+                     num_experts, num_tokens, num_rows, row_bytes, rows_per_list};
+    const dim3 grid((unsigned)p->num_blocks()), block((unsigned)(3 + helpers) * 64);
+    if (out)
+        hipLaunchKernelGGL(sg_moe_kernel<RowRMSNorm>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),
+                           p->get_sg_queue(), RowRMSNorm{(uint8_t*)out, weight, eps}, m);
+    else
+        hipLaunchKernelGGL(sg_moe_kernel<NoCompute>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),
+                           p->get_sg_queue(), NoCompute{}, m);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : fail(e, "gfd_sg_session_launch_moe: launch failed");
+}

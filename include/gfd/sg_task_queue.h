@@ -92,6 +92,8 @@ constexpr uint64_t SG_ERR_SLOT_WAIT = 1;     // transfer wave: the compute wave 
 constexpr uint64_t SG_ERR_COMPUTE_WAIT = 2;  // compute wave: the transfer wave never handed a list over
 constexpr uint64_t SG_ERR_RING_WAIT = 4;     // GPU submitter: a ring slot never became free
 constexpr uint64_t SG_ERR_HELPER_WAIT = 8;   // transfer waves: a copy job's hand-off stalled
+constexpr uint64_t SG_ERR_BAD_ROW = 16;      // GPU submitter: a routing entry out of range (skipped)
+constexpr uint64_t SG_ERR_LIST_WAIT = 32;    // GPU submitter: its lists did not all land in time
 static_assert(sizeof(SGDeviceCounters) == 128, "SGDeviceCounters is two cache lines");
 
 GFD_HD inline SGDeviceCounters* sg_device_counters(const SGTaskQueue* sq) {

@@ -370,6 +370,25 @@ int gfd_sg_session_launch_gpu_submit(gfd_sg_session_t s, const gfd_device_sg_ent
  * list and `extra_gpu_lists` GPU-submitted lists to land, sets terminate,
  * waits for the kernel.  Nonzero if lists did not land or the kernel
  * reported an error. */
+/* The MoE-routed gather through the session (the SG MoE workload of
+ * examples/09_sg_warp_spec.cu:78-294 with lists built on the GPU): submitter
+ * waves cut expert e's rows [offsets[e], offsets[e+1]) of gfd_moe_route's
+ * expert-major order into lists of at most rows_per_list (1..64) rows
+ * (list ids 0.. over experts in order); entry r: src = host_base +
+ * row_token[r] * token_stride (pinned host), dst = dst + r * row_bytes (HBM),
+ * tag = r.  The transfer waves copy each list; with out != NULL the compute
+ * wave writes the bf16 RMSNorm x / sqrt(mean(x^2) + eps) * weight of every
+ * landed row to out + r * row_bytes (row_bytes a multiple of 1024, at most
+ * 14 KiB), else it does nothing.  offsets / row_token / weight are
+ * device-readable; at most 64 experts and MAX_SG_POOL_ENTRIES rows (lists
+ * beyond MAX_SG_LISTS reuse ring slots; their ids get no d_list_done word).  The kernel ends
+ * itself once every list has landed: synchronise the stream, then call
+ * gfd_sg_session_synchronize(s, 0).  Routing entries out of range are
+ * skipped and reported as error bit 16. */
+int gfd_sg_session_launch_moe(gfd_sg_session_t s, const void* host_base, uint64_t token_stride, int num_tokens,
+                              const int* offsets, const int* row_token, int num_experts, int num_rows,
+                              uint32_t row_bytes, uint32_t rows_per_list, void* dst, void* out,
+                              const uint16_t* weight, float eps, void* stream);
 int gfd_sg_session_synchronize(gfd_sg_session_t s, uint64_t extra_gpu_lists);
 int gfd_sg_session_reset(gfd_sg_session_t s);
 int gfd_sg_session_stats(gfd_sg_session_t s, gfd_session_result* out);

@@ -1,0 +1,116 @@
+"""GPU parity of the MoE-routed gather through SGWarpSpecSession (the SG MoE
+workload of the reference's examples/09_sg_warp_spec.cu:78-294 run through
+the session API, include/gfd/sg_warp_spec.cuh): routing on the GPU, per-expert
+row lists built by GPU submitter waves and posted with the sg:: primitives,
+rows copied by the session's transfer waves, a bf16 RMSNorm on every landed
+list by the compute wave.  Rows byte-exact against the oracle, RMSNorm within
+one bf16 ulp of the fp32 oracle, list / entry / byte counts exact."""
+import numpy as np
+import pytest
+
+import gfd_amd
+import oracle
+from test_gpu_moe import Moe
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert gfd_amd.device_count() > 0, "no GPU visible to libgfd_amd.so"
+    assert gfd_amd.lib().gfd_set_device(0) == 0
+
+
+def expected_lists(offsets, rows_per_list):
+    counts = np.diff(offsets.astype(np.int64))
+    return int(np.sum((counts + rows_per_list - 1) // rows_per_list))
+
+
+def run_session(m, sess, with_norm, rows_per_list, eps=1e-6):
+    m.d_dst.fill(0xCD)
+    m.d_out.fill(0xCD)
+    n = 2 * m.T
+    sess.reset()
+    sess.launch_moe(m.host.ptr, m.stride, m.T, m.d_offsets.ptr, m.d_rows.ptr, m.E, n, m.row_bytes, m.d_dst.ptr,
+                    m.d_out.ptr if with_norm else None, m.d_weight.ptr, eps, rows_per_list)
+    gfd_amd.synchronize()  # the kernel ends once every list has landed
+    sess.synchronize(0)
+    return sess.stats()
+
+
+@pytest.mark.parametrize("T,E,dim,rpl,blocks", [(4096, 64, 7168, 8, 0), (4096, 64, 7168, 64, 16),
+                                                (4096, 64, 7168, 2, 0), (64, 8, 512, 4, 2), (300, 5, 1024, 7, 0),
+                                                (1000, 16, 2048, 1, 8)])
+def test_moe_through_session(T, E, dim, rpl, blocks):
+    print("moe session T=%d E=%d dim=%d rows/list=%d blocks=%d" % (T, E, dim, rpl, blocks), flush=True)
+    m = Moe(T, E, dim)
+    m.route()
+    assert (m.d_rows.download().view(np.int32) == m.row_token).all()
+    n = 2 * T
+    rows = m.expected_rows()
+    ref = oracle.rmsnorm_rows(oracle.bf16_to_f32(rows), oracle.bf16_to_f32(m.weight), 1e-6)
+    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=blocks, idle_limit_ms=10000)
+    try:
+        for with_norm in (False, True, True):  # two overlapped launches: the session's state carries over
+            st = run_session(m, sess, with_norm, rpl)
+            assert st["error_bits"] == 0
+            assert st["lists_done"] == expected_lists(m.offsets, rpl)
+            assert st["units_done"] == n and st["bytes"] == n * m.row_bytes
+            got = m.d_dst.download()
+            assert (got[:n * m.row_bytes].view(np.uint16).reshape(n, dim) == rows).all()
+            assert (got[n * m.row_bytes:] == 0xCD).all()
+            out = m.d_out.download()
+            if not with_norm:
+                assert (out == 0xCD).all()
+                continue
+            y = oracle.bf16_to_f32(out[:n * m.row_bytes].view(np.uint16).reshape(n, dim))
+            assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-6)
+            assert np.mean(oracle.f32_to_bf16(ref) == oracle.f32_to_bf16(y)) > 0.99
+            assert (out[n * m.row_bytes:] == 0xCD).all()
+    finally:
+        sess.close()
+
+
+def test_moe_session_skips_out_of_range_rows():
+    """A routing entry outside the token range is reported (error bit 16) and
+    its row skipped; every other row lands."""
+    m = Moe(64, 8, 512)
+    m.route()
+    rt = m.row_token.copy()
+    rt[5] = m.T + 3
+    m.d_rows.upload(rt)
+    n = 2 * m.T
+    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=2, idle_limit_ms=10000)
+    try:
+        m.d_dst.fill(0xCD)
+        sess.reset()
+        sess.launch_moe(m.host.ptr, m.stride, m.T, m.d_offsets.ptr, m.d_rows.ptr, m.E, n, m.row_bytes, m.d_dst.ptr,
+                        None, None, 1e-6, 16)
+        gfd_amd.synchronize()
+        with pytest.raises(gfd_amd.GfdError):
+            sess.synchronize(0)
+        assert sess.stats()["error_bits"] & 16
+        got = m.d_dst.download()[:n * m.row_bytes].view(np.uint16).reshape(n, m.dim)
+        rows = m.values[np.clip(rt, 0, m.T - 1)]
+        keep = np.arange(n) != 5
+        assert (got[keep] == rows[keep]).all()
+        assert (got[5].view(np.uint8) == 0xCD).all()
+    finally:
+        sess.close()
+
+
+def test_moe_session_rejects_bad_arguments():
+    m = Moe(64, 8, 512)
+    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=2, idle_limit_ms=1000)
+    try:
+        with pytest.raises(gfd_amd.GfdError):  # 65 rows per list
+            sess.launch_moe(m.host.ptr, m.stride, m.T, m.d_offsets.ptr, m.d_rows.ptr, m.E, 2 * m.T, m.row_bytes,
+                            m.d_dst.ptr, None, None, 1e-6, 65)
+        with pytest.raises(gfd_amd.GfdError):  # more rows than the entry pool holds
+            sess.launch_moe(m.host.ptr, m.stride, m.T, m.d_offsets.ptr, m.d_rows.ptr, m.E, 16385, m.row_bytes,
+                            m.d_dst.ptr, None, None, 1e-6, 16)
+        with pytest.raises(gfd_amd.GfdError):  # RMSNorm needs whole 1 KiB row blocks
+            sess.launch_moe(m.host.ptr, m.stride, m.T, m.d_offsets.ptr, m.d_rows.ptr, m.E, 2 * m.T, 1000,
+                            m.d_dst.ptr, m.d_out.ptr, m.d_weight.ptr, 1e-6, 16)
+    finally:
+        sess.close()
