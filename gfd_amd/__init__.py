@@ -160,6 +160,7 @@ def _declare(L):
         "gfd_zero_copy_gather_tokens": ([vp, vp, c_u32, c_int, vp], c_int),
         "gfd_zero_copy_gather": ([vp, c_int, vp], c_int),
         "gfd_moe_route": ([vp, c_int, c_int, vp, vp, vp, vp], c_int),
+        "gfd_moe_route_noalloc": ([vp, c_int, c_int, vp, vp, vp], c_int),
         "gfd_sg_gather_rmsnorm": ([vp, c_u64, c_int, vp, c_int, c_u32, vp, vp, vp, ctypes.c_float, c_int, vp, vp],
                                   c_int),
         "gfd_queue_alloc": ([pvp], c_int),

@@ -20,9 +20,19 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
+#include "capi_error.h"
 #include "gfd/wave_ops.h"
 #include "gfd_capi.h"
+
+// Scratch of gfd_moe_route_noalloc: the top-2 expert pairs between its two
+// kernels, for up to kNoAllocMaxTokens tokens (512 KiB per GPU, held until the
+// process ends).  Host code never uses this name as an address: each
+// device's copy is reached through the pointer hipGetSymbolAddress returns
+// for it (moe_scratch_ptr below).
+constexpr int kNoAllocMaxTokens = 65536;
+static __device__ __align__(256) int scratch[2 * kNoAllocMaxTokens];
 
 namespace {
 
@@ -262,19 +272,64 @@ int cus() {
     return g_cus;
 }
 
-}  // namespace
+// Device address of this device's `scratch`, looked up once per device with
+// that device current; 0 or a HIP error.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
 
-extern "C" int gfd_moe_route(const float* logits, int num_tokens, int num_experts, int* top2, int* offsets,
-                             int* row_token, void* stream) {
-    if (num_tokens <= 0 || num_experts < 2 || num_experts > 64 || !logits || !top2 || !offsets || !row_token)
-        return (int)hipErrorInvalidValue;
-    hipStream_t st = (hipStream_t)stream;
+int moe_scratch_ptr(int** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = static_cast<int*>(g_scratch_ptr[dev]);
+    return 0;
+}
+
+int launch_route(const float* logits, int num_tokens, int num_experts, int* top2, int* offsets, int* row_token,
+                 hipStream_t st) {
     const int waves_per_block = 256 / kWave;
     hipLaunchKernelGGL(moe_top2_kernel, dim3((num_tokens + waves_per_block - 1) / waves_per_block), dim3(256), 0, st,
                        logits, num_tokens, num_experts, top2);
     hipLaunchKernelGGL(moe_lists_kernel, dim3(num_experts), dim3(256), 0, st, top2, num_tokens, num_experts, offsets,
                        row_token);
     return (int)hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int gfd_moe_route_noalloc(const float* logits, int num_tokens, int num_experts, int* offsets,
+                                     int* row_token, void* stream) {
+    if (num_tokens <= 0 || num_experts < 2 || num_experts > 64 || !logits || !offsets || !row_token) {
+        gfd_internal_set_error("gfd_moe_route_noalloc: invalid argument");
+        return (int)hipErrorInvalidValue;
+    }
+    if (num_tokens > kNoAllocMaxTokens) {
+        gfd_internal_set_error("gfd_moe_route_noalloc: num_tokens exceeds the scratch maximum of 65536 tokens");
+        return (int)hipErrorInvalidValue;
+    }
+    int* top2 = nullptr;
+    const int rc = moe_scratch_ptr(&top2);
+    if (rc != 0) {
+        gfd_internal_set_error("gfd_moe_route_noalloc: hipGetSymbolAddress of the scratch array failed");
+        return rc;
+    }
+    return launch_route(logits, num_tokens, num_experts, top2, offsets, row_token, (hipStream_t)stream);
+}
+
+extern "C" int gfd_moe_route(const float* logits, int num_tokens, int num_experts, int* top2, int* offsets,
+                             int* row_token, void* stream) {
+    if (num_tokens <= 0 || num_experts < 2 || num_experts > 64 || !logits || !top2 || !offsets || !row_token)
+        return (int)hipErrorInvalidValue;
+    return launch_route(logits, num_tokens, num_experts, top2, offsets, row_token, (hipStream_t)stream);
 }
 
 extern "C" int gfd_sg_gather_rmsnorm(const void* host_base, uint64_t token_stride, int num_tokens, const int* row_token,

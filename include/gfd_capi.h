@@ -208,6 +208,16 @@ int gfd_zero_copy_scatter_tokens(const uint64_t* dst_addrs, const void* src, uin
  * token order: offsets[num_experts+1], row_token[2*num_tokens] (expert-major). */
 int gfd_moe_route(const float* logits, int num_tokens, int num_experts, int* top2, int* offsets,
                   int* row_token, void* stream);
+/* gfd_moe_route for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc); no
+ * counterpart in the reference.  The same offsets and row_token, with the
+ * top-2 pairs kept in a scratch array the library holds in device memory
+ * (one per GPU, 512 KiB, until the process ends) instead of a caller buffer.
+ * Allocates nothing.  num_tokens <= 65536 (larger: an error, nothing launched).
+ * Every call on one GPU shares that GPU's scratch: calls that overlap on one
+ * GPU (other streams or threads) race; calls ordered on one stream do not. */
+int gfd_moe_route_noalloc(const float* logits, int num_tokens, int num_experts, int* offsets,
+                          int* row_token, void* stream);
 /* Row r: token row_token[r] (host_base + token*token_stride, row_bytes bytes,
  * pinned host memory) -> dst + r*row_bytes (HBM).  out != NULL: producer waves
  * fetch into an LDS ring and consumer waves write the bf16 RMSNorm
