@@ -177,7 +177,23 @@ Status CopyEngineManager::submit_scatter_gather(const SGEntry* entries, int coun
 Status CopyEngineManager::submit_after(DevicePtr dst, const void* src, size_t size, uint64_t after_begin,
                                        uint64_t after_end, uint64_t also_after) {
     if (!initialized_) return GFD_SUCCESS;
-    if (backend_ == BACKEND_SDMA) {
+    if (backend_ == BACKEND_SDMA && sdma_->channels_in_order()) {
+        // One engine per channel, each finishing its copies in order: the
+        // newest copy of every channel since after_begin stands for all of
+        // that channel's, so the write depends on at most channels + 1
+        // copies and nothing is waited for on the host.
+        uint64_t deps[MAX_CE_CHANNELS + 1];
+        int nd = sdma_->channel_tails(after_begin, deps);
+        const uint64_t tail = sdma_->retire();
+        if (also_after != kNoFence && also_after >= tail) {
+            bool have = false;
+            for (int i = 0; i < nd; i++) have |= deps[i] == also_after;
+            if (!have) deps[nd++] = also_after;
+        }
+        int st = sdma_->copy(last_channel_, dst, src, size, nullptr, deps, nd);
+        if (st) return st;
+    } else if (backend_ == BACKEND_SDMA) {
+        // Runtime-chosen engines: no order between copies to lean on.
         uint64_t deps[16];
         int nd = 0;
         const uint64_t tail = sdma_->retire();

@@ -126,6 +126,7 @@ int SdmaQueue::init(int device, int channels, int pin_engines) {
     slot_bytes_.assign(kRing, 0);
     slot_channel_.assign(kRing, 0);
     waiter_.assign(kRing, 0);
+    ch_last_.assign((size_t)channels_, 0);
     uint64_t freq = 0;
     if (hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP_FREQUENCY, &freq) == HSA_STATUS_SUCCESS && freq)
         tick_ns_ = 1e9 / (double)freq;
@@ -134,6 +135,14 @@ int SdmaQueue::init(int device, int channels, int pin_engines) {
     inited_ = true;
     GFD_LOG_DEBUG("SDMA: engines mask 0x%x, %d channel(s), pinned=%d\n", engine_mask_, channels_, (int)pin_);
     return 0;
+}
+
+int SdmaQueue::channel_tails(uint64_t begin, uint64_t* deps) {
+    retire();
+    int n = 0;
+    for (uint64_t last : ch_last_)
+        if (last > 0 && last - 1 >= begin && last - 1 >= tail_) deps[n++] = last - 1;
+    return n;
 }
 
 uint64_t SdmaQueue::retire() {
@@ -251,6 +260,7 @@ int SdmaQueue::copy(int channel, uint64_t dst, const void* src, size_t bytes, ui
         return (int)st;
     }
     for (uint32_t i = 0; i < nd; i++) waiter_[dep_slots[i]] = s + 1;
+    ch_last_[(size_t)channel % ch_last_.size()] = s + 1;
     slot_bytes_[s % kRing] = bytes;
     slot_channel_[s % kRing] = (uint32_t)channel;
     next_seq_ = s + 1;

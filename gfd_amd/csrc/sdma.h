@@ -46,6 +46,14 @@ public:
              const uint64_t* deps = nullptr, int ndeps = 0);
 
     uint64_t issued() const { return next_seq_; }
+    // True when every channel is one SDMA engine (its copies finish in the
+    // order they were issued on it).
+    bool channels_in_order() const { return pin_; }
+    // Copies that order everything issued from fence `begin` on, when
+    // channels_in_order(): the newest copy of each channel issued at or after
+    // `begin` and not yet known complete.  Writes at most num_channels()
+    // sequence numbers to deps; returns how many.
+    int channel_tails(uint64_t begin, uint64_t* deps);
     // Advance past completed copies; returns the first sequence number not yet
     // known complete (every copy below it has finished).
     uint64_t retire();
@@ -99,6 +107,7 @@ private:
     // signal's value at that moment, so a slot is not handed to a new copy
     // until every copy that depends on its previous occupant has finished.
     std::vector<uint64_t> waiter_;
+    std::vector<uint64_t> ch_last_;  // per channel: 1 + sequence of its newest copy (0 = none)
     uint64_t next_seq_ = 0;
     uint64_t tail_ = 0;  // all seq < tail_ complete
     int error_ = 0;

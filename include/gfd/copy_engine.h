@@ -94,7 +94,11 @@ public:
     // Enqueue a small copy that starts only after the copies with fence
     // numbers in [after_begin, after_end) have finished, and after copy
     // `also_after` if given (ordered on the copy engines, no host wait).
-    // Used for completion flags in HBM.
+    // Used for completion flags in HBM.  With one engine per channel
+    // (pinned engines, the default) the copy waits for the newest copy of
+    // each channel issued since after_begin, at most channels + 1 signals:
+    // that covers every copy issued since after_begin, a superset of the
+    // range when after_end is not the current fence.
     static constexpr uint64_t kNoFence = ~0ull;
     Status submit_after(DevicePtr dst, const void* src, size_t size, uint64_t after_begin,
                         uint64_t after_end, uint64_t also_after = kNoFence);

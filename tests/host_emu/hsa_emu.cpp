@@ -276,6 +276,13 @@ hsa_status_t HSA_API hsa_amd_memory_async_copy_on_engine(void* dst, hsa_agent_t,
                                                          hsa_amd_sdma_engine_id_t engine_id, bool) {
     const uint32_t id = (uint32_t)engine_id;
     if (id == 0 || (id & (id - 1))) return HSA_STATUS_ERROR_INVALID_ARGUMENT;
+    // Copies on pinned engines depend on at most one copy per channel plus
+    // the previous flag write (CopyEngineManager::submit_after): at most
+    // MAX_CE_CHANNELS + 1 = 9 signals.
+    if (num_dep_signals > 9) {
+        std::fprintf(stderr, "emulated SDMA: copy with %u dependency signals (bound 9)\n", num_dep_signals);
+        std::abort();
+    }
     return enqueue(__builtin_ctz(id), dst, src, size, num_dep_signals, dep_signals, completion_signal);
 }
 

@@ -240,7 +240,9 @@ def test_submit_direct_copy_timeline(direct_poller):
     assert len(c) >= 2, "a pipelined 32 MiB gather issues several chunk copies"
     assert int(c["bytes"].sum()) == n * t
     assert (c["start_ns"] <= c["end_ns"]).all()
-    assert int(c["start_ns"].min()) >= t0 and int(c["end_ns"].max()) <= t1
+    # Engine timestamps and the host's reading of the same clock can be a
+    # fraction of a microsecond apart: allow 2 us at either end of the window.
+    assert int(c["start_ns"].min()) >= t0 - 2000 and int(c["end_ns"].max()) <= t1 + 2000
     assert np.all(np.diff(c["seq"].astype(np.int64)) > 0)
 
 
