@@ -613,8 +613,9 @@ def run_helper_waves(oracle, iters, warmup):
 
 
 TRACE_NAMES = {1: "batch_first_read", 2: "flush", 3: "copies_issued", 4: "done_published", 5: "gap_flush",
-               7: "chunk_copy_issued", 9: "gather_entry", 10: "gather_idle", 11: "gather_published",
-               12: "gather_first_slice", 13: "gather_built"}
+               7: "chunk_copy_issued", 8: "direct_end", 9: "gather_entry", 10: "gather_idle",
+               11: "gather_published", 12: "gather_first_slice", 13: "gather_built", 14: "zc_kernel_launched",
+               15: "zc_done_seen"}
 
 
 def _phase_medians(rows):
@@ -667,28 +668,33 @@ def run_timeline(oracle, calls=30):
     assert direct.init_direct_ce(), "init_direct_ce failed"
     for n, t in shapes:
         L = Layout(oracle, n, t)
-        for _ in range(10):
-            assert direct.submit_direct(L.entries, L.n) > 0
-        direct.set_trace(True)
-        direct.set_copy_timing(True)
-        direct.read_trace()
-        direct.read_copy_times()
-        win = []
-        for _ in range(calls):
-            a = time.monotonic_ns()
-            assert direct.submit_direct(L.entries, L.n) > 0
-            win.append((a, time.monotonic_ns()))
-        tr, cp = direct.read_trace(), direct.read_copy_times()
-        direct.set_trace(False)
-        direct.set_copy_timing(False)
-        L.verify("direct (timeline)")
-        rows = []
-        for a, b in win:
-            begin = tr[(tr["kind"] == 6) & (tr["t_ns"] >= a) & (tr["t_ns"] <= b)]
-            t0 = int(begin["t_ns"][0]) if len(begin) else a
-            rows.append(_call_phases(tr, cp[cp["path"] == 1], t0, b))
-        out["direct_%dx%d" % (n, t)] = _phase_medians(rows)
-        log("  timeline direct %dx%d: %s" % (n, t, out["direct_%dx%d" % (n, t)]))
+        routes = [("", DIRECT_ZC_MAX)] + ([("_staged", 0)] if n * t <= DIRECT_ZC_MAX else [])
+        for suffix, zc_max in routes:
+            direct.set_direct_zero_copy_max_bytes(zc_max)
+            for _ in range(10):
+                assert direct.submit_direct(L.entries, L.n) > 0
+            direct.set_trace(True)
+            direct.set_copy_timing(True)
+            direct.read_trace()
+            direct.read_copy_times()
+            win = []
+            for _ in range(calls):
+                a = time.monotonic_ns()
+                assert direct.submit_direct(L.entries, L.n) > 0
+                win.append((a, time.monotonic_ns()))
+            tr, cp = direct.read_trace(), direct.read_copy_times()
+            direct.set_trace(False)
+            direct.set_copy_timing(False)
+            L.verify("direct (timeline)")
+            rows = []
+            for a, b in win:
+                begin = tr[(tr["kind"] == 6) & (tr["t_ns"] >= a) & (tr["t_ns"] <= b)]
+                t0 = int(begin["t_ns"][0]) if len(begin) else a
+                rows.append(_call_phases(tr, cp[cp["path"] == 1], t0, b))
+            key = "direct%s_%dx%d" % (suffix, n, t)
+            out[key] = _phase_medians(rows)
+            log("  timeline %s: %s" % (key, out[key]))
+        direct.set_direct_zero_copy_max_bytes(DIRECT_ZC_MAX)
         del L
     direct.close()
 

@@ -115,17 +115,22 @@ int CpuPollingThread::zc_wait(uint64_t gen) {
 // Every source lies in pinned host memory the GPU reads at its host address.
 // Checked against the last pinned range found, entry by entry; with
 // fill_src_table the sources are also written to zc_src_table_ (uniform lists).
+// zc_src_table_ holds at least `count` addresses (pinned memory the kernel reads).
+bool CpuPollingThread::ensure_zc_src_table(int count) {
+    if (zc_src_cap_ >= count) return true;
+    if (zc_src_table_) gfd_hip_host_free(zc_src_table_);
+    zc_src_table_ = nullptr;
+    zc_src_cap_ = 0;
+    const int cap = std::max(count, 4096);
+    void* t = nullptr;
+    if (gfd_hip_host_alloc(&t, (size_t)cap * sizeof(uint64_t), GFD_HOST_DEFAULT) != 0) return false;
+    zc_src_table_ = static_cast<uint64_t*>(t);
+    zc_src_cap_ = cap;
+    return true;
+}
+
 bool CpuPollingThread::zc_sources_pinned(const SGEntry* entries, int count, bool fill_src_table) {
-    if (fill_src_table && zc_src_cap_ < count) {
-        if (zc_src_table_) gfd_hip_host_free(zc_src_table_);
-        zc_src_table_ = nullptr;
-        zc_src_cap_ = 0;
-        const int cap = std::max(count, 4096);
-        void* t = nullptr;
-        if (gfd_hip_host_alloc(&t, (size_t)cap * sizeof(uint64_t), GFD_HOST_DEFAULT) != 0) return false;
-        zc_src_table_ = static_cast<uint64_t*>(t);
-        zc_src_cap_ = cap;
-    }
+    if (fill_src_table && !ensure_zc_src_table(count)) return false;
     uintptr_t lo = 1, hi = 0;  // empty range: the first entry looks it up
     for (int i = 0; i < count; i++) {
         const uintptr_t a = (uintptr_t)entries[i].src, b = a + entries[i].size;
@@ -155,10 +160,11 @@ bool CpuPollingThread::zc_dst_in_device(uint64_t lo, uint64_t hi) {
 // per token); others pass the whole entry table.  Returns 0, kZcNotTaken
 // when the list does not qualify (the caller then takes the staged route), or
 // an error.
-int CpuPollingThread::direct_zero_copy(const SGEntry* entries, int count, size_t total, bool uniform) {
+int CpuPollingThread::direct_zero_copy(const SGEntry* entries, int count, size_t total, bool uniform,
+                                       bool sources_checked) {
     if (!zc_ready()) return kZcNotTaken;
     if (!zc_dst_in_device(entries[0].dst, entries[0].dst + total)) return kZcNotTaken;
-    if (!zc_sources_pinned(entries, count, uniform)) return kZcNotTaken;
+    if (!sources_checked && !zc_sources_pinned(entries, count, uniform)) return kZcNotTaken;
     const uint64_t gen = ++zc_gen_;
     int rc;
     if (uniform) {
@@ -181,7 +187,10 @@ int CpuPollingThread::direct_zero_copy(const SGEntry* entries, int count, size_t
                                          zc_done_, gen, zc_stream_);
     }
     if (rc != 0) return rc;
-    return zc_wait(gen);
+    trace(TRACE_ZC_LAUNCH, (uint32_t)count, total);
+    rc = zc_wait(gen);
+    trace(TRACE_ZC_DONE, 0, gen);
+    return rc;
 }
 
 // Destinations scattered over more runs than are worth one SDMA copy each
@@ -267,14 +276,39 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
     if (!direct_ce_manager_.is_initialized() || count <= 0 || !entries) return -1.0;
     std::lock_guard<std::mutex> direct_lock(direct_mutex_);
     const auto t0 = std::chrono::steady_clock::now();
-    if (gather_) gather_->prewake();  // workers wake while the list is inspected
     if (direct_ce_manager_.pin_context() != 0) return -1.0;
 
     // Total bytes and the three list properties the route depends on (split
     // over the gather workers for long lists).
     size_t total = entries[0].size;
     bool dst_contig = true, src_contig = true, uniform = true;
-    if (gather_) {
+    int zc_pinned = -1;  // zero-copy route: sources checked pinned and table filled (1), not pinned (0), unknown
+    if (count <= GatherEngine::kCallerScanMax && direct_zc_max_bytes_ > 0 && ensure_zc_src_table(count)) {
+        // Short list: one pass on this thread gives the route's properties and,
+        // for the zero-copy route, the pinned check and the source table.
+        // The gather workers are not woken: this route does not use them.
+        bool pinned = true;
+        uintptr_t lo = 1, hi = 0;
+        for (int i = 0; i < count; i++) {
+            const SGEntry& e = entries[i];
+            if (i > 0) {
+                const SGEntry& p = entries[i - 1];
+                total += e.size;
+                dst_contig &= e.dst == p.dst + p.size;
+                src_contig &= (const char*)e.src == (const char*)p.src + p.size;
+                uniform &= e.size == p.size;
+            }
+            const uintptr_t a = (uintptr_t)e.src, b = a + e.size;
+            if (pinned && (a < lo || b > hi)) {
+                pinned = direct_ce_manager_.host_source_ok(e.src, e.size);
+                direct_ce_manager_.last_pinned_range(&lo, &hi);
+                if (a < lo || b > hi) lo = a, hi = b;
+            }
+            zc_src_table_[i] = (uint64_t)a;
+        }
+        zc_pinned = pinned ? 1 : 0;
+    } else if (gather_) {
+        gather_->prewake();  // workers wake while the list is inspected
         std::lock_guard<std::mutex> lock(gather_mutex_);
         const GatherEngine::ListScan sc = gather_->scan(entries, count);
         total = sc.total;
@@ -309,8 +343,8 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
             err = direct_ce_manager_.submit_on_channel(c, entries[0].dst + off,
                                                        (const char*)entries[0].src + off, len);
         }
-    } else if (dst_contig && total <= direct_zc_max_bytes_ && count > 1 &&
-               (err = direct_zero_copy(entries, count, total, uniform)) != kZcNotTaken) {
+    } else if (dst_contig && total <= direct_zc_max_bytes_ && count > 1 && zc_pinned != 0 &&
+               (err = direct_zero_copy(entries, count, total, uniform, zc_pinned == 1)) != kZcNotTaken) {
         // done by the zero-copy kernel (err 0) or failed
     } else if (dst_contig && direct_staging_ && total <= direct_staging_size_) {
         err = 0;

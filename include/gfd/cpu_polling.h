@@ -151,6 +151,8 @@ public:
         TRACE_GATHER_PUBLISHED = 11,   // job visible to the workers: a = workers asleep at that moment
         TRACE_GATHER_FIRST_SLICE = 12, // first slice copied: a = threads that copied
         TRACE_GATHER_BUILT = 13,       // job state built (slices cut)
+        TRACE_ZC_LAUNCH = 14,          // Direct: zero-copy kernel launched: a = entries, b = bytes
+        TRACE_ZC_DONE = 15,            // Direct: its completion word seen by the host
     };
     struct TraceEvent {
         uint64_t t_ns;
@@ -204,8 +206,9 @@ private:
     bool gather_through_staging(const SGEntry* e, int count, size_t total, const DstRun* runs = nullptr,
                                 int nruns = 0, int uniform_hint = -1);
     int direct_scattered(const SGEntry* entries, int count, size_t total, bool uniform);
-    int direct_zero_copy(const SGEntry* entries, int count, size_t total, bool uniform);
+    int direct_zero_copy(const SGEntry* entries, int count, size_t total, bool uniform, bool sources_checked);
     bool zc_sources_pinned(const SGEntry* entries, int count, bool fill_src_table);
+    bool ensure_zc_src_table(int count);
     bool zc_dst_in_device(uint64_t lo, uint64_t hi);
     bool zc_ready();
     int zc_wait(uint64_t gen);

@@ -116,7 +116,8 @@ void gfd_poller_reset_stats(gfd_poller_t p);                         /* reset_st
 int gfd_poller_get_info(gfd_poller_t p, gfd_poller_info* out);
 /* Timeline trace of the poller and direct path (no reference counterpart):
  * t_ns (CLOCK_MONOTONIC), kind (1 batch-first, 2 flush, 3 issued, 4 done,
- * 5 gap-flush, 6 direct-begin, 7 chunk, 8 direct-end), a, b as documented in
+ * 5 gap-flush, 6 direct-begin, 7 chunk, 8 direct-end, 9-13 gather job phases,
+ * 14 zero-copy launch, 15 zero-copy completion seen), a, b as documented in
  * include/gfd/cpu_polling.h.  read_trace drains up to max events. */
 typedef struct gfd_trace_event {
     uint64_t t_ns;
