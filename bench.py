@@ -32,9 +32,9 @@ PCIE_GEN5_X16_GBPS = 32.0 * 16 * 128.0 / 130.0 / 8.0  # 63.0 GB/s per direction
 # Bytes one zc_gather_tokens launch moves at 8192 x 4 KiB, from two
 # rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of `bench.py --only zc,calib`,
 # each scaled by the same counter on a 32 MiB device-to-device copy
-# (FETCH x 1.9985, WRITE x 1.0).  Reads are host-link reads through the L2's
+# (FETCH x 1.99853, WRITE x 1.0).  Reads are host-link reads through the L2's
 # external interface; writes land in HBM.
-ZC_TRAFFIC_8192x4KB = {"read_bytes": 32901 * 1024, "write_bytes": 32768 * 1024}
+ZC_TRAFFIC_8192x4KB = {"read_bytes": 32891 * 1024, "write_bytes": 32772 * 1024}
 METRIC = "scattered H2D GB/s + % of PCIe5 x16 peak at 8192x4KB and 2048x64KB"
 DIRECT_ZC_MAX = 8 << 20  # submit_direct's default zero-copy route limit (bytes)
 PD = ctypes.POINTER(ctypes.c_double)
