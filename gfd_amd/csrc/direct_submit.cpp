@@ -91,6 +91,38 @@ bool CpuPollingThread::zc_ready() {
     return true;
 }
 
+// Everything the zero-copy route sets up on its first use, done ahead of it:
+// the stream and completion words, both address tables, and one 16-byte
+// launch of each kernel the route uses (the first launch of a kernel loads
+// its code object and creates the stream's hardware queue, ~0.5 ms).  The
+// launches copy 16 unused bytes of the pinned completion page into the unused
+// upper half of the 256-byte counter allocation.
+bool CpuPollingThread::zc_warm_up() {
+    if (!zc_ready() || !ensure_zc_src_table(4096)) return false;
+    if (zc_table_cap_ < 4096) {
+        if (zc_table_) gfd_hip_host_free(zc_table_);
+        zc_table_ = nullptr;
+        zc_table_cap_ = 0;
+        void* t = nullptr;
+        if (gfd_hip_host_alloc(&t, 4096 * sizeof(SGEntry), GFD_HOST_DEFAULT) != 0) return false;
+        zc_table_ = static_cast<SGEntry*>(t);
+        zc_table_cap_ = 4096;
+    }
+    char* spare_src = reinterpret_cast<char*>(zc_done_) + 32;
+    const uint64_t spare_dst = (uint64_t)(uintptr_t)zc_counter_ + 128;
+    zc_src_table_[0] = (uint64_t)(uintptr_t)spare_src;
+    uint64_t gen = ++zc_gen_;
+    if (gfd_zero_copy_gather_tokens_signal(zc_src_table_, (void*)(uintptr_t)spare_dst, 16, 1, zc_counter_, zc_done_,
+                                           gen, zc_stream_) != 0 ||
+        zc_wait(gen) != 0)
+        return false;
+    zc_table_[0] = SGEntry{spare_dst + 16, spare_src, 16};
+    gen = ++zc_gen_;
+    return gfd_zero_copy_gather_signal(reinterpret_cast<const gfd_sg_entry*>(zc_table_), 1, zc_counter_, zc_done_,
+                                       gen, zc_stream_) == 0 &&
+           zc_wait(gen) == 0;
+}
+
 // Wait until the grid launched with generation `gen` has raised the host
 // word (every byte it wrote is then in HBM).  Bounded: after
 // GFD_DIRECT_TIMEOUT_MS (10 s) the stream is synchronised to surface the
@@ -268,6 +300,10 @@ bool CpuPollingThread::init_direct_ce() {
             return false;
         }
         direct_staging_size_ = total_cpu_size_;
+    }
+    if (direct_zc_max_bytes_ > 0 && !zc_warm_up()) {
+        GFD_LOG_ERROR("zero-copy route set-up failed\n");
+        return false;
     }
     return start_workers();
 }

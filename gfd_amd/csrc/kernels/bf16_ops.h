@@ -17,5 +17,15 @@ __device__ __forceinline__ uint32_t from_f32(float f) {
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// Two fp32 values to one word of two bf16 (lo in the low half) with the
+// hardware conversion (v_cvt_pk_bf16_f32 on gfx950), rounding to nearest
+// even as from_f32 does, in one instruction instead of ten.
+__device__ __forceinline__ uint32_t pack(float lo, float hi) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
 }  // namespace bf16
 }  // namespace gfd

@@ -10,7 +10,8 @@
 // Lists: expert e's rows [offsets[e], offsets[e+1]) in the expert-major order
 // of gfd_moe_route, cut into lists of at most rows_per_list (<= 64) rows, so
 // a workgroup gets several lists and the RMSNorm of one overlaps the copy of
-// the next.  List ids run 0 .. total-1 over experts in order (lists past
+// the next.  List ids run 0 .. total-1: first every expert's full lists, in
+// expert order, then every expert's shorter remainder list (lists past
 // MAX_SG_LISTS reuse ring slots once landed; ids from MAX_SG_LISTS on have no
 // d_list_done word, which the kernel does not need).  Entry k of the
 // list for rows [r, r + n): src = host_base + row_token[r + k] * token_stride,
@@ -32,15 +33,19 @@ using gfd::sg_warp_spec::SGListView;
 
 // y = x / sqrt(mean(x^2) + eps) * w per landed row, fp32 arithmetic, bf16
 // round-to-nearest-even out, to out + row * row_bytes (the entry's tag is the
-// row).  V = row_bytes / 1 KiB vectors per lane, a template parameter so each
-// lane issues its V loads of a row (and of the weights) back to back.
+// row).  V = row_bytes / 1 KiB vectors per lane.
+//
+// The entries live in host memory and the rows were just written to HBM by
+// the transfer waves of this workgroup, so a row's own arithmetic is short
+// and its latency is what counts.  Per list: up to 64 entries are read in one
+// request (lane i reads entry i) instead of one host round trip per row, and
+// the weights are loaded once per list and parked in LDS, each lane reading
+// back only the vectors it stored itself (in registers they would not fit
+// beside a row and its fp32 values).  Entries whose
+// size is not row_bytes (rows skipped for a bad token id have size 0) are
+// left alone.
 template <int V>
-__device__ __forceinline__ void rmsnorm_row(uint64_t src, uint64_t o, const uint16_t* weight, float eps,
-                                            uint32_t lane) {
-    using gfd::wave::vec4u;
-    vec4u x[V];
-#pragma unroll
-    for (int k = 0; k < V; k++) x[k] = gfd::wave::gload(src + (uint64_t)(k * 64 + lane) * 16);
+__device__ __forceinline__ float sum_squares(const gfd::wave::vec4u (&x)[V]) {
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < V; k++)
@@ -49,21 +54,60 @@ __device__ __forceinline__ void rmsnorm_row(uint64_t src, uint64_t o, const uint
             const float a = gfd::bf16::lo(x[k][j]), b = gfd::bf16::hi(x[k][j]);
             ss += a * a + b * b;
         }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-    const float scale = 1.0f / sqrtf(ss / (float)(V * 512) + eps);
+    return ss;
+}
+
+template <int V>
+__device__ __forceinline__ void store_normalised(const gfd::wave::vec4u (&x)[V], const gfd::wave::vec4u* w_lds,
+                                                 float scale, uint64_t o, uint32_t lane) {
+    using gfd::wave::vec4u;
 #pragma unroll
     for (int k = 0; k < V; k++) {
-        const uint64_t off = (uint64_t)(k * 64 + lane) * 16;
-        const vec4u w = gfd::wave::gload((uint64_t)(uintptr_t)weight + off);
+        // volatile: read where it is used, not hoisted out of the row loop
+        // (the weights would then sit in registers again).
+        const vec4u w = *reinterpret_cast<const volatile vec4u*>(&w_lds[k * 64 + lane]);
         vec4u y;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const float l = gfd::bf16::lo(x[k][j]) * scale * gfd::bf16::lo(w[j]);
             const float h = gfd::bf16::hi(x[k][j]) * scale * gfd::bf16::hi(w[j]);
-            y[j] = gfd::bf16::from_f32(l) | (gfd::bf16::from_f32(h) << 16);
+            y[j] = gfd::bf16::pack(l, h);
         }
-        gfd::wave::gstore(o + off, y);
+        gfd::wave::gstore(o + (uint64_t)(k * 64 + lane) * 16, y);
+    }
+}
+
+template <int V>
+__device__ __forceinline__ void rmsnorm_list(const SGListView& view, uint8_t* out, const uint16_t* weight,
+                                             float eps, gfd::wave::vec4u* w_lds) {
+    using gfd::wave::vec4u;
+    constexpr uint32_t kRow = (uint32_t)V * 1024;
+    const uint32_t lane = (uint32_t)view.lane_id;
+#pragma unroll
+    for (int k = 0; k < V; k++)
+        w_lds[k * 64 + lane] = gfd::wave::gload((uint64_t)(uintptr_t)weight + (uint64_t)(k * 64 + lane) * 16);
+    for (uint32_t base = 0; base < view.count; base += 64) {
+        uint64_t src = 0;
+        uint32_t tag = 0;
+        bool ok = false;
+        if (base + lane < view.count) {
+            const gfd::DeviceSGEntry d = view.get_entry(base + lane);
+            ok = d.size == kRow;
+            src = d.dst_addr;  // the landed row in HBM
+            tag = d.tag;
+        }
+        for (uint64_t rows = __ballot(ok); rows; rows &= rows - 1) {
+            const int j = __builtin_ctzll(rows);
+            const uint64_t s0 = __shfl(src, j, 64);
+            const uint64_t o0 = (uint64_t)(uintptr_t)out + (uint64_t)(uint32_t)__shfl((int)tag, j, 64) * kRow;
+            vec4u x[V];
+#pragma unroll
+            for (int k = 0; k < V; k++) x[k] = gfd::wave::gload(s0 + (uint64_t)(k * 64 + lane) * 16);
+            float ss = sum_squares<V>(x);
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+            store_normalised<V>(x, w_lds, 1.0f / sqrtf(ss / (float)(V * 512) + eps), o0, lane);
+        }
     }
 }
 
@@ -71,20 +115,17 @@ struct RowRMSNorm {
     uint8_t* out;
     const uint16_t* weight;
     float eps;
+    uint32_t row_bytes;
     __device__ void operator()(SGListView v) const {
-        const uint32_t lane = (uint32_t)v.lane_id;
-        for (uint32_t e = 0; e < v.count; e++) {
-            const gfd::DeviceSGEntry d = v.get_entry(e);
-            const uint64_t o = (uint64_t)(uintptr_t)out + (uint64_t)d.tag * d.size;
-            switch (d.size) {  // skipped rows (size 0) and other sizes do nothing
-#define GFD_RMS_CASE(v) \
-    case v * 1024: rmsnorm_row<v>(d.dst_addr, o, weight, eps, lane); break;
-                GFD_RMS_CASE(1) GFD_RMS_CASE(2) GFD_RMS_CASE(3) GFD_RMS_CASE(4) GFD_RMS_CASE(5) GFD_RMS_CASE(6)
-                GFD_RMS_CASE(7) GFD_RMS_CASE(8) GFD_RMS_CASE(9) GFD_RMS_CASE(10) GFD_RMS_CASE(11) GFD_RMS_CASE(12)
-                GFD_RMS_CASE(13) GFD_RMS_CASE(14)
+        __shared__ gfd::wave::vec4u w_lds[14 * 64];  // weights of rows up to 14 KiB
+        switch (row_bytes) {
+#define GFD_RMS_CASE(n) \
+    case n * 1024: rmsnorm_list<n>(v, out, weight, eps, w_lds); break;
+            GFD_RMS_CASE(1) GFD_RMS_CASE(2) GFD_RMS_CASE(3) GFD_RMS_CASE(4) GFD_RMS_CASE(5) GFD_RMS_CASE(6)
+            GFD_RMS_CASE(7) GFD_RMS_CASE(8) GFD_RMS_CASE(9) GFD_RMS_CASE(10) GFD_RMS_CASE(11) GFD_RMS_CASE(12)
+            GFD_RMS_CASE(13) GFD_RMS_CASE(14)
 #undef GFD_RMS_CASE
-                default: break;
-            }
+            default: break;
         }
     }
 };
@@ -110,9 +151,12 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
     using namespace gfd;
     const int lane = wave::lane_id();
     SGDeviceCounters* cnt = sg_device_counters(sq);
-    // Lists per expert (one lane per expert, at most 64 experts) and their
-    // exclusive prefix: the first list id of each expert.
-    int a = 0, b = 0, nl = 0;
+    // Lists per expert (one lane per expert, at most 64 experts): `full`
+    // lists of rows_per_list rows and at most one shorter one with the rest.
+    // Full lists get the first ids (expert-major), the shorter ones the last,
+    // so the lists the transfer waves claim last are the short ones and the
+    // end of the launch waits on less work.
+    int a = 0, b = 0, full = 0, part = 0;
     if (lane < m.num_experts) {
         a = m.offsets[lane];
         b = m.offsets[lane + 1];
@@ -120,23 +164,30 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
             __hip_atomic_fetch_or(&cnt->error, SG_ERR_BAD_ROW, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             a = b = 0;
         }
-        nl = (int)(((uint32_t)(b - a) + m.rows_per_list - 1) / m.rows_per_list);
+        full = (int)((uint32_t)(b - a) / m.rows_per_list);
+        part = (uint32_t)(b - a) % m.rows_per_list != 0;
     }
-    int incl = nl;
+    int full_incl = full, part_incl = part;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int t = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += t;
+        const int tf = __shfl_up(full_incl, o, 64), tp = __shfl_up(part_incl, o, 64);
+        if (lane >= o) full_incl += tf, part_incl += tp;
     }
-    const int excl = incl - nl;
-    const uint32_t total = (uint32_t)__shfl(incl, 63, 64);
+    const int full_excl = full_incl - full, part_excl = part_incl - part;
+    const uint32_t nfull = (uint32_t)__shfl(full_incl, 63, 64);
+    const uint32_t total = nfull + (uint32_t)__shfl(part_incl, 63, 64);
     for (uint32_t L = blockIdx.x; L < total; L += gridDim.x) {
-        // The expert of list L: the highest expert whose first list id is <= L.
-        const uint64_t mask = __ballot(lane < m.num_experts && (uint32_t)excl <= L);
+        // The expert of list L: the highest expert whose first list id (of
+        // this kind) is <= L's index among lists of its kind.
+        const bool is_full = L < nfull;
+        const uint32_t k = is_full ? L : L - nfull;
+        const int excl = is_full ? full_excl : part_excl;
+        const uint64_t mask = __ballot(lane < m.num_experts && (uint32_t)excl <= k);
         const int e = 63 - __builtin_clzll(mask);
-        const int ea = __shfl(a, e, 64), eb = __shfl(b, e, 64), efirst = __shfl(excl, e, 64);
-        const uint32_t r0 = (uint32_t)ea + (L - (uint32_t)efirst) * m.rows_per_list;
-        const uint32_t n = min(m.rows_per_list, (uint32_t)eb - r0);
+        const uint32_t ea = (uint32_t)__shfl(a, e, 64), eb = (uint32_t)__shfl(b, e, 64);
+        const uint32_t r0 = is_full ? ea + (k - (uint32_t)__shfl(excl, e, 64)) * m.rows_per_list
+                                    : eb - (eb - ea) % m.rows_per_list;
+        const uint32_t n = min(m.rows_per_list, eb - r0);
         if (!sg::sg_wait_entry_space(sq, n) || !sg::sg_wait_list_space(sq)) {
             if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_RING_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
@@ -199,7 +250,7 @@ extern "C" int gfd_sg_session_launch_moe(gfd_sg_session_t s, const void* host_ba
     const dim3 grid((unsigned)p->num_blocks()), block((unsigned)(3 + helpers) * 64);
     if (out)
         hipLaunchKernelGGL(sg_moe_kernel<RowRMSNorm>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),
-                           p->get_sg_queue(), RowRMSNorm{(uint8_t*)out, weight, eps}, m);
+                           p->get_sg_queue(), RowRMSNorm{(uint8_t*)out, weight, eps, row_bytes}, m);
     else
         hipLaunchKernelGGL(sg_moe_kernel<NoCompute>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),
                            p->get_sg_queue(), NoCompute{}, m);

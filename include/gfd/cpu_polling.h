@@ -211,6 +211,7 @@ private:
     bool ensure_zc_src_table(int count);
     bool zc_dst_in_device(uint64_t lo, uint64_t hi);
     bool zc_ready();
+    bool zc_warm_up();
     int zc_wait(uint64_t gen);
     void copy_runs(const SGEntry* e, int count);
     void signal_device_u64(uint64_t* dst, uint64_t value, uint64_t after_begin);

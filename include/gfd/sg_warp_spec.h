@@ -73,10 +73,17 @@ __device__ __forceinline__ bool _wait_committed(SGTaskQueue* sq, SGDeviceCounter
     const int lane = wave::lane_id();
     const SGList& mine = sq->lists[idx % MAX_SG_LISTS];
     const uint64_t t0 = wall_clock64();
-    uint32_t grace = 0;
     for (;;) {
         const uint64_t known = __hip_atomic_load(&cnt->list_known, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (idx <= known) {
+            // terminate is read before the sequence.  Whoever sets terminate
+            // does so after every list it expects has been committed, with a
+            // release store; the acquire load that reads it orders the
+            // sequence load after those commits.  So a list still uncommitted
+            // once terminate reads 1 was never submitted, and the wave can
+            // stop at once.  (Read the other way round, a commit could land
+            // between the two loads and be dropped.)
+            const uint32_t term = wave::load_system32(&sq->terminate);
             if (wave::load_system(&mine.sequence) == idx + 1) {
                 if (idx == known) {
                     // Leader: find the committed run idx, idx+1, ... and publish it.
@@ -90,7 +97,7 @@ __device__ __forceinline__ bool _wait_committed(SGTaskQueue* sq, SGDeviceCounter
                 }
                 return true;
             }
-            if (wave::load_system32(&sq->terminate) && ++grace > 64) {
+            if (term) {
                 if (lane == 0) __hip_atomic_store(&cnt->stop, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 return false;
             }

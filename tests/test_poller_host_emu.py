@@ -23,6 +23,7 @@ Host threads follow the kernels' device protocols:
   copy source.
 Every landed byte is compared with the expected image, list checksums exactly.
 """
+import fcntl
 import os
 import shutil
 import subprocess
@@ -38,7 +39,11 @@ BIN = os.path.join(EMU, "_build", "poller_emu")
 def poller_emu():
     if shutil.which("g++") is None or not os.path.isdir("/opt/rocm/include/hsa"):
         pytest.skip("g++ or the HSA headers are not available")
-    subprocess.check_call(["make", "-s", "-j8", "-C", EMU], timeout=600)
+    # One build at a time: parallel test workers each reach this fixture.
+    os.makedirs(os.path.join(EMU, "_build"), exist_ok=True)
+    with open(os.path.join(EMU, "_build", ".lock"), "w") as lock:
+        fcntl.flock(lock, fcntl.LOCK_EX)
+        subprocess.check_call(["make", "-s", "-j8", "-C", EMU], timeout=600)
     return BIN
 
 
