@@ -37,6 +37,7 @@ PCIE_GEN5_X16_GBPS = 32.0 * 16 * 128.0 / 130.0 / 8.0  # 63.0 GB/s per direction
 ZC_TRAFFIC_8192x4KB = {"read_bytes": 32891 * 1024, "write_bytes": 32772 * 1024}
 METRIC = "scattered H2D GB/s + % of PCIe5 x16 peak at 8192x4KB and 2048x64KB"
 DIRECT_ZC_MAX = 8 << 20  # submit_direct's default zero-copy route limit (bytes)
+DIRECT_ZC_HEAD = 2 << 20  # and the zero-copy head of larger staged lists
 PD = ctypes.POINTER(ctypes.c_double)
 
 
@@ -241,23 +242,26 @@ def run_zero_copy(L, iters, warmup):
 
 
 def run_direct(poller, L, iters, warmup):
-    """submit_direct as configured (lists up to 8 MiB on the zero-copy route);
-    for those, also the staged SDMA route alone (staged_sdma)."""
+    """submit_direct as configured: lists up to 8 MiB on the zero-copy route,
+    larger ones staged for the copy engines with their first 2 MiB moved by
+    the zero-copy kernel meanwhile.  Also the staged SDMA route alone
+    (staged_sdma: no kernel at all)."""
     t = np.zeros(iters)
-    rc = gfd_amd.lib().gfd_bench_submit_direct(poller._h, ctypes.cast(L.entries, ctypes.c_void_p), L.n, warmup,
-                                               iters, t.ctypes.data_as(PD))
-    assert rc == 0, gfd_amd.lib().gfd_last_error()
-    L.verify("direct")
-    out = {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3),
-           "route": "zero-copy kernel" if L.bytes <= DIRECT_ZC_MAX else "staged SDMA"}
-    if L.bytes <= DIRECT_ZC_MAX:
-        poller.set_direct_zero_copy_max_bytes(0)
+
+    def timed_calls(what):
         rc = gfd_amd.lib().gfd_bench_submit_direct(poller._h, ctypes.cast(L.entries, ctypes.c_void_p), L.n, warmup,
                                                    iters, t.ctypes.data_as(PD))
-        poller.set_direct_zero_copy_max_bytes(DIRECT_ZC_MAX)
         assert rc == 0, gfd_amd.lib().gfd_last_error()
-        L.verify("direct (staged SDMA)")
-        out["staged_sdma"] = {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3)}
+        L.verify(what)
+        return {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3)}
+
+    out = timed_calls("direct")
+    head = poller.set_direct_zero_copy_head_bytes(DIRECT_ZC_HEAD)
+    out["route"] = ("zero-copy kernel" if L.bytes <= DIRECT_ZC_MAX else
+                    "staged SDMA + zero-copy head of %d KiB" % (head >> 10))
+    poller.set_direct_zero_copy_max_bytes(0)  # also switches the head off
+    out["staged_sdma"] = timed_calls("direct (staged SDMA)")
+    poller.set_direct_zero_copy_max_bytes(DIRECT_ZC_MAX)
     return out
 
 
@@ -292,7 +296,8 @@ def sdma_occupancy(copies, t0, t1):
         m = c["engine"] == e
         per_engine["0x%x" % int(e)] = round(_busy_union([(int(a), int(b)) for a, b in
                                                          zip(c["start_ns"][m], c["end_ns"][m])]) / win, 4)
-    return {"copies": int(len(c)), "window_us": round(win / 1e3, 2), "busy_frac_any": round(busy / win, 4),
+    return {"copies": int(len(c)), "bytes": int(c["bytes"].sum()), "window_us": round(win / 1e3, 2),
+            "busy_frac_any": round(busy / win, 4),
             "busy_frac_per_engine": per_engine, "link_GBps_while_busy": round(int(c["bytes"].sum()) / busy, 3),
             "first_copy_start_us": round((int(c["start_ns"].min()) - t0) / 1e3, 2),
             "tail_after_last_copy_us": round((t1 - int(c["end_ns"].max())) / 1e3, 2)}
@@ -317,7 +322,8 @@ def direct_timeline(poller, L, calls=20):
         return None
     med = lambda k: round(float(np.median([o[k] for o in per])), 4)
     engines = sorted(set(k for o in per for k in o["busy_frac_per_engine"]))
-    return {"calls": len(per), "copies_per_call": med("copies"), "window_us": med("window_us"),
+    return {"calls": len(per), "copies_per_call": med("copies"), "sdma_bytes_per_call": med("bytes"),
+            "window_us": med("window_us"),
             "busy_frac_any": med("busy_frac_any"), "link_GBps_while_busy": med("link_GBps_while_busy"),
             "first_copy_start_us": med("first_copy_start_us"), "tail_after_last_copy_us": med("tail_after_last_copy_us"),
             "busy_frac_per_engine": {e: round(float(np.median([o["busy_frac_per_engine"].get(e, 0.0) for o in per])), 4)
@@ -964,7 +970,8 @@ def main():
                 "link_GBps_while_busy": dsd["link_GBps_while_busy"], "busy_frac_any": dsd["busy_frac_any"],
                 "frac": round(r_main["bytes"] / (dsd["window_us"] * 1e3) / PCIE_GEN5_X16_GBPS, 4),
                 "frac_while_busy": round(dsd["link_GBps_while_busy"] / PCIE_GEN5_X16_GBPS, 4),
-                "first_copy_start_us": dsd["first_copy_start_us"], "copies_per_call": dsd["copies_per_call"]}
+                "first_copy_start_us": dsd["first_copy_start_us"], "copies_per_call": dsd["copies_per_call"],
+                "sdma_bytes_per_call": dsd["sdma_bytes_per_call"]}
     for r in [r_main, r_kv] + r_small:
         if not r:
             continue

@@ -149,6 +149,7 @@ def _declare(L):
         "gfd_poller_copy_clock_ns": ([vp], c_u64),
         "gfd_poller_set_direct_chunk_bytes": ([vp, c_u64], None),
         "gfd_poller_set_direct_zero_copy_max_bytes": ([vp, c_u64], None),
+        "gfd_poller_set_direct_zero_copy_head_bytes": ([vp, c_u64], c_u64),
         "gfd_bench_zero_copy_tokens_signal": ([vp, vp, c_u32, c_int, c_int, c_int, pd], c_int),
         "gfd_zero_copy_gather_tokens_signal": ([vp, vp, c_u32, c_int, vp, vp, c_u64, vp], c_int),
         "gfd_zero_copy_scatter_tokens_signal": ([vp, vp, c_u32, c_int, vp, vp, c_u64, vp], c_int),
@@ -417,6 +418,12 @@ class CpuPollingThread:
         """Lists up to b bytes (destination-contiguous, pinned sources) use the
         zero-copy kernel; 0 = always the staged SDMA route."""
         lib().gfd_poller_set_direct_zero_copy_max_bytes(self._h, b)
+
+    def set_direct_zero_copy_head_bytes(self, b):
+        """Larger lists (destination-contiguous, pinned sources): the zero-copy
+        kernel moves the first entries, up to b bytes, while the rest is staged
+        for the copy engines; 0 = staged only.  Returns the previous value."""
+        return int(lib().gfd_poller_set_direct_zero_copy_head_bytes(self._h, b))
 
     def set_gather_slice_bytes(self, b):
         lib().gfd_poller_set_gather_slice_bytes(self._h, b)

@@ -225,6 +225,41 @@ int CpuPollingThread::direct_zero_copy(const SGEntry* entries, int count, size_t
     return rc;
 }
 
+// The zero-copy head of a staged Direct call: launches the kernel on the
+// first entries, up to direct_zc_head_bytes_ bytes, when their sources are
+// pinned and the destination lies in device memory.  Returns the number of
+// entries launched (0: none; the staged route then takes the whole list) and
+// their bytes and generation; the caller waits with zc_wait(*gen).
+int CpuPollingThread::zc_launch_head(const SGEntry* entries, int count, size_t total, bool uniform,
+                                     size_t* head_bytes, uint64_t* gen) {
+    if (direct_zc_head_bytes_ == 0 || direct_zc_max_bytes_ == 0 || count < 2 || total <= direct_zc_head_bytes_)
+        return 0;
+    int k = 0;
+    size_t bytes = 0;
+    while (k < count - 1 && bytes + entries[k].size <= direct_zc_head_bytes_) bytes += entries[k++].size;
+    if (k == 0 || (!uniform && zc_table_cap_ < k) || !zc_ready() ||
+        !zc_dst_in_device(entries[0].dst, entries[0].dst + total) || !zc_sources_pinned(entries, k, uniform))
+        return 0;
+    const uint64_t g = ++zc_gen_;
+    int rc;
+    if (uniform) {
+        rc = gfd_zero_copy_gather_tokens_signal(zc_src_table_, (void*)(uintptr_t)entries[0].dst,
+                                                (uint32_t)entries[0].size, k, zc_counter_, zc_done_, g, zc_stream_);
+    } else {
+        std::memcpy(zc_table_, entries, (size_t)k * sizeof(SGEntry));
+        rc = gfd_zero_copy_gather_signal(reinterpret_cast<const gfd_sg_entry*>(zc_table_), k, zc_counter_, zc_done_,
+                                         g, zc_stream_);
+    }
+    if (rc != 0) {
+        --zc_gen_;
+        return 0;
+    }
+    trace(TRACE_ZC_LAUNCH, (uint32_t)k, bytes);
+    *head_bytes = bytes;
+    *gen = g;
+    return k;
+}
+
 // Destinations scattered over more runs than are worth one SDMA copy each
 // (paged KV caches): the zero-copy kernel writes every entry straight to its
 // destination.  Sources that are pinned host memory are read in place;
@@ -386,11 +421,20 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
         err = 0;
         std::lock_guard<std::mutex> lock(gather_mutex_);
         if (gather_) {
-            DirectCtx ctx{this, &direct_ce_manager_, entries[0].dst, direct_staging_, nch, 0};
-            gather_->run(entries, count, total, direct_staging_, direct_chunk_bytes_, direct_chunk, &ctx,
-                         uniform ? 1 : 0);
+            // The kernel moves the head while the first staged chunk is gathered.
+            size_t head_bytes = 0;
+            uint64_t head_gen = 0;
+            const int head = zc_launch_head(entries, count, total, uniform, &head_bytes, &head_gen);
+            DirectCtx ctx{this, &direct_ce_manager_, entries[head].dst, direct_staging_, nch, 0};
+            gather_->run(entries + head, count - head, total - head_bytes, direct_staging_, direct_chunk_bytes_,
+                         direct_chunk, &ctx, uniform ? 1 : 0);
             err = ctx.err;
             trace_gather_run();
+            if (head) {
+                const int zerr = zc_wait(head_gen);
+                trace(TRACE_ZC_DONE, 0, head_gen);
+                if (zerr && !err) err = zerr;
+            }
         } else {
             size_t off = 0;
             for (int i = 0; i < count; i++) {

@@ -124,6 +124,13 @@ public:
     // a few MiB the copy engines' fixed start-up latency dominates.
     void set_direct_zero_copy_max_bytes(size_t b) { direct_zc_max_bytes_ = b; }
     size_t direct_zero_copy_max_bytes() const { return direct_zc_max_bytes_; }
+    // Larger destination-contiguous lists with pinned sources: the zero-copy
+    // kernel moves the first entries, up to this many bytes, while the gather
+    // workers stage the rest for the copy engines, so the host link carries
+    // data before the first staged chunk is ready (0 = off;
+    // GFD_DIRECT_ZC_HEAD_BYTES; needs the zero-copy route enabled).
+    void set_direct_zero_copy_head_bytes(size_t b) { direct_zc_head_bytes_ = b; }
+    size_t direct_zero_copy_head_bytes() const { return direct_zc_head_bytes_; }
     // Chunk size of the pipelined gather (payload bytes per copy).
     void set_direct_chunk_bytes(size_t b) { direct_chunk_bytes_ = b ? b : 1; }
     size_t direct_chunk_bytes() const { return direct_chunk_bytes_; }
@@ -207,6 +214,8 @@ private:
                                 int nruns = 0, int uniform_hint = -1);
     int direct_scattered(const SGEntry* entries, int count, size_t total, bool uniform);
     int direct_zero_copy(const SGEntry* entries, int count, size_t total, bool uniform, bool sources_checked);
+    int zc_launch_head(const SGEntry* entries, int count, size_t total, bool uniform, size_t* head_bytes,
+                       uint64_t* gen);
     bool zc_sources_pinned(const SGEntry* entries, int count, bool fill_src_table);
     bool ensure_zc_src_table(int count);
     bool zc_dst_in_device(uint64_t lo, uint64_t hi);
@@ -297,6 +306,7 @@ private:
     uint64_t* zc_src_table_ = nullptr;
     int zc_src_cap_ = 0;
     size_t direct_zc_max_bytes_ = 8u << 20;
+    size_t direct_zc_head_bytes_ = 2u << 20;
     uint64_t zc_dst_lo_ = 0, zc_dst_hi_ = 0;  // last device allocation found for a destination
     std::vector<uint32_t> tile_scratch_;
     size_t slice_bytes_ = 0;

@@ -35,6 +35,10 @@ bool find_alloc(const void* p, size_t n, Kind k, uintptr_t* base, size_t* size);
 // GPU-side base of the locked range starting at `base`.
 uintptr_t locked_agent_base(uintptr_t base);
 
+// Launches of the emulated zero-copy kernels (the Direct path's kernel
+// route), so a scenario can tell which route a call took.
+unsigned zero_copy_launches();
+
 // Engine stall watchdog: an engine that has polled one dependency for longer
 // than this (GFD_EMU_STALL_MS, default 5000) prints what it waits on and ends
 // the process with kStallExit, since in-order engines that wait on each other

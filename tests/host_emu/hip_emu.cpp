@@ -1,6 +1,7 @@
 // Emulated gfd_hip_* shim (include/gfd/hip_shim.h) over host memory, plus
 // the allocation registry of emu.h.  Streams and events are inert handles:
 // the copy engine's SDMA backend (the one under test) never uses them.
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -80,6 +81,13 @@ void* alloc_aligned(size_t bytes) {
 int g_handle = 0;
 
 }  // namespace
+
+namespace {
+std::atomic<unsigned> g_zc_launches{0};
+}
+namespace emu {
+unsigned zero_copy_launches() { return g_zc_launches.load(); }
+}  // namespace emu
 
 extern "C" {
 
@@ -204,6 +212,7 @@ int gfd_zero_copy_gather_tokens_signal(const uint64_t* src_addrs, void* dst, uin
                                        void*) {
     if (!done_counter || !done_word || num_tokens < 0 || (num_tokens > 0 && (!src_addrs || !dst || !token_size)))
         return 1;
+    g_zc_launches++;
     for (int j = 0; j < num_tokens; j++)
         std::memcpy((char*)dst + (size_t)j * token_size, (const void*)(uintptr_t)src_addrs[j], token_size);
     __atomic_store_n(done_counter, 0u, __ATOMIC_RELAXED);
@@ -214,6 +223,7 @@ int gfd_zero_copy_gather_tokens_signal(const uint64_t* src_addrs, void* dst, uin
 int gfd_zero_copy_gather_signal(const gfd_sg_entry* entries, int count, unsigned int* done_counter,
                                 uint64_t* done_word, uint64_t done_value, void*) {
     if (!done_counter || !done_word || count < 0 || (count > 0 && !entries)) return 1;
+    g_zc_launches++;
     for (int i = 0; i < count; i++)
         std::memcpy((void*)(uintptr_t)entries[i].dst, (const void*)(uintptr_t)entries[i].src, entries[i].size);
     __atomic_store_n(done_counter, 0u, __ATOMIC_RELAXED);

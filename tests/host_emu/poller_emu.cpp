@@ -396,7 +396,9 @@ int run_ragged(const std::string& path, uint32_t n, uint32_t nruns, int rounds, 
         for (int rnd = 0; rnd < rounds && rc == 0; rnd++) {
             std::printf("ragged direct %u entries, %u runs, call %d\n", n, nruns, rnd);
             std::memset(dst, kSentinel, want.size());
+            const unsigned zc0 = emu::zero_copy_launches();
             if (p.submit_direct(sg.data(), (int)n) < 0) return 3;
+            std::printf("zero-copy launches: %u\n", emu::zero_copy_launches() - zc0);
             rc = check_image(dst, want, "ragged direct", rnd);
         }
     } else {

@@ -80,12 +80,31 @@ def test_queue_mode(poller_emu, n, t, scattered):
     run(poller_emu, ["queue", n, t, scattered, 2, 3])
 
 
+def zero_copy_launches(out):
+    return [int(l.split(":")[1]) for l in out.splitlines() if l.startswith("zero-copy launches:")]
+
+
 @pytest.mark.parametrize("path,nruns", [("direct", 1), ("direct", 8), ("direct", 40), ("queue", 1), ("queue", 8),
                                         ("queue", 100)])
 def test_ragged_entries_over_destination_runs(poller_emu, path, nruns):
     # Entries of 1..8999 bytes at every alignment: staged gathers with one
-    # copy per chunk or per run piece, and per-run copies.
-    run(poller_emu, ["ragged", path, 700, nruns, 2, 3])
+    # copy per chunk or per run piece, and per-run copies.  A Direct list with
+    # one destination run (about 3 MiB) takes the zero-copy route; with
+    # several runs it does not.
+    out = run(poller_emu, ["ragged", path, 700, nruns, 2, 3])
+    if path == "direct":
+        assert zero_copy_launches(out) == [1 if nruns == 1 else 0] * 2, out[-2000:]
+
+
+@pytest.mark.parametrize("head,launches", [(512 << 10, 1), (0, 0)])
+def test_direct_staged_route_with_zero_copy_head(poller_emu, head, launches):
+    # The same contiguous ragged list above the zero-copy route's limit (set
+    # to 1 MiB here): staged through the gather workers and the copy engines,
+    # with its first 512 KiB moved by the zero-copy kernel meanwhile, or with
+    # the head switched off.  Every byte is compared either way.
+    out = run(poller_emu, ["ragged", "direct", 700, 1, 2, 3],
+              env={"GFD_DIRECT_ZC_MAX_BYTES": str(1 << 20), "GFD_DIRECT_ZC_HEAD_BYTES": str(head)})
+    assert zero_copy_launches(out) == [launches] * 2, out[-2000:]
 
 
 @pytest.mark.parametrize("tiles,T,C,ts,whole,hbm", [(8, 128, 32, 4096, 0, 1), (8, 128, 32, 4096, 1, 1),
