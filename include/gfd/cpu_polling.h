@@ -214,8 +214,8 @@ private:
                                 int nruns = 0, int uniform_hint = -1);
     int direct_scattered(const SGEntry* entries, int count, size_t total, bool uniform);
     int direct_zero_copy(const SGEntry* entries, int count, size_t total, bool uniform, bool sources_checked);
-    int zc_launch_head(const SGEntry* entries, int count, size_t total, bool uniform, size_t* head_bytes,
-                       uint64_t* gen);
+    int zc_plan_head(const SGEntry* entries, int count, size_t total, bool uniform, size_t* head_bytes);
+    int zc_launch_head(const SGEntry* entries, int k, bool uniform, uint64_t* gen);
     bool zc_sources_pinned(const SGEntry* entries, int count, bool fill_src_table);
     bool ensure_zc_src_table(int count);
     bool zc_dst_in_device(uint64_t lo, uint64_t hi);
