@@ -4,7 +4,11 @@ destinations form one or more runs, the reference's generic path
 are 1..8999 bytes from seeded random sources in pinned memory; destinations
 follow the list order, cut into runs by gaps of odd length, so copies start
 and end at every alignment:
-  1 run         -> staged gather, one copy per staging chunk;
+  1 run         -> Direct: the zero-copy kernel (about 3 MiB), or, with the
+                   kernel route's limit lowered to 1 MiB, the staged gather with
+                   one copy per staging chunk and the first 512 KiB of entries
+                   moved by the kernel, or the staged gather alone;
+                   Queue: staged gather, one copy per staging chunk;
   8 / 40 runs   -> staged gather, one copy per run piece (unaligned pieces);
   100 runs      -> Direct: the zero-copy kernel; Queue: one copy per run.
 Every byte of the destination region is compared with the closed form
@@ -81,9 +85,10 @@ def direct_poller():
     p.close()
 
 
-@pytest.mark.parametrize("nruns", [1, 8, 40, 100])
-def test_direct_ragged_entries(direct_poller, nruns):
-    log("submit_direct ragged, %d runs" % nruns)
+@pytest.mark.parametrize("nruns,route", [(1, "default"), (1, "staged+head"), (1, "staged"), (8, "default"),
+                                         (40, "default"), (100, "default")])
+def test_direct_ragged_entries(direct_poller, nruns, route):
+    log("submit_direct ragged, %d runs, %s route" % (nruns, route))
     c = RaggedCase(700, nruns, seed=nruns)
     c.dst.fill(SENTINEL)
     entries = (gfd_amd.SGEntry * c.n)()
@@ -91,9 +96,16 @@ def test_direct_ragged_entries(direct_poller, nruns):
     a[:, 0] = c.dst_addrs()
     a[:, 1] = c.src_addrs()
     a[:, 2] = c.sizes
-    for rep in range(2):
-        assert direct_poller.submit_direct(entries, c.n) > 0
-        c.check("direct, %d runs, call %d" % (nruns, rep))
+    limit = {"default": 8 << 20, "staged+head": 1 << 20, "staged": 0}[route]
+    direct_poller.set_direct_zero_copy_max_bytes(limit)
+    head = direct_poller.set_direct_zero_copy_head_bytes(512 << 10)
+    try:
+        for rep in range(2):
+            assert direct_poller.submit_direct(entries, c.n) > 0
+            c.check("direct, %d runs, %s route, call %d" % (nruns, route, rep))
+    finally:
+        direct_poller.set_direct_zero_copy_max_bytes(8 << 20)
+        direct_poller.set_direct_zero_copy_head_bytes(head)
 
 
 def queue_ring(q):
