@@ -183,7 +183,8 @@ Status CopyEngineManager::submit_after(DevicePtr dst, const void* src, size_t si
         // that channel's, so the write depends on at most channels + 1
         // copies and nothing is waited for on the host.
         uint64_t deps[MAX_CE_CHANNELS + 1];
-        int nd = sdma_->channel_tails(after_begin, deps);
+        int nd = sdma_->channel_tails(after_begin, deps, MAX_CE_CHANNELS);
+        if (nd < 0) return -1;
         const uint64_t tail = sdma_->retire();
         if (also_after != kNoFence && also_after >= tail) {
             bool have = false;

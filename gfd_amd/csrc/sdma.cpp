@@ -137,11 +137,14 @@ int SdmaQueue::init(int device, int channels, int pin_engines) {
     return 0;
 }
 
-int SdmaQueue::channel_tails(uint64_t begin, uint64_t* deps) {
+int SdmaQueue::channel_tails(uint64_t begin, uint64_t* deps, int max_deps) {
     retire();
     int n = 0;
     for (uint64_t last : ch_last_)
-        if (last > 0 && last - 1 >= begin && last - 1 >= tail_) deps[n++] = last - 1;
+        if (last > 0 && last - 1 >= begin && last - 1 >= tail_) {
+            if (n == max_deps) return -1;  // more channels than the caller has room for
+            deps[n++] = last - 1;
+        }
     return n;
 }
 

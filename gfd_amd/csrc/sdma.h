@@ -51,9 +51,9 @@ public:
     bool channels_in_order() const { return pin_; }
     // Copies that order everything issued from fence `begin` on, when
     // channels_in_order(): the newest copy of each channel issued at or after
-    // `begin` and not yet known complete.  Writes at most num_channels()
-    // sequence numbers to deps; returns how many.
-    int channel_tails(uint64_t begin, uint64_t* deps);
+    // `begin` and not yet known complete.  Writes at most max_deps sequence
+    // numbers to deps; returns how many, or -1 if there were more.
+    int channel_tails(uint64_t begin, uint64_t* deps, int max_deps);
     // Advance past completed copies; returns the first sequence number not yet
     // known complete (every copy below it has finished).
     uint64_t retire();
