@@ -38,6 +38,10 @@ ZC_TRAFFIC_8192x4KB = {"read_bytes": 32891 * 1024, "write_bytes": 32772 * 1024}
 METRIC = "scattered H2D GB/s + % of PCIe5 x16 peak at 8192x4KB and 2048x64KB"
 DIRECT_ZC_MAX = 8 << 20  # submit_direct's default zero-copy route limit (bytes)
 DIRECT_ZC_HEAD = 2 << 20  # and the zero-copy head of larger staged lists
+# MoE through SGWarpSpecSession: workgroups, compute waves sharing each list
+# in the RMSNorm, rows per GPU-built list (swept: 24-128 workgroups, 1-3
+# compute waves, 2-64 rows per list).
+MOE_SESSION_BLOCKS, MOE_SESSION_COMPUTE_WAVES, MOE_SESSION_ROWS_PER_LIST = 32, 3, 48
 PD = ctypes.POINTER(ctypes.c_double)
 
 
@@ -442,19 +446,22 @@ def run_moe(oracle, iters, warmup, tokens=4096, experts=64, dim=7168):
                 raise SystemExit("PARITY FAILURE: MoE RMSNorm outside bf16 tolerance")
         res[name] = {"us_p50": round(p50(t), 2), "GBps": round(gbps(n * row_bytes, p50(t)), 3)}
     # The same workload through SGWarpSpecSession: GPU submitter waves build
-    # lists of <= 32 rows from the routing output, the session's transfer
-    # waves copy them, its compute wave runs the RMSNorm.  Timed with HIP
+    # lists of <= 48 rows from the routing output, the session's transfer
+    # waves copy them, its compute waves (3 sharing each list, or the
+    # reference's single one) run the RMSNorm.  Timed with HIP
     # events around launch_moe on the stream (the session's per-launch set-up
     # included); the kernel ends itself once every list has landed.
-    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=0, idle_limit_ms=10000)
-    try:
-        for name, with_norm in (("session_transfer_only", False), ("session_overlapped_rmsnorm", True)):
+    for name, with_norm, cw in (("session_transfer_only", False, 1),
+                                ("session_overlapped_rmsnorm", True, MOE_SESSION_COMPUTE_WAVES),
+                                ("session_overlapped_rmsnorm_1_compute_wave", True, 1)):
+        sess = gfd_amd.SGWarpSpecSession(num_compute_warps=cw, num_blocks=MOE_SESSION_BLOCKS, idle_limit_ms=10000)
+        try:
             t = []
             for i in range(-warmup, iters):
                 sess.reset()
                 L.gfd_event_record(ea, st)
                 sess.launch_moe(host.ptr, stride, tokens, d_off.ptr, d_rows.ptr, experts, n, row_bytes, d_dst.ptr,
-                                d_out.ptr if with_norm else None, d_w.ptr, 1e-6, 32, st)
+                                d_out.ptr if with_norm else None, d_w.ptr, 1e-6, MOE_SESSION_ROWS_PER_LIST, st)
                 L.gfd_event_record(eb, st)
                 L.gfd_event_synchronize(eb)
                 sess.synchronize(0)
@@ -473,9 +480,10 @@ def run_moe(oracle, iters, warmup, tokens=4096, experts=64, dim=7168):
                 if not np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-6):
                     raise SystemExit("PARITY FAILURE: MoE session RMSNorm outside bf16 tolerance")
             res[name] = {"us_p50": round(p50(t), 2), "GBps": round(gbps(n * row_bytes, p50(t)), 3),
-                         "lists": stt["lists_done"], "grid": stt["grid"], "rows_per_list": 32}
-    finally:
-        sess.close()
+                         "lists": stt["lists_done"], "grid": stt["grid"], "rows_per_list": MOE_SESSION_ROWS_PER_LIST,
+                         "compute_waves": cw}
+        finally:
+            sess.close()
     L.gfd_event_destroy(ea)
     L.gfd_event_destroy(eb)
     L.gfd_stream_destroy(st)

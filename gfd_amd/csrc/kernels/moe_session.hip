@@ -18,6 +18,7 @@
 // dst = dst + (r + k) * row_bytes, size = row_bytes, tag = r + k (the row).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 
 #include "bf16_ops.h"
@@ -80,6 +81,9 @@ __device__ __forceinline__ void store_normalised(const gfd::wave::vec4u (&x)[V],
 template <int V>
 __device__ __forceinline__ void rmsnorm_list(const SGListView& view, uint8_t* out, const uint16_t* weight,
                                              float eps, gfd::wave::vec4u* w_lds) {
+    // With several compute waves on the list, this one takes entries
+    // part, part + parts, ...
+    const uint32_t part = view.part, parts = view.parts ? view.parts : 1;
     using gfd::wave::vec4u;
     constexpr uint32_t kRow = (uint32_t)V * 1024;
     const uint32_t lane = (uint32_t)view.lane_id;
@@ -90,7 +94,7 @@ __device__ __forceinline__ void rmsnorm_list(const SGListView& view, uint8_t* ou
         uint64_t src = 0;
         uint32_t tag = 0;
         bool ok = false;
-        if (base + lane < view.count) {
+        if (base + lane < view.count && (base + lane) % parts == part) {
             const gfd::DeviceSGEntry d = view.get_entry(base + lane);
             ok = d.size == kRow;
             src = d.dst_addr;  // the landed row in HBM
@@ -112,15 +116,19 @@ __device__ __forceinline__ void rmsnorm_list(const SGListView& view, uint8_t* ou
 }
 
 struct RowRMSNorm {
+    // Up to SG_MAX_COMPUTE compute waves share each list, row by row.
+    static constexpr bool kSharesLists = true;
     uint8_t* out;
     const uint16_t* weight;
     float eps;
     uint32_t row_bytes;
     __device__ void operator()(SGListView v) const {
-        __shared__ gfd::wave::vec4u w_lds[14 * 64];  // weights of rows up to 14 KiB
+        // Weights of rows up to 14 KiB, one copy per compute wave.
+        __shared__ gfd::wave::vec4u w_lds[gfd::sg_warp_spec::SG_MAX_COMPUTE][14 * 64];
+        gfd::wave::vec4u* w = w_lds[v.part < (uint32_t)gfd::sg_warp_spec::SG_MAX_COMPUTE ? v.part : 0];
         switch (row_bytes) {
 #define GFD_RMS_CASE(n) \
-    case n * 1024: rmsnorm_list<n>(v, out, weight, eps, w_lds); break;
+    case n * 1024: rmsnorm_list<n>(v, out, weight, eps, w); break;
             GFD_RMS_CASE(1) GFD_RMS_CASE(2) GFD_RMS_CASE(3) GFD_RMS_CASE(4) GFD_RMS_CASE(5) GFD_RMS_CASE(6)
             GFD_RMS_CASE(7) GFD_RMS_CASE(8) GFD_RMS_CASE(9) GFD_RMS_CASE(10) GFD_RMS_CASE(11) GFD_RMS_CASE(12)
             GFD_RMS_CASE(13) GFD_RMS_CASE(14)
@@ -218,12 +226,13 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
     }
 }
 
-// Wave 0 transfer, wave 1 compute, wave 2 submitter, waves 3.. transfer helpers.
+// Wave 0 transfer, waves 1 .. C compute (C = 1 unless the functor shares
+// lists), wave C + 1 submitter, the waves after it transfer helpers.
 template <typename F>
-__global__ __launch_bounds__(6 * 64) void sg_moe_kernel(gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq, F fn,
-                                                        MoeLists m) {
-    gfd::sg_warp_spec::_sg_transfer_warp_loop(dq, sq, fn);  // waves 0, 1 and 3.. run here; wave 2 returns
-    if (gfd::wave::wave_id() == 2) moe_submit(sq, m);
+__global__ __launch_bounds__(8 * 64) void sg_moe_kernel(gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq, F fn,
+                                                        MoeLists m, int submitter_wave) {
+    gfd::sg_warp_spec::_sg_transfer_warp_loop(dq, sq, fn);  // the submitter wave returns from it
+    if (gfd::wave::wave_id() == submitter_wave) moe_submit(sq, m);
 }
 
 int fail(int code, const char* what) {
@@ -244,16 +253,19 @@ extern "C" int gfd_sg_session_launch_moe(gfd_sg_session_t s, const void* host_ba
         return fail(hipErrorInvalidValue, "gfd_sg_session_launch_moe: invalid argument");
     auto* p = static_cast<gfd::SGWarpSpecSession*>(s);
     const int helpers = p->helper_waves();
-    p->before_launch(stream, helpers);
+    // The RMSNorm consumer shares each list between the session's compute
+    // waves (num_compute_warps, at most SG_MAX_COMPUTE); transfer only needs one.
+    const int compute = out ? std::min(p->compute_waves(), gfd::sg_warp_spec::SG_MAX_COMPUTE) : 1;
+    p->before_launch(stream, helpers, compute);
     const MoeLists m{(uint64_t)(uintptr_t)host_base, token_stride, (uint64_t)(uintptr_t)dst, offsets, row_token,
                      num_experts, num_tokens, num_rows, row_bytes, rows_per_list};
-    const dim3 grid((unsigned)p->num_blocks()), block((unsigned)(3 + helpers) * 64);
+    const dim3 grid((unsigned)p->num_blocks()), block((unsigned)(2 + compute + helpers) * 64);
     if (out)
         hipLaunchKernelGGL(sg_moe_kernel<RowRMSNorm>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),
-                           p->get_sg_queue(), RowRMSNorm{(uint8_t*)out, weight, eps, row_bytes}, m);
+                           p->get_sg_queue(), RowRMSNorm{(uint8_t*)out, weight, eps, row_bytes}, m, 1 + compute);
     else
         hipLaunchKernelGGL(sg_moe_kernel<NoCompute>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),
-                           p->get_sg_queue(), NoCompute{}, m);
+                           p->get_sg_queue(), NoCompute{}, m, 2);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : fail(e, "gfd_sg_session_launch_moe: launch failed");
 }

@@ -271,7 +271,7 @@ uint64_t SGWarpSpecSession::submit_sg_list(const DeviceSGEntry* entries, uint32_
     return idx;
 }
 
-void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves) {
+void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int compute_waves) {
     if (running_) synchronize();
     if (!ok_) return;
     __atomic_store_n(&sq_->terminate, 0u, __ATOMIC_RELEASE);
@@ -287,6 +287,7 @@ void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves) {
     c.list_known = consumed_lists_;
     c.list_base = consumed_lists_;
     c.helpers = (uint64_t)(helper_waves < 0 ? config_.transfer_helper_waves : helper_waves);
+    c.compute_waves = (uint64_t)(compute_waves < 0 ? this->compute_waves() : compute_waves);
     gfd_hip_memset_d8((uint64_t)(uintptr_t)sq_->d_list_done, 0, MAX_SG_LISTS * sizeof(uint64_t));
     gfd_hip_memcpy_h2d((uint64_t)(uintptr_t)sg_device_counters(sq_), &c, sizeof(c));
     stream_ = stream;

@@ -83,7 +83,11 @@ struct SGDeviceCounters {
     uint64_t list_base;       // first ring index of this launch
     uint64_t bytes_done;      // bytes landed during this launch
     uint64_t helpers;         // transfer helper waves per workgroup (waves 2 .. 1 + helpers)
-    uint64_t _pad[5];
+    // Compute waves per workgroup that share each landed list (waves 1 ..
+    // compute_waves), for compute functors that declare kSharesLists; 0 or 1
+    // and every other functor: wave 1 alone.
+    uint64_t compute_waves;
+    uint64_t _pad[4];
 };
 constexpr int SG_DEVICE_COUNTER_WORDS = (int)(sizeof(SGDeviceCounters) / sizeof(uint64_t));
 

@@ -11,6 +11,13 @@
 // its opening barrier, so a kernel may call the loop from every wave and give
 // the others work of its own afterwards (a GPU submitter, for instance).
 //
+// A compute functor that declares `static constexpr bool kSharesLists = true`
+// may have several compute waves (waves 1 .. SGDeviceCounters::compute_waves,
+// at most SG_MAX_COMPUTE): each landed list then goes to all of them, with
+// SGListView::part / parts telling a wave its share, and the list's slot is
+// free again once every part is done.  Functors without the declaration see
+// each list exactly once, on wave 1, as with the reference.
+//
 // The transfer wave claims the next ring index (device-scope atomic on an
 // HBM counter), waits for that list to be committed, copies every entry's
 // bytes from pinned host memory into HBM itself together with the helpers
@@ -44,6 +51,10 @@ struct SGListView {
     int lane_id;
     uint32_t pool_offset;
     const SGTaskQueue* sq;
+    // This wave's share of the list when several compute waves share it
+    // (functors with kSharesLists): part in [0, parts).  0 / 1 otherwise.
+    uint32_t part;
+    uint32_t parts;
 
     __device__ __forceinline__ DeviceSGEntry get_entry(uint32_t idx) const {
         return sq->entries[(pool_offset + idx) % MAX_SG_POOL_ENTRIES];
@@ -57,8 +68,21 @@ struct SGListView {
 
 struct _SGSlot {
     uint32_t list_id, count, pool_offset, flags;
-    int seq;   // k + 1 once the k-th list of this slot is ready
-    int free;  // 1 while the slot may be (re)filled
+    int seq;         // k + 1 once the k-th list of this slot is ready
+    int free;        // 1 while the slot may be (re)filled
+    int parts_done;  // compute waves finished with the slot's current list
+};
+
+// At most this many compute waves share a list.
+constexpr int SG_MAX_COMPUTE = 3;
+
+template <typename F, typename = void>
+struct _shares_lists {
+    static constexpr bool value = false;
+};
+template <typename F>
+struct _shares_lists<F, decltype((void)F::kSharesLists)> {
+    static constexpr bool value = F::kSharesLists;
 };
 
 __device__ __forceinline__ uint64_t _idle_limit_ticks(const SGTaskQueue* sq) {
@@ -180,6 +204,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
     if (threadIdx.x < 2) {
         slots[threadIdx.x].seq = 0;
         slots[threadIdx.x].free = 1;
+        slots[threadIdx.x].parts_done = 0;
     }
     if (threadIdx.x == 0) {
         terminated = 0;
@@ -196,6 +221,14 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
     if (helpers > nwaves - 2) helpers = nwaves > 2 ? nwaves - 2 : 0;
     const int first_helper = nwaves - helpers;
     const int unroll = wave::transfer_unroll(gridDim.x * (1u + (unsigned)helpers));
+    // Compute waves 1 .. ncompute (never into the helpers).
+    int ncompute = 1;
+    if (_shares_lists<ComputeFn>::value) {
+        ncompute = (int)__hip_atomic_load(&cnt->compute_waves, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (ncompute > SG_MAX_COMPUTE) ncompute = SG_MAX_COMPUTE;
+        if (ncompute > first_helper - 1) ncompute = first_helper - 1;
+        if (ncompute < 1) ncompute = 1;
+    }
 
     if (w == 0) {
         // ---------------- transfer wave (leader)
@@ -292,9 +325,9 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             }
             want = seq + 1;
         }
-    } else if (w == 1) {
-        // ---------------- compute wave: bounded by the transfer wave's idle
-        // limit (plus 1 s), the longest the transfer wave can stay silent.
+    } else if (has_compute && w >= 1 && w <= ncompute) {
+        // ---------------- compute wave(s): bounded by the transfer wave's
+        // idle limit (plus 1 s), the longest the transfer wave can stay silent.
         const uint64_t limit = _idle_limit_ticks(sq) + 100000000ull;
         for (uint64_t k = 0;; k++) {
             const int s = (int)(k & 1);
@@ -325,8 +358,23 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             view.lane_id = lane;
             view.pool_offset = slots[s].pool_offset;
             view.sq = sq;
+            view.part = (uint32_t)(w - 1);
+            view.parts = (uint32_t)ncompute;
             compute_fn(view);
-            if (lane == 0) wave::lds_store(&slots[s].free, 1);
+            if (lane == 0) {
+                // The last part frees the slot.  Its reset of parts_done is
+                // ordered before the slot's next list by the release of free
+                // (the transfer wave acquires free before refilling the slot,
+                // and the compute waves acquire seq before their next add).
+                const int done = ncompute == 1 ? 1
+                                               : __hip_atomic_fetch_add(&slots[s].parts_done, 1, __ATOMIC_ACQ_REL,
+                                                                        __HIP_MEMORY_SCOPE_WORKGROUP) + 1;
+                if (done == ncompute) {
+                    if (ncompute > 1)
+                        __hip_atomic_store(&slots[s].parts_done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    wave::lds_store(&slots[s].free, 1);
+                }
+            }
         }
     }
     // further waves return to the caller

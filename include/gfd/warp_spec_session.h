@@ -211,7 +211,10 @@ public:
 
     // Internal: called by launch().  helper_waves < 0: the configured count;
     // kernels whose extra waves have other work (a GPU submitter) pass their own.
-    void before_launch(gfd_stream_t stream, int helper_waves = -1);
+    // compute_waves < 0: num_compute_warps (used only by functors that share
+    // lists between compute waves).
+    void before_launch(gfd_stream_t stream, int helper_waves = -1, int compute_waves = -1);
+    int compute_waves() const { return config_.num_compute_warps > 0 ? config_.num_compute_warps : 1; }
 
 private:
     struct Pending {

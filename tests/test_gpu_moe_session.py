@@ -3,7 +3,7 @@ workload of the reference's examples/09_sg_warp_spec.cu:78-294 run through
 the session API, include/gfd/sg_warp_spec.cuh): routing on the GPU, per-expert
 row lists built by GPU submitter waves and posted with the sg:: primitives,
 rows copied by the session's transfer waves, a bf16 RMSNorm on every landed
-list by the compute wave.  Rows byte-exact against the oracle, RMSNorm within
+list by the compute wave, or by up to three compute waves sharing each list.  Rows byte-exact against the oracle, RMSNorm within
 one bf16 ulp of the fp32 oracle, list / entry / byte counts exact."""
 import numpy as np
 import pytest
@@ -38,18 +38,23 @@ def run_session(m, sess, with_norm, rows_per_list, eps=1e-6):
     return sess.stats()
 
 
-@pytest.mark.parametrize("T,E,dim,rpl,blocks", [(4096, 64, 7168, 8, 0), (4096, 64, 7168, 64, 16),
-                                                (4096, 64, 7168, 2, 0), (64, 8, 512, 4, 2), (300, 5, 1024, 7, 0),
-                                                (1000, 16, 2048, 1, 8)])
-def test_moe_through_session(T, E, dim, rpl, blocks):
-    print("moe session T=%d E=%d dim=%d rows/list=%d blocks=%d" % (T, E, dim, rpl, blocks), flush=True)
+# cw: compute waves sharing each landed list (the RMSNorm consumer splits a
+# list's rows between them); 1 = the reference's single compute wave.
+@pytest.mark.parametrize("T,E,dim,rpl,blocks,cw", [(4096, 64, 7168, 8, 0, 1), (4096, 64, 7168, 64, 16, 1),
+                                                   (4096, 64, 7168, 2, 0, 1), (64, 8, 512, 4, 2, 1),
+                                                   (300, 5, 1024, 7, 0, 1), (1000, 16, 2048, 1, 8, 1),
+                                                   (4096, 64, 7168, 32, 0, 3), (4096, 64, 7168, 7, 4, 2),
+                                                   (300, 5, 1024, 1, 2, 3)])
+def test_moe_through_session(T, E, dim, rpl, blocks, cw):
+    print("moe session T=%d E=%d dim=%d rows/list=%d blocks=%d compute waves=%d" % (T, E, dim, rpl, blocks, cw),
+          flush=True)
     m = Moe(T, E, dim)
     m.route()
     assert (m.d_rows.download().view(np.int32) == m.row_token).all()
     n = 2 * T
     rows = m.expected_rows()
     ref = oracle.rmsnorm_rows(oracle.bf16_to_f32(rows), oracle.bf16_to_f32(m.weight), 1e-6)
-    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=blocks, idle_limit_ms=10000)
+    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=cw, num_blocks=blocks, idle_limit_ms=10000)
     try:
         for with_norm in (False, True, True):  # two overlapped launches: the session's state carries over
             st = run_session(m, sess, with_norm, rpl)
