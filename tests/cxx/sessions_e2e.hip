@@ -9,7 +9,11 @@
 // Known answers as in the reference: the SG list lands floats i + 1 (every
 // one compared); the double-buffered tiles give per-token sums (t + 1) * dim
 // for tile counts 1, 2, 3, 4, 5 and 7 (test_db_small_tiles' cases).  The
-// functors stride over 64-lane waves.  Prints PASSED and exits 0 on success.
+// functors stride over 64-lane waves.  Added: eight lists on a session with
+// three compute waves, where a functor declaring kSharesLists has each list
+// split between the three and one without it sees each list once; every
+// entry must be marked exactly once either way.  Prints PASSED and exits 0 on
+// success.
 #include <gfd/gfd.h>
 #include <gfd/sg_warp_spec.cuh>
 #include <gfd/warp_spec.cuh>
@@ -17,6 +21,7 @@
 
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <vector>
 
 #define HIP_OK(call)                                                                  \
@@ -107,6 +112,90 @@ static bool sg_e2e() {
     return ok && errors == 0;
 }
 
+// Marks every entry it is given (by tag) once.  With kSharesLists the
+// session's compute waves share each list: wave `part` takes entries part,
+// part + parts, ...
+struct SharedTouch {
+    static constexpr bool kSharesLists = true;
+    unsigned int* touched;
+    unsigned int* parts_seen;
+    __device__ void operator()(gfd::sg_warp_spec::SGListView list) {
+        if (list.lane_id == 0) atomicMax(parts_seen, list.parts);
+        for (uint32_t i = list.part + (uint32_t)list.lane_id * list.parts; i < list.count; i += 64u * list.parts)
+            atomicAdd(&touched[list.get_entry(i).tag], 1u);
+    }
+};
+GFD_SG_WARP_SPEC_KERNEL(sg_shared_kernel, SharedTouch);
+
+// The same marking without kSharesLists: one compute wave per list, however
+// many the session has.
+struct SoloTouch {
+    unsigned int* touched;
+    unsigned int* parts_seen;
+    __device__ void operator()(gfd::sg_warp_spec::SGListView list) {
+        if (list.lane_id == 0) atomicMax(parts_seen, list.parts);
+        for (uint32_t i = (uint32_t)list.lane_id; i < list.count; i += 64u)
+            atomicAdd(&touched[list.get_entry(i).tag], 1u);
+    }
+};
+GFD_SG_WARP_SPEC_KERNEL(sg_solo_kernel, SoloTouch);
+
+// 8 lists of 100 entries, 3 compute waves per workgroup: every entry must be
+// marked exactly once, by 3 sharing waves or by wave 1 alone.
+template <typename Functor, typename Kernel>
+static bool sg_compute_waves(Kernel kernel, unsigned int want_parts, const char* name) {
+    constexpr int LISTS = 8, PER = 100, N = LISTS * PER;
+    constexpr size_t TOKEN = 1024;
+    char* cpu_data = nullptr;
+    HIP_OK(hipHostMalloc((void**)&cpu_data, (size_t)N * TOKEN, hipHostMallocDefault));
+    for (size_t i = 0; i < (size_t)N * TOKEN; i++) cpu_data[i] = (char)(i * 7 + 3);
+    char* gpu_data = nullptr;
+    unsigned int *touched = nullptr, *parts_seen = nullptr;
+    HIP_OK(hipMalloc((void**)&gpu_data, (size_t)N * TOKEN));
+    HIP_OK(hipMalloc((void**)&touched, N * sizeof(unsigned int)));
+    HIP_OK(hipMalloc((void**)&parts_seen, sizeof(unsigned int)));
+    HIP_OK(hipMemset(touched, 0, N * sizeof(unsigned int)));
+    HIP_OK(hipMemset(parts_seen, 0, sizeof(unsigned int)));
+    HIP_OK(hipDeviceSynchronize());
+    gfd::SGWarpSpecConfig config;
+    config.num_compute_warps = 3;
+    config.num_blocks = 4;
+    config.idle_limit_ms = 10000;
+    bool ok = true;
+    {
+        gfd::SGWarpSpecSession session(config);
+        std::vector<gfd::DeviceSGEntry> e(PER);
+        for (int l = 0; l < LISTS; l++) {
+            for (int i = 0; i < PER; i++) {
+                const int k = l * PER + i;
+                e[i].src_addr = (uint64_t)(uintptr_t)cpu_data + (uint64_t)k * TOKEN;
+                e[i].dst_addr = (uint64_t)(uintptr_t)gpu_data + (uint64_t)k * TOKEN;
+                e[i].size = TOKEN;
+                e[i].tag = (uint32_t)k;
+            }
+            if (session.submit_sg_list(e.data(), PER, (uint32_t)l, gfd::SG_FLAG_HOST_SUBMITTED) == ~0ull) ok = false;
+        }
+        session.launch(kernel, Functor{touched, parts_seen});
+        if (!session.synchronize()) ok = false;
+    }
+    std::vector<unsigned int> h(N);
+    std::vector<char> landed((size_t)N * TOKEN);
+    unsigned int h_parts = 0;
+    HIP_OK(hipMemcpy(h.data(), touched, N * sizeof(unsigned int), hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(&h_parts, parts_seen, sizeof(h_parts), hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(landed.data(), gpu_data, landed.size(), hipMemcpyDeviceToHost));
+    int wrong = 0;
+    for (int k = 0; k < N; k++) wrong += h[k] != 1;
+    const bool bytes_ok = std::memcmp(landed.data(), cpu_data, landed.size()) == 0;
+    std::printf("  %s: %d of %d entries not marked exactly once, parts %u (want %u), data %s\n", name, wrong, N,
+                h_parts, want_parts, bytes_ok ? "ok" : "MISMATCH");
+    HIP_OK(hipFree(parts_seen));
+    HIP_OK(hipFree(touched));
+    HIP_OK(hipFree(gpu_data));
+    HIP_OK(hipHostFree(cpu_data));
+    return ok && wrong == 0 && h_parts == want_parts && bytes_ok;
+}
+
 static bool db_tiles(int total_tokens, int tokens_per_tile, int tokens_per_chunk, int token_dim, int num_cus) {
     const int num_tiles = total_tokens / tokens_per_tile;
     const size_t token_size = (size_t)token_dim * sizeof(float);
@@ -157,6 +246,8 @@ int main() {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess) return 1;
     bool ok = sg_e2e();
+    ok = sg_compute_waves<SharedTouch>(sg_shared_kernel, 3, "3 compute waves sharing each list") && ok;
+    ok = sg_compute_waves<SoloTouch>(sg_solo_kernel, 1, "3 compute waves, functor without kSharesLists") && ok;
     for (int tiles : {1, 2, 3, 4, 5, 7}) ok = db_tiles(tiles * 64, 64, 16, 128, cus) && ok;
     std::printf("  Verify:    %s\n", ok ? "PASSED" : "FAILED");
     return ok ? 0 : 1;
