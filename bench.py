@@ -157,6 +157,8 @@ def cpu_baseline(oracle, seconds, info):
         pool.close()
         os.sched_setaffinity(0, allowed)
     us, us_warm = p50(cold), p50(warm)
+    product = product_gather([b.ptr for b in srcs], perm, n, t, staging, cpus, workers,
+                             lambda k: oracle.expected_gather(srcs[k].array, perm, t, 2 * t))
     out = {
         "value": round(gbps(n * t, us), 3), "unit": "GB/s", "cores": workers + 1, "kind": "port",
         "sample": "8192 x 4KiB ParallelGather into pinned staging, cold source: rotating over %d regions of "
@@ -166,6 +168,7 @@ def cpu_baseline(oracle, seconds, info):
         "warm_sample": "the same gather repeated on one 64 MiB region (source in CPU caches): %d gathers, "
                        "P50 %.1f us" % (len(warm), us_warm),
     }
+    out["product_gather"] = product
     for b in srcs:
         b.free()
     # The CPU-only layout: 256 x 4 KiB from a 2 MiB source into 1 MiB of
@@ -196,9 +199,33 @@ def cpu_baseline(oracle, seconds, info):
         c1["W%d" % w] = {"us_p50": round(p50(tt), 2), "GBps": round(gbps(n1 * t, p50(tt)), 3),
                          "threads": w + 1, "cpus": len(set(wcpus)),
                          "oversubscribed": w + 1 > len(allowed), "iterations": len(tt)}
+        # The product's gather engine on the same list and threads.
+        pg = product_gather([src1.ptr], perm1, n1, t, stg1, wcpus, w, lambda k: expect1, iters=2000)
+        c1["W%d" % w]["product_gather"] = {"us_p50": pg["us_p50"], "GBps": pg["GBps"]}
     out["c1_256x4KB"] = c1
     log("  cpu baseline 256 x 4KiB: %s" % c1)
     return out
+
+
+def product_gather(region_ptrs, perm, n, t, staging, cpus, workers, expected, iters=3000):
+    """The product's gather engine (gfd_bench_host_gather: the Direct path's
+    staging step without the copies) on the layout of cpu_baseline: tokens at
+    2x stride in each region, the same order, W workers pinned to cpus[1..]
+    and the caller on cpus[0]; gather k reads region k % len(region_ptrs)."""
+    lists = [gfd_amd.make_entries(np.uint64(r) + perm.astype(np.uint64) * np.uint64(2 * t), 0, t)
+             for r in region_ptrs]
+    ptrs = (ctypes.c_void_p * len(lists))(*[ctypes.cast(l, ctypes.c_void_p) for l in lists])
+    cpu_ids = (ctypes.c_int * (workers + 1))(*cpus[:workers + 1])
+    tt = np.zeros(iters)
+    rc = gfd_amd.lib().gfd_bench_host_gather(ptrs, len(lists), n, staging.ptr, 2 << 20, workers, cpu_ids,
+                                             len(lists) * 2, iters, tt.ctypes.data_as(PD))
+    assert rc == 0, gfd_amd.lib().gfd_last_error()
+    # The last gather read region (warmup + iters - 1) % len(regions).
+    last = (len(lists) * 2 + iters - 1) % len(lists)
+    if not (staging.array == expected(last)).all():
+        raise SystemExit("PARITY FAILURE: product host gather (region %d)" % last)
+    return {"us_p50": round(p50(tt), 2), "GBps": round(gbps(n * t, p50(tt)), 3), "workers": workers,
+            "cpus": list(cpus[:workers + 1]), "gathers": iters, "regions": len(lists)}
 
 
 def bench_peak(nbytes, iters, warmup):

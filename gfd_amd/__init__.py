@@ -173,6 +173,7 @@ def _declare(L):
         "gfd_bench_memcpy_contiguous": ([vp, vp, c_sz, c_int, c_int, c_int, pd], c_int),
         "gfd_bench_sdma_contiguous": ([vp, vp, c_sz, c_int, c_int, c_int, c_int, pd, ctypes.POINTER(c_u32)], c_int),
         "gfd_bench_submit_direct": ([vp, vp, c_int, c_int, c_int, pd], c_int),
+        "gfd_bench_host_gather": ([vp, c_int, c_int, vp, c_u64, c_int, vp, c_int, c_int, pd], c_int),
         "gfd_bench_zero_copy_tokens": ([vp, vp, c_u32, c_int, c_int, c_int, pd, pd], c_int),
         "gfd_zero_copy_scatter_tokens": ([vp, vp, c_u32, c_int, vp], c_int),
         "gfd_plan_expert_entries": ([vp, c_int, c_int, vp, c_u64, vp, c_u32, vp, vp, vp], c_int),

@@ -3,6 +3,9 @@
 // the measurement loops of the gfd_bench_* helpers.
 #include "gfd_capi.h"
 
+#include <pthread.h>
+#include <sched.h>
+
 #include <algorithm>
 #include <chrono>
 #include <cstring>
@@ -274,6 +277,9 @@ void record_chunk(void* p, int chunk, size_t, size_t) {
     if (c->order && c->n < c->cap) c->order[c->n] = chunk;
     c->n++;
 }
+
+void no_chunk_report(void*, int, size_t, size_t) {}
+
 }  // namespace
 
 int gfd_host_gather(const gfd_sg_entry* entries, int count, void* out, uint64_t chunk_bytes,
@@ -298,6 +304,49 @@ int gfd_host_gather(const gfd_sg_entry* entries, int count, void* out, uint64_t 
     OrderCtx ctx{chunk_order, chunk_order ? chunk_order_cap : 0, 0};
     engine.run(e, count, total, (char*)out, chunk_bytes, record_chunk, &ctx);
     return ctx.n;
+}
+
+int gfd_bench_host_gather(const gfd_sg_entry* const* lists, int nlists, int count, void* out,
+                          uint64_t chunk_bytes, int num_workers, const int* cpus, int warmup, int iters,
+                          double* times_us) {
+    if (!lists || nlists <= 0 || count <= 0 || !out || num_workers < 0 || num_workers > 64 || !cpus ||
+        warmup < 0 || iters <= 0 || !times_us) {
+        g_last_error = "gfd_bench_host_gather: invalid argument";
+        return -1;
+    }
+    for (int i = 0; i < nlists; i++)
+        if (!lists[i]) {
+            g_last_error = "gfd_bench_host_gather: null list";
+            return -1;
+        }
+    std::vector<gfd::GatherEngine::ListScan> scans;
+    std::vector<int> worker_cpus(cpus + 1, cpus + 1 + num_workers);
+    gfd::GatherEngine engine(worker_cpus);
+    for (int i = 0; i < nlists; i++) {
+        scans.push_back(engine.scan(reinterpret_cast<const gfd::SGEntry*>(lists[i]), count));
+        if (!scans.back().dst_contig) {
+            g_last_error = "gfd_bench_host_gather: destinations are not contiguous";
+            return -1;
+        }
+    }
+    cpu_set_t saved;
+    const bool have_saved = pthread_getaffinity_np(pthread_self(), sizeof(saved), &saved) == 0;
+    if (cpus[0] >= 0) {
+        cpu_set_t one;
+        CPU_ZERO(&one);
+        CPU_SET(cpus[0], &one);
+        pthread_setaffinity_np(pthread_self(), sizeof(one), &one);
+    }
+    for (int it = -warmup; it < iters; it++) {
+        const int k = (it + warmup) % nlists;
+        const auto t0 = std::chrono::steady_clock::now();
+        engine.run(reinterpret_cast<const gfd::SGEntry*>(lists[k]), count, scans[(size_t)k].total, (char*)out,
+                   chunk_bytes, no_chunk_report, nullptr);
+        const auto t1 = std::chrono::steady_clock::now();
+        if (it >= 0) times_us[it] = std::chrono::duration<double, std::micro>(t1 - t0).count();
+    }
+    if (have_saved) pthread_setaffinity_np(pthread_self(), sizeof(saved), &saved);
+    return 0;
 }
 
 int gfd_staging_pool_init(int num_gpus, size_t buf_size, int numa_node) {

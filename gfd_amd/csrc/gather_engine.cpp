@@ -108,61 +108,80 @@ inline uint64_t mono_ns() {
 
 GatherEngine::GatherEngine(const std::vector<int>& worker_cpus) {
     if (const char* v = std::getenv("GFD_GATHER_PREFETCH_BYTES")) prefetch_bytes_ = std::strtoull(v, nullptr, 0);
+    mail_.reset(new Mailbox[worker_cpus.empty() ? 1 : worker_cpus.size()]);
     for (size_t w = 0; w < worker_cpus.size(); w++)
         threads_.emplace_back(&GatherEngine::worker_main, this, (int)w, worker_cpus[w]);
 }
 
 GatherEngine::~GatherEngine() {
     running_.store(false, std::memory_order_seq_cst);
-    epoch_.fetch_add(1, std::memory_order_seq_cst);
+    const uint32_t e = epoch_.fetch_add(1, std::memory_order_seq_cst) + 1;
+    for (size_t w = 0; w < threads_.size(); w++) mail_[w].go.store(e, std::memory_order_seq_cst);
     futex_wake_all(&epoch_);
     for (auto& t : threads_)
         if (t.joinable()) t.join();
 }
 
-// Job hand-off.  run() builds the job, sets open_, bumps epoch_ and wakes
-// sleepers; when every chunk is complete it clears open_ and returns without
-// waiting for the workers.  A worker joins a job by raising active_ and then
-// checking open_; run() rebuilds job state only after active_ has dropped to
-// zero.  With sequentially consistent operations on both counters, a worker
-// either is counted before run() looks (and run() waits for it) or sees open_
-// cleared and leaves without touching the job.
+// Job hand-off.  The caller builds the job, sets open_, takes the next job
+// number, writes it to every worker's mailbox and wakes sleepers; when every
+// chunk is complete it clears open_ and returns without waiting for the
+// workers.  A worker that sees a new number in its mailbox raises its in_job
+// flag and then checks open_; the caller rebuilds job state only after every
+// in_job flag is down.  With sequentially consistent operations on open_ and
+// the flags, a worker either is seen inside (and the caller waits for it) or
+// sees open_ cleared and leaves without touching the job.
+void GatherEngine::publish() {
+    open_.store(true, std::memory_order_seq_cst);
+    const uint32_t e = epoch_.fetch_add(1, std::memory_order_seq_cst) + 1;
+    for (size_t w = 0; w < threads_.size(); w++) mail_[w].go.store(e, std::memory_order_release);
+}
+
+void GatherEngine::wait_workers_out() {
+    for (size_t w = 0; w < threads_.size(); w++)
+        while (mail_[w].in_job.load(std::memory_order_seq_cst) != 0) cpu_relax();
+}
+
 void GatherEngine::worker_main(int w, int cpu) {
-    (void)w;
     if (cpu >= 0) {
         cpu_set_t cs;
         CPU_ZERO(&cs);
         CPU_SET(cpu, &cs);
         pthread_setaffinity_np(pthread_self(), sizeof(cs), &cs);
     }
+    Mailbox& mb = mail_[w];
     const uint64_t spin_ns = spin_limit_ns();
-    uint32_t seen = epoch_.load(std::memory_order_acquire);
+    // Workers start before any job (the constructor creates them with every
+    // mailbox at 0), so a job published before this thread first runs still
+    // counts as new.
+    uint32_t seen = 0;
     for (;;) {
         if (!running_.load(std::memory_order_acquire)) break;
-        const uint32_t e = epoch_.load(std::memory_order_acquire);
-        if (e != seen) {
-            seen = e;
-            active_.fetch_add(1, std::memory_order_seq_cst);
-            if (open_.load(std::memory_order_seq_cst)) do_job();
-            active_.fetch_sub(1, std::memory_order_seq_cst);
+        const uint32_t g = mb.go.load(std::memory_order_acquire);
+        if (g != seen) {
+            seen = g;
+            mb.in_job.store(1, std::memory_order_seq_cst);
+            if (open_.load(std::memory_order_seq_cst) && running_.load(std::memory_order_relaxed)) do_job();
+            mb.in_job.store(0, std::memory_order_seq_cst);
             continue;
         }
         bool moved = false;
         const uint64_t t_end = mono_ns() + spin_ns;
         for (unsigned i = 1;; i++) {
             cpu_relax();
-            if (epoch_.load(std::memory_order_relaxed) != seen) {
+            if (mb.go.load(std::memory_order_relaxed) != seen) {
                 moved = true;
                 break;
             }
             if ((i & 255) == 0 && mono_ns() >= t_end) break;
         }
         if (moved) continue;
-        // Dekker handshake with run(): either run() sees sleepers_ > 0 and
-        // wakes us, or we see the new epoch here and do not sleep.
+        // Dekker handshake with publish(): either the caller sees sleepers_ > 0
+        // and wakes us after bumping epoch_, or we see the new job here and
+        // do not sleep.  futex_wait returns at once if epoch_ has moved on.
         sleepers_.fetch_add(1, std::memory_order_seq_cst);
-        if (epoch_.load(std::memory_order_seq_cst) == seen && running_.load(std::memory_order_seq_cst))
-            futex_wait(&epoch_, seen);
+        const uint32_t e = epoch_.load(std::memory_order_seq_cst);
+        if (mb.go.load(std::memory_order_seq_cst) == seen && running_.load(std::memory_order_seq_cst))
+            futex_wait(&epoch_, e);
         sleepers_.fetch_sub(1, std::memory_order_seq_cst);
     }
 }
@@ -276,7 +295,7 @@ GatherEngine::ListScan GatherEngine::scan(const SGEntry* entries, int count) {
         }
         return r;
     }
-    while (active_.load(std::memory_order_seq_cst) != 0) cpu_relax();
+    wait_workers_out();
     entries_ = entries;
     count_ = count;
     scan_parts_ = (count + kScanPartEntries - 1) / kScanPartEntries;
@@ -284,8 +303,7 @@ GatherEngine::ListScan GatherEngine::scan(const SGEntry* entries, int count) {
     scan_left_.store(scan_parts_, std::memory_order_relaxed);
     next_slice_.store(0, std::memory_order_relaxed);
     scan_job_ = true;
-    open_.store(true, std::memory_order_seq_cst);
-    epoch_.fetch_add(1, std::memory_order_seq_cst);
+    publish();
     if (sleepers_.load(std::memory_order_seq_cst) > 0 && mono_ns() - last_prewake_ns_.load(std::memory_order_relaxed) > 200000ull)
         futex_wake_all(&epoch_);
     do_scan_parts();
@@ -298,7 +316,7 @@ GatherEngine::ListScan GatherEngine::scan(const SGEntry* entries, int count) {
         r.src_contig &= o.src_contig;
         r.uniform &= o.uniform;
     }
-    // The next run() waits for active_ to drop before reusing job state.
+    // The next run() waits for the workers to leave before reusing job state.
     return r;
 }
 
@@ -351,7 +369,7 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     times_.entry = mono_ns();
     if (chunk_bytes == 0 || chunk_bytes > total) chunk_bytes = total;
     // Workers still inside the previous job must leave before its state changes.
-    while (active_.load(std::memory_order_seq_cst) != 0) cpu_relax();
+    wait_workers_out();
     times_.idle = mono_ns();
     first_slice_ns_.store(0, std::memory_order_relaxed);
     copiers_.store(0, std::memory_order_relaxed);
@@ -364,6 +382,7 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     size_t first = first_chunk_bytes_ ? first_chunk_bytes_ : chunk_bytes / 8;
     if (first < 64 * 1024) first = 64 * 1024;
     if (first > chunk_bytes) first = chunk_bytes;
+
     chunk_end_.clear();
     size_t size = first;
     for (size_t end = first;;) {
@@ -455,11 +474,11 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     next_slice_.store(0, std::memory_order_relaxed);
     scan_job_ = false;
 
+    // The caller copies slices too: workers are helpers (one that is asleep
+    // or late sits the job out), so the caller alone can always finish it.
     const int nw = num_workers();
-    const bool caller_copy = caller_copies_ != 0 || nw == 0;
     times_.built = mono_ns();
-    open_.store(true, std::memory_order_seq_cst);
-    epoch_.fetch_add(1, std::memory_order_seq_cst);
+    publish();
     times_.sleepers = sleepers_.load(std::memory_order_seq_cst);
     // Workers are helpers: the caller can finish the job alone.  If they were
     // woken just before (prewake), do not pay for a second wake syscall here;
@@ -482,7 +501,7 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
         // the hand-off of this one by that long.  With no such slice left it
         // spins until the workers finish the chunk.
         const int peek = next_slice_.load(std::memory_order_relaxed);
-        if (caller_copy && (nw == 0 || (peek < ns && chunk_of(peek) <= ready))) {
+        if (nw == 0 || (peek < ns && chunk_of(peek) <= ready)) {
             const int s = next_slice_.fetch_add(1, std::memory_order_relaxed);
             if (s < ns) {
                 const Slice sl = slice_at(s);

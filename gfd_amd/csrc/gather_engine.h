@@ -38,10 +38,6 @@ public:
     int num_workers() const { return (int)threads_.size(); }
     void set_slice_bytes(size_t b) { slice_bytes_ = b < 4096 ? 4096 : b; }
     size_t slice_bytes() const { return slice_bytes_; }
-    // Whether the calling thread copies slices too (default yes: between
-    // chunk hand-offs it claims slices like a worker, so a gather never waits
-    // on a worker that is still waking up).
-    void set_caller_copies(bool on) { caller_copies_ = on; }
     // Size of the first chunk (0 = chunk_bytes / 8, at least 64 KiB): a short
     // first chunk starts the first copy early.
     void set_first_chunk_bytes(size_t b) { first_chunk_bytes_ = b; }
@@ -105,11 +101,22 @@ private:
     Slice slice_at(int s) const;
     int chunk_of(int s) const;
 
+    void publish();
+    void wait_workers_out();
+
     std::vector<std::thread> threads_;
+    // Per worker, on a cache line of its own: the job number the caller asks
+    // it to join, and whether it is inside a job.  Each line has two users
+    // (the caller and that worker), so publishing a job and joining it cost
+    // one line transfer per worker, not a queue of them on one shared line.
+    struct alignas(64) Mailbox {
+        std::atomic<uint32_t> go{0};
+        std::atomic<uint32_t> in_job{0};
+    };
+    std::unique_ptr<Mailbox[]> mail_;
     // Job counter; 32-bit so idle workers can sleep on it with a futex.
     alignas(64) std::atomic<uint32_t> epoch_{0};
     alignas(64) std::atomic<int> sleepers_{0};
-    alignas(64) std::atomic<int> active_{0};   // workers inside a job
     alignas(64) std::atomic<bool> open_{false};  // job state valid to read
     alignas(64) std::atomic<bool> running_{true};
     alignas(64) std::atomic<int> next_slice_{0};
@@ -155,7 +162,6 @@ private:
     size_t slice_bytes_ = 128 * 1024;
     size_t first_chunk_bytes_ = 0;
     bool ramp_ = true;
-    bool caller_copies_ = true;
 };
 
 }  // namespace gfd

@@ -293,6 +293,17 @@ int gfd_bench_sdma_contiguous(void* dst, const void* src, size_t bytes, int chan
                               int warmup, int iters, double* times_us, uint32_t* engine_mask);
 int gfd_bench_submit_direct(gfd_poller_t p, const gfd_sg_entry* entries, int count, int warmup,
                             int iters, double* times_us);
+/* The product's host gather alone (the staging step of the Direct path,
+ * reference counterpart CpuPollingThread::parallel_gather,
+ * src/parallel_gather.cpp:74): one GatherEngine with num_workers threads
+ * pinned to cpus[1..num_workers] and the caller pinned to cpus[0] for the
+ * call (num_workers + 1 CPU ids), timing `iters` gathers after `warmup`;
+ * gather k reads lists[k % nlists] (each `count` entries with contiguous
+ * destinations, landing at out + (dst - lists[i][0].dst)), so several lists
+ * over separate source regions give a cold source. */
+int gfd_bench_host_gather(const gfd_sg_entry* const* lists, int nlists, int count, void* out,
+                          uint64_t chunk_bytes, int num_workers, const int* cpus, int warmup, int iters,
+                          double* times_us);
 /* Zero-copy tokens kernel with its completion signalled to a host word:
  * wall time from the launch call until the host sees the word. */
 int gfd_bench_zero_copy_tokens_signal(const uint64_t* src_addrs, void* dst, uint32_t token_size,

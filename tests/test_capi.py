@@ -71,6 +71,36 @@ def test_host_gather_matches_oracle(workers, n, t, chunk, slice_):
     assert order.tolist() == list(range(len(order)))  # chunks reported in order
 
 
+def test_bench_host_gather_rotates_over_regions():
+    """gfd_bench_host_gather (the product gather timed beside the reference
+    restatement): gather k reads list k % nlists; after warmup + iters
+    gathers the output holds the last list's tokens, byte-exact, and every
+    time is positive."""
+    import ctypes
+    n, t = 256, 4096
+    regions = []
+    lists = []
+    for seed in (1, 2, 3):
+        region, perm, stride = _layout(n, t)
+        region[:] = np.random.default_rng(seed).integers(0, 256, region.size, dtype=np.uint8)
+        regions.append((region, perm, stride))
+        lists.append(gfd_amd.make_entries(region.ctypes.data + perm.astype(np.uint64) * np.uint64(stride), 0, t))
+    ptrs = (ctypes.c_void_p * 3)(*[ctypes.cast(l, ctypes.c_void_p) for l in lists])
+    cpus = (ctypes.c_int * 4)(-1, -1, -1, -1)
+    out = np.zeros(n * t, np.uint8)
+    times = np.zeros(10)
+    warmup, iters = 3, 10
+    rc = gfd_amd.lib().gfd_bench_host_gather(ptrs, 3, n, out.ctypes.data, 1 << 20, 3, cpus, warmup, iters,
+                                             times.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    assert rc == 0, gfd_amd.lib().gfd_last_error()
+    region, perm, stride = regions[(warmup + iters - 1) % 3]
+    assert (out == oracle.expected_gather(region, perm, t, stride)).all()
+    assert (times > 0).all()
+    bad = gfd_amd.lib().gfd_bench_host_gather(ptrs, 0, n, out.ctypes.data, 1 << 20, 3, cpus, warmup, iters,
+                                              times.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    assert bad == -1
+
+
 def _ramp_chunks(total, chunk):
     """Chunk count of the gather engine's ramp: a first chunk of chunk/8
     (at least 64 KiB, at most chunk), then doubling up to chunk."""
