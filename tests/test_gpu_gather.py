@@ -199,11 +199,12 @@ def test_submit_direct_parity(direct_poller, n, t, chunk, route):
         direct_poller.set_direct_zero_copy_max_bytes(8 << 20)
 
 
-@pytest.mark.parametrize("n,t", [(2048, 512), (300, 1000)])
+@pytest.mark.parametrize("n,t", [(2048, 512), (300, 1000), (2048, 8192), (4096, 3000)])
 def test_submit_direct_small_list_from_pageable_sources(direct_poller, n, t):
     """Sources in pageable (not pinned) memory cannot be read by the GPU: a
     small list must take the staged route (gather into pinned staging, then
-    SDMA) and still land byte-exact."""
+    SDMA), and a list above the kernel route's limit (16 MiB, 11.7 MiB ragged
+    in size) must get no zero-copy head; either way every byte lands."""
     log("submit_direct pageable sources n=%d t=%d" % (n, t))
     region = np.empty(n * 2 * t, np.uint8)
     oracle.fill_tokens(region, n, t, 2 * t)
@@ -217,6 +218,33 @@ def test_submit_direct_small_list_from_pageable_sources(direct_poller, n, t):
         assert (got[:n * t] == oracle.expected_gather(region, perm, t, 2 * t)).all()
         assert (got[n * t:] == SENTINEL).all()
         dst.fill(SENTINEL)
+
+
+def test_submit_direct_head_from_pinned_rest_pageable(direct_poller):
+    """A 32 MiB list whose first 1024 tokens are in pinned memory and the
+    rest in pageable memory: the zero-copy head takes pinned entries only
+    (its check covers the head alone), the gather stages the rest, and every
+    byte lands; then the same list with the pinned part moved to the end, so
+    the head's sources are pageable and it is refused."""
+    n, t, split = 8192, 4096, 1024
+    log("submit_direct pinned head + pageable rest n=%d t=%d" % (n, t))
+    pinned = gfd_amd.HostBuffer(split * 2 * t)
+    pageable = np.empty((n - split) * 2 * t, np.uint8)
+    oracle.fill_tokens(pinned.array, split, t, 2 * t)
+    oracle.fill_tokens(pageable, n - split, t, 2 * t, seed=0x1234567)
+    want = np.concatenate([pinned.array.reshape(split, 2 * t)[:, :t].reshape(-1),
+                           pageable.reshape(n - split, 2 * t)[:, :t].reshape(-1)])
+    src = np.concatenate([np.uint64(pinned.ptr) + np.arange(split, dtype=np.uint64) * np.uint64(2 * t),
+                          np.uint64(pageable.ctypes.data) + np.arange(n - split, dtype=np.uint64) * np.uint64(2 * t)])
+    dst = gfd_amd.DeviceBuffer(n * t + TAIL)
+    for order in ("pinned first", "pinned last"):
+        idx = np.arange(n) if order == "pinned first" else np.roll(np.arange(n), -split)
+        entries = gfd_amd.make_entries(src[idx], dst.ptr, t)
+        dst.fill(SENTINEL)
+        assert direct_poller.submit_direct(entries, n) > 0
+        got = dst.download()
+        assert (got[:n * t].reshape(n, t) == want.reshape(n, t)[idx]).all(), order
+        assert (got[n * t:] == SENTINEL).all()
 
 
 def test_submit_direct_copy_timeline(direct_poller):
