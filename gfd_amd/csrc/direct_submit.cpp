@@ -128,7 +128,10 @@ bool CpuPollingThread::zc_warm_up() {
 // GFD_DIRECT_TIMEOUT_MS (10 s) the stream is synchronised to surface the
 // error and -1 (or the stream's error) is returned.
 int CpuPollingThread::zc_wait(uint64_t gen) {
-    static const uint64_t limit_us = (uint64_t)std::max(1ll, std::atoll(std::getenv("GFD_DIRECT_TIMEOUT_MS") ? std::getenv("GFD_DIRECT_TIMEOUT_MS") : "10000")) * 1000ull;
+    static const uint64_t limit_us = [] {
+        const char* v = std::getenv("GFD_DIRECT_TIMEOUT_MS");
+        return (uint64_t)std::max(1ll, v && *v ? std::atoll(v) : 10000ll) * 1000ull;
+    }();
     const auto t0 = std::chrono::steady_clock::now();
     for (unsigned i = 1;; i++) {
         if (__atomic_load_n(zc_done_, __ATOMIC_ACQUIRE) == gen) return 0;
@@ -341,8 +344,9 @@ bool CpuPollingThread::init_direct_ce() {
         direct_staging_size_ = total_cpu_size_;
     }
     if (direct_zc_max_bytes_ > 0 && !zc_warm_up()) {
-        GFD_LOG_ERROR("zero-copy route set-up failed\n");
-        return false;
+        // The staged route (gather + copy engines) still serves every list.
+        GFD_LOG_ERROR("zero-copy route set-up failed; submit_direct uses the copy engines only\n");
+        direct_zc_max_bytes_ = 0;
     }
     return start_workers();
 }
