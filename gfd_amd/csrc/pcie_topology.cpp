@@ -155,17 +155,22 @@ void TopologyConfig::get_exclusive_cores(int gpu_id, int& out_base_cpu, int& out
     }
     const int per = (int)g.node_cores.size() / sharing;
     if (per <= 0) return;
-    // The share is a run of the node's physical cores in ascending order.
-    // stride is their spacing when they are evenly spaced (1 on a node whose
-    // cores are numbered consecutively), else 1.
+    // The share is a run of `per` of the node's physical cores in ascending
+    // order, reported as base, base + stride, ..., base + (num - 1) * stride:
+    // stride is the spacing of the share's first two cores (1 on a node whose
+    // cores are numbered consecutively).  Where the numbering inside the share
+    // is not evenly spaced, num stops at the first core off that progression,
+    // so the triple never names a CPU outside the share.
     const size_t first = (size_t)(idx * per);
     out_base_cpu = g.node_cores[first];
-    out_num_cores = per;
+    out_num_cores = 1;
     if (per > 1) {
         const int step = g.node_cores[first + 1] - g.node_cores[first];
-        bool even = step > 0;
-        for (int k = 1; k < per && even; k++) even = g.node_cores[first + (size_t)k] - g.node_cores[first + (size_t)k - 1] == step;
-        out_stride = even ? step : 1;
+        if (step <= 0) return;
+        while (out_num_cores < per &&
+               g.node_cores[first + (size_t)out_num_cores] == out_base_cpu + out_num_cores * step)
+            out_num_cores++;
+        out_stride = step;
     }
 }
 

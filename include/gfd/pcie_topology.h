@@ -48,7 +48,11 @@ struct TopologyConfig {
 
     // This GPU's share of its node's physical cores: the node's cores split
     // evenly between the GPUs on that node, in GPU order (the reference's
-    // partition rule, pcie_topology.h:41-60).  stride is 1.
+    // partition rule, pcie_topology.h:41-60), as CPUs base, base + stride,
+    // ..., base + (num - 1) * stride.  stride is 1 on nodes numbered
+    // consecutively (the reference's only case); a share whose numbering has
+    // a gap is cut at the gap.  num is 0 for an unknown gpu_id or a node with
+    // fewer cores than GPUs.
     void get_exclusive_cores(int gpu_id, int& out_base_cpu, int& out_num_cores, int& out_stride) const;
 };
 

@@ -69,3 +69,27 @@ def test_reference_style_callers_build(tmp_path):
                         text=True, timeout=60).stdout
     for sym in ("CpuPollingThread", "submit_direct", "StagingPool", "discover_topology"):
         assert sym in nm, sym
+
+
+def test_exclusive_core_partition_on_synthetic_topologies(tmp_path):
+    """TopologyConfig::get_exclusive_cores on hand-built multi-GPU, multi-NUMA
+    topologies (tests/cxx/topology_partition.cpp): the reference's values on
+    consecutively numbered nodes (its include/gfd/pcie_topology.h:41-60),
+    disjoint equal shares of each node's own cores on every layout, and the
+    edge cases.  Host code only: it runs without a GPU."""
+    lib = os.path.join(ROOT, "gfd_amd", "libgfd_amd.so")
+    if not os.path.isfile(lib):
+        pytest.skip("libgfd_amd.so not built")
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    exe = tmp_path / "topology_partition"
+    r = subprocess.run(["make", "-s", "-B", "-C", os.path.join(ROOT, "tests", "cxx"), "OUT=%s" % tmp_path, str(exe)],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    # Built outside tests/cxx/_build, so the program's relative rpath does not
+    # reach gfd_amd/: name the library's folder instead.
+    env = dict(os.environ)
+    env["LD_LIBRARY_PATH"] = os.pathsep.join(p for p in (os.path.dirname(lib), env.get("LD_LIBRARY_PATH")) if p)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60, env=env)
+    assert r.returncode == 0, r.stderr
+    assert "PASSED" in r.stdout
