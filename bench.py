@@ -41,7 +41,7 @@ DIRECT_ZC_HEAD = 2 << 20  # and the zero-copy head of larger staged lists
 # MoE through SGWarpSpecSession: workgroups, compute waves sharing each list
 # in the RMSNorm, rows per GPU-built list (swept: 24-128 workgroups, 1-3
 # compute waves, 2-64 rows per list).
-MOE_SESSION_BLOCKS, MOE_SESSION_COMPUTE_WAVES, MOE_SESSION_ROWS_PER_LIST = 32, 3, 48
+MOE_SESSION_BLOCKS, MOE_SESSION_COMPUTE_WAVES, MOE_SESSION_ROWS_PER_LIST = 32, 3, 24
 PD = ctypes.POINTER(ctypes.c_double)
 
 
@@ -473,7 +473,7 @@ def run_moe(oracle, iters, warmup, tokens=4096, experts=64, dim=7168):
                 raise SystemExit("PARITY FAILURE: MoE RMSNorm outside bf16 tolerance")
         res[name] = {"us_p50": round(p50(t), 2), "GBps": round(gbps(n * row_bytes, p50(t)), 3)}
     # The same workload through SGWarpSpecSession: GPU submitter waves build
-    # lists of <= 48 rows from the routing output, the session's transfer
+    # lists of <= 24 rows from the routing output, the session's transfer
     # waves copy them, its compute waves (3 sharing each list, or the
     # reference's single one) run the RMSNorm.  Timed with HIP
     # events around launch_moe on the stream (the session's per-launch set-up
@@ -509,12 +509,37 @@ def run_moe(oracle, iters, warmup, tokens=4096, experts=64, dim=7168):
             res[name] = {"us_p50": round(p50(t), 2), "GBps": round(gbps(n * row_bytes, p50(t)), 3),
                          "lists": stt["lists_done"], "grid": stt["grid"], "rows_per_list": MOE_SESSION_ROWS_PER_LIST,
                          "compute_waves": cw}
+            # One more launch with the per-list device timeline (untimed):
+            # where the kernel's time goes around the copies.
+            sess.enable_trace(1024)
+            sess.reset()
+            sess.launch_moe(host.ptr, stride, tokens, d_off.ptr, d_rows.ptr, experts, n, row_bytes, d_dst.ptr,
+                            d_out.ptr if with_norm else None, d_w.ptr, 1e-6, MOE_SESSION_ROWS_PER_LIST, st)
+            L.gfd_stream_synchronize(st)
+            sess.synchronize(0)
+            res[name]["timeline"] = session_timeline(*sess.trace(), sess.stats()["lists_done"])
         finally:
             sess.close()
     L.gfd_event_destroy(ea)
     L.gfd_event_destroy(eb)
     L.gfd_stream_destroy(st)
     return res
+
+
+def session_timeline(lists, blocks, nlists):
+    """Summary of one traced SG session launch (device wall clock, us from the
+    first workgroup's start): first copy start, last landing, the kernel's
+    last wave exit, the spread of the workgroups' last landings, and the mean
+    time from a transfer wave looking for a list to its header being read."""
+    u = lists[:nlists]
+    t0 = int(blocks["start"].min())
+    us = lambda x: (np.asarray(x, dtype=np.int64) - t0) / gfd_amd.SG_TRACE_TICKS_PER_US
+    last = [float(us(u["landed"][u["block"] == b].max())) for b in range(len(blocks)) if (u["block"] == b).any()]
+    return {"first_copy_us": round(float(us(u["ready"].min())), 1),
+            "last_landing_us": round(float(us(u["landed"].max())), 1),
+            "last_exit_us": round(float(us(blocks["exit"].max())), 1),
+            "workgroup_last_landing_us": [round(min(last), 1), round(float(np.median(last)), 1), round(max(last), 1)],
+            "claim_to_ready_mean_us": round(float(np.mean(us(u["ready"]) - us(u["claimed"]))), 2)}
 
 
 def run_offload(oracle, iters, warmup):

@@ -203,6 +203,9 @@ def _declare(L):
         "gfd_sg_session_reset": ([vp], c_int),
         "gfd_sg_session_stats": ([vp, ctypes.POINTER(SessionResult)], c_int),
         "gfd_sg_session_queue": ([vp], vp),
+        "gfd_sg_session_enable_trace": ([vp, c_u32], c_int),
+        "gfd_sg_session_read_trace": ([vp, vp, c_u32, vp, c_u32, ctypes.POINTER(c_u32), ctypes.POINTER(c_u32)],
+                                      c_int),
         "gfd_bench_sg_session": ([vp, vp, c_u32, c_u32, c_int, c_int, pd], c_int),
     }
     for name, (args, res) in sig.items():
@@ -644,6 +647,13 @@ def device_sg_entries(src, dst, size, tag=0):
     return a
 
 
+# gfd_sg_trace_list / gfd_sg_trace_block (include/gfd_capi.h).
+SG_TRACE_LIST_DTYPE = np.dtype([("claimed", "<u8"), ("ready", "<u8"), ("landed", "<u8"), ("block", "<u4"),
+                                ("list_id", "<u4")])
+SG_TRACE_BLOCK_DTYPE = np.dtype([("start", "<u8"), ("exit", "<u8"), ("lists", "<u8"), ("_pad", "<u8")])
+SG_TRACE_TICKS_PER_US = 100  # the device wall clock runs at 100 MHz
+
+
 class SGWarpSpecSession:
     """gfd::SGWarpSpecSession (reference include/gfd/warp_spec_session.h:142-258,
     src/sg_warp_spec_session.cpp) with the built-in consumers of the C-ABI."""
@@ -698,6 +708,26 @@ class SGWarpSpecSession:
 
     def queue_ptr(self):
         return lib().gfd_sg_session_queue(self._h)
+
+    def enable_trace(self, max_lists):
+        """Record the first max_lists lists and every workgroup of each later
+        launch (0 switches it off); read them with trace() after synchronize()."""
+        _check(lib().gfd_sg_session_enable_trace(self._h, max_lists), "gfd_sg_session_enable_trace")
+        self._trace_cap = max_lists
+
+    def trace(self):
+        """The last launch's timeline: (lists, blocks) structured arrays
+        (SG_TRACE_LIST_DTYPE in ring order, SG_TRACE_BLOCK_DTYPE per
+        workgroup), in ticks of the device's 100 MHz wall clock."""
+        cap = getattr(self, "_trace_cap", 0)
+        nb = self.stats()["grid"]
+        lists = np.zeros(cap, dtype=SG_TRACE_LIST_DTYPE)
+        blocks = np.zeros(nb, dtype=SG_TRACE_BLOCK_DTYPE)
+        n_l, n_b = ctypes.c_uint32(), ctypes.c_uint32()
+        _check(lib().gfd_sg_session_read_trace(self._h, lists.ctypes.data if cap else None, cap,
+                                               blocks.ctypes.data if nb else None, nb, ctypes.byref(n_l),
+                                               ctypes.byref(n_b)), "gfd_sg_session_read_trace")
+        return lists[:n_l.value], blocks[:n_b.value]
 
     def bench(self, entries, entries_per_list, warmup=2, iters=10):
         entries = np.ascontiguousarray(entries, dtype=DEVICE_SG_ENTRY_DTYPE)

@@ -11,7 +11,8 @@
 // of gfd_moe_route, cut into lists of at most rows_per_list (<= 64) rows, so
 // a workgroup gets several lists and the RMSNorm of one overlaps the copy of
 // the next.  List ids run 0 .. total-1: first every expert's full lists, in
-// expert order, then every expert's shorter remainder list (lists past
+// expert order, then every expert's shorter remainder list, longest first
+// (ties in expert order) (lists past
 // MAX_SG_LISTS reuse ring slots once landed; ids from MAX_SG_LISTS on have no
 // d_list_done word, which the kernel does not need).  Entry k of the
 // list for rows [r, r + n): src = host_base + row_token[r + k] * token_stride,
@@ -148,6 +149,9 @@ struct MoeLists {
     const int* row_token;
     int num_experts, num_tokens, num_rows;
     uint32_t row_bytes, rows_per_list;
+    // The launch's lists and entries fit the ring and the pool
+    // (SGWarpSpecSession::gpu_lists_fit): no space or slot waits.
+    int fits;
 };
 
 // Submitter wave: posts this workgroup's share of the lists (list L goes to
@@ -162,9 +166,11 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
     // Lists per expert (one lane per expert, at most 64 experts): `full`
     // lists of rows_per_list rows and at most one shorter one with the rest.
     // Full lists get the first ids (expert-major), the shorter ones the last,
-    // so the lists the transfer waves claim last are the short ones and the
-    // end of the launch waits on less work.
+    // longest first, so the lists the transfer waves claim last are the
+    // shortest and the end of the launch waits on the least work (longest
+    // processing time first).
     int a = 0, b = 0, full = 0, part = 0;
+    uint32_t rem = 0;
     if (lane < m.num_experts) {
         a = m.offsets[lane];
         b = m.offsets[lane + 1];
@@ -173,7 +179,8 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
             a = b = 0;
         }
         full = (int)((uint32_t)(b - a) / m.rows_per_list);
-        part = (uint32_t)(b - a) % m.rows_per_list != 0;
+        rem = (uint32_t)(b - a) % m.rows_per_list;
+        part = rem != 0;
     }
     int full_incl = full, part_incl = part;
 #pragma unroll
@@ -181,22 +188,36 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
         const int tf = __shfl_up(full_incl, o, 64), tp = __shfl_up(part_incl, o, 64);
         if (lane >= o) full_incl += tf, part_incl += tp;
     }
-    const int full_excl = full_incl - full, part_excl = part_incl - part;
+    const int full_excl = full_incl - full;
+    // The host's fit check assumed the experts' ranges hold at most num_rows
+    // rows together (true for gfd_moe_route's offsets); otherwise wait for
+    // space as usual.
+    int rows = b - a;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) rows += __shfl_xor(rows, o, 64);
+    const bool fits = m.fits && rows <= m.num_rows;
     const uint32_t nfull = (uint32_t)__shfl(full_incl, 63, 64);
     const uint32_t total = nfull + (uint32_t)__shfl(part_incl, 63, 64);
+    // Rank of this expert's remainder list among all remainders: longer
+    // first, ties in expert order.  Distinct for every expert with one.
+    int rank = 0;
+    for (int j = 0; j < 64; j++) {
+        const uint32_t rj = (uint32_t)__shfl((int)rem, j, 64);
+        rank += rj > rem || (rj == rem && j < lane);
+    }
     for (uint32_t L = blockIdx.x; L < total; L += gridDim.x) {
-        // The expert of list L: the highest expert whose first list id (of
-        // this kind) is <= L's index among lists of its kind.
+        // The expert of list L.  A full list: the highest expert whose first
+        // full-list id is <= L.  A remainder: the expert of that rank.
         const bool is_full = L < nfull;
         const uint32_t k = is_full ? L : L - nfull;
-        const int excl = is_full ? full_excl : part_excl;
-        const uint64_t mask = __ballot(lane < m.num_experts && (uint32_t)excl <= k);
-        const int e = 63 - __builtin_clzll(mask);
+        const uint64_t mask = is_full ? __ballot(lane < m.num_experts && (uint32_t)full_excl <= k)
+                                      : __ballot(part && (uint32_t)rank == k);
+        const int e = is_full ? 63 - __builtin_clzll(mask) : __builtin_ctzll(mask);
         const uint32_t ea = (uint32_t)__shfl(a, e, 64), eb = (uint32_t)__shfl(b, e, 64);
-        const uint32_t r0 = is_full ? ea + (k - (uint32_t)__shfl(excl, e, 64)) * m.rows_per_list
+        const uint32_t r0 = is_full ? ea + (k - (uint32_t)__shfl(full_excl, e, 64)) * m.rows_per_list
                                     : eb - (eb - ea) % m.rows_per_list;
         const uint32_t n = min(m.rows_per_list, eb - r0);
-        if (!sg::sg_wait_entry_space(sq, n) || !sg::sg_wait_list_space(sq)) {
+        if (!fits && (!sg::sg_wait_entry_space(sq, n) || !sg::sg_wait_list_space(sq))) {
             if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_RING_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
@@ -217,12 +238,17 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
             }
         }
         const uint64_t slot = sg::sg_alloc_list(sq);
-        if (!sg::sg_commit_list(sq, slot, (uint32_t)(pool % MAX_SG_POOL_ENTRIES), n, L, SG_FLAG_NONE)) break;
+        if (!sg::sg_commit_list(sq, slot, (uint32_t)(pool % MAX_SG_POOL_ENTRIES), n, L, SG_FLAG_NONE, fits))
+            break;
     }
     if (blockIdx.x == 0) {
-        if (!sg::sg_wait_list_done(sq, total) && lane == 0)
-            __hip_atomic_fetch_or(&cnt->error, SG_ERR_LIST_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sg::sg_terminate(sq);
+        if (sg::sg_wait_list_done(sq, total)) {
+            sg::sg_terminate_all_landed(sq);
+        } else {
+            if (lane == 0)
+                __hip_atomic_fetch_or(&cnt->error, SG_ERR_LIST_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sg::sg_terminate(sq);
+        }
     }
 }
 
@@ -257,8 +283,11 @@ extern "C" int gfd_sg_session_launch_moe(gfd_sg_session_t s, const void* host_ba
     // waves (num_compute_warps, at most SG_MAX_COMPUTE); transfer only needs one.
     const int compute = out ? std::min(p->compute_waves(), gfd::sg_warp_spec::SG_MAX_COMPUTE) : 1;
     p->before_launch(stream, helpers, compute);
+    // At most one list more per expert than whole lists of rows.
+    const uint64_t max_lists = (uint64_t)num_experts + (uint64_t)num_rows / rows_per_list;
     const MoeLists m{(uint64_t)(uintptr_t)host_base, token_stride, (uint64_t)(uintptr_t)dst, offsets, row_token,
-                     num_experts, num_tokens, num_rows, row_bytes, rows_per_list};
+                     num_experts, num_tokens, num_rows, row_bytes, rows_per_list,
+                     p->gpu_lists_fit(max_lists, (uint64_t)num_rows) ? 1 : 0};
     const dim3 grid((unsigned)p->num_blocks()), block((unsigned)(2 + compute + helpers) * 64);
     if (out)
         hipLaunchKernelGGL(sg_moe_kernel<RowRMSNorm>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),

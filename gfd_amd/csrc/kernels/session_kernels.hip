@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstring>
 #include <vector>
 
 #include "gfd/sg_device_primitives.h"
@@ -146,9 +147,22 @@ __global__ __launch_bounds__(6 * 64) void sg_gpu_submit_kernel(gfd::DescriptorQu
         }
     }
     if (blockIdx.x == 0) {
-        gfd::sg::sg_wait_list_done(sq, num_lists);
-        gfd::sg::sg_terminate(sq);
+        if (gfd::sg::sg_wait_list_done(sq, num_lists))
+            gfd::sg::sg_terminate_all_landed(sq);
+        else
+            gfd::sg::sg_terminate(sq);
     }
+}
+
+// Per-launch set-up of an SG session, on the launch stream ahead of the
+// session kernel: d_list_done[0 .. MAX_SG_LISTS) zeroed, the device counters
+// after them written, trace_words words of trace records zeroed.
+__global__ __launch_bounds__(256) void sg_prepare_kernel(uint64_t* d_list_done, gfd::SGDeviceCounters c,
+                                                        uint64_t* trace, uint64_t trace_words) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x, n = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t k = i; k < (uint64_t)gfd::MAX_SG_LISTS; k += n) d_list_done[k] = 0;
+    if (i == 0) *reinterpret_cast<gfd::SGDeviceCounters*>(d_list_done + gfd::MAX_SG_LISTS) = c;
+    for (uint64_t k = i; k < trace_words; k += n) trace[k] = 0;
 }
 
 int fail(int code, const char* what) {
@@ -305,6 +319,16 @@ extern "C" int gfd_sg_session_launch_gpu_submit(gfd_sg_session_t s, const gfd_de
     return e == hipSuccess ? 0 : fail(e, "gfd_sg_session_launch_gpu_submit: launch failed");
 }
 
+extern "C" int gfd_sg_prepare_launch(uint64_t* d_list_done, const void* counters, uint64_t* trace,
+                                     uint64_t trace_words, gfd_stream_t stream) {
+    if (!d_list_done || !counters || (trace_words && !trace)) return (int)hipErrorInvalidValue;
+    gfd::SGDeviceCounters c;
+    std::memcpy(&c, counters, sizeof(c));
+    hipLaunchKernelGGL(sg_prepare_kernel, dim3(4), dim3(256), 0, (hipStream_t)stream, d_list_done, c, trace,
+                       trace_words);
+    return (int)hipGetLastError();
+}
+
 extern "C" int gfd_sg_session_synchronize(gfd_sg_session_t s, uint64_t extra_gpu_lists) {
     if (!s) return fail(hipErrorInvalidValue, "gfd_sg_session_synchronize: NULL session");
     return S(s)->synchronize(extra_gpu_lists) ? 0 : fail(hipErrorLaunchFailure, "gfd_sg_session_synchronize: lists did not land or the kernel reported an error");
@@ -332,6 +356,30 @@ extern "C" int gfd_sg_session_stats(gfd_sg_session_t s, gfd_session_result* r) {
 }
 
 extern "C" void* gfd_sg_session_queue(gfd_sg_session_t s) { return s ? (void*)S(s)->get_sg_queue() : nullptr; }
+
+static_assert(sizeof(gfd_sg_trace_list) == sizeof(gfd::SGTraceList), "gfd_sg_trace_list must match gfd::SGTraceList");
+static_assert(sizeof(gfd_sg_trace_block) == sizeof(gfd::SGTraceBlock), "gfd_sg_trace_block must match gfd::SGTraceBlock");
+
+extern "C" int gfd_sg_session_enable_trace(gfd_sg_session_t s, uint32_t max_lists) {
+    if (!s) return fail(hipErrorInvalidValue, "gfd_sg_session_enable_trace: NULL session");
+    return S(s)->enable_trace(max_lists) ? 0 : fail(hipErrorOutOfMemory, "gfd_sg_session_enable_trace: allocation failed");
+}
+
+extern "C" int gfd_sg_session_read_trace(gfd_sg_session_t s, gfd_sg_trace_list* lists, uint32_t max_lists,
+                                         gfd_sg_trace_block* blocks, uint32_t max_blocks, uint32_t* n_lists,
+                                         uint32_t* n_blocks) {
+    if (!s || !n_lists || !n_blocks || (max_lists && !lists) || (max_blocks && !blocks))
+        return fail(hipErrorInvalidValue, "gfd_sg_session_read_trace: invalid argument");
+    std::vector<gfd::SGTraceList> l;
+    std::vector<gfd::SGTraceBlock> b;
+    if (!S(s)->read_trace(l, b))
+        return fail(hipErrorNotReady, "gfd_sg_session_read_trace: tracing is off, the launch is still running, or the copy failed");
+    *n_lists = (uint32_t)std::min<size_t>(l.size(), max_lists);
+    *n_blocks = (uint32_t)std::min<size_t>(b.size(), max_blocks);
+    if (*n_lists) std::memcpy(lists, l.data(), *n_lists * sizeof(gfd_sg_trace_list));
+    if (*n_blocks) std::memcpy(blocks, b.data(), *n_blocks * sizeof(gfd_sg_trace_block));
+    return 0;
+}
 
 // Host-submitted SG transfer timed from launch until the host has seen every
 // list land (done markers), then terminate + sync.  times_us[iters].

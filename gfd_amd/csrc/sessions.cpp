@@ -202,6 +202,7 @@ SGWarpSpecSession::SGWarpSpecSession(const SGWarpSpecConfig& config) : config_(c
 
 SGWarpSpecSession::~SGWarpSpecSession() {
     if (running_) synchronize();
+    if (trace_buf_) gfd_hip_free(trace_buf_);
     if (sq_) {
         if (sq_->d_list_done) gfd_hip_free(sq_->d_list_done);
         gfd_hip_host_free(sq_);
@@ -288,8 +289,19 @@ void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int
     c.list_base = consumed_lists_;
     c.helpers = (uint64_t)(helper_waves < 0 ? config_.transfer_helper_waves : helper_waves);
     c.compute_waves = (uint64_t)(compute_waves < 0 ? this->compute_waves() : compute_waves);
-    gfd_hip_memset_d8((uint64_t)(uintptr_t)sq_->d_list_done, 0, MAX_SG_LISTS * sizeof(uint64_t));
-    gfd_hip_memcpy_h2d((uint64_t)(uintptr_t)sg_device_counters(sq_), &c, sizeof(c));
+    uint64_t trace_words = 0;
+    if (trace_buf_) {
+        c.trace = (uint64_t)(uintptr_t)trace_buf_;
+        c.trace_cap = trace_cap_;
+        c.trace_blocks = (uint64_t)num_blocks_;
+        trace_words = ((uint64_t)trace_cap_ * sizeof(SGTraceList) + (uint64_t)num_blocks_ * sizeof(SGTraceBlock)) / 8;
+    }
+    // On the launch stream, ahead of the kernel: no host wait per launch.
+    const int rc = gfd_sg_prepare_launch(sq_->d_list_done, &c, static_cast<uint64_t*>(trace_buf_), trace_words, stream);
+    if (rc != 0) {
+        GFD_LOG_ERROR("SGWarpSpecSession: launch set-up failed: %s\n", gfd_hip_error_string(rc));
+        error_bits_ |= 1ull << 63;
+    }
     stream_ = stream;
     launch_time_ = std::chrono::steady_clock::now();
     running_ = true;
@@ -350,11 +362,57 @@ void SGWarpSpecSession::reset() {
     sq_->d_list_done = d;
     sq_->idle_limit_ms = idle;
     if (dq_) std::memset((void*)dq_, 0, sizeof(DescriptorQueue));
-    if (d)
+    // Waited for: the next launch's set-up runs on the caller's stream, which
+    // need not be ordered after the null stream this memset runs on.
+    if (d) {
         gfd_hip_memset_d8((uint64_t)(uintptr_t)d, 0, ((size_t)MAX_SG_LISTS + SG_DEVICE_COUNTER_WORDS) * sizeof(uint64_t));
+        gfd_hip_stream_synchronize(nullptr);
+    }
     pending_.clear();
     consumed_lists_ = consumed_entries_ = 0;
     error_bits_ = entries_done_ = bytes_done_ = lists_done_ = 0;
+}
+
+bool SGWarpSpecSession::gpu_lists_fit(uint64_t lists, uint64_t entries) const {
+    const uint64_t host_lists = sq_ ? sq_->list_alloc_idx - consumed_lists_ : 0;
+    const uint64_t host_entries = sq_ ? sq_->entry_alloc_idx - consumed_entries_ : 0;
+    return host_lists + lists < (uint64_t)MAX_SG_LISTS - 1 && host_entries + entries <= (uint64_t)MAX_SG_POOL_ENTRIES;
+}
+
+bool SGWarpSpecSession::enable_trace(uint32_t max_lists) {
+    if (running_) synchronize();
+    if (trace_buf_) gfd_hip_free(trace_buf_);
+    trace_buf_ = nullptr;
+    trace_cap_ = 0;
+    if (!ok_ || max_lists == 0) return ok_;
+    void* d = nullptr;
+    const size_t bytes = (size_t)max_lists * sizeof(SGTraceList) + (size_t)num_blocks_ * sizeof(SGTraceBlock);
+    if (gfd_hip_malloc(&d, bytes) != 0) {
+        GFD_LOG_ERROR("SGWarpSpecSession: trace buffer allocation failed\n");
+        return false;
+    }
+    gfd_hip_memset_d8((uint64_t)(uintptr_t)d, 0, bytes);
+    gfd_hip_stream_synchronize(nullptr);
+    trace_buf_ = d;
+    trace_cap_ = max_lists;
+    return true;
+}
+
+bool SGWarpSpecSession::read_trace(std::vector<SGTraceList>& lists, std::vector<SGTraceBlock>& blocks) const {
+    lists.clear();
+    blocks.clear();
+    if (!trace_buf_ || running_) return false;
+    lists.resize(trace_cap_);
+    blocks.resize((size_t)num_blocks_);
+    const uint64_t base = (uint64_t)(uintptr_t)trace_buf_;
+    if (gfd_hip_memcpy_d2h(lists.data(), base, lists.size() * sizeof(SGTraceList)) != 0 ||
+        gfd_hip_memcpy_d2h(blocks.data(), base + lists.size() * sizeof(SGTraceList),
+                           blocks.size() * sizeof(SGTraceBlock)) != 0) {
+        lists.clear();
+        blocks.clear();
+        return false;
+    }
+    return true;
 }
 
 SGWarpSpecSession::Stats SGWarpSpecSession::get_stats() const {

@@ -62,6 +62,14 @@ int gfd_hip_stream_write_u64(gfd_stream_t s, uint64_t dst, uint64_t value);
 }
 
 extern "C" {
+// Stream-ordered set-up of an SG session launch (a small kernel on `stream`):
+// d_list_done[0 .. MAX_SG_LISTS) = 0, the SGDeviceCounters after them =
+// *counters, trace[0 .. trace_words) = 0.  A HIP error code, 0 on success.
+int gfd_sg_prepare_launch(uint64_t* d_list_done, const void* counters, uint64_t* trace, uint64_t trace_words,
+                          gfd_stream_t stream);
+}
+
+extern "C" {
 // 1 if `p` is device (HBM) memory, 0 if host / unknown.
 int gfd_hip_pointer_is_device(const void* p);
 // 1 and the device allocation [*base, *base + *size) holding ptr, or 0.

@@ -107,10 +107,14 @@ __device__ __forceinline__ bool sg_wait_slot_free(SGTaskQueue* sq, uint64_t slot
 
 // Write the header and publish the list.  The system-scope release orders
 // every entry and header store of this wave before the sequence store.
-// False (nothing published) if the ring slot never became free.
+// False (nothing published) if the ring slot never became free.  slot_free:
+// the caller knows the slot's previous list has landed (the session's
+// gpu_lists_fit held for the launch), so the wait, a read of host memory, is
+// skipped.
 __device__ __forceinline__ bool sg_commit_list(SGTaskQueue* sq, uint64_t slot, uint32_t pool_offset,
-                                               uint32_t count, uint32_t list_id, uint32_t flags) {
-    if (!sg_wait_slot_free(sq, slot)) {
+                                               uint32_t count, uint32_t list_id, uint32_t flags,
+                                               bool slot_free = false) {
+    if (!slot_free && !sg_wait_slot_free(sq, slot)) {
         if (wave::lane_id() == 0)
             __hip_atomic_fetch_or(&counters(sq)->error, SG_ERR_RING_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return false;
@@ -162,6 +166,18 @@ __device__ __forceinline__ bool sg_wait_list_id_done(SGTaskQueue* sq, uint32_t l
 __device__ __forceinline__ void sg_terminate(SGTaskQueue* sq) {
     if (wave::lane_id() == 0)
         __hip_atomic_store(const_cast<uint32_t*>(&sq->terminate), 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// sg_terminate for a submitter whose sg_wait_list_done has just returned true
+// for every list of the launch: with nothing left to copy, it also raises the
+// HBM stop word that waiting transfer waves poll, so they exit without first
+// having one of them read terminate across PCIe.  Not for any other case: a
+// wave waiting for a committed list that no wave has seen yet would stop
+// without copying it.
+__device__ __forceinline__ void sg_terminate_all_landed(SGTaskQueue* sq) {
+    sg_terminate(sq);
+    if (wave::lane_id() == 0)
+        __hip_atomic_store(&counters(sq)->stop, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace sg

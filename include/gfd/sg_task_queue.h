@@ -87,8 +87,38 @@ struct SGDeviceCounters {
     // compute_waves), for compute functors that declare kSharesLists; 0 or 1
     // and every other functor: wave 1 alone.
     uint64_t compute_waves;
-    uint64_t _pad[4];
+    // Per-list timeline (0: off).  Device address of trace_cap SGTraceList
+    // records, one per ring index of the launch (list_base + k -> record k),
+    // followed by trace_blocks SGTraceBlock records, one per workgroup.
+    uint64_t trace;
+    uint64_t trace_cap;
+    uint64_t trace_blocks;
+    uint64_t _pad;
 };
+
+// One list of a traced launch, in wall-clock ticks (100 MHz): when its
+// transfer wave started looking for it, when its header had been read (the
+// copy starts), and when its bytes had been released device-wide.  Records of
+// ring indices beyond trace_cap are not written; a record still 0 was not
+// claimed.
+struct SGTraceList {
+    uint64_t claimed;
+    uint64_t ready;
+    uint64_t landed;
+    uint32_t block;
+    uint32_t list_id;
+};
+static_assert(sizeof(SGTraceList) == 32, "SGTraceList must be 32 bytes");
+
+// One workgroup of a traced launch: when its transfer wave started and
+// exited, and how many lists it copied.
+struct SGTraceBlock {
+    uint64_t start;
+    uint64_t exit;
+    uint64_t lists;
+    uint64_t _pad;
+};
+static_assert(sizeof(SGTraceBlock) == 32, "SGTraceBlock must be 32 bytes");
 constexpr int SG_DEVICE_COUNTER_WORDS = (int)(sizeof(SGDeviceCounters) / sizeof(uint64_t));
 
 // Bits of SGDeviceCounters::error.

@@ -34,7 +34,8 @@
 // list is committed it reads the next 64 sequences at once (one per lane) and
 // advances list_known past the committed run, releasing that many waiting
 // waves; the others poll list_known in HBM.  Idle waves thus put one read at
-// a time on PCIe instead of one per wave.
+// a time on PCIe instead of one per wave, and a wave whose index is already
+// below list_known goes straight to the list's header.
 #include "gfd/descriptor_queue.h"
 #include "gfd/sg_device_primitives.h"
 #include "gfd/sg_task_queue.h"
@@ -99,45 +100,56 @@ __device__ __forceinline__ bool _wait_committed(SGTaskQueue* sq, SGDeviceCounter
     const uint64_t t0 = wall_clock64();
     for (;;) {
         const uint64_t known = __hip_atomic_load(&cnt->list_known, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (idx <= known) {
-            // terminate is read before the sequence.  Whoever sets terminate
-            // does so after every list it expects has been committed, with a
-            // release store; the acquire load that reads it orders the
-            // sequence load after those commits.  So a list still uncommitted
-            // once terminate reads 1 was never submitted, and the wave can
-            // stop at once.  (Read the other way round, a commit could land
-            // between the two loads and be dropped.)
+        if (idx < known) {
+            // A leader saw this list committed.  The acquire fence pairs with
+            // its release when it raised list_known, so the header and
+            // entries read next are those written before that commit.
+            wave::acquire_agent();
+            return true;
+        }
+        if (idx == known) {
+            // Leader.  terminate is read before the sequence.  Whoever sets
+            // terminate does so after every list it expects has been
+            // committed, with a release store; the acquire load that reads it
+            // orders the sequence load after those commits.  So a list still
+            // uncommitted once terminate reads 1 was never submitted, and the
+            // wave can stop at once.  (Read the other way round, a commit
+            // could land between the two loads and be dropped.)
             const uint32_t term = wave::load_system32(&sq->terminate);
             if (wave::load_system(&mine.sequence) == idx + 1) {
-                if (idx == known) {
-                    // Leader: find the committed run idx, idx+1, ... and publish it.
-                    const uint64_t j = idx + (uint64_t)lane;
-                    const bool c = wave::load_system(&sq->lists[j % MAX_SG_LISTS].sequence) == j + 1;
-                    const uint64_t mask = __ballot(c);
-                    const uint64_t run = (~mask == 0) ? 64 : (uint64_t)__builtin_ctzll(~mask);
-                    if (lane == 0)
-                        __hip_atomic_fetch_max(&cnt->list_known, idx + (run ? run : 1), __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                }
+                // Find the committed run idx, idx+1, ... and publish it.
+                const uint64_t j = idx + (uint64_t)lane;
+                const bool c = wave::load_system(&sq->lists[j % MAX_SG_LISTS].sequence) == j + 1;
+                const uint64_t mask = __ballot(c);
+                const uint64_t run = (~mask == 0) ? 64 : (uint64_t)__builtin_ctzll(~mask);
+                // Release: the 64 sequence loads above (all lanes, one
+                // instruction, complete before this store issues) are
+                // ordered before the new list_known.
+                if (lane == 0)
+                    __hip_atomic_fetch_max(&cnt->list_known, idx + (run ? run : 1), __ATOMIC_RELEASE,
+                                           __HIP_MEMORY_SCOPE_AGENT);
                 return true;
             }
             if (term) {
                 if (lane == 0) __hip_atomic_store(&cnt->stop, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 return false;
             }
+            // A GPU submitter that saw every list land raises stop directly.
+            if (__hip_atomic_load(&cnt->stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
             __builtin_amdgcn_s_sleep(4);
         } else {
             if (__hip_atomic_load(&cnt->stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
             // Back off in proportion to how many commits this wave is still
-            // waiting for: device-scope loads bypass the XCD-local L2, so
-            // hundreds of idle waves polling at full rate would crowd the
-            // fabric the copies use.  Up to ~25 us between polls.
+            // waiting for, up to ~3.5 us between polls: device-scope loads
+            // bypass the XCD-local L2, so hundreds of idle waves polling at
+            // full rate would crowd the fabric the copies use, while a longer
+            // nap delays the end of the launch (the waves still waiting then
+            // see stop only at their next poll).
             const uint64_t dist = idx - known;
             if (dist < 8) {
                 for (uint64_t i = 0; i < dist; i++) __builtin_amdgcn_s_sleep(16);
             } else {
-                const uint32_t naps = dist < 64 ? (uint32_t)(dist / 8) : 8u;
-                for (uint32_t i = 0; i < naps; i++) __builtin_amdgcn_s_sleep(127);
+                __builtin_amdgcn_s_sleep(127);
             }
         }
         if (wall_clock64() - t0 > idle_ticks) return false;
@@ -233,12 +245,20 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
     if (w == 0) {
         // ---------------- transfer wave (leader)
         const uint64_t idle_ticks = _idle_limit_ticks(sq);
+        // Timeline of this launch's lists, when the session asks for one.
+        const uint64_t t_start = (uint64_t)wall_clock64();
+        SGTraceList* const trace =
+            reinterpret_cast<SGTraceList*>(__hip_atomic_load(&cnt->trace, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        const uint64_t trace_cap = __hip_atomic_load(&cnt->trace_cap, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t list_base = __hip_atomic_load(&cnt->list_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint64_t nlists = 0;
         for (uint64_t iter = 0;; iter++) {
             const int s = (int)(iter & 1);
             if (has_compute && !wave::wait_lds_eq(&slots[s].free, 1)) {
                 if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_SLOT_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
+            const uint64_t t_claimed = (uint64_t)wall_clock64();
             uint64_t idx = 0;
             if (lane == 0) idx = sg::atomic_add_dev(&cnt->list_claim, 1);
             idx = wave::broadcast0(idx);
@@ -246,6 +266,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             SGList& l = sq->lists[idx % MAX_SG_LISTS];
             const uint32_t pool_offset = l.pool_offset, count = l.count, list_id = l.list_id, flags = l.flags;
             if (lane == 0) wave::store_system(&l.sequence, 0);  // claimed
+            const uint64_t t_ready = (uint64_t)wall_clock64();
 
             // Publish the copy job, copy batches with the helpers, wait for
             // every batch and every helper's acknowledgement.
@@ -274,7 +295,10 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             bytes = __hip_atomic_load(&job.bytes, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
             wave::acquire_agent();
             wave::release_agent();  // the list's bytes (all transfer waves') are visible device-wide
+            nlists++;
             if (lane == 0) {
+                if (trace && idx - list_base < trace_cap)
+                    trace[idx - list_base] = SGTraceList{t_claimed, t_ready, (uint64_t)wall_clock64(), blockIdx.x, list_id};
                 if (list_id < (uint32_t)MAX_SG_LISTS)
                     __hip_atomic_store(&sq->d_list_done[list_id], 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
                 sg::atomic_add_dev(&cnt->entries_done, count);
@@ -294,6 +318,9 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
         if (lane == 0) {
             wave::lds_store(&job.seq, -1);  // helpers exit
             wave::lds_store(&terminated, 1);
+            if (trace && blockIdx.x < __hip_atomic_load(&cnt->trace_blocks, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                reinterpret_cast<SGTraceBlock*>(trace + trace_cap)[blockIdx.x] =
+                    SGTraceBlock{t_start, (uint64_t)wall_clock64(), nlists, 0};
         }
     } else if (helpers > 0 && w >= first_helper) {
         // ---------------- transfer helper: copies batches of the leader's

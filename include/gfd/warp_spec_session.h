@@ -12,6 +12,7 @@
 #include <cstdint>
 #include <deque>
 #include <functional>
+#include <vector>
 
 #include "gfd/cpu_polling.h"
 #include "gfd/hip_shim.h"
@@ -146,6 +147,8 @@ private:
     uint64_t tiles_done_ = 0;
     std::chrono::steady_clock::time_point launch_time_;
     double last_elapsed_ms_ = 0;
+    void* trace_buf_ = nullptr;  // HBM: trace_cap_ SGTraceList + num_blocks_ SGTraceBlock
+    uint32_t trace_cap_ = 0;
 };
 
 struct SGWarpSpecConfig {
@@ -215,6 +218,19 @@ public:
     // lists between compute waves).
     void before_launch(gfd_stream_t stream, int helper_waves = -1, int compute_waves = -1);
     int compute_waves() const { return config_.num_compute_warps > 0 ? config_.num_compute_warps : 1; }
+    // True when GPU submitters posting at most `lists` lists and `entries`
+    // entries in the next launch can never find the ring, a ring slot or the
+    // entry pool still in use (the host's queued lists included), so they
+    // may skip those waits.
+    bool gpu_lists_fit(uint64_t lists, uint64_t entries) const;
+
+    // Per-list device timeline (not in the reference).  From the next launch
+    // on, the transfer waves record each of the launch's first max_lists
+    // lists (SGTraceList, in ring order) and each workgroup (SGTraceBlock);
+    // 0 switches it off.  False if the record buffer cannot be allocated.
+    bool enable_trace(uint32_t max_lists);
+    // The last launch's records (after synchronize()); false if tracing is off.
+    bool read_trace(std::vector<SGTraceList>& lists, std::vector<SGTraceBlock>& blocks) const;
 
 private:
     struct Pending {
@@ -241,6 +257,8 @@ private:
     uint64_t entries_done_ = 0, bytes_done_ = 0, lists_done_ = 0;  // last launch
     std::chrono::steady_clock::time_point launch_time_;
     double last_elapsed_ms_ = 0;
+    void* trace_buf_ = nullptr;  // HBM: trace_cap_ SGTraceList + num_blocks_ SGTraceBlock
+    uint32_t trace_cap_ = 0;
 };
 
 // The reference's spelling in the north-star text.

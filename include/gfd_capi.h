@@ -399,8 +399,9 @@ int gfd_sg_session_launch_gpu_submit(gfd_sg_session_t s, const gfd_device_sg_ent
 /* The MoE-routed gather through the session (the SG MoE workload of
  * examples/09_sg_warp_spec.cu:78-294 with lists built on the GPU): submitter
  * waves cut expert e's rows [offsets[e], offsets[e+1]) of gfd_moe_route's
- * expert-major order into lists of at most rows_per_list (1..64) rows
- * (list ids 0.. over experts in order); entry r: src = host_base +
+ * expert-major order into lists of at most rows_per_list (1..64) rows (list
+ * ids 0..: every expert's full lists in expert order, then the shorter
+ * remainder lists, longest first); entry r: src = host_base +
  * row_token[r] * token_stride (pinned host), dst = dst + r * row_bytes (HBM),
  * tag = r.  The transfer waves copy each list; with out != NULL the compute
  * wave writes the bf16 RMSNorm x / sqrt(mean(x^2) + eps) * weight of every
@@ -419,6 +420,27 @@ int gfd_sg_session_synchronize(gfd_sg_session_t s, uint64_t extra_gpu_lists);
 int gfd_sg_session_reset(gfd_sg_session_t s);
 int gfd_sg_session_stats(gfd_sg_session_t s, gfd_session_result* out);
 void* gfd_sg_session_queue(gfd_sg_session_t s); /* get_sg_queue(): the SGTaskQueue */
+/* Per-list device timeline of the session's launches; no counterpart in the
+ * reference.  From the next launch on, the transfer waves record each of the
+ * launch's first max_lists lists, in ring order, and each workgroup
+ * (max_lists 0 switches it off).  Times are ticks of the device's 100 MHz
+ * wall clock: claimed = the transfer wave starts looking for the list, ready =
+ * its header is read and the copy starts, landed = its bytes are released
+ * device-wide.  A list record still all 0 was not claimed. */
+typedef struct {
+    uint64_t claimed, ready, landed;
+    uint32_t block, list_id;
+} gfd_sg_trace_list;
+/* start / exit of the workgroup's transfer wave, lists it copied */
+typedef struct {
+    uint64_t start, exit, lists, _pad;
+} gfd_sg_trace_block;
+int gfd_sg_session_enable_trace(gfd_sg_session_t s, uint32_t max_lists);
+/* The last launch's records, after gfd_sg_session_synchronize: up to
+ * max_lists / max_blocks records; their counts in *n_lists / *n_blocks. */
+int gfd_sg_session_read_trace(gfd_sg_session_t s, gfd_sg_trace_list* lists, uint32_t max_lists,
+                              gfd_sg_trace_block* blocks, uint32_t max_blocks, uint32_t* n_lists,
+                              uint32_t* n_blocks);
 /* Host-submitted SG transfer (`count` entries in lists of entries_per_list,
  * at most 16384 entries / 512 lists), no-op consumer: wall time from launch
  * until every list's done marker is up, times_us[iters]. */

@@ -76,6 +76,53 @@ def test_moe_through_session(T, E, dim, rpl, blocks, cw):
         sess.close()
 
 
+def test_moe_session_trace():
+    """The per-list device timeline: every list of the launch is recorded once,
+    in ring order, with claimed <= ready <= landed; each workgroup's record
+    brackets its lists and the workgroups' list counts add up; the session's
+    results are unchanged; with tracing off there is nothing to read."""
+    T, E, dim, rpl = 4096, 64, 7168, 48
+    m = Moe(T, E, dim)
+    m.route()
+    n = 2 * T
+    rows = m.expected_rows()
+    total = expected_lists(m.offsets, rpl)
+    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=3, num_blocks=32, idle_limit_ms=10000)
+    try:
+        sess.enable_trace(1024)
+        for launch in range(2):  # records are cleared for every launch
+            print("traced moe session launch %d" % launch, flush=True)
+            st = run_session(m, sess, True, rpl)
+            assert st["error_bits"] == 0 and st["lists_done"] == total
+            got = m.d_dst.download()[:n * m.row_bytes].view(np.uint16).reshape(n, dim)
+            assert (got == rows).all()
+            lists, blocks = sess.trace()
+            assert len(lists) == 1024 and len(blocks) == 32
+            used, rest = lists[:total], lists[total:]
+            assert (rest["claimed"] == 0).all() and (rest["landed"] == 0).all()
+            assert sorted(used["list_id"].tolist()) == list(range(total))
+            assert (used["claimed"] > 0).all()
+            assert (used["claimed"] <= used["ready"]).all() and (used["ready"] <= used["landed"]).all()
+            assert (used["block"] < 32).all()
+            assert int(blocks["lists"].sum()) == total
+            for b in range(32):
+                mine = used[used["block"] == b]
+                assert len(mine) == int(blocks["lists"][b])
+                assert blocks["start"][b] > 0 and blocks["exit"][b] >= blocks["start"][b]
+                if len(mine):
+                    assert blocks["start"][b] <= mine["claimed"].min()
+                    assert blocks["exit"][b] >= mine["landed"].max()
+            span_us = (used["landed"].max() - blocks["start"].min()) / gfd_amd.SG_TRACE_TICKS_PER_US
+            print("first start to last landing: %.1f us" % span_us, flush=True)
+            assert 0 < span_us < 10e6
+        sess.enable_trace(0)
+        run_session(m, sess, False, rpl)
+        with pytest.raises(gfd_amd.GfdError):
+            sess.trace()
+    finally:
+        sess.close()
+
+
 def test_moe_session_skips_out_of_range_rows():
     """A routing entry outside the token range is reported (error bit 16) and
     its row skipped; every other row lands."""
