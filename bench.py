@@ -5,7 +5,9 @@ stride in pinned host memory, in a seeded random order, into one contiguous
 HBM buffer.  Also measured in the same run: 2048 x 64 KiB (KV-cache pages),
 2048 x {512 B, 1 KiB, 2 KiB}, the contiguous-copy link peak, per-token
 hipMemcpyAsync, the CPU ParallelGather restatement on the host cores, and the
-reverse path (offload of the same layouts from HBM to pinned host).
+reverse path (offload of the same layouts from HBM to pinned host).  The
+zero-copy kernel's HBM-side traffic comes from two rocprofv3 --pmc passes run
+as child processes at the end (about 30 s).
 Timing: W warm-up + K timed iterations, P50 (examples/04_benchmark.cu:58-90).
 GB/s = bytes / (us * 1e3).
 
@@ -15,9 +17,15 @@ Prints ONE JSON line on stdout; progress goes to stderr.
 """
 import argparse
 import ctypes
+import csv
+import glob
 import json
 import os
+import shutil
+import signal
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -33,7 +41,8 @@ PCIE_GEN5_X16_GBPS = 32.0 * 16 * 128.0 / 130.0 / 8.0  # 63.0 GB/s per direction
 # rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of `bench.py --only zc,calib`,
 # each scaled by the same counter on a 32 MiB device-to-device copy
 # (FETCH x 1.99853, WRITE x 1.0).  Reads are host-link reads through the L2's
-# external interface; writes land in HBM.
+# external interface; writes land in HBM.  A default run measures them again
+# (measure_traffic); these profiled values stand in only if that fails.
 ZC_TRAFFIC_8192x4KB = {"read_bytes": 32891 * 1024, "write_bytes": 32772 * 1024}
 METRIC = "scattered H2D GB/s + % of PCIe5 x16 peak at 8192x4KB and 2048x64KB"
 DIRECT_ZC_MAX = 8 << 20  # submit_direct's default zero-copy route limit (bytes)
@@ -542,6 +551,79 @@ def session_timeline(lists, blocks, nlists):
             "claim_to_ready_mean_us": round(float(np.mean(us(u["ready"]) - us(u["claimed"]))), 2)}
 
 
+def _pmc_pass(exe, counter, workdir, timeout_s):
+    """One rocprofv3 --pmc pass over `bench.py --only zc,calib` (5 device-to-
+    device copies of 32 MiB, then 12 launches of the 8192 x 4 KiB gather), in
+    its own process group under a time limit.  Per-dispatch counter values
+    (KiB): (calibration copies, gather launches), or a reason string."""
+    out = os.path.join(workdir, counter)
+    cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "p", "--", sys.executable,
+           os.path.join(ROOT, "bench.py"), "--only", "zc,calib", "--cpu-seconds", "0", "--steps", "5", "--warmup", "1"]
+    env = dict(os.environ, TMPDIR="/tmp")
+    with open(os.path.join(workdir, counter + ".log"), "w") as logf:
+        p = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=logf, stderr=subprocess.STDOUT, start_new_session=True)
+        try:
+            rc = p.wait(timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            os.killpg(p.pid, signal.SIGKILL)
+            p.wait()
+            return "%s pass did not finish in %d s" % (counter, timeout_s)
+    files = glob.glob(os.path.join(out, "**", "p_counter_collection.csv"), recursive=True)
+    if not files:
+        return "%s pass wrote no counter file (exit %d)" % (counter, rc)
+    copies, gathers = [], []
+    with open(files[0]) as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") != counter:
+                continue
+            name, v = row["Kernel_Name"], float(row["Counter_Value"])
+            if "copyBuffer" in name:
+                copies.append((int(row["Dispatch_Id"]), v))
+            elif "zc_gather_tokens" in name:
+                gathers.append((int(row["Grid_Size"]), v))
+    # The calibration copies run before anything else that could use the
+    # runtime's copy kernel: the first five dispatches of it.  The gathers:
+    # the launches of the 8192 x 4 KiB job, the largest grid (the poller's
+    # set-up also launches the kernel once on 16 bytes).
+    copies = [v for _, v in sorted(copies)[:5]]
+    big = max((g for g, _ in gathers), default=0)
+    gathers = [v for g, v in gathers if g == big]
+    if len(copies) < 5 or not gathers:
+        return "%s pass: %d calibration copies, %d gathers counted (exit %d)" % (counter, len(copies),
+                                                                                 len(gathers), rc)
+    return copies, gathers
+
+
+def measure_traffic(timeout_s=150):
+    """HBM-side traffic of one 8192 x 4 KiB zc_gather_tokens launch, measured
+    in this run: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) from two
+    rocprofv3 --pmc passes, each scaled by the same counter on a 32 MiB
+    device-to-device copy of known size.  (read_bytes, write_bytes, detail) or
+    (None, None, reason)."""
+    exe = shutil.which("rocprofv3")
+    if not exe:
+        return None, None, "rocprofv3 not on PATH"
+    with tempfile.TemporaryDirectory(dir="/tmp") as td:
+        got = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            log("traffic: rocprofv3 --pmc %s pass ..." % counter)
+            r = _pmc_pass(exe, counter, td, timeout_s)
+            if isinstance(r, str):
+                return None, None, r
+            got[counter] = r
+    detail = {}
+    val = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        copies, gathers = got[counter]
+        cal = float(np.median(copies))
+        scale = 32768.0 / cal  # KiB the 32 MiB copy moves through that interface per KiB counted
+        val[counter] = float(np.mean(gathers)) * scale * 1024.0
+        detail[counter] = {"gather_kib_per_dispatch": round(float(np.mean(gathers)), 2),
+                           "gather_dispatches": len(gathers), "copy_kib_per_dispatch": round(cal, 2),
+                           "scale": round(scale, 5)}
+    return int(round(val["FETCH_SIZE"])), int(round(val["WRITE_SIZE"])), detail
+
+
 def run_offload(oracle, iters, warmup):
     """Offload (HBM -> pinned host, the reverse path): n tokens contiguous in
     HBM written to the seeded 2x-stride slots of a pinned host region by the
@@ -870,7 +952,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="",
                     help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions,scattered,offload,"
-                         "firstcall,helpers,timeline (helpers and timeline are not in the default run) "
+                         "firstcall,pmc,helpers,timeline (helpers and timeline are not in the default run; pmc: "
+                         "the two rocprofv3 --pmc passes behind roofline.traffic, with zc) "
                          "(calib: add a 32 MiB D2D copy)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -1003,20 +1086,32 @@ def main():
         ach = zc["kernel_GBps"]
         alg_read = r_main["bytes"] + 8 * r_main["tokens"]  # tokens over the host link + the page table
         alg_write = r_main["bytes"]                         # tokens into HBM
-        meas = ZC_TRAFFIC_8192x4KB["read_bytes"] + ZC_TRAFFIC_8192x4KB["write_bytes"]
+        # traffic: bytes through the L2's memory interface per launch (reads: host-link reads + page
+        # table; writes: HBM), measured in this run by two rocprofv3 --pmc passes when the default
+        # run asks for them; algorithmic_traffic is the same sum of the algorithmic bytes.
+        rd, wr, tdetail = (None, None, "not measured in this run (bench.py --only without pmc)")
+        if want("pmc"):
+            rd, wr, tdetail = measure_traffic()
+            log("traffic:", rd, wr, tdetail)
+        if rd is not None:
+            source = "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes of this run, each scaled by a 32 MiB D2D copy"
+        else:
+            source = ("profiles/zc_gather_tokens_8192x4KB.md (an earlier run's --pmc passes); this run: %s"
+                      % tdetail)
+            rd, wr, tdetail = ZC_TRAFFIC_8192x4KB["read_bytes"], ZC_TRAFFIC_8192x4KB["write_bytes"], None
+        meas = rd + wr
         roofline = {"bound": "pcie", "kernel": "zc_gather_tokens", "achieved": ach,
                     "peak": round(PCIE_GEN5_X16_GBPS, 2), "unit": "GB/s",
                     "frac": round(ach / PCIE_GEN5_X16_GBPS, 4),
-                    # traffic: bytes through the L2's memory interface per launch (reads: host-link
-                    # reads + page table; writes: HBM), from the FETCH_SIZE / WRITE_SIZE runs in
-                    # profiles/; algorithmic_traffic is the same sum of the algorithmic bytes.
                     "traffic": meas,
+                    "traffic_source": source,
                     "algorithmic_traffic": alg_read + alg_write,
                     "traffic_over_algorithmic": round(meas / (alg_read + alg_write), 4),
-                    "traffic_detail": dict(ZC_TRAFFIC_8192x4KB, algorithmic_read=alg_read,
+                    "traffic_detail": dict(read_bytes=rd, write_bytes=wr, algorithmic_read=alg_read,
                                            algorithmic_write=alg_write,
-                                           read_over_algorithmic=round(ZC_TRAFFIC_8192x4KB["read_bytes"] / alg_read, 4),
-                                           write_over_algorithmic=round(ZC_TRAFFIC_8192x4KB["write_bytes"] / alg_write, 4)),
+                                           read_over_algorithmic=round(rd / alg_read, 4),
+                                           write_over_algorithmic=round(wr / alg_write, 4),
+                                           counters=tdetail),
                     "peak_measured": peak_meas,
                     "frac_of_measured": round(ach / peak_meas, 4) if peak_meas else None,
                     "algorithmic_bytes_per_launch": r_main["bytes"],
