@@ -261,7 +261,7 @@ private:
     uint32_t trace_cap_ = 0;
 };
 
-// The reference's spelling in the north-star text.
+// The spelling SgWarpSpecSession, which callers also use for this class.
 using SgWarpSpecSession = SGWarpSpecSession;
 
 }  // namespace gfd
