@@ -627,9 +627,9 @@ def measure_traffic(timeout_s=150):
 def run_offload(oracle, iters, warmup):
     """Offload (HBM -> pinned host, the reverse path): n tokens contiguous in
     HBM written to the seeded 2x-stride slots of a pinned host region by the
-    zero-copy scatter kernel; checked against the oracle's closed form.  The
-    link reference is one contiguous device->host hipMemcpyAsync of the same
-    bytes."""
+    zero-copy scatter kernel, and again as SG lists through a session;
+    checked against the oracle's closed form.  The link reference is one
+    contiguous device->host hipMemcpyAsync of the same bytes."""
     out = {}
     for n, t in ((8192, 4096), (2048, 65536)):
         nbytes, stride = n * t, 2 * t
@@ -655,12 +655,26 @@ def run_offload(oracle, iters, warmup):
         assert rc == 0, gfd_amd.lib().gfd_last_error()
         d2h = gbps(nbytes, p50(tc))
         k_gbps = gbps(nbytes, float(ev.mean()))
+        # The same eviction as host-submitted SG lists drained by a running
+        # session's transfer waves (lists of 128 tokens; launch until the host
+        # has seen every list's done marker).
+        host.array[:] = 0xCD
+        epl = 128 if n >= 4096 else 32
+        ent = gfd_amd.device_sg_entries(src.ptr + np.arange(n, dtype=np.uint64) * np.uint64(t),
+                                        host.ptr + perm.astype(np.uint64) * np.uint64(stride), t)
+        sess = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=0, idle_limit_ms=10000)
+        sus = sess.bench(ent, epl, warmup=warmup, iters=iters)
+        sst = sess.stats()
+        sess.close()
+        assert np.array_equal(host.array, want_region), "session offload %dx%d: bytes differ" % (n, t)
         out["%dx%d" % (n, t)] = {
             "bytes": nbytes, "zero_copy_scatter": {
                 "us_p50": round(p50(wall), 2), "GBps": round(gbps(nbytes, p50(wall)), 3),
                 "kernel_us_mean": round(float(ev.mean()), 2), "kernel_GBps": round(k_gbps, 3),
                 "of_theoretical": round(k_gbps / PCIE_GEN5_X16_GBPS, 4),
                 "of_d2h_contiguous": round(k_gbps / d2h, 4) if d2h else None},
+            "sg_session": {"us_p50": round(p50(sus), 2), "GBps": round(gbps(nbytes, p50(sus)), 3),
+                           "lists": n // epl, "grid": sst["grid"]},
             "d2h_contiguous_GBps": round(d2h, 3)}
         log("  offload %dx%d: %s" % (n, t, out["%dx%d" % (n, t)]))
         for b in (src, host, table, contig):

@@ -268,6 +268,39 @@ def test_sg_ragged_lists_checksum(blocks, compute, helpers):
     s.close()
 
 
+@pytest.mark.parametrize("blocks,helpers,t", [(0, 0, 4096), (4, 3, 4096), (0, 0, 1000)])
+def test_sg_session_offload_lists(blocks, helpers, t):
+    """Eviction through the SG session: host-submitted lists whose entries
+    copy tokens from HBM (contiguous, token j at j*T) to scattered slots of a
+    pinned host region (token j at perm[j]*2T), the reverse of the usual
+    direction; no reference counterpart.  Every byte of the region is checked
+    against the oracle's offload closed form, the gaps kept."""
+    n = 2048
+    log("sg offload lists blocks=%d helpers=%d T=%d" % (blocks, helpers, t))
+    rng = np.random.default_rng(7 + t)
+    toks = rng.integers(0, 256, n * t, dtype=np.uint8)
+    src = gfd_amd.DeviceBuffer(n * t)
+    src.upload(toks)
+    region = gfd_amd.HostBuffer(2 * n * t)
+    region.array[:] = SENTINEL
+    before = region.array.copy()
+    perm = oracle.permutation(n)
+    ent = entries_array(src.ptr + np.arange(n, dtype=np.uint64) * np.uint64(t),
+                        region.ptr + perm.astype(np.uint64) * np.uint64(2 * t), t)
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=blocks, idle_limit_ms=5000, helper_waves=helpers)
+    try:
+        for lid in range(16):
+            s.submit_sg_list(ent[lid * 128:(lid + 1) * 128], list_id=lid)
+        s.launch()
+        s.synchronize()
+        want = oracle.expected_scatter(before, toks, perm, t, 2 * t)
+        assert (region.array == want).all()
+        st = s.stats()
+        assert st["units_done"] == n and st["bytes"] == n * t and st["lists_done"] == 16 and st["error_bits"] == 0
+    finally:
+        s.close()
+
+
 def test_sg_empty_and_tiny_lists_with_helpers():
     """Lists with fewer batches than transfer waves (empty, 1 entry, 65
     entries) keep every helper's acknowledgement in step."""
