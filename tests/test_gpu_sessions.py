@@ -445,3 +445,34 @@ def test_sg_gpu_submit(blocks, n_lists, epl, t, helpers):
     st = s.stats()
     assert st["lists_done"] == n_lists and st["units_done"] == n and st["error_bits"] == 0
     s.close()
+
+
+@pytest.mark.parametrize("blocks,helpers", [(0, 0), (8, 3)])
+def test_sg_gpu_submit_offload(blocks, helpers):
+    """Eviction lists posted by GPU submitter waves (test/test_sg_gpu_submit.cu's
+    pattern with the copy direction reversed; no reference counterpart): 64
+    lists of 32 entries, each a 4 KiB token from HBM to its scattered slot in
+    a pinned host region.  Every byte of the region against the oracle."""
+    n_lists, epl, t = 64, 32, 4096
+    n = n_lists * epl
+    log("sg gpu submit offload blocks=%d helpers=%d" % (blocks, helpers))
+    toks = np.random.default_rng(3).integers(0, 256, n * t, dtype=np.uint8)
+    src = gfd_amd.DeviceBuffer(n * t)
+    src.upload(toks)
+    region = gfd_amd.HostBuffer(2 * n * t)
+    region.array[:] = SENTINEL
+    before = region.array.copy()
+    perm = oracle.permutation(n)
+    arr = entries_array(src.ptr + np.arange(n, dtype=np.uint64) * np.uint64(t),
+                        region.ptr + perm.astype(np.uint64) * np.uint64(2 * t), t)
+    d_ent = gfd_amd.DeviceBuffer(arr.nbytes)
+    d_ent.upload(arr.view(np.uint8))
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=blocks, idle_limit_ms=5000, helper_waves=helpers)
+    try:
+        s.launch_gpu_submit(d_ent.ptr, epl, n_lists)
+        s.synchronize(extra_gpu_lists=n_lists)
+        assert (region.array == oracle.expected_scatter(before, toks, perm, t, 2 * t)).all()
+        st = s.stats()
+        assert st["lists_done"] == n_lists and st["units_done"] == n and st["error_bits"] == 0
+    finally:
+        s.close()
