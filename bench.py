@@ -686,7 +686,8 @@ def run_sessions(oracle, iters, warmup):
     """Wave-specialised sessions.  WarpSpecSession on linear tiles (token t at
     cpu_src + t*T -> gpu_dst + t*T; T = 128 tokens, automatic chunking, no-op
     consumer), single and double buffered: 8192 x 16 KiB = 128 MiB (the shape
-    of the reference's warp-spec example) and 8192 x 4 KiB.  SGWarpSpecSession
+    of the reference's warp-spec example) and 8192 x 4 KiB; the 128 MiB shape
+    again with the example's RMSNorm + sinf consumer.  SGWarpSpecSession
     (no-op consumer) on 16384 scattered 4 KiB tokens (2x stride, Fisher-Yates
     order) = 64 MiB in 128 host-submitted lists of 128 entries, timed from
     the launch until the host sees every list's done marker.  Every output is
@@ -708,6 +709,41 @@ def run_sessions(oracle, iters, warmup):
                         "chunks_per_tile": res["chunks_per_tile"]}
             log("  %s: %s" % (key, out[key]))
         del host, dst
+    # The reference's warp-spec example with its RMSNorm + sinf consumer
+    # (examples/07_warp_spec_simple.cu: 8192 tokens of 4096 floats): seeded
+    # standard-normal floats, the per-token result checked against float64.
+    n, t = 8192, 16384
+    nf = t // 4
+    host = gfd_amd.HostBuffer(n * t)
+    xs = np.random.default_rng(7).standard_normal(n * nf).astype(np.float32)
+    host.array.view(np.float32)[:] = xs
+    dst = gfd_amd.DeviceBuffer(n * t)
+    outb = gfd_amd.DeviceBuffer(n * 4)
+    x64 = xs.reshape(n, nf).astype(np.float64)
+    y64 = x64 / np.sqrt(np.mean(x64 * x64, axis=1) + 1e-6)[:, None]
+    terms = np.sin(y64) * y64
+    want, mag = terms.sum(axis=1), np.abs(terms).sum(axis=1)
+    del x64, y64, terms
+    # Two tile shapes: 64-token tiles of 8-token chunks, single buffered (the
+    # best of a sweep: the consumer's work left after the last chunk lands is
+    # smallest), and the example's own 128-token tiles of 32-token chunks,
+    # double buffered.
+    for key, tile, chunk, db in (("warp_spec_%dx%dKB_rms_sin" % (n, t // 1024), 64, 8, False),
+                                 ("warp_spec_%dx%dKB_rms_sin_example_shape_db" % (n, t // 1024), 128, 32, True)):
+        dst.fill(0)
+        outb.fill(0)
+        res, kms = gfd_amd.warp_spec_run_rms_sin(host.ptr, dst.ptr, n, t, outb.ptr, tile, chunk, db,
+                                                 iters=warmup + iters)
+        got = outb.download().view(np.float32).astype(np.float64)
+        if not (dst.download() == host.array).all() or not np.all(np.abs(got - want) <= 1e-4 * mag + 1e-6):
+            raise SystemExit("PARITY FAILURE: WarpSpecSession RMSNorm + sinf (%s)" % key)
+        us = kms[warmup:] * 1000.0
+        out[key] = {"bytes": n * t, "kernel_us_p50": round(p50(us), 2), "GBps": round(gbps(n * t, p50(us)), 3),
+                    "grid": res["grid"], "block": res["block"], "tokens_per_tile": tile,
+                    "tokens_per_chunk": res["tokens_per_chunk"], "chunks_per_tile": res["chunks_per_tile"],
+                    "double_buffer": db}
+        log("  %s: %s" % (key, out[key]))
+    del host, dst, outb
     n, t, epl = 16384, 4096, 128
     host = gfd_amd.HostBuffer(n * 2 * t)
     oracle.fill_tokens(host.array, n, t, 2 * t)

@@ -191,6 +191,8 @@ def _declare(L):
         "gfd_bench_queue": ([vp, vp, vp, c_int, c_u32, ctypes.POINTER(c_u64), c_int, c_int, c_u64, pd], c_int),
         "gfd_warp_spec_run": ([vp, vp, c_u32, c_u32, c_u32, c_u32, c_int, c_int, c_int, c_int, vp, c_int, pd,
                                ctypes.POINTER(SessionResult)], c_int),
+        "gfd_warp_spec_run_rms_sin": ([vp, vp, c_u32, c_u32, c_u32, c_u32, c_int, c_int, c_int, vp, c_int, pd,
+                                       ctypes.POINTER(SessionResult)], c_int),
         "gfd_sg_session_create": ([c_int, c_int, c_u32, c_int, pvp], c_int),
         "gfd_sg_session_destroy": ([vp], None),
         "gfd_sg_session_submit": ([vp, vp, c_u32, c_u32, c_u32], ctypes.c_int64),
@@ -633,6 +635,21 @@ def warp_spec_run(cpu_src, gpu_dst, total_tokens, token_size, tokens_per_tile=12
                                    token_sums, iters,
                                    times.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), ctypes.byref(res)),
            "gfd_warp_spec_run")
+    return res.as_dict(), times
+
+
+def warp_spec_run_rms_sin(cpu_src, gpu_dst, total_tokens, token_size, out, tokens_per_tile=128,
+                          tokens_per_chunk=0, double_buffer=False, num_blocks=0, iters=1, helper_waves=-1):
+    """warp_spec_run with the RMSNorm + sinf consumer of the reference's
+    examples/07_warp_spec_simple.cu (out: device float[total_tokens], token t
+    -> sum of sin(x r) x r over its floats, r = 1/sqrt(mean(x^2) + 1e-6)).
+    Returns (result dict, kernel times in ms)."""
+    res = SessionResult()
+    times = np.zeros(max(iters, 1), dtype=np.float64)
+    _check(lib().gfd_warp_spec_run_rms_sin(cpu_src, gpu_dst, total_tokens, token_size, tokens_per_tile,
+                                           tokens_per_chunk, int(bool(double_buffer)), num_blocks, helper_waves, out,
+                                           iters, times.ctypes.data_as(ctypes.POINTER(ctypes.c_double)),
+                                           ctypes.byref(res)), "gfd_warp_spec_run_rms_sin")
     return res.as_dict(), times
 
 

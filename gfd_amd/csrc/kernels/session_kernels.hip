@@ -62,6 +62,44 @@ struct TokenSum {
     }
 };
 
+// out[global token] = sum over the token's floats x of sin(x r) x r, with
+// r = 1 / sqrt(mean(x^2) + 1e-6): the RMSNorm + sinf consumer of
+// examples/07_warp_spec_simple.cu:35-58 (VectorReduce).  There one lane
+// walks a whole token twice; here the wave shares each token, lane-strided
+// 16-byte loads from HBM for both passes, with wave sums in between.
+struct TokenRmsSin {
+    float* out;
+    __device__ void operator()(ChunkView c) const {
+        const uint32_t nf = c.token_size / 4;
+        for (uint32_t i = 0; i < c.size; i++) {
+            const float* t = c.data<float>((int)i);
+            // Whole float4 vectors where the token is 16-byte aligned; the
+            // rest (or all of an unaligned token) one float at a time.
+            const uint32_t nv = ((uintptr_t)t & 15) == 0 ? nf / 4 : 0;
+            const float4* t4 = reinterpret_cast<const float4*>(t);
+            float ss = 0.f;
+            for (uint32_t k = (uint32_t)c.lane_id; k < nv; k += 64) {
+                const float4 v = t4[k];
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+            for (uint32_t k = nv * 4 + (uint32_t)c.lane_id; k < nf; k += 64) ss += t[k] * t[k];
+            const float r = rsqrtf(wave_sum(ss) / (float)nf + 1e-6f);
+            float acc = 0.f;
+            for (uint32_t k = (uint32_t)c.lane_id; k < nv; k += 64) {
+                const float4 v = t4[k];
+                const float a = v.x * r, b = v.y * r, d = v.z * r, e = v.w * r;
+                acc += sinf(a) * a + sinf(b) * b + sinf(d) * d + sinf(e) * e;
+            }
+            for (uint32_t k = nv * 4 + (uint32_t)c.lane_id; k < nf; k += 64) {
+                const float a = t[k] * r;
+                acc += sinf(a) * a;
+            }
+            acc = wave_sum(acc);
+            if (c.lane_id == 0) out[c.global_idx((int)i)] = acc;
+        }
+    }
+};
+
 struct NullChunk {
     __device__ void operator()(ChunkView) const {}
 };
@@ -122,6 +160,8 @@ struct EntryL2Norm {
 
 GFD_WARP_SPEC_KERNEL(ws_token_sum_kernel, TokenSum)
 GFD_WARP_SPEC_KERNEL_DB(ws_token_sum_kernel_db, TokenSum)
+GFD_WARP_SPEC_KERNEL(ws_rms_sin_kernel, TokenRmsSin)
+GFD_WARP_SPEC_KERNEL_DB(ws_rms_sin_kernel_db, TokenRmsSin)
 GFD_WARP_SPEC_KERNEL(ws_null_kernel, NullChunk)
 GFD_WARP_SPEC_KERNEL_DB(ws_null_kernel_db, NullChunk)
 GFD_SG_WARP_SPEC_KERNEL(sg_checksum_kernel, ListChecksum)
@@ -189,11 +229,17 @@ gfd::SGWarpSpecSession* S(gfd_sg_session_t s) { return static_cast<gfd::SGWarpSp
 
 }  // namespace
 
-extern "C" int gfd_warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t total_tokens, uint32_t token_size,
-                                 uint32_t tokens_per_tile, uint32_t tokens_per_chunk, int double_buffer,
-                                 int per_tile_mode, int num_blocks, int helper_waves, float* token_sums, int iters,
-                                 double* kernel_ms, gfd_session_result* res) {
-    if (!cpu_src || !gpu_dst || total_tokens == 0 || token_size == 0 || iters < 1 || !res)
+namespace {
+
+// The consumers gfd_warp_spec_run can launch.
+enum WsConsumer { kWsNull, kWsTokenSum, kWsRmsSin };
+
+int warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t total_tokens, uint32_t token_size,
+                  uint32_t tokens_per_tile, uint32_t tokens_per_chunk, int double_buffer, int per_tile_mode,
+                  int num_blocks, int helper_waves, WsConsumer consumer, float* out, int iters, double* kernel_ms,
+                  gfd_session_result* res) {
+    if (!cpu_src || !gpu_dst || total_tokens == 0 || token_size == 0 || iters < 1 || !res ||
+        (consumer != kWsNull && !out))
         return fail(hipErrorInvalidValue, "gfd_warp_spec_run: invalid argument");
     gfd::WarpSpecConfig c;
     c.total_tokens = total_tokens;
@@ -222,13 +268,20 @@ extern "C" int gfd_warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t to
         // clears the signals with a blocking memset first.
         s.before_launch(nullptr);
         (void)hipEventRecord(e0, nullptr);
-        if (token_sums) {
+        if (consumer == kWsTokenSum) {
             if (c.double_buffer)
                 hipLaunchKernelGGL(ws_token_sum_kernel_db, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
-                                   p.cpu_base, TokenSum{token_sums});
+                                   p.cpu_base, TokenSum{out});
             else
                 hipLaunchKernelGGL(ws_token_sum_kernel, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
-                                   p.cpu_base, TokenSum{token_sums});
+                                   p.cpu_base, TokenSum{out});
+        } else if (consumer == kWsRmsSin) {
+            if (c.double_buffer)
+                hipLaunchKernelGGL(ws_rms_sin_kernel_db, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
+                                   p.cpu_base, TokenRmsSin{out});
+            else
+                hipLaunchKernelGGL(ws_rms_sin_kernel, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
+                                   p.cpu_base, TokenRmsSin{out});
         } else {
             if (c.double_buffer)
                 hipLaunchKernelGGL(ws_null_kernel_db, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
@@ -250,6 +303,27 @@ extern "C" int gfd_warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t to
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     return rc;
+}
+
+}  // namespace
+
+extern "C" int gfd_warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t total_tokens, uint32_t token_size,
+                                 uint32_t tokens_per_tile, uint32_t tokens_per_chunk, int double_buffer,
+                                 int per_tile_mode, int num_blocks, int helper_waves, float* token_sums, int iters,
+                                 double* kernel_ms, gfd_session_result* res) {
+    return warp_spec_run(cpu_src, gpu_dst, total_tokens, token_size, tokens_per_tile, tokens_per_chunk, double_buffer,
+                         per_tile_mode, num_blocks, helper_waves, token_sums ? kWsTokenSum : kWsNull, token_sums,
+                         iters, kernel_ms, res);
+}
+
+extern "C" int gfd_warp_spec_run_rms_sin(const void* cpu_src, void* gpu_dst, uint32_t total_tokens,
+                                         uint32_t token_size, uint32_t tokens_per_tile, uint32_t tokens_per_chunk,
+                                         int double_buffer, int num_blocks, int helper_waves, float* out, int iters,
+                                         double* kernel_ms, gfd_session_result* res) {
+    if (token_size % 4 != 0)
+        return fail(hipErrorInvalidValue, "gfd_warp_spec_run_rms_sin: tokens must be whole floats");
+    return warp_spec_run(cpu_src, gpu_dst, total_tokens, token_size, tokens_per_tile, tokens_per_chunk, double_buffer,
+                         0, num_blocks, helper_waves, kWsRmsSin, out, iters, kernel_ms, res);
 }
 
 extern "C" int gfd_sg_session_create(int num_compute_warps, int num_blocks, uint32_t idle_limit_ms, int helper_waves,

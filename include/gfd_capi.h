@@ -364,6 +364,13 @@ int gfd_warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t total_tokens,
                       uint32_t tokens_per_tile, uint32_t tokens_per_chunk, int double_buffer,
                       int per_tile_mode, int num_blocks, int helper_waves, float* token_sums, int iters,
                       double* kernel_ms, gfd_session_result* res);
+/* The same run with the RMSNorm + sinf consumer of
+ * examples/07_warp_spec_simple.cu:35-58 (VectorReduce): out[t] = sum over
+ * token t's floats x of sin(x r) x r, r = 1 / sqrt(mean(x^2) + 1e-6), in
+ * fp32 (device float[total_tokens]).  token_size a multiple of 4; chunk mode. */
+int gfd_warp_spec_run_rms_sin(const void* cpu_src, void* gpu_dst, uint32_t total_tokens, uint32_t token_size,
+                              uint32_t tokens_per_tile, uint32_t tokens_per_chunk, int double_buffer, int num_blocks,
+                              int helper_waves, float* out, int iters, double* kernel_ms, gfd_session_result* res);
 
 typedef void* gfd_sg_session_t;
 /* SGWarpSpecSession(SGWarpSpecConfig{num_compute_warps, num_blocks}); idle_limit_ms

@@ -167,6 +167,44 @@ def test_warp_spec_helper_waves_token_sums():
     assert res["helper_waves"] == 3 and res["error_bits"] == 0
 
 
+def rms_sin_reference(tokens):
+    """examples/07_warp_spec_simple.cu:35-58 in float64: per token,
+    sum of sin(x r) x r with r = 1/sqrt(mean(x^2) + 1e-6); also the sum of
+    the terms' magnitudes, which bounds fp32 rounding."""
+    x = tokens.astype(np.float64)
+    r = 1.0 / np.sqrt(np.mean(x * x, axis=1) + 1e-6)
+    y = x * r[:, None]
+    terms = np.sin(y) * y
+    return terms.sum(axis=1), np.abs(terms).sum(axis=1)
+
+
+@pytest.mark.parametrize("total,ts,tile,chunk,db", [(256, 16384, 128, 32, False), (256, 16384, 128, 32, True),
+                                                    (200, 4100, 64, 16, False), (128, 256, 64, 16, True)])
+def test_warp_spec_rms_sin(total, ts, tile, chunk, db):
+    """The RMSNorm + sinf consumer of examples/07_warp_spec_simple.cu through
+    WarpSpecSession: every landed token's bytes, and out[t] within fp32
+    rounding of a float64 restatement (tolerance 1e-4 of the sum of the
+    terms' magnitudes).  Tokens past the last whole tile are not moved and
+    their out slots stay untouched."""
+    log("warp spec rms+sin total=%d ts=%d tile=%d chunk=%d db=%d" % (total, ts, tile, chunk, db))
+    nf = ts // 4
+    host = gfd_amd.HostBuffer(total * ts)
+    host.array.view(np.float32)[:] = np.random.default_rng(ts + total).standard_normal(total * nf).astype(np.float32)
+    dst = gfd_amd.DeviceBuffer(total * ts)
+    dst.fill(0)
+    out = gfd_amd.DeviceBuffer(total * 4)
+    out.fill(0xCD)
+    res, _ = gfd_amd.warp_spec_run_rms_sin(host.ptr, dst.ptr, total, ts, out.ptr, tile, chunk, db)
+    moved = (total // tile) * tile
+    assert res["error_bits"] == 0 and res["units_done"] == moved
+    assert (dst.download()[:moved * ts] == host.array[:moved * ts]).all()
+    got = out.download()
+    want, mag = rms_sin_reference(host.array.view(np.float32).reshape(total, nf)[:moved])
+    y = got[:moved * 4].view(np.float32).astype(np.float64)
+    assert np.all(np.abs(y - want) <= 1e-4 * mag + 1e-6), np.max(np.abs(y - want) / (mag + 1e-30))
+    assert (got[moved * 4:] == 0xCD).all()
+
+
 def test_warp_spec_rejects_oversized_block():
     host = gfd_amd.HostBuffer(4096 * 64)
     dst = gfd_amd.DeviceBuffer(4096 * 64)
