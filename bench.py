@@ -370,6 +370,38 @@ def direct_timeline(poller, L, calls=20):
                                      for e in engines}}
 
 
+# The reference's published Direct points (README.md:60-65 and 86-89; in-order
+# tokens at 2x stride, RTX PRO 5000, P50 of 50): tokens -> microseconds.
+REFERENCE_DIRECT_4KB_US = {16: 9.7, 64: 14.2, 256: 31.0, 1024: 91.7, 2048: 170.2, 4096: 328.3, 8192: 645.0}
+REFERENCE_DIRECT_64KB_US = {16: 41.4, 64: 96.7, 256: 360.8, 1024: 1269.0, 2048: 2534.8}
+
+
+def run_direct_sizes(oracle, poller, iters, warmup):
+    """submit_direct over the token counts the reference publishes (4 KiB
+    tokens: 16 ... 4096; 64 KiB tokens: 16 ... 1024), on the bench's layout
+    (seeded random order, 2x stride), each checked byte-exact; the
+    reference's figure beside each."""
+    out = {}
+    for t, ref in ((4096, REFERENCE_DIRECT_4KB_US), (65536, REFERENCE_DIRECT_64KB_US)):
+        row = {}
+        for n in sorted(ref):
+            if (t == 4096 and n == 8192) or (t == 65536 and n == 2048):
+                continue  # the main configurations, measured above
+            L = Layout(oracle, n, t)
+            tt = np.zeros(iters)
+            rc = gfd_amd.lib().gfd_bench_submit_direct(poller._h, ctypes.cast(L.entries, ctypes.c_void_p), n, warmup,
+                                                       iters, tt.ctypes.data_as(PD))
+            assert rc == 0, gfd_amd.lib().gfd_last_error()
+            L.verify("direct %d x %d" % (n, t))
+            row[str(n)] = {"us_p50": round(p50(tt), 2), "GBps": round(gbps(n * t, p50(tt)), 3),
+                           "route": "zero-copy kernel" if n * t <= DIRECT_ZC_MAX else "staged SDMA + zero-copy head",
+                           "reference_us": ref[n], "reference_GBps": round(gbps(n * t, ref[n]), 2)}
+            del L
+        out["%dKB" % (t // 1024)] = row
+        log("  direct sizes %d KiB: %s" % (t // 1024, {k: v["us_p50"] for k, v in row.items()}))
+    return out
+
+
 def run_direct_scattered(oracle, poller, iters, warmup):
     """GFD Direct with non-contiguous destinations, 8192 x 4 KiB tokens
     (scattered sources as in the main layout): 'pages' = a paged KV cache,
@@ -1002,7 +1034,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="",
                     help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions,scattered,offload,"
-                         "firstcall,pmc,helpers,timeline (helpers and timeline are not in the default run; pmc: "
+                         "firstcall,sizes,pmc,helpers,timeline (helpers and timeline are not in the default run; pmc: "
                          "the two rocprofv3 --pmc passes behind roofline.traffic, with zc) "
                          "(calib: add a 32 MiB D2D copy)")
     args = ap.parse_args()
@@ -1078,6 +1110,10 @@ def main():
     r_scat = None
     if want("direct") and want("scattered"):
         r_scat = run_direct_scattered(oracle, direct, K, W)
+    r_sizes = None
+    if want("direct") and want("sizes"):
+        log("direct at the reference's published token counts ...")
+        r_sizes = run_direct_sizes(oracle, direct, K, W)
     direct.close()
 
     r_sessions = None
@@ -1197,6 +1233,7 @@ def main():
         "results_8192x4KB": r_main, "results_2048x64KB": r_kv, "results_small": r_small, "results_sg_moe": r_moe,
         "results_sessions": r_sessions,
         "results_direct_scattered_dst_8192x4KB": r_scat,
+        "results_direct_sizes": r_sizes,
         "results_offload": r_offload,
         "results_helper_waves": r_helpers,
         "results_timeline": r_timeline,
