@@ -603,8 +603,22 @@ def _pmc_pass(exe, counter, workdir, timeout_s):
     files = glob.glob(os.path.join(out, "**", "p_counter_collection.csv"), recursive=True)
     if not files:
         return "%s pass wrote no counter file (exit %d)" % (counter, rc)
+    copies, gathers = parse_pmc_counters(files[0], counter)
+    if len(copies) < 5 or not gathers:
+        return "%s pass: %d calibration copies, %d gathers counted (exit %d)" % (counter, len(copies),
+                                                                                 len(gathers), rc)
+    return copies, gathers
+
+
+def parse_pmc_counters(path, counter):
+    """Per-dispatch values of `counter` in a rocprofv3 counter_collection.csv:
+    (the calibration copies, the gather launches).  The calibration copies
+    run before anything else that could use the runtime's copy kernel: the
+    first five dispatches of it.  The gathers: the launches of the 8192 x 4
+    KiB job, the largest grid (the poller's set-up also launches the kernel
+    once on 16 bytes)."""
     copies, gathers = [], []
-    with open(files[0]) as f:
+    with open(path) as f:
         for row in csv.DictReader(f):
             if row.get("Counter_Name") != counter:
                 continue
@@ -613,17 +627,9 @@ def _pmc_pass(exe, counter, workdir, timeout_s):
                 copies.append((int(row["Dispatch_Id"]), v))
             elif "zc_gather_tokens" in name:
                 gathers.append((int(row["Grid_Size"]), v))
-    # The calibration copies run before anything else that could use the
-    # runtime's copy kernel: the first five dispatches of it.  The gathers:
-    # the launches of the 8192 x 4 KiB job, the largest grid (the poller's
-    # set-up also launches the kernel once on 16 bytes).
     copies = [v for _, v in sorted(copies)[:5]]
     big = max((g for g, _ in gathers), default=0)
-    gathers = [v for g, v in gathers if g == big]
-    if len(copies) < 5 or not gathers:
-        return "%s pass: %d calibration copies, %d gathers counted (exit %d)" % (counter, len(copies),
-                                                                                 len(gathers), rc)
-    return copies, gathers
+    return copies, [v for g, v in gathers if g == big]
 
 
 def measure_traffic(timeout_s=150):
