@@ -60,7 +60,7 @@ struct Engine {
 struct Runtime {
     std::mutex mu;
     int refs = 0;
-    bool stop = false;
+    std::atomic<bool> stop{false};  // written under each engine's lock in turn, read under another's
     std::vector<Engine*> engines;
     std::atomic<uint64_t> next_id{0};
     std::atomic<unsigned> rr{0};
@@ -86,7 +86,7 @@ void engine_loop(Engine* e) {
         Packet p;
         {
             std::unique_lock<std::mutex> g(e->mu);
-            e->cv.wait(g, [&] { return r.stop || !e->ring.empty(); });
+            e->cv.wait(g, [&] { return r.stop.load() || !e->ring.empty(); });
             if (e->ring.empty()) return;
             p = e->ring.front();  // stays at the head while it executes
         }
@@ -150,7 +150,7 @@ hsa_status_t HSA_API hsa_init() {
     Runtime& r = rt();
     std::lock_guard<std::mutex> g(r.mu);
     if (r.refs++ > 0) return HSA_STATUS_SUCCESS;
-    r.stop = false;
+    r.stop.store(false);
     r.copy_ns = env_long("GFD_EMU_COPY_NS", 300);
     r.ps_per_byte = env_long("GFD_EMU_PS_PER_BYTE", 20);
     r.stall_ms = env_long("GFD_EMU_STALL_MS", 5000);
@@ -172,7 +172,7 @@ hsa_status_t HSA_API hsa_shut_down() {
     for (Engine* e : r.engines) {
         {
             std::lock_guard<std::mutex> ge(e->mu);
-            r.stop = true;
+            r.stop.store(true);
         }
         e->cv.notify_all();
     }

@@ -237,7 +237,9 @@ int run_sg(const std::string& kase, int rounds, uint64_t seed) {
             std::fflush(stdout);
             std::memset(dst, kSentinel, off);
             std::memset(sq->d_list_done, 0, flag_words * 8);
-            sq->lists_completed = 0;
+            // The previous round's count is complete (checked below), so
+            // the poller adds nothing more to it.
+            __atomic_store_n(&sq->lists_completed, 0ull, __ATOMIC_RELAXED);
             std::vector<uint64_t> sums(sizes.size(), 0);
             std::atomic<int> timed_out{-1};
             std::vector<std::thread> wg;
@@ -273,6 +275,17 @@ int run_sg(const std::string& kase, int rounds, uint64_t seed) {
                     std::printf("sg %s round %d: list %zu checksum\n", kase.c_str(), rnd, l);
                     rc = 3;
                 }
+            // lists_completed is raised when a list's completion point
+            // retires, possibly after its flag: every list of the round,
+            // once each (an empty list is never posted).
+            size_t posted = 0;
+            for (size_t l = 0; l < sizes.size(); l++) posted += offs[l + 1] > offs[l];
+            if (rc == 0 && (!wait_u64(&sq->lists_completed, posted) ||
+                            __atomic_load_n(&sq->lists_completed, __ATOMIC_ACQUIRE) != posted)) {
+                std::printf("sg %s round %d: lists_completed %llu, want %zu\n", kase.c_str(), rnd,
+                            (unsigned long long)__atomic_load_n(&sq->lists_completed, __ATOMIC_ACQUIRE), posted);
+                rc = 5;
+            }
         }
         p.stop();
     }

@@ -47,6 +47,17 @@ def poller_emu():
     return BIN
 
 
+@pytest.fixture(scope="module")
+def poller_emu_tsan():
+    if shutil.which("g++") is None or not os.path.isdir("/opt/rocm/include/hsa"):
+        pytest.skip("g++ or the HSA headers are not available")
+    os.makedirs(os.path.join(EMU, "_build_tsan"), exist_ok=True)
+    with open(os.path.join(EMU, "_build_tsan", ".lock"), "w") as lock:
+        fcntl.flock(lock, fcntl.LOCK_EX)
+        subprocess.check_call(["make", "-s", "-j8", "-C", EMU, "tsan"], timeout=600)
+    return os.path.join(EMU, "_build_tsan", "poller_emu")
+
+
 def run(binary, args, env=None):
     e = dict(os.environ)
     e.update(env or {})
@@ -140,3 +151,15 @@ def test_registered_host_memory_at_another_gpu_address_is_not_a_copy_source(poll
     # address different from its host address cannot be handed to SDMA copies
     # or the zero-copy kernel by its host address; at the same address it can.
     run(poller_emu, ["locked_source"])
+
+
+# The same stack built with ThreadSanitizer instead: the poller, gather
+# workers, copy engines and the host threads that play the kernels' protocols
+# must show no data race (a report makes the run exit 66).
+@pytest.mark.parametrize("args", [["sg", "split_small_tokens", 2, 1], ["sg", "pages", 2, 1],
+                                  ["queue", 4096, 1000, 1, 2, 3], ["ragged", "direct", 700, 1, 2, 3],
+                                  ["tiled", 8, 128, 32, 4096, 1, 1, 2, 5], ["staging_pool", 2, 5],
+                                  ["sdma_slot_reuse"]])
+def test_no_data_race_under_tsan(poller_emu_tsan, args):
+    out = run(poller_emu_tsan, args, env={"TSAN_OPTIONS": "halt_on_error=0 exitcode=66"})
+    assert "ThreadSanitizer" not in out, out[-3000:]
