@@ -297,10 +297,21 @@ void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int
         trace_words = ((uint64_t)trace_cap_ * sizeof(SGTraceList) + (uint64_t)num_blocks_ * sizeof(SGTraceBlock)) / 8;
     }
     // On the launch stream, ahead of the kernel: no host wait per launch.
-    const int rc = gfd_sg_prepare_launch(sq_->d_list_done, &c, static_cast<uint64_t*>(trace_buf_), trace_words, stream);
+    // Should that launch fail, the same state is written with blocking
+    // copies instead, so the kernel never starts on stale counters.
+    int rc = gfd_sg_prepare_launch(sq_->d_list_done, &c, static_cast<uint64_t*>(trace_buf_), trace_words, stream);
     if (rc != 0) {
-        GFD_LOG_ERROR("SGWarpSpecSession: launch set-up failed: %s\n", gfd_hip_error_string(rc));
-        error_bits_ |= 1ull << 63;
+        GFD_LOG_ERROR("SGWarpSpecSession: launch set-up kernel failed (%s); writing the state directly\n",
+                      gfd_hip_error_string(rc));
+        rc = gfd_hip_stream_synchronize(stream);
+        if (!rc && trace_words) rc = gfd_hip_memset_d8(c.trace, 0, trace_words * 8);
+        if (!rc) rc = gfd_hip_memset_d8((uint64_t)(uintptr_t)sq_->d_list_done, 0, MAX_SG_LISTS * sizeof(uint64_t));
+        if (!rc) rc = gfd_hip_memcpy_h2d((uint64_t)(uintptr_t)sg_device_counters(sq_), &c, sizeof(c));
+        if (!rc) rc = gfd_hip_device_synchronize();
+        if (rc) {
+            GFD_LOG_ERROR("SGWarpSpecSession: launch set-up failed: %s\n", gfd_hip_error_string(rc));
+            error_bits_ |= 1ull << 63;
+        }
     }
     stream_ = stream;
     launch_time_ = std::chrono::steady_clock::now();
