@@ -720,6 +720,56 @@ def run_offload(oracle, iters, warmup):
     return out
 
 
+def run_tiled_baseline(oracle, iters, warmup):
+    """The poller's tiled mode at the reference's warp-spec example shape
+    (examples/07_warp_spec_simple.cu's global-wait baseline: 8192 tokens of
+    16 KiB, 128-token tiles, 32-token chunks): one workgroup per tile
+    submits its chunks as descriptors and waits for the tile's progress word,
+    which the poller raises (copy-engine writes into HBM) after the tile's
+    copies; then each token's u32-word checksum.  Timed from the launch until
+    the kernel has finished, the poller already running.  The example's
+    consumer is RMSNorm + sinf; this one is the checksum used in the tests."""
+    tiles, T, C, ts = 64, 128, 32, 16384
+    n = tiles * T
+    host = gfd_amd.HostBuffer(n * ts)
+    host.array[:] = np.random.default_rng(3).integers(0, 256, n * ts, dtype=np.uint8)
+    dst = gfd_amd.DeviceBuffer(n * ts)
+    sums = gfd_amd.DeviceBuffer(n * 8)
+    status = gfd_amd.HostBuffer(64)
+    tq = gfd_amd.TiledQueue(tiles, T, C, ts, device_signals=True)
+    p = gfd_amd.CpuPollingThread(tq, dst.ptr, host.ptr, host.nbytes, numa_node=-1)
+    times = []
+    try:
+        p.set_tiled_queue(tq)
+        assert p.init_copy_engine()
+        for i in range(-warmup, iters):
+            p.stop()
+            tq.reset()
+            p.reset_stats()
+            status.array.view(np.int32)[0] = 0
+            p.start()
+            t0 = time.perf_counter()
+            gfd_amd.tiled_poller_run(tq, host.ptr, dst.ptr, sums.ptr, status.ptr, whole_tile=False)
+            gfd_amd.synchronize()
+            t1 = time.perf_counter()
+            if int(status.array.view(np.int32)[0]) != 0:
+                raise SystemExit("tiled poller baseline: a tile wait timed out")
+            if i >= 0:
+                times.append((t1 - t0) * 1e6)
+        if not (dst.download() == host.array).all():
+            raise SystemExit("PARITY FAILURE: tiled poller baseline")
+        want = [oracle.u32_word_checksum(host.array[g * ts:(g + 1) * ts]) for g in range(0, n, 97)]
+        got = sums.download().view(np.uint64)[::97]
+        if [int(x) for x in got] != want:
+            raise SystemExit("PARITY FAILURE: tiled poller baseline checksums")
+    finally:
+        p.stop()
+        p.close()
+        tq.free()
+    return {"bytes": n * ts, "us_p50": round(p50(times), 2), "GBps": round(gbps(n * ts, p50(times)), 3),
+            "tiles": tiles, "tokens_per_tile": T, "tokens_per_chunk": C}
+
+
 def run_sessions(oracle, iters, warmup):
     """Wave-specialised sessions.  WarpSpecSession on linear tiles (token t at
     cpu_src + t*T -> gpu_dst + t*T; T = 128 tokens, automatic chunking, no-op
@@ -762,16 +812,17 @@ def run_sessions(oracle, iters, warmup):
     terms = np.sin(y64) * y64
     want, mag = terms.sum(axis=1), np.abs(terms).sum(axis=1)
     del x64, y64, terms
-    # Two tile shapes: 64-token tiles of 8-token chunks, single buffered (the
-    # best of a sweep: the consumer's work left after the last chunk lands is
-    # smallest), and the example's own 128-token tiles of 32-token chunks,
-    # double buffered.
-    for key, tile, chunk, db in (("warp_spec_%dx%dKB_rms_sin" % (n, t // 1024), 64, 8, False),
-                                 ("warp_spec_%dx%dKB_rms_sin_example_shape_db" % (n, t // 1024), 128, 32, True)):
+    # Two tile shapes: 64-token tiles of 8-token chunks, single buffered, on
+    # 64 workgroups (the best of a sweep: the consumer's work left after the
+    # last chunk lands is smallest), and the example's own 128-token tiles of
+    # 32-token chunks, double buffered, on the default grid.
+    for key, tile, chunk, db, blocks in (("warp_spec_%dx%dKB_rms_sin" % (n, t // 1024), 64, 8, False, 64),
+                                         ("warp_spec_%dx%dKB_rms_sin_example_shape_db" % (n, t // 1024), 128, 32,
+                                          True, 0)):
         dst.fill(0)
         outb.fill(0)
         res, kms = gfd_amd.warp_spec_run_rms_sin(host.ptr, dst.ptr, n, t, outb.ptr, tile, chunk, db,
-                                                 iters=warmup + iters)
+                                                 num_blocks=blocks, iters=warmup + iters)
         got = outb.download().view(np.float32).astype(np.float64)
         if not (dst.download() == host.array).all() or not np.all(np.abs(got - want) <= 1e-4 * mag + 1e-6):
             raise SystemExit("PARITY FAILURE: WarpSpecSession RMSNorm + sinf (%s)" % key)
@@ -1126,6 +1177,9 @@ def main():
     if want("sessions"):
         log("wave-specialised sessions ...")
         r_sessions = run_sessions(oracle, K, W)
+        log("poller tiled mode (the example's global-wait baseline) ...")
+        r_sessions["tiled_poller_baseline_8192x16KB"] = run_tiled_baseline(oracle, max(5, K // 5), 2)
+        log("  tiled poller baseline: %s" % r_sessions["tiled_poller_baseline_8192x16KB"])
 
     r_timeline = None
     if "timeline" in only:
