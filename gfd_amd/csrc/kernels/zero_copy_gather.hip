@@ -56,6 +56,8 @@ constexpr int kDefaultLds = 0;
 constexpr uint64_t kScatterBytesPerWave = 512 * 1024;
 constexpr int kScatterMinWaves = 16, kScatterMaxWaves = 64;
 constexpr int kScatterUnroll = 8;
+// Smallest piece a token is cut into when a list has fewer tokens than waves.
+constexpr int kMinPiece = 4096;
 
 using gfd::wave::BatchLds;
 using gfd::wave::GridDone;
@@ -64,24 +66,33 @@ using gfd::wave::GridDone;
 constexpr int kStageVecs = 16 * 64;
 
 // Page-table form: token j of num_tokens lives at src_addrs[j] (host) and
-// lands at dst + j * token_size.  Wave w copies tokens [w*per_wave, ...)
-// strided over the grid, per_wave <= 64 at a time.  kLds: stage through LDS.
+// lands at dst + j * token_size.  The unit of work is a piece: each token is
+// cut into 2^piece_shift pieces of token_size >> piece_shift bytes (the host
+// splits only when the list has fewer tokens than the grid has waves, and
+// only into whole multiples of 16 bytes), so unit u is piece u & (2^s - 1) of
+// token u >> s and lands at dst + u * piece.  Wave w copies units
+// [w*per_wave, ...) strided over the grid, per_wave <= 64 at a time.
+// kLds: stage through LDS.
 template <bool kLds>
 __global__ __launch_bounds__(kBlock) void zc_gather_tokens(const uint64_t* __restrict__ src_addrs, uint64_t dst,
                                                            uint32_t token_size, uint32_t num_tokens,
-                                                           uint32_t per_wave, int unroll, GridDone done) {
+                                                           uint32_t piece_shift, uint32_t per_wave, int unroll,
+                                                           GridDone done) {
     __shared__ BatchLds lds[kWavesPerBlock];
     __shared__ gfd::wave::vec4u stage[kLds ? kWavesPerBlock : 1][kLds ? kStageVecs : 1];
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const uint64_t wave = (uint64_t)blockIdx.x * kWavesPerBlock + wid;
     const uint64_t stride = (uint64_t)gridDim.x * kWavesPerBlock * per_wave;
-    for (uint64_t first = wave * per_wave; first < num_tokens; first += stride) {
-        const uint32_t nb = (uint32_t)min((uint64_t)per_wave, num_tokens - first);
+    const uint64_t units = (uint64_t)num_tokens << piece_shift;
+    const uint64_t piece = token_size >> piece_shift, piece_mask = (1ull << piece_shift) - 1;
+    for (uint64_t first = wave * per_wave; first < units; first += stride) {
+        const uint32_t nb = (uint32_t)min((uint64_t)per_wave, units - first);
         uint64_t md = 0, ms = 0, mn = 0;
         if (lane < nb) {
-            ms = src_addrs[first + lane];
-            md = dst + (first + lane) * token_size;
-            mn = token_size;
+            const uint64_t u = first + lane;
+            ms = src_addrs[u >> piece_shift] + (u & piece_mask) * piece;
+            md = dst + u * piece;
+            mn = piece;
         }
         gfd::wave::copy_batch(unroll, md, ms, mn, nb, &lds[wid], kLds ? stage[wid] : nullptr);
     }
@@ -92,23 +103,27 @@ __global__ __launch_bounds__(kBlock) void zc_gather_tokens(const uint64_t* __res
 // at src + j * token_size and stored to dst_addrs[j] in pinned host memory.
 // HBM loads return in ~1-2 us, and the 16-byte stores become posted PCIe
 // writes, so each wave moves its batch as one vector stream, exactly as the
-// gather does.
+// gather does.  Tokens are cut into pieces exactly as in zc_gather_tokens.
 template <bool kLds>
 __global__ __launch_bounds__(kBlock) void zc_scatter_tokens(const uint64_t* __restrict__ dst_addrs, uint64_t src,
                                                             uint32_t token_size, uint32_t num_tokens,
-                                                            uint32_t per_wave, int unroll, GridDone done) {
+                                                            uint32_t piece_shift, uint32_t per_wave, int unroll,
+                                                            GridDone done) {
     __shared__ BatchLds lds[kWavesPerBlock];
     __shared__ gfd::wave::vec4u stage[kLds ? kWavesPerBlock : 1][kLds ? kStageVecs : 1];
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const uint64_t wave = (uint64_t)blockIdx.x * kWavesPerBlock + wid;
     const uint64_t stride = (uint64_t)gridDim.x * kWavesPerBlock * per_wave;
-    for (uint64_t first = wave * per_wave; first < num_tokens; first += stride) {
-        const uint32_t nb = (uint32_t)min((uint64_t)per_wave, num_tokens - first);
+    const uint64_t units = (uint64_t)num_tokens << piece_shift;
+    const uint64_t piece = token_size >> piece_shift, piece_mask = (1ull << piece_shift) - 1;
+    for (uint64_t first = wave * per_wave; first < units; first += stride) {
+        const uint32_t nb = (uint32_t)min((uint64_t)per_wave, units - first);
         uint64_t md = 0, ms = 0, mn = 0;
         if (lane < nb) {
-            md = dst_addrs[first + lane];
-            ms = src + (first + lane) * token_size;
-            mn = token_size;
+            const uint64_t u = first + lane;
+            md = dst_addrs[u >> piece_shift] + (u & piece_mask) * piece;
+            ms = src + u * piece;
+            mn = piece;
         }
         gfd::wave::copy_batch(unroll, md, ms, mn, nb, &lds[wid], kLds ? stage[wid] : nullptr);
     }
@@ -146,6 +161,7 @@ int env_int(const char* name, int dflt) {
 // Launch shape for n entries: (blocks, entries per wave, unroll).
 struct Shape {
     uint32_t blocks, per_wave;
+    uint32_t piece_shift;  // tokens cut into 2^piece_shift pieces
     int unroll;
     bool lds;  // stage through LDS
 };
@@ -161,18 +177,37 @@ constexpr ShapeDefaults kGatherShape{kBytesPerWave, kMinWaves, kMaxWaves, kDefau
 constexpr ShapeDefaults kScatterShape{kScatterBytesPerWave, kScatterMinWaves, kScatterMaxWaves, kScatterUnroll,
                                       "GFD_ZCS_WAVES", "GFD_ZCS_UNROLL"};
 
-Shape shape_for(uint64_t n, uint64_t total_bytes, const ShapeDefaults& d = kGatherShape) {
+// n entries of total_bytes.  token_size != 0: the entries are tokens of that
+// size, which may be cut into pieces: a list of fewer tokens than the target
+// number of waves would leave waves idle and give each busy wave a whole large
+// token to stream on its own (4 x 64 KiB on 4 waves ran at 7 GB/s).  Tokens
+// are then halved while twice the units still fit the target, the halves stay
+// whole multiples of 16 bytes and at least GFD_ZC_MIN_PIECE bytes (4 KiB: one
+// pass of a wave at 4 loads per lane), so every unit gets a wave of its own.
+// Lists of more than half the target in tokens are never cut.
+Shape shape_for(uint64_t n, uint64_t total_bytes, const ShapeDefaults& d = kGatherShape, uint32_t token_size = 0) {
     // Read per call (a getenv is ~100 ns against a launch of microseconds),
     // so a process can sweep launch shapes.
     const int dflt = (int)std::min<uint64_t>(
         std::max<uint64_t>(total_bytes / d.bytes_per_wave, (uint64_t)d.min_waves), (uint64_t)d.max_waves);
     const int target = std::max(4, env_int(d.waves_env, dflt));
     const int unroll_env = env_int(d.unroll_env, d.unroll);
+    uint32_t shift = 0;
+    if (token_size != 0) {
+        const uint64_t min_piece = (uint64_t)std::max(16, env_int("GFD_ZC_MIN_PIECE", kMinPiece));
+        while ((n << (shift + 1)) <= (uint64_t)target && shift < 16) {
+            const uint64_t half = (uint64_t)token_size >> (shift + 1);
+            if (half < min_piece || (half & 15) != 0 || (half << (shift + 1)) != token_size) break;
+            shift++;
+        }
+    }
+    n <<= shift;
     uint64_t per_wave = (n + target - 1) / target;
     per_wave = std::min<uint64_t>(std::max<uint64_t>(per_wave, 1), 64);
     const uint64_t waves = (n + per_wave - 1) / per_wave;
     Shape s;
     s.per_wave = (uint32_t)per_wave;
+    s.piece_shift = shift;
     s.blocks = (uint32_t)((waves + kWavesPerBlock - 1) / kWavesPerBlock);
     s.unroll = unroll_env >= 16 ? 16 : (unroll_env >= 8 ? 8 : 4);
     s.lds = env_int("GFD_ZC_LDS", kDefaultLds) != 0;
@@ -186,13 +221,15 @@ int launch_gather_tokens(const uint64_t* src_addrs, void* dst, uint32_t token_si
         return (int)hipErrorInvalidValue;
     if (num_tokens == 0) return 0;
     if ((uint64_t)token_size >= (1ull << 30)) return (int)hipErrorInvalidValue;  // 1 GiB per token at most
-    const Shape s = shape_for((uint64_t)num_tokens, (uint64_t)num_tokens * token_size);
+    const Shape s = shape_for((uint64_t)num_tokens, (uint64_t)num_tokens * token_size, kGatherShape, token_size);
     if (s.lds)
         hipLaunchKernelGGL(zc_gather_tokens<true>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, src_addrs,
-                           (uint64_t)(uintptr_t)dst, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll, done);
+                           (uint64_t)(uintptr_t)dst, token_size, (uint32_t)num_tokens, s.piece_shift, s.per_wave,
+                           s.unroll, done);
     else
         hipLaunchKernelGGL(zc_gather_tokens<false>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, src_addrs,
-                           (uint64_t)(uintptr_t)dst, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll, done);
+                           (uint64_t)(uintptr_t)dst, token_size, (uint32_t)num_tokens, s.piece_shift, s.per_wave,
+                           s.unroll, done);
     return (int)hipGetLastError();
 }
 
@@ -202,13 +239,15 @@ int launch_scatter_tokens(const uint64_t* dst_addrs, const void* src, uint32_t t
         return (int)hipErrorInvalidValue;
     if (num_tokens == 0) return 0;
     if ((uint64_t)token_size >= (1ull << 30)) return (int)hipErrorInvalidValue;  // 1 GiB per token at most
-    const Shape s = shape_for((uint64_t)num_tokens, (uint64_t)num_tokens * token_size, kScatterShape);
+    const Shape s = shape_for((uint64_t)num_tokens, (uint64_t)num_tokens * token_size, kScatterShape, token_size);
     if (s.lds)
         hipLaunchKernelGGL(zc_scatter_tokens<true>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, dst_addrs,
-                           (uint64_t)(uintptr_t)src, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll, done);
+                           (uint64_t)(uintptr_t)src, token_size, (uint32_t)num_tokens, s.piece_shift, s.per_wave,
+                           s.unroll, done);
     else
         hipLaunchKernelGGL(zc_scatter_tokens<false>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, dst_addrs,
-                           (uint64_t)(uintptr_t)src, token_size, (uint32_t)num_tokens, s.per_wave, s.unroll, done);
+                           (uint64_t)(uintptr_t)src, token_size, (uint32_t)num_tokens, s.piece_shift, s.per_wave,
+                           s.unroll, done);
     return (int)hipGetLastError();
 }
 

@@ -65,6 +65,31 @@ def test_zero_copy_tokens_parity(n, t):
     L.check()
 
 
+# A list of few tokens is cut into pieces for the grid's 64 waves (halving
+# each token while twice the pieces fit 64 and the halves stay multiples of 16
+# bytes and at least GFD_ZC_MIN_PIECE): 4 x 64 KiB -> 64 pieces of 4 KiB,
+# 5 x 24 KiB -> 20 of 6 KiB, 3 x 1 MiB -> 48 of 64 KiB; with a 16-byte floor
+# 3 x 4 KiB -> 48 of 256 B and 7 x 64 B -> 28 of 16 B; 1 x 4112 B (257
+# vectors), 6 x 8200 B (halves not multiples of 16) and 64 x 64 KiB stay whole.
+SPLIT_CASES = [(4, 65536, 4096), (5, 24576, 4096), (3, 1 << 20, 4096), (3, 4096, 16), (7, 64, 16), (1, 4112, 16),
+               (6, 8200, 16), (64, 65536, 4096)]
+
+
+@pytest.mark.parametrize("n,t,min_piece", SPLIT_CASES)
+def test_zero_copy_tokens_split_into_pieces(n, t, min_piece, monkeypatch):
+    log("zero_copy_tokens pieces n=%d t=%d min_piece=%d" % (n, t, min_piece))
+    monkeypatch.setenv("GFD_ZC_MIN_PIECE", str(min_piece))
+    L = Layout(n, t)
+    table = gfd_amd.DeviceBuffer(n * 8)
+    table.upload(L.src_addrs)
+    for lds in ("0", "1"):
+        monkeypatch.setenv("GFD_ZC_LDS", lds)
+        gfd_amd.zero_copy_gather_tokens(table.ptr, L.dst.ptr, t, n)
+        gfd_amd.synchronize()
+        L.check()
+        L.reset()
+
+
 @pytest.mark.parametrize("n,t,waves,unroll", [(8192, 4096, 0, 4), (2048, 65536, 0, 16), (97, 1000, 0, 8),
                                               (2048, 512, 64, 8), (300, 48, 4, 16)])
 def test_zero_copy_lds_staged_parity(n, t, waves, unroll, monkeypatch):
@@ -172,7 +197,7 @@ def direct_poller():
 
 DIRECT_CASES = [(256, 4096, 2 << 20), (8192, 4096, 2 << 20), (8192, 4096, 256 << 10), (2048, 65536, 2 << 20),
                 (2048, 512, 2 << 20), (2048, 1024, 64 << 10), (2048, 2048, 2 << 20), (97, 1000, 10000),
-                (40, 4096, 2 << 20)]
+                (40, 4096, 2 << 20), (4, 65536, 2 << 20), (3, 1 << 20, 2 << 20)]
 
 
 @pytest.mark.parametrize("route", ["default", "staged"])

@@ -66,6 +66,23 @@ def test_zero_copy_scatter_tokens_parity(n, t):
     c.check()
 
 
+# Few tokens are cut into pieces as in the gather, for the offload grid's 16
+# waves: 4 x 64 KiB -> 16 of 16 KiB, 2 x 1 MiB -> 16 of 128 KiB, 5 x 24 KiB ->
+# 10 of 12 KiB; with a 16-byte floor 3 x 4 KiB -> 12 of 1 KiB and 6 x 8200 B
+# stays whole.
+@pytest.mark.parametrize("n,t,min_piece", [(4, 65536, 4096), (2, 1 << 20, 4096), (5, 24576, 4096), (3, 4096, 16),
+                                           (6, 8200, 16)])
+def test_zero_copy_scatter_tokens_split_into_pieces(n, t, min_piece, monkeypatch):
+    log("zero_copy_scatter pieces n=%d t=%d min_piece=%d" % (n, t, min_piece))
+    monkeypatch.setenv("GFD_ZC_MIN_PIECE", str(min_piece))
+    c = Offload(n, t)
+    table = gfd_amd.DeviceBuffer(n * 8)
+    table.upload(c.dst_addrs)
+    gfd_amd.zero_copy_scatter_tokens(table.ptr, c.src.ptr, t, n)
+    gfd_amd.synchronize()
+    c.check()
+
+
 @pytest.mark.parametrize("waves,unroll", [(16, 4), (64, 16), (256, 8), (4, 4)])
 def test_zero_copy_scatter_launch_shapes(waves, unroll, monkeypatch):
     """Bytes do not depend on the launch shape (GFD_ZCS_WAVES / _UNROLL)."""
