@@ -46,6 +46,15 @@ PCIE_GEN5_X16_GBPS = 32.0 * 16 * 128.0 / 130.0 / 8.0  # 63.0 GB/s per direction
 ZC_TRAFFIC_8192x4KB = {"read_bytes": 32891 * 1024, "write_bytes": 32772 * 1024}
 METRIC = "scattered H2D GB/s + % of PCIe5 x16 peak at 8192x4KB and 2048x64KB"
 DIRECT_ZC_MAX = 8 << 20  # submit_direct's default zero-copy route limit (bytes)
+DIRECT_ZC_MIN = 64 << 10  # lists up to this size take the staged route
+
+
+def direct_route(nbytes):
+    """The route submit_direct takes by default for a destination-contiguous
+    list of scattered tokens with pinned sources."""
+    if nbytes <= DIRECT_ZC_MIN:
+        return "staged SDMA"
+    return "zero-copy kernel" if nbytes <= DIRECT_ZC_MAX else "staged SDMA + zero-copy head"
 DIRECT_ZC_HEAD = 2 << 20  # and the zero-copy head of larger staged lists
 # MoE through SGWarpSpecSession: workgroups, compute waves sharing each list
 # in the RMSNorm, rows per GPU-built list (swept: 24-128 workgroups, 1-3
@@ -297,8 +306,7 @@ def run_direct(poller, L, iters, warmup):
 
     out = timed_calls("direct")
     head = poller.set_direct_zero_copy_head_bytes(DIRECT_ZC_HEAD)
-    out["route"] = ("zero-copy kernel" if L.bytes <= DIRECT_ZC_MAX else
-                    "staged SDMA + zero-copy head of %d KiB" % (head >> 10))
+    out["route"] = direct_route(L.bytes) + (" of %d KiB" % (head >> 10) if L.bytes > DIRECT_ZC_MAX else "")
     poller.set_direct_zero_copy_max_bytes(0)  # also switches the head off
     out["staged_sdma"] = timed_calls("direct (staged SDMA)")
     poller.set_direct_zero_copy_max_bytes(DIRECT_ZC_MAX)
@@ -394,7 +402,7 @@ def run_direct_sizes(oracle, poller, iters, warmup):
             assert rc == 0, gfd_amd.lib().gfd_last_error()
             L.verify("direct %d x %d" % (n, t))
             row[str(n)] = {"us_p50": round(p50(tt), 2), "GBps": round(gbps(n * t, p50(tt)), 3),
-                           "route": "zero-copy kernel" if n * t <= DIRECT_ZC_MAX else "staged SDMA + zero-copy head",
+                           "route": direct_route(n * t),
                            "reference_us": ref[n], "reference_GBps": round(gbps(n * t, ref[n]), 2)}
             del L
         out["%dKB" % (t // 1024)] = row

@@ -149,6 +149,7 @@ def _declare(L):
         "gfd_poller_copy_clock_ns": ([vp], c_u64),
         "gfd_poller_set_direct_chunk_bytes": ([vp, c_u64], None),
         "gfd_poller_set_direct_zero_copy_max_bytes": ([vp, c_u64], None),
+        "gfd_poller_set_direct_zero_copy_min_bytes": ([vp, c_u64], c_u64),
         "gfd_poller_set_direct_zero_copy_head_bytes": ([vp, c_u64], c_u64),
         "gfd_bench_zero_copy_tokens_signal": ([vp, vp, c_u32, c_int, c_int, c_int, pd], c_int),
         "gfd_zero_copy_gather_tokens_signal": ([vp, vp, c_u32, c_int, vp, vp, c_u64, vp], c_int),
@@ -424,6 +425,11 @@ class CpuPollingThread:
         """Lists up to b bytes (destination-contiguous, pinned sources) use the
         zero-copy kernel; 0 = always the staged SDMA route."""
         lib().gfd_poller_set_direct_zero_copy_max_bytes(self._h, b)
+
+    def set_direct_zero_copy_min_bytes(self, b):
+        """Lists of at most b bytes take the staged SDMA route (default
+        64 KiB).  Returns the previous value."""
+        return int(lib().gfd_poller_set_direct_zero_copy_min_bytes(self._h, b))
 
     def set_direct_zero_copy_head_bytes(self, b):
         """Larger lists (destination-contiguous, pinned sources): the zero-copy

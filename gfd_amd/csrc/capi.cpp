@@ -253,6 +253,12 @@ uint64_t gfd_poller_copy_clock_ns(gfd_poller_t p) { return p ? P(p)->copy_clock_
 void gfd_poller_set_direct_zero_copy_max_bytes(gfd_poller_t p, uint64_t b) {
     if (p) P(p)->set_direct_zero_copy_max_bytes(b);
 }
+uint64_t gfd_poller_set_direct_zero_copy_min_bytes(gfd_poller_t p, uint64_t b) {
+    if (!p) return 0;
+    const uint64_t prev = P(p)->direct_zero_copy_min_bytes();
+    P(p)->set_direct_zero_copy_min_bytes(b);
+    return prev;
+}
 uint64_t gfd_poller_set_direct_zero_copy_head_bytes(gfd_poller_t p, uint64_t b) {
     if (!p) return 0;
     const uint64_t prev = P(p)->direct_zero_copy_head_bytes();

@@ -111,6 +111,7 @@ CpuPollingThread::CpuPollingThread(DescriptorQueue* queue, void* gpu_base, void*
     gfd_hip_get_device(&device_);
     direct_chunk_bytes_ = env_size("GFD_DIRECT_CHUNK_BYTES", direct_chunk_bytes_);
     direct_zc_max_bytes_ = env_size("GFD_DIRECT_ZC_MAX_BYTES", direct_zc_max_bytes_);
+    direct_zc_min_bytes_ = env_size("GFD_DIRECT_ZC_MIN_BYTES", direct_zc_min_bytes_);
     direct_zc_head_bytes_ = env_size("GFD_DIRECT_ZC_HEAD_BYTES", direct_zc_head_bytes_);
     fifo_ = new CompletionFifo();
     if (env_size("GFD_TRACE", 0)) set_trace(true);

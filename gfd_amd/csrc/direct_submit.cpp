@@ -422,7 +422,8 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
             err = direct_ce_manager_.submit_on_channel(c, entries[0].dst + off,
                                                        (const char*)entries[0].src + off, len);
         }
-    } else if (dst_contig && total <= direct_zc_max_bytes_ && count > 1 && zc_pinned != 0 &&
+    } else if (dst_contig && total <= direct_zc_max_bytes_ && total > direct_zc_min_bytes_ && count > 1 &&
+               zc_pinned != 0 &&
                (err = direct_zero_copy(entries, count, total, uniform, zc_pinned == 1)) != kZcNotTaken) {
         // done by the zero-copy kernel (err 0) or failed
     } else if (dst_contig && direct_staging_ && total <= direct_staging_size_) {

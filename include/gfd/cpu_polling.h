@@ -124,6 +124,11 @@ public:
     // a few MiB the copy engines' fixed start-up latency dominates.
     void set_direct_zero_copy_max_bytes(size_t b) { direct_zc_max_bytes_ = b; }
     size_t direct_zero_copy_max_bytes() const { return direct_zc_max_bytes_; }
+    // Lists of at most this many bytes take the staged SDMA route even when
+    // the zero-copy kernel could move them: at these sizes a copy-engine copy
+    // starts sooner than a kernel launch (GFD_DIRECT_ZC_MIN_BYTES; 64 KiB).
+    void set_direct_zero_copy_min_bytes(size_t b) { direct_zc_min_bytes_ = b; }
+    size_t direct_zero_copy_min_bytes() const { return direct_zc_min_bytes_; }
     // Larger destination-contiguous lists with pinned sources: the zero-copy
     // kernel moves the first entries, up to this many bytes, while the gather
     // workers stage the rest for the copy engines, so the host link carries
@@ -306,6 +311,7 @@ private:
     uint64_t* zc_src_table_ = nullptr;
     int zc_src_cap_ = 0;
     size_t direct_zc_max_bytes_ = 8u << 20;
+    size_t direct_zc_min_bytes_ = 64u << 10;
     size_t direct_zc_head_bytes_ = 2u << 20;
     uint64_t zc_dst_lo_ = 0, zc_dst_hi_ = 0;  // last device allocation found for a destination
     std::vector<uint32_t> tile_scratch_;

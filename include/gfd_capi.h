@@ -143,6 +143,10 @@ void gfd_poller_set_direct_chunk_bytes(gfd_poller_t p, uint64_t bytes);
 /* Destination-contiguous lists of at most `bytes` with pinned sources go
  * through the zero-copy kernel (0 = never). */
 void gfd_poller_set_direct_zero_copy_max_bytes(gfd_poller_t p, uint64_t bytes);
+/* Lists of at most `bytes` take the staged copy-engine route whatever the
+ * maximum above (default 64 KiB: there a copy-engine copy completes sooner
+ * than a kernel launch).  Returns the previous value. */
+uint64_t gfd_poller_set_direct_zero_copy_min_bytes(gfd_poller_t p, uint64_t bytes);
 /* Larger destination-contiguous lists with pinned sources: the zero-copy
  * kernel moves the first entries, up to `bytes`, while the rest is staged
  * for the copy engines (0 = staged only).  Returns the previous value. */

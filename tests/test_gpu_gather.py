@@ -272,6 +272,31 @@ def test_submit_direct_head_from_pinned_rest_pageable(direct_poller):
         assert (got[n * t:] == SENTINEL).all()
 
 
+@pytest.mark.parametrize("n,t", [(16, 4096), (4, 16384), (2, 32768)])
+def test_submit_direct_small_list_route(direct_poller, n, t):
+    """Lists of at most 64 KiB (the default minimum of the zero-copy route)
+    are staged for the copy engines: no kernel launch in the trace.  With the
+    minimum at 0 the same list goes through the zero-copy kernel.  Every
+    byte lands either way."""
+    log("submit_direct small-list route n=%d t=%d" % (n, t))
+    L = Layout(n, t)
+    entries = gfd_amd.make_entries(L.src_addrs, L.dst.ptr, t)
+    prev = direct_poller.set_direct_zero_copy_min_bytes(64 << 10)
+    try:
+        for zc_min, launches in ((64 << 10, 0), (0, 1)):
+            direct_poller.set_direct_zero_copy_min_bytes(zc_min)
+            direct_poller.set_trace(True)
+            direct_poller.read_trace()
+            assert direct_poller.submit_direct(entries, n) > 0
+            tr = direct_poller.read_trace()
+            direct_poller.set_trace(False)
+            assert int(np.count_nonzero(tr["kind"] == 14)) == launches, "min %d" % zc_min
+            L.check()
+            L.reset()
+    finally:
+        direct_poller.set_direct_zero_copy_min_bytes(prev)
+
+
 def test_submit_direct_copy_timeline(direct_poller):
     """The SDMA copy timeline of a Direct call: every copy inside the call's
     window on the copy clock, bytes summing to the gathered bytes."""

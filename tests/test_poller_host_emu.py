@@ -107,6 +107,16 @@ def test_ragged_entries_over_destination_runs(poller_emu, path, nruns):
         assert zero_copy_launches(out) == [1 if nruns == 1 else 0] * 2, out[-2000:]
 
 
+@pytest.mark.parametrize("zc_min,launches", [(0, 1), (64 << 20, 0)])
+def test_direct_zero_copy_minimum(poller_emu, zc_min, launches):
+    # The one-run list of about 3 MiB: on the zero-copy route with no minimum,
+    # staged once the minimum (GFD_DIRECT_ZC_MIN_BYTES) is above its size (the
+    # staged route's zero-copy head is off here, so no kernel runs at all).
+    out = run(poller_emu, ["ragged", "direct", 700, 1, 2, 3],
+              env={"GFD_DIRECT_ZC_MIN_BYTES": str(zc_min), "GFD_DIRECT_ZC_HEAD_BYTES": "0"})
+    assert zero_copy_launches(out) == [launches] * 2, out[-2000:]
+
+
 @pytest.mark.parametrize("head,launches", [(512 << 10, 1), (0, 0)])
 def test_direct_staged_route_with_zero_copy_head(poller_emu, head, launches):
     # The same contiguous ragged list above the zero-copy route's limit (set
