@@ -78,9 +78,12 @@ def test_zero_copy_scatter_tokens_split_into_pieces(n, t, min_piece, monkeypatch
     c = Offload(n, t)
     table = gfd_amd.DeviceBuffer(n * 8)
     table.upload(c.dst_addrs)
-    gfd_amd.zero_copy_scatter_tokens(table.ptr, c.src.ptr, t, n)
-    gfd_amd.synchronize()
-    c.check()
+    for lds in ("0", "1"):
+        monkeypatch.setenv("GFD_ZC_LDS", lds)
+        c.host.array[:] = SENTINEL
+        gfd_amd.zero_copy_scatter_tokens(table.ptr, c.src.ptr, t, n)
+        gfd_amd.synchronize()
+        c.check()
 
 
 @pytest.mark.parametrize("waves,unroll", [(16, 4), (64, 16), (256, 8), (4, 4)])
