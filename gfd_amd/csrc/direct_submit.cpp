@@ -49,6 +49,35 @@ constexpr int kZcNotTaken = INT_MIN;               // direct_zero_copy: the list
 
 void no_chunk(void*, int, size_t, size_t) {}
 
+// The zero-copy SG kernel gives each entry of a short list a wave of its own,
+// so a list of fewer entries than its 64 waves leaves waves idle while a few
+// stream whole large entries.  Such a list's entries are cut into pieces of
+// at least 4 KiB, a multiple of 16 bytes each (an entry's last piece takes
+// what is left), so the pieces keep each entry's alignment.  Writes the
+// table to out (at most cap records) and returns its length, or copies the
+// entries unchanged when the list is long enough or the pieces would not fit.
+int zc_fill_sg_table(const SGEntry* in, int count, size_t total, SGEntry* out, int cap) {
+    constexpr int kWaves = 64;
+    constexpr size_t kMinPiece = 4096;
+    if (count < kWaves && total / (size_t)count >= 2 * kMinPiece) {
+        const size_t piece = std::max(kMinPiece, ((total + kWaves - 1) / kWaves + 15) & ~(size_t)15);
+        int n = 0;
+        for (int i = 0; i < count && n >= 0; i++) {
+            for (size_t off = 0; off < in[i].size; off += piece) {
+                if (n == cap) {
+                    n = -1;
+                    break;
+                }
+                const size_t len = std::min(piece, in[i].size - off);
+                out[n++] = SGEntry{in[i].dst + off, (const char*)in[i].src + off, len};
+            }
+        }
+        if (n >= 0) return n;
+    }
+    std::memcpy(out, in, (size_t)count * sizeof(SGEntry));
+    return count;
+}
+
 }  // namespace
 
 void run_copy_chunk(void* p, int chunk, size_t off, size_t len) {
@@ -217,8 +246,8 @@ int CpuPollingThread::direct_zero_copy(const SGEntry* entries, int count, size_t
             zc_table_ = static_cast<SGEntry*>(t);
             zc_table_cap_ = cap;
         }
-        std::memcpy(zc_table_, entries, (size_t)count * sizeof(SGEntry));
-        rc = gfd_zero_copy_gather_signal(reinterpret_cast<const gfd_sg_entry*>(zc_table_), count, zc_counter_,
+        const int n = zc_fill_sg_table(entries, count, total, zc_table_, zc_table_cap_);
+        rc = gfd_zero_copy_gather_signal(reinterpret_cast<const gfd_sg_entry*>(zc_table_), n, zc_counter_,
                                          zc_done_, gen, zc_stream_);
     }
     if (rc != 0) return rc;
@@ -257,8 +286,10 @@ int CpuPollingThread::zc_launch_head(const SGEntry* entries, int k, bool uniform
         rc = gfd_zero_copy_gather_tokens_signal(zc_src_table_, (void*)(uintptr_t)entries[0].dst,
                                                 (uint32_t)entries[0].size, k, zc_counter_, zc_done_, g, zc_stream_);
     } else {
-        std::memcpy(zc_table_, entries, (size_t)k * sizeof(SGEntry));
-        rc = gfd_zero_copy_gather_signal(reinterpret_cast<const gfd_sg_entry*>(zc_table_), k, zc_counter_, zc_done_,
+        size_t bytes = 0;
+        for (int i = 0; i < k; i++) bytes += entries[i].size;
+        const int n = zc_fill_sg_table(entries, k, bytes, zc_table_, zc_table_cap_);
+        rc = gfd_zero_copy_gather_signal(reinterpret_cast<const gfd_sg_entry*>(zc_table_), n, zc_counter_, zc_done_,
                                          g, zc_stream_);
     }
     if (rc != 0) return rc;

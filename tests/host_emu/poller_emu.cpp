@@ -374,8 +374,11 @@ int run_ragged(const std::string& path, uint32_t n, uint32_t nruns, int rounds, 
     Rng rng(seed);
     std::vector<uint32_t> sizes(n);
     size_t total = 0;
+    // Entry sizes 1 .. GFD_EMU_MAX_ENTRY bytes (8999 unless set).
+    const char* me = std::getenv("GFD_EMU_MAX_ENTRY");
+    const uint32_t max_entry = me && *me ? (uint32_t)std::strtoul(me, nullptr, 10) : 8999u;
     for (auto& s : sizes) {
-        s = 1 + (uint32_t)rng.below(8999);
+        s = 1 + (uint32_t)rng.below(max_entry);
         total += s;
     }
     const size_t host_bytes = 2 * total + 64;

@@ -44,10 +44,10 @@ def gpu():
 class RaggedCase:
     """n ragged entries; destinations in list order, cut into nruns runs."""
 
-    def __init__(self, n, nruns, seed):
+    def __init__(self, n, nruns, seed, max_size=9000):
         rng = np.random.default_rng(seed)
         self.n = n
-        self.sizes = rng.integers(1, 9000, n).astype(np.uint64)
+        self.sizes = rng.integers(1, max_size, n).astype(np.uint64)
         self.host = gfd_amd.HostBuffer(int(self.sizes.sum()) * 2 + 64)
         self.host.array[:] = rng.integers(0, 256, self.host.nbytes, dtype=np.uint8)
         self.src_offs = np.array([int(rng.integers(0, self.host.nbytes - int(s))) for s in self.sizes], np.uint64)
@@ -103,6 +103,33 @@ def test_direct_ragged_entries(direct_poller, nruns, route):
         for rep in range(2):
             assert direct_poller.submit_direct(entries, c.n) > 0
             c.check("direct, %d runs, %s route, call %d" % (nruns, route, rep))
+    finally:
+        direct_poller.set_direct_zero_copy_max_bytes(8 << 20)
+        direct_poller.set_direct_zero_copy_head_bytes(head)
+
+
+@pytest.mark.parametrize("n,max_size,route", [(5, 200000, "default"), (3, 100000, "default"),
+                                              (40, 70000, "default"), (12, 400000, "staged+head")])
+def test_direct_few_large_ragged_entries(direct_poller, n, max_size, route):
+    """A short list of large ragged entries is cut into pieces of at least
+    4 KiB for the zero-copy kernel's waves (the whole list on the kernel
+    route, or the head of a staged list); every byte lands, at every source
+    alignment."""
+    log("submit_direct few large ragged entries n=%d max=%d %s" % (n, max_size, route))
+    c = RaggedCase(n, 1, seed=n, max_size=max_size)
+    c.dst.fill(SENTINEL)
+    entries = (gfd_amd.SGEntry * c.n)()
+    a = np.frombuffer(entries, dtype=np.uint64).reshape(c.n, 3)
+    a[:, 0] = c.dst_addrs()
+    a[:, 1] = c.src_addrs()
+    a[:, 2] = c.sizes
+    limit = {"default": 8 << 20, "staged+head": 1 << 20}[route]
+    direct_poller.set_direct_zero_copy_max_bytes(limit)
+    head = direct_poller.set_direct_zero_copy_head_bytes(512 << 10)
+    try:
+        for rep in range(2):
+            assert direct_poller.submit_direct(entries, c.n) > 0
+            c.check("direct, %d entries up to %d B, %s, call %d" % (n, max_size, route, rep))
     finally:
         direct_poller.set_direct_zero_copy_max_bytes(8 << 20)
         direct_poller.set_direct_zero_copy_head_bytes(head)

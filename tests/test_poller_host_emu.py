@@ -107,6 +107,16 @@ def test_ragged_entries_over_destination_runs(poller_emu, path, nruns):
         assert zero_copy_launches(out) == [1 if nruns == 1 else 0] * 2, out[-2000:]
 
 
+@pytest.mark.parametrize("n,max_entry", [(5, 200000), (40, 70000), (63, 9000), (3, 100000)])
+def test_direct_short_ragged_list_cut_into_pieces(poller_emu, n, max_entry):
+    # A short destination-contiguous list of large ragged entries: the
+    # zero-copy route cuts the entries into pieces of at least 4 KiB (16-byte
+    # multiples) for the kernel's waves; every byte is compared, under
+    # AddressSanitizer, against the list's own image.
+    out = run(poller_emu, ["ragged", "direct", n, 1, 2, 5], env={"GFD_EMU_MAX_ENTRY": str(max_entry)})
+    assert zero_copy_launches(out) == [1] * 2, out[-2000:]
+
+
 @pytest.mark.parametrize("zc_min,launches", [(0, 1), (64 << 20, 0)])
 def test_direct_zero_copy_minimum(poller_emu, zc_min, launches):
     # The one-run list of about 3 MiB: on the zero-copy route with no minimum,
