@@ -56,7 +56,7 @@ constexpr int kDefaultLds = 0;
 constexpr uint64_t kScatterBytesPerWave = 512 * 1024;
 constexpr int kScatterMinWaves = 16, kScatterMaxWaves = 64;
 constexpr int kScatterUnroll = 8;
-// Smallest piece a token is cut into when a list has fewer tokens than waves.
+// Smallest piece a token is cut into when a list has too few tokens for its waves.
 constexpr int kMinPiece = 4096;
 
 using gfd::wave::BatchLds;
@@ -68,8 +68,8 @@ constexpr int kStageVecs = 16 * 64;
 // Page-table form: token j of num_tokens lives at src_addrs[j] (host) and
 // lands at dst + j * token_size.  The unit of work is a piece: each token is
 // cut into 2^piece_shift pieces of token_size >> piece_shift bytes (the host
-// splits only when the list has fewer tokens than the grid has waves, and
-// only into whole multiples of 16 bytes), so unit u is piece u & (2^s - 1) of
+// splits only lists of at most half as many tokens as the waves it targets,
+// and only into whole multiples of 16 bytes), so unit u is piece u & (2^s - 1) of
 // token u >> s and lands at dst + u * piece.  Wave w copies units
 // [w*per_wave, ...) strided over the grid, per_wave <= 64 at a time.
 // kLds: stage through LDS.
