@@ -131,22 +131,32 @@ __global__ __launch_bounds__(kBlock) void zc_scatter_tokens(const uint64_t* __re
 }
 
 // Generic SG list: any sizes, any (disjoint) destinations, same batching.
+// The sizes are in the table, which the host does not read, so a short list
+// is split by count instead: each entry is cut into `pieces` slices of
+// ceil(size / pieces) bytes rounded up to 16 (keeping the entry's alignment;
+// the last slice takes the rest and slices past the end are empty), and
+// unit u is slice u % pieces of entry u / pieces.
 template <bool kLds>
 __global__ __launch_bounds__(kBlock) void zc_gather_sg(const gfd_sg_entry* __restrict__ entries, uint32_t count,
-                                                       uint32_t per_wave, int unroll, GridDone done) {
+                                                       uint32_t pieces, uint32_t per_wave, int unroll,
+                                                       GridDone done) {
     __shared__ BatchLds lds[kWavesPerBlock];
     __shared__ gfd::wave::vec4u stage[kLds ? kWavesPerBlock : 1][kLds ? kStageVecs : 1];
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const uint64_t wave = (uint64_t)blockIdx.x * kWavesPerBlock + wid;
     const uint64_t stride = (uint64_t)gridDim.x * kWavesPerBlock * per_wave;
-    for (uint64_t first = wave * per_wave; first < count; first += stride) {
-        const uint32_t nb = (uint32_t)min((uint64_t)per_wave, count - first);
+    const uint64_t units = (uint64_t)count * pieces;
+    for (uint64_t first = wave * per_wave; first < units; first += stride) {
+        const uint32_t nb = (uint32_t)min((uint64_t)per_wave, units - first);
         uint64_t md = 0, ms = 0, mn = 0;
         if (lane < nb) {
-            const gfd_sg_entry e = entries[first + lane];
-            md = e.dst;
-            ms = e.src;
-            mn = e.size;
+            const uint64_t u = first + lane;
+            const gfd_sg_entry e = entries[u / pieces];
+            const uint64_t step = ((e.size + pieces - 1) / pieces + 15) & ~15ull;
+            const uint64_t off = min((u % pieces) * step, e.size);
+            md = e.dst + off;
+            ms = e.src + off;
+            mn = min(step, e.size - off);
         }
         gfd::wave::copy_batch(unroll, md, ms, mn, nb, &lds[wid], kLds ? stage[wid] : nullptr);
     }
@@ -254,14 +264,18 @@ int launch_scatter_tokens(const uint64_t* dst_addrs, const void* src, uint32_t t
 int launch_gather_sg(const gfd_sg_entry* entries, int count, void* stream, GridDone done) {
     if (count < 0 || (count > 0 && !entries)) return (int)hipErrorInvalidValue;
     if (count == 0) return 0;
-    // Sizes are in the entry table, not known here: shape for 4 KiB entries.
-    const Shape s = shape_for((uint64_t)count, (uint64_t)count * 4096);
+    // Sizes are in the entry table, not known here: shape for 4 KiB entries,
+    // and give a list of at most half the target waves' entries
+    // target / count waves per entry (slices of a small entry may be empty).
+    const int target = std::max(4, env_int(kGatherShape.waves_env, kGatherShape.min_waves));
+    const uint32_t pieces = 2 * count <= target ? (uint32_t)(target / count) : 1u;
+    const Shape s = shape_for((uint64_t)count * pieces, (uint64_t)count * pieces * 4096);
     if (s.lds)
         hipLaunchKernelGGL(zc_gather_sg<true>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, entries,
-                           (uint32_t)count, s.per_wave, s.unroll, done);
+                           (uint32_t)count, pieces, s.per_wave, s.unroll, done);
     else
         hipLaunchKernelGGL(zc_gather_sg<false>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, entries,
-                           (uint32_t)count, s.per_wave, s.unroll, done);
+                           (uint32_t)count, pieces, s.per_wave, s.unroll, done);
     return (int)hipGetLastError();
 }
 

@@ -141,12 +141,15 @@ def _ragged_entries(dst_base, src_base, rng, count, max_size):
     return sizes, src_offs, dst_offs
 
 
+# Lists of at most 32 entries are cut into 64 // count slices per entry in the
+# kernel (the host does not read the sizes): 5 large entries, one 1 MiB
+# entry, 3 tiny ones (empty slices), and 32 entries (2 slices each).
+@pytest.mark.parametrize("count,max_size", [(700, 9000), (5, 300000), (1, 1 << 20), (3, 20), (32, 70000)])
 @pytest.mark.parametrize("where", ["device", "host"])
-def test_zero_copy_sg_generic_ragged(where):
-    log("zero_copy_sg ragged (%s entries)" % where)
-    rng = np.random.default_rng(11)
-    count = 700
-    sizes, src_offs, dst_offs = _ragged_entries(0, 0, rng, count, 9000)
+def test_zero_copy_sg_generic_ragged(where, count, max_size):
+    log("zero_copy_sg ragged (%s entries, %d up to %d B)" % (where, count, max_size))
+    rng = np.random.default_rng(11 + count)
+    sizes, src_offs, dst_offs = _ragged_entries(0, 0, rng, count, max_size)
     src = gfd_amd.HostBuffer(int(src_offs[-1] + sizes[-1] + 64))
     src.array[:] = rng.integers(0, 256, src.nbytes, dtype=np.uint8)
     dst_len = int(dst_offs[-1] + sizes[-1])
