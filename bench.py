@@ -384,6 +384,75 @@ REFERENCE_DIRECT_4KB_US = {16: 9.7, 64: 14.2, 256: 31.0, 1024: 91.7, 2048: 170.2
 REFERENCE_DIRECT_64KB_US = {16: 41.4, 64: 96.7, 256: 360.8, 1024: 1269.0, 2048: 2534.8}
 
 
+def run_short_lists(oracle, poller, iters, warmup):
+    """Short lists of large entries, which the zero-copy kernels spread over
+    their 64 waves: submit_direct on 4 tokens of 64 KiB (cut into pieces in
+    the token kernel) and on 4 ragged entries of about 256 KiB (cut on the
+    host), and gfd_zero_copy_gather on one 1 MiB entry with its table in HBM
+    (sliced in the kernel; HIP events on a stream).  Each output is checked
+    byte for byte."""
+    out = {}
+    L = Layout(oracle, 4, 65536)
+    t = np.zeros(iters)
+    rc = gfd_amd.lib().gfd_bench_submit_direct(poller._h, ctypes.cast(L.entries, ctypes.c_void_p), L.n, warmup,
+                                               iters, t.ctypes.data_as(PD))
+    assert rc == 0, gfd_amd.lib().gfd_last_error()
+    L.verify("direct 4 x 64 KiB")
+    out["direct_4x64KB"] = {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3)}
+    del L
+    rng = np.random.default_rng(3)
+    lib = gfd_amd.lib()
+    for key, sizes in (("direct_ragged_4x256KB", [262144, 262160, 262128, 262144]),
+                       ("zero_copy_sg_1x1MB", [1 << 20])):
+        sizes = np.array(sizes, np.uint64)
+        n, slot = len(sizes), int(sizes.max()) + 16
+        host = gfd_amd.HostBuffer(slot * n)
+        host.array[:] = rng.integers(0, 256, host.nbytes, dtype=np.uint8)
+        order = rng.permutation(n).astype(np.uint64)
+        dst = gfd_amd.DeviceBuffer(int(sizes.sum()))
+        dst_offs = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.uint64)
+        ent = np.zeros((n, 3), np.uint64)
+        ent[:, 0] = np.uint64(dst.ptr) + dst_offs
+        ent[:, 1] = np.uint64(host.ptr) + order * np.uint64(slot)
+        ent[:, 2] = sizes
+        if key.startswith("direct"):
+            entries = (gfd_amd.SGEntry * n)()
+            np.frombuffer(entries, dtype=np.uint64).reshape(n, 3)[:] = ent
+            rc = lib.gfd_bench_submit_direct(poller._h, ctypes.cast(entries, ctypes.c_void_p), n, warmup, iters,
+                                             t.ctypes.data_as(PD))
+            assert rc == 0, lib.gfd_last_error()
+            us = p50(t)
+        else:
+            tab = gfd_amd.DeviceBuffer(ent.nbytes)
+            tab.upload(ent.view(np.uint8).reshape(-1))
+            st, ea, eb = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+            lib.gfd_stream_create(ctypes.byref(st))
+            lib.gfd_event_create(ctypes.byref(ea))
+            lib.gfd_event_create(ctypes.byref(eb))
+            ts = []
+            for i in range(-warmup, iters):
+                lib.gfd_event_record(ea, st)
+                assert lib.gfd_zero_copy_gather(tab.ptr, n, st) == 0, lib.gfd_last_error()
+                lib.gfd_event_record(eb, st)
+                lib.gfd_event_synchronize(eb)
+                ms = ctypes.c_float(0)
+                lib.gfd_event_elapsed_ms(ctypes.byref(ms), ea, eb)
+                if i >= 0:
+                    ts.append(ms.value * 1000.0)
+            lib.gfd_event_destroy(ea)
+            lib.gfd_event_destroy(eb)
+            lib.gfd_stream_destroy(st)
+            us = p50(np.array(ts))
+        got = dst.download()
+        for i in range(n):
+            so, do, s = int(order[i]) * slot, int(dst_offs[i]), int(sizes[i])
+            if not (got[do:do + s] == host.array[so:so + s]).all():
+                raise SystemExit("PARITY FAILURE: %s entry %d" % (key, i))
+        out[key] = {"us_p50": round(us, 2), "GBps": round(gbps(int(sizes.sum()), us), 3), "entries": n}
+    log("  short lists: %s" % {k: v["us_p50"] for k, v in out.items()})
+    return out
+
+
 def run_direct_sizes(oracle, poller, iters, warmup):
     """submit_direct over the token counts the reference publishes (4 KiB
     tokens: 16 ... 4096; 64 KiB tokens: 16 ... 1024), on the bench's layout
@@ -1179,6 +1248,10 @@ def main():
     if want("direct") and want("sizes"):
         log("direct at the reference's published token counts ...")
         r_sizes = run_direct_sizes(oracle, direct, K, W)
+    r_short = None
+    if want("direct") and want("short"):
+        log("short lists of large entries ...")
+        r_short = run_short_lists(oracle, direct, K, W)
     direct.close()
 
     r_sessions = None
@@ -1302,6 +1375,7 @@ def main():
         "results_sessions": r_sessions,
         "results_direct_scattered_dst_8192x4KB": r_scat,
         "results_direct_sizes": r_sizes,
+        "results_short_lists": r_short,
         "results_offload": r_offload,
         "results_helper_waves": r_helpers,
         "results_timeline": r_timeline,

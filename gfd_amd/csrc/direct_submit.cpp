@@ -53,14 +53,17 @@ void no_chunk(void*, int, size_t, size_t) {}
 // so a list of fewer entries than its 64 waves leaves waves idle while a few
 // stream whole large entries.  Such a list's entries are cut into pieces of
 // at least 4 KiB, a multiple of 16 bytes each (an entry's last piece takes
-// what is left), so the pieces keep each entry's alignment.  Writes the
+// what is left), so the pieces keep each entry's alignment.  The piece size
+// is set for 64 - count waves, since each entry's last piece may be a short
+// one: the table then has at most 64 records, one per wave.  Writes the
 // table to out (at most cap records) and returns its length, or copies the
 // entries unchanged when the list is long enough or the pieces would not fit.
 int zc_fill_sg_table(const SGEntry* in, int count, size_t total, SGEntry* out, int cap) {
     constexpr int kWaves = 64;
     constexpr size_t kMinPiece = 4096;
     if (count < kWaves && total / (size_t)count >= 2 * kMinPiece) {
-        const size_t piece = std::max(kMinPiece, ((total + kWaves - 1) / kWaves + 15) & ~(size_t)15);
+        const size_t waves = (size_t)(kWaves - count);
+        const size_t piece = std::max(kMinPiece, ((total + waves - 1) / waves + 15) & ~(size_t)15);
         int n = 0;
         for (int i = 0; i < count && n >= 0; i++) {
             for (size_t off = 0; off < in[i].size; off += piece) {
