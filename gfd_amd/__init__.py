@@ -86,6 +86,12 @@ class SessionResult(ctypes.Structure):
 
 MAX_TILES = 1024
 MAX_SG_LISTS = 512
+# Bits of an SG session's error word (include/gfd/sg_task_queue.h).
+SG_ERR_RING_WAIT = 4
+SG_ERR_LIST_WAIT = 32
+SG_ERR_DEADLINE = 64
+# offsetof(gfd::SGTaskQueue, list_alloc_idx) (static_assert in sg_poller_kernels.hip).
+SG_QUEUE_LIST_ALLOC_IDX_OFFSET = 409600
 MAX_SG_POOL_ENTRIES = 16384
 SG_FLAG_NONE, SG_FLAG_HOST_SUBMITTED = 0, 1
 
@@ -155,6 +161,8 @@ def _declare(L):
         "gfd_zero_copy_gather_tokens_signal": ([vp, vp, c_u32, c_int, vp, vp, c_u64, vp], c_int),
         "gfd_zero_copy_scatter_tokens_signal": ([vp, vp, c_u32, c_int, vp, vp, c_u64, vp], c_int),
         "gfd_zero_copy_gather_signal": ([vp, c_int, vp, vp, c_u64, vp], c_int),
+        "gfd_zero_copy_gather_signal_presliced": ([vp, c_int, vp, vp, c_u64, vp], c_int),
+        "gfd_zero_copy_target_waves": ([], c_int),
         "gfd_poller_set_gather_slice_bytes": ([vp, c_u64], None),
         "gfd_host_gather": ([vp, c_int, vp, c_u64, c_u64, c_int, vp, c_int], c_int),
         "gfd_staging_pool_init": ([c_int, c_sz, c_int], c_int),

@@ -89,6 +89,12 @@ void CopyEngineManager::last_pinned_range(uintptr_t* lo, uintptr_t* hi) const {
     *lo = *hi = 0;
     if (sdma_) sdma_->last_pinned_range(lo, hi);
 }
+void CopyEngineManager::forget_pinned_range() {
+    if (sdma_) sdma_->forget_pinned_range();
+}
+void CopyEngineManager::trust_range(const void* p, size_t n) {
+    if (sdma_) sdma_->trust_range(p, n);
+}
 uint32_t CopyEngineManager::sdma_engine_mask() const { return sdma_ ? sdma_->engine_mask() : 0; }
 
 Status CopyEngineManager::pin_context() {

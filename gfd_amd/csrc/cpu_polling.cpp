@@ -118,6 +118,7 @@ CpuPollingThread::CpuPollingThread(DescriptorQueue* queue, void* gpu_base, void*
 }
 
 CpuPollingThread::~CpuPollingThread() {
+    stop_hook_ = nullptr;  // its owner may be half destroyed
     stop();
     delete gather_;
     gather_ = nullptr;
@@ -299,6 +300,7 @@ bool CpuPollingThread::init_copy_engine() {
     }
     num_staging_bufs_ = got;
     for (int b = 0; b < NUM_STAGING_BUFS; b++) staging_fence_[b] = 0;
+    for (int b = 0; b < got; b++) ce_manager_.trust_range(staging_bufs_[b], staging_buffer_size_);
     GFD_LOG_INFO("queue staging: %d x %zu bytes (NUMA %d), %d copy channel(s), SDMA engines 0x%x\n", got,
                  staging_buffer_size_, numa_node_, ce_manager_.num_channels(), ce_manager_.sdma_engine_mask());
     return start_workers();
@@ -332,6 +334,7 @@ void CpuPollingThread::start() {
 void CpuPollingThread::stop() {
     running_.store(false, std::memory_order_release);
     if (thread_.joinable()) thread_.join();
+    if (stop_hook_) stop_hook_();
 }
 
 void CpuPollingThread::publish_done(uint64_t value) {
@@ -471,6 +474,9 @@ void CpuPollingThread::polling_loop() {
 
 void CpuPollingThread::flush_batch(Descriptor* batch, int& count, uint32_t& or_flags) {
     if (count == 0) return;
+    // A source range found pinned for an earlier batch may have been freed
+    // and reused since: batches look their caller-owned sources up again.
+    ce_manager_.forget_pinned_range();
     const uint64_t cur_read = queue_->read_idx;
     if (trace_on_.load(std::memory_order_relaxed)) {
         uint64_t bytes = 0;

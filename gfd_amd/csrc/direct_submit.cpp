@@ -50,17 +50,21 @@ constexpr int kZcNotTaken = INT_MIN;               // direct_zero_copy: the list
 void no_chunk(void*, int, size_t, size_t) {}
 
 // The zero-copy SG kernel gives each entry of a short list a wave of its own,
-// so a list of fewer entries than its 64 waves leaves waves idle while a few
-// stream whole large entries.  Such a list's entries are cut into pieces of
-// at least 4 KiB, a multiple of 16 bytes each (an entry's last piece takes
-// what is left), so the pieces keep each entry's alignment.  The piece size
-// is set for 64 - count waves, since each entry's last piece may be a short
-// one: the table then has at most 64 records, one per wave.  Writes the
-// table to out (at most cap records) and returns its length, or copies the
-// entries unchanged when the list is long enough or the pieces would not fit.
-int zc_fill_sg_table(const SGEntry* in, int count, size_t total, SGEntry* out, int cap) {
-    constexpr int kWaves = 64;
+// so a list of fewer entries than its target waves (W, the kernel's own
+// figure: gfd_zero_copy_target_waves) leaves waves idle while a few stream
+// whole large entries.  Such a list's entries are cut into pieces of at least
+// 4 KiB, a multiple of 16 bytes each (an entry's last piece takes what is
+// left), so the pieces keep each entry's alignment.  The piece size is set for
+// W - count waves, since each entry's last piece may be a short one: the table
+// then has at most W records, one per wave, and goes to the kernel's
+// presliced launch (*presliced = true), which does not cut them again.  Writes
+// the table to out (at most cap records) and returns its length, or copies
+// the entries unchanged (*presliced = false) when the list is long enough or
+// the pieces would not fit.
+int zc_fill_sg_table(const SGEntry* in, int count, size_t total, SGEntry* out, int cap, bool* presliced) {
+    static const int kWaves = gfd_zero_copy_target_waves();
     constexpr size_t kMinPiece = 4096;
+    *presliced = false;
     if (count < kWaves && total / (size_t)count >= 2 * kMinPiece) {
         const size_t waves = (size_t)(kWaves - count);
         const size_t piece = std::max(kMinPiece, ((total + waves - 1) / waves + 15) & ~(size_t)15);
@@ -75,7 +79,10 @@ int zc_fill_sg_table(const SGEntry* in, int count, size_t total, SGEntry* out, i
                 out[n++] = SGEntry{in[i].dst + off, (const char*)in[i].src + off, len};
             }
         }
-        if (n >= 0) return n;
+        if (n >= 0) {
+            *presliced = true;
+            return n;
+        }
     }
     std::memcpy(out, in, (size_t)count * sizeof(SGEntry));
     return count;
@@ -249,9 +256,10 @@ int CpuPollingThread::direct_zero_copy(const SGEntry* entries, int count, size_t
             zc_table_ = static_cast<SGEntry*>(t);
             zc_table_cap_ = cap;
         }
-        const int n = zc_fill_sg_table(entries, count, total, zc_table_, zc_table_cap_);
-        rc = gfd_zero_copy_gather_signal(reinterpret_cast<const gfd_sg_entry*>(zc_table_), n, zc_counter_,
-                                         zc_done_, gen, zc_stream_);
+        bool cut = false;
+        const int n = zc_fill_sg_table(entries, count, total, zc_table_, zc_table_cap_, &cut);
+        rc = (cut ? gfd_zero_copy_gather_signal_presliced : gfd_zero_copy_gather_signal)(
+            reinterpret_cast<const gfd_sg_entry*>(zc_table_), n, zc_counter_, zc_done_, gen, zc_stream_);
     }
     if (rc != 0) return rc;
     trace(TRACE_ZC_LAUNCH, (uint32_t)count, total);
@@ -291,9 +299,10 @@ int CpuPollingThread::zc_launch_head(const SGEntry* entries, int k, bool uniform
     } else {
         size_t bytes = 0;
         for (int i = 0; i < k; i++) bytes += entries[i].size;
-        const int n = zc_fill_sg_table(entries, k, bytes, zc_table_, zc_table_cap_);
-        rc = gfd_zero_copy_gather_signal(reinterpret_cast<const gfd_sg_entry*>(zc_table_), n, zc_counter_, zc_done_,
-                                         g, zc_stream_);
+        bool cut = false;
+        const int n = zc_fill_sg_table(entries, k, bytes, zc_table_, zc_table_cap_, &cut);
+        rc = (cut ? gfd_zero_copy_gather_signal_presliced : gfd_zero_copy_gather_signal)(
+            reinterpret_cast<const gfd_sg_entry*>(zc_table_), n, zc_counter_, zc_done_, g, zc_stream_);
     }
     if (rc != 0) return rc;
     trace(TRACE_ZC_LAUNCH, (uint32_t)k, 0);
@@ -377,6 +386,7 @@ bool CpuPollingThread::init_direct_ce() {
         }
         direct_staging_size_ = total_cpu_size_;
     }
+    direct_ce_manager_.trust_range(direct_staging_, direct_staging_size_);
     if (direct_zc_max_bytes_ > 0 && !zc_warm_up()) {
         // The staged route (gather + copy engines) still serves every list.
         GFD_LOG_ERROR("zero-copy route set-up failed; submit_direct uses the copy engines only\n");
@@ -390,6 +400,11 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
     std::lock_guard<std::mutex> direct_lock(direct_mutex_);
     const auto t0 = std::chrono::steady_clock::now();
     if (direct_ce_manager_.pin_context() != 0) return -1.0;
+    // Address ranges found pinned (sources) or in device memory (destinations)
+    // by an earlier call may have been freed and reused since: look them up
+    // again, once per distinct allocation, in this call.
+    direct_ce_manager_.forget_pinned_range();
+    zc_dst_lo_ = zc_dst_hi_ = 0;
 
     // Total bytes and the three list properties the route depends on (split
     // over the gather workers for long lists).

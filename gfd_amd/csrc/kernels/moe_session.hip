@@ -242,7 +242,10 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
             break;
     }
     if (blockIdx.x == 0) {
-        if (sg::sg_wait_list_done(sq, total)) {
+        // Host lists queued before the launch land in it too: wait for those
+        // and this launch's `total`, so stop is raised only once nothing is
+        // left to copy.
+        if (sg::sg_wait_gpu_lists_done(sq, total)) {
             sg::sg_terminate_all_landed(sq);
         } else {
             if (lane == 0)
@@ -282,7 +285,7 @@ extern "C" int gfd_sg_session_launch_moe(gfd_sg_session_t s, const void* host_ba
     // The RMSNorm consumer shares each list between the session's compute
     // waves (num_compute_warps, at most SG_MAX_COMPUTE); transfer only needs one.
     const int compute = out ? std::min(p->compute_waves(), gfd::sg_warp_spec::SG_MAX_COMPUTE) : 1;
-    p->before_launch(stream, helpers, compute);
+    p->before_launch(stream, helpers, compute, p->idle_limit_ms());
     // At most one list more per expert than whole lists of rows.
     const uint64_t max_lists = (uint64_t)num_experts + (uint64_t)num_rows / rows_per_list;
     const MoeLists m{(uint64_t)(uintptr_t)host_base, token_stride, (uint64_t)(uintptr_t)dst, offsets, row_token,

@@ -224,10 +224,13 @@ __global__ __launch_bounds__(6 * 64) void sg_gpu_submit_kernel(gfd::DescriptorQu
         }
     }
     if (blockIdx.x == 0) {
-        if (gfd::sg::sg_wait_list_done(sq, num_lists))
+        if (gfd::sg::sg_wait_gpu_lists_done(sq, num_lists)) {
             gfd::sg::sg_terminate_all_landed(sq);
-        else
+        } else {
+            if (gfd::wave::lane_id() == 0)
+                __hip_atomic_fetch_or(&cnt->error, gfd::SG_ERR_LIST_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             gfd::sg::sg_terminate(sq);
+        }
     }
 }
 
@@ -238,7 +241,12 @@ __global__ __launch_bounds__(256) void sg_prepare_kernel(uint64_t* d_list_done, 
                                                         uint64_t* trace, uint64_t trace_words) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x, n = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t k = i; k < (uint64_t)gfd::MAX_SG_LISTS; k += n) d_list_done[k] = 0;
-    if (i == 0) *reinterpret_cast<gfd::SGDeviceCounters*>(d_list_done + gfd::MAX_SG_LISTS) = c;
+    if (i == 0) {
+        // The launch deadline arrives relative (ticks); it starts now, just
+        // ahead of the session kernel on the same stream.
+        if (c.deadline) c.deadline += (uint64_t)wall_clock64();
+        *reinterpret_cast<gfd::SGDeviceCounters*>(d_list_done + gfd::MAX_SG_LISTS) = c;
+    }
     for (uint64_t k = i; k < trace_words; k += n) trace[k] = 0;
 }
 
@@ -417,7 +425,9 @@ extern "C" int gfd_sg_session_launch_gpu_submit(gfd_sg_session_t s, const gfd_de
         return fail(hipErrorInvalidValue, "gfd_sg_session_launch_gpu_submit: invalid argument");
     gfd::SGWarpSpecSession* p = S(s);
     const int helpers = p->helper_waves();
-    p->before_launch(stream, helpers);
+    // Every list comes from the kernel's own submitters: a stall anywhere
+    // ends the launch at the deadline with error bits.
+    p->before_launch(stream, helpers, -1, p->idle_limit_ms());
     const auto* ents = reinterpret_cast<const gfd::DeviceSGEntry*>(d_entries);
     const dim3 grid((unsigned)p->num_blocks()), block((unsigned)(3 + helpers) * 64);
     if (list_sums)

@@ -17,6 +17,7 @@
 #include "gfd_capi.h"
 
 // Offsets the Python binding reads (gfd_amd.SGTaskQueue).
+static_assert(offsetof(gfd::SGTaskQueue, list_alloc_idx) == 409600, "SGTaskQueue layout");
 static_assert(offsetof(gfd::SGTaskQueue, lists_completed) == 409856, "SGTaskQueue layout");
 static_assert(offsetof(gfd::SGTaskQueue, d_list_done) == 409872, "SGTaskQueue layout");
 

@@ -261,14 +261,19 @@ int launch_scatter_tokens(const uint64_t* dst_addrs, const void* src, uint32_t t
     return (int)hipGetLastError();
 }
 
-int launch_gather_sg(const gfd_sg_entry* entries, int count, void* stream, GridDone done) {
+// Waves a short list is aimed at (GFD_ZC_WAVES, else the minimum grid).
+int short_list_waves() { return std::max(4, env_int(kGatherShape.waves_env, kGatherShape.min_waves)); }
+
+// slice: the table is the caller's list as it is, so a list of at most half
+// the target waves' entries gets target / count waves per entry (slices of a
+// small entry may be empty).  Without it, each record is one wave's work (the
+// caller has cut the list into pieces already).
+int launch_gather_sg(const gfd_sg_entry* entries, int count, void* stream, GridDone done, bool slice = true) {
     if (count < 0 || (count > 0 && !entries)) return (int)hipErrorInvalidValue;
     if (count == 0) return 0;
-    // Sizes are in the entry table, not known here: shape for 4 KiB entries,
-    // and give a list of at most half the target waves' entries
-    // target / count waves per entry (slices of a small entry may be empty).
-    const int target = std::max(4, env_int(kGatherShape.waves_env, kGatherShape.min_waves));
-    const uint32_t pieces = 2 * count <= target ? (uint32_t)(target / count) : 1u;
+    // Sizes are in the entry table, not known here: shape for 4 KiB entries.
+    const int target = short_list_waves();
+    const uint32_t pieces = slice && 2 * count <= target ? (uint32_t)(target / count) : 1u;
     const Shape s = shape_for((uint64_t)count * pieces, (uint64_t)count * pieces * 4096);
     if (s.lds)
         hipLaunchKernelGGL(zc_gather_sg<true>, dim3(s.blocks), dim3(kBlock), 0, (hipStream_t)stream, entries,
@@ -318,3 +323,12 @@ extern "C" int gfd_zero_copy_gather_signal(const gfd_sg_entry* entries, int coun
     if (!done_counter || !done_word) return (int)hipErrorInvalidValue;
     return launch_gather_sg(entries, count, stream, grid_done(done_counter, done_word, done_value));
 }
+
+extern "C" int gfd_zero_copy_gather_signal_presliced(const gfd_sg_entry* entries, int count,
+                                                     unsigned int* done_counter, uint64_t* done_word,
+                                                     uint64_t done_value, void* stream) {
+    if (!done_counter || !done_word) return (int)hipErrorInvalidValue;
+    return launch_gather_sg(entries, count, stream, grid_done(done_counter, done_word, done_value), false);
+}
+
+extern "C" int gfd_zero_copy_target_waves(void) { return short_list_waves(); }

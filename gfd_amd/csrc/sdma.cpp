@@ -203,8 +203,17 @@ int SdmaQueue::wait(uint64_t seq_end) {
     return error_ ? -1 : 0;
 }
 
+void SdmaQueue::trust_range(const void* p, size_t n) {
+    if (!p || n == 0 || ntrusted_ == kMaxTrusted) return;
+    trusted_lo_[ntrusted_] = (uintptr_t)p;
+    trusted_hi_[ntrusted_] = (uintptr_t)p + n;
+    ntrusted_++;
+}
+
 bool SdmaQueue::host_source_ok(const void* p, size_t n) {
     const uintptr_t lo = (uintptr_t)p, hi = lo + n;
+    for (int i = 0; i < ntrusted_; i++)
+        if (lo >= trusted_lo_[i] && hi <= trusted_hi_[i]) return true;
     if (lo >= ok_lo_ && hi <= ok_hi_) return true;
     hsa_amd_pointer_info_t info;
     std::memset(&info, 0, sizeof(info));

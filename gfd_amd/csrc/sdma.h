@@ -87,6 +87,15 @@ public:
         *lo = ok_lo_;
         *hi = ok_hi_;
     }
+    // Forget the remembered pinned range.  Called at the start of every call
+    // that takes caller-owned sources: a pinned allocation freed since the
+    // last call may have been replaced by pageable memory at the same
+    // addresses, which no copy engine or kernel may be handed.
+    void forget_pinned_range() { ok_lo_ = ok_hi_ = 0; }
+    // A pinned range the owner allocated itself and keeps for as long as this
+    // queue lives (staging buffers): a legal source that is never looked up
+    // or forgotten.  At most kMaxTrusted ranges; further ones are ignored.
+    void trust_range(const void* p, size_t n);
 
 private:
     struct Slot;
@@ -112,6 +121,9 @@ private:
     uint64_t tail_ = 0;  // all seq < tail_ complete
     int error_ = 0;
     uintptr_t ok_lo_ = 0, ok_hi_ = 0;  // last pinned range found
+    static constexpr int kMaxTrusted = 8;
+    uintptr_t trusted_lo_[kMaxTrusted] = {}, trusted_hi_[kMaxTrusted] = {};
+    int ntrusted_ = 0;
 
     // copy timing
     std::atomic<bool> timing_{false};

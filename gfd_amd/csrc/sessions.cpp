@@ -4,7 +4,9 @@
 // The sessions own their queues (fine-grained host memory, so kernels read
 // them with system-scope loads) and HBM arrays (per-tile / per-list
 // completion words plus the device counters the kernels claim work from).
-// No CPU poller runs: the kernels' transfer waves move the data themselves.
+// The kernels' transfer waves move the data themselves; the CPU poller a
+// session hands out through get_poller() is created on first use and serves
+// kernels the caller launches around its start()/stop().
 #include <algorithm>
 #include <chrono>
 #include <cstring>
@@ -30,6 +32,20 @@ double ms_between(std::chrono::steady_clock::time_point a, std::chrono::steady_c
 
 uint64_t load_acquire(const volatile uint64_t* p) { return __atomic_load_n(const_cast<uint64_t*>(p), __ATOMIC_ACQUIRE); }
 void store_release(volatile uint64_t* p, uint64_t v) { __atomic_store_n(const_cast<uint64_t*>(p), v, __ATOMIC_RELEASE); }
+
+// Staging of a session's poller: five buffers of this size.  Descriptors of a
+// larger batch are copied run by run from their (pinned) sources instead.
+constexpr size_t kSessionPollerStaging = 8u << 20;
+
+// A poller over `queue` with its copy engines set up; logs and still returns
+// the object if the set-up fails, as the reference's sessions do.
+CpuPollingThread* make_session_poller(DescriptorQueue* queue, void* gpu_base, void* cpu_base, size_t staging,
+                                      TiledQueue* tiled) {
+    auto* p = new CpuPollingThread(queue, gpu_base, cpu_base, staging, true, -1);
+    if (tiled) p->set_tiled_queue(tiled);
+    if (!p->init_copy_engine()) GFD_LOG_ERROR("session poller: copy engine set-up failed\n");
+    return p;
+}
 
 }  // namespace
 
@@ -95,6 +111,8 @@ WarpSpecSession::WarpSpecSession(const WarpSpecConfig& config) : config_(config)
 
 WarpSpecSession::~WarpSpecSession() {
     if (running_) synchronize();
+    delete poller_;
+    poller_ = nullptr;
     if (d_signals_) gfd_hip_free(d_signals_);
     if (tq_) gfd_hip_host_free(tq_);
 }
@@ -119,6 +137,19 @@ void WarpSpecSession::reset() {
     tq_->scheduler.next_tile = 0;
     error_bits_ = 0;
     tiles_done_ = 0;
+    landed_tiles_total_ = 0;
+    if (poller_) poller_->reset_stats();
+}
+
+CpuPollingThread* WarpSpecSession::get_poller() const {
+    if (!poller_ && ok_) {
+        const size_t total = (size_t)config_.total_tokens * config_.token_size;
+        poller_ = make_session_poller(&tq_->base, config_.gpu_dst, config_.cpu_src,
+                                      std::min(total, kSessionPollerStaging), tq_);
+        const uint64_t tokens = landed_tiles_total_ * config_.tokens_per_tile;
+        poller_->add_device_landed(tokens, tokens * config_.token_size, landed_tiles_total_);
+    }
+    return poller_;
 }
 
 void WarpSpecSession::before_launch(gfd_stream_t stream) {
@@ -141,6 +172,11 @@ bool WarpSpecSession::synchronize() {
         const uint32_t n = std::min<uint32_t>(config_.total_tiles(), (uint32_t)MAX_TILES);
         if (n) gfd_hip_memcpy_d2h((void*)tq_->tile_chunk_done, (uint64_t)(uintptr_t)d_signals_, n * sizeof(uint64_t));
         tq_->scheduler.next_tile = (uint32_t)std::min<uint64_t>(c.next_tile, config_.total_tiles());
+        landed_tiles_total_ += tiles_done_;
+        if (poller_) {
+            const uint64_t tokens = tiles_done_ * config_.tokens_per_tile;
+            poller_->add_device_landed(tokens, tokens * config_.token_size, tiles_done_);
+        }
     } else {
         GFD_LOG_ERROR("WarpSpecSession: synchronize failed: %s\n", gfd_hip_error_string(rc));
         error_bits_ |= 1ull << 63;
@@ -202,6 +238,8 @@ SGWarpSpecSession::SGWarpSpecSession(const SGWarpSpecConfig& config) : config_(c
 
 SGWarpSpecSession::~SGWarpSpecSession() {
     if (running_) synchronize();
+    delete poller_;  // clears its stop hook first
+    poller_ = nullptr;
     if (trace_buf_) gfd_hip_free(trace_buf_);
     if (sq_) {
         if (sq_->d_list_done) gfd_hip_free(sq_->d_list_done);
@@ -272,7 +310,7 @@ uint64_t SGWarpSpecSession::submit_sg_list(const DeviceSGEntry* entries, uint32_
     return idx;
 }
 
-void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int compute_waves) {
+void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int compute_waves, uint32_t deadline_ms) {
     if (running_) synchronize();
     if (!ok_) return;
     __atomic_store_n(&sq_->terminate, 0u, __ATOMIC_RELEASE);
@@ -289,6 +327,9 @@ void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int
     c.list_base = consumed_lists_;
     c.helpers = (uint64_t)(helper_waves < 0 ? config_.transfer_helper_waves : helper_waves);
     c.compute_waves = (uint64_t)(compute_waves < 0 ? this->compute_waves() : compute_waves);
+    c.host_lists = sq_->list_alloc_idx - consumed_lists_;
+    // Relative here (100 MHz ticks); the set-up kernel adds the GPU clock.
+    c.deadline = (uint64_t)deadline_ms * 100000ull;
     uint64_t trace_words = 0;
     if (trace_buf_) {
         c.trace = (uint64_t)(uintptr_t)trace_buf_;
@@ -304,6 +345,7 @@ void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int
         GFD_LOG_ERROR("SGWarpSpecSession: launch set-up kernel failed (%s); writing the state directly\n",
                       gfd_hip_error_string(rc));
         rc = gfd_hip_stream_synchronize(stream);
+        c.deadline = 0;  // the host cannot read the GPU clock: no launch deadline this time
         if (!rc && trace_words) rc = gfd_hip_memset_d8(c.trace, 0, trace_words * 8);
         if (!rc) rc = gfd_hip_memset_d8((uint64_t)(uintptr_t)sq_->d_list_done, 0, MAX_SG_LISTS * sizeof(uint64_t));
         if (!rc) rc = gfd_hip_memcpy_h2d((uint64_t)(uintptr_t)sg_device_counters(sq_), &c, sizeof(c));
@@ -342,6 +384,19 @@ bool SGWarpSpecSession::synchronize(uint64_t extra_gpu_lists) {
         error_bits_ |= 1ull << 63;
         return false;
     }
+    absorb(c);
+    // A kernel the caller launches next, without launch(), starts from here.
+    if (poller_) prepare_raw_launch();
+    if (!landed || !pending_.empty()) {
+        GFD_LOG_ERROR("SGWarpSpecSession: %zu submitted lists did not land\n", pending_.size());
+        pending_.clear();
+        landed = false;
+    }
+    if (error_bits_) GFD_LOG_ERROR("SGWarpSpecSession: kernel reported error bits 0x%llx\n", (unsigned long long)error_bits_);
+    return landed && error_bits_ == 0;
+}
+
+void SGWarpSpecSession::absorb(const SGDeviceCounters& c) {
     error_bits_ |= c.error;
     entries_done_ = c.entries_done - consumed_entries_;
     bytes_done_ = c.bytes_done;
@@ -355,13 +410,55 @@ bool SGWarpSpecSession::synchronize(uint64_t extra_gpu_lists) {
     sq_->entry_consumed_idx = consumed_entries_;
     sq_->lists_completed = lists_done_;
     retire_done();
-    if (!landed || !pending_.empty()) {
-        GFD_LOG_ERROR("SGWarpSpecSession: %zu submitted lists did not land\n", pending_.size());
-        pending_.clear();
-        landed = false;
+    landed_entries_total_ += entries_done_;
+    landed_bytes_total_ += bytes_done_;
+    landed_lists_total_ += lists_done_;
+    if (poller_) poller_->add_device_landed(entries_done_, bytes_done_, lists_done_);
+}
+
+void SGWarpSpecSession::prepare_raw_launch() {
+    __atomic_store_n(&sq_->terminate, 0u, __ATOMIC_RELEASE);
+    SGDeviceCounters c{};
+    c.list_claim = c.list_known = c.list_base = consumed_lists_;
+    c.list_alloc = sq_->list_alloc_idx;
+    c.entry_alloc = sq_->entry_alloc_idx;
+    c.entries_done = consumed_entries_;
+    c.compute_waves = 1;  // the caller's kernel layout is its own: no helpers, one compute wave
+    c.host_lists = sq_->list_alloc_idx - consumed_lists_;
+    const uint64_t d = (uint64_t)(uintptr_t)sq_->d_list_done;
+    if (gfd_hip_memset_d8(d, 0, MAX_SG_LISTS * sizeof(uint64_t)) != 0 ||
+        gfd_hip_memcpy_h2d((uint64_t)(uintptr_t)sg_device_counters(sq_), &c, sizeof(c)) != 0 ||
+        gfd_hip_device_synchronize() != 0) {
+        GFD_LOG_ERROR("SGWarpSpecSession: writing the counters for the next launch failed\n");
+        error_bits_ |= 1ull << 63;
     }
+}
+
+void SGWarpSpecSession::after_raw_launch() {
+    // A launch made through launch() is taken in by synchronize().
+    if (!ok_ || running_) return;
+    SGDeviceCounters c{};
+    if (gfd_hip_memcpy_d2h(&c, (uint64_t)(uintptr_t)sg_device_counters(sq_), sizeof(c)) != 0) {
+        GFD_LOG_ERROR("SGWarpSpecSession: reading the device counters failed\n");
+        error_bits_ |= 1ull << 63;
+        return;
+    }
+    // Every transfer wave claims at least one ring index before it can see
+    // terminate, so an untouched claim counter means no kernel ran.
+    if (c.list_claim == c.list_base && c.lists_done == 0 && c.error == 0) return;
+    absorb(c);
     if (error_bits_) GFD_LOG_ERROR("SGWarpSpecSession: kernel reported error bits 0x%llx\n", (unsigned long long)error_bits_);
-    return landed && error_bits_ == 0;
+    prepare_raw_launch();
+}
+
+CpuPollingThread* SGWarpSpecSession::get_poller() const {
+    if (!poller_ && ok_) {
+        auto* self = const_cast<SGWarpSpecSession*>(this);
+        poller_ = make_session_poller(dq_, nullptr, nullptr, kSessionPollerStaging, nullptr);
+        poller_->add_device_landed(landed_entries_total_, landed_bytes_total_, landed_lists_total_);
+        poller_->set_stop_hook([self]() { self->after_raw_launch(); });
+    }
+    return poller_;
 }
 
 void SGWarpSpecSession::reset() {
@@ -382,6 +479,8 @@ void SGWarpSpecSession::reset() {
     pending_.clear();
     consumed_lists_ = consumed_entries_ = 0;
     error_bits_ = entries_done_ = bytes_done_ = lists_done_ = 0;
+    landed_entries_total_ = landed_bytes_total_ = landed_lists_total_ = 0;
+    if (poller_) poller_->reset_stats();
 }
 
 bool SGWarpSpecSession::gpu_lists_fit(uint64_t lists, uint64_t entries) const {

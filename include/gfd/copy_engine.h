@@ -137,6 +137,11 @@ public:
     // Bounds of the pinned allocation the last successful host_source_ok found
     // (both 0 without the SDMA backend).
     void last_pinned_range(uintptr_t* lo, uintptr_t* hi) const;
+    // Forget the remembered pinned range (start of each call taking
+    // caller-owned sources); mark a range this library allocated pinned and
+    // keeps while the manager lives as always legal (staging buffers).
+    void forget_pinned_range();
+    void trust_range(const void* p, size_t n);
 
     // Engine timestamps of each copy (SDMA backend only; see SdmaQueue).
     struct CopyTime {

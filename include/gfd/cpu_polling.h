@@ -16,6 +16,7 @@
 // and its own copy channels.
 #include <atomic>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <thread>
 #include <utility>
@@ -112,6 +113,19 @@ public:
     }
 
     // ---- MI355X additions -------------------------------------------------
+    // Data moved by the transfer waves of the session that owns this poller
+    // (sessions copy with their own waves, not through the poller): the
+    // session adds what each launch landed, so the stats getters above count
+    // it (entries as descriptors, lists or tiles as batches, and bytes).
+    void add_device_landed(uint64_t entries, uint64_t bytes, uint64_t batches) {
+        descriptors_processed_.fetch_add(entries, std::memory_order_relaxed);
+        total_bytes_copied_.fetch_add(bytes, std::memory_order_relaxed);
+        batches_submitted_.fetch_add(batches, std::memory_order_relaxed);
+    }
+    // Called at the end of every stop() (set by an owning session, which then
+    // takes in the results of a kernel the caller launched itself between
+    // start() and stop(); an empty function clears it).
+    void set_stop_hook(std::function<void()> hook) { stop_hook_ = std::move(hook); }
     int num_gather_workers() const;
     const std::vector<int>& worker_cpus() const { return worker_cpus_; }
     int poller_cpu() const { return poller_cpu_; }
@@ -330,6 +344,7 @@ private:
 
     std::atomic<bool> running_{false};
     std::thread thread_;
+    std::function<void()> stop_hook_;
 
     static constexpr int TRACE_CAP = 16384;
     std::vector<TraceEvent> trace_buf_;

@@ -8,7 +8,8 @@
 // SGDeviceCounters in HBM (never atomics across PCIe into host memory);
 // entries and headers are written to the host-resident SGTaskQueue with plain
 // stores and committed with a system-scope release store of `sequence`;
-// waits are bounded and return false when they give up.
+// waits are bounded (a poll count, and the launch's deadline when it has one)
+// and return false when they give up.
 //
 // Ring slots: list index i lives in lists[i % MAX_SG_LISTS].  Before the
 // header of index i is written, the list that used the slot before it
@@ -34,12 +35,22 @@ __device__ __forceinline__ uint64_t load_dev(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The launch's deadline (SGDeviceCounters::deadline; 0: none), read once per
+// wait, and whether it has passed.
+__device__ __forceinline__ uint64_t launch_deadline(SGTaskQueue* sq) {
+    return __hip_atomic_load(&counters(sq)->deadline, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool past(uint64_t deadline) {
+    return deadline != 0 && (uint64_t)wall_clock64() > deadline;
+}
+
 // Wait until `needed` more pool entries can be allocated without overwriting
 // entries whose data has not landed yet.
 __device__ __forceinline__ bool sg_wait_entry_space(SGTaskQueue* sq, uint32_t needed) {
     if (needed > (uint32_t)MAX_SG_POOL_ENTRIES) return false;
     SGDeviceCounters* c = counters(sq);
-    for (uint64_t n = 0; n < wave::kSpinLimit; n++) {
+    const uint64_t dl = launch_deadline(sq);
+    for (uint64_t n = 0; n < wave::kSpinLimit && !past(dl); n++) {
         const uint64_t alloc = load_dev(&c->entry_alloc);
         const uint64_t done = load_dev(&c->entries_done);
         if (alloc - done <= (uint64_t)(MAX_SG_POOL_ENTRIES - needed)) return true;
@@ -51,7 +62,8 @@ __device__ __forceinline__ bool sg_wait_entry_space(SGTaskQueue* sq, uint32_t ne
 // Wait until fewer than MAX_SG_LISTS - 1 lists of this launch are in flight.
 __device__ __forceinline__ bool sg_wait_list_space(SGTaskQueue* sq) {
     SGDeviceCounters* c = counters(sq);
-    for (uint64_t n = 0; n < wave::kSpinLimit; n++) {
+    const uint64_t dl = launch_deadline(sq);
+    for (uint64_t n = 0; n < wave::kSpinLimit && !past(dl); n++) {
         const uint64_t in_flight = load_dev(&c->list_alloc) - load_dev(&c->list_base) - load_dev(&c->lists_done);
         if (in_flight < (uint64_t)(MAX_SG_LISTS - 1)) return true;
         __builtin_amdgcn_s_sleep(2);
@@ -98,7 +110,8 @@ __device__ __forceinline__ bool sg_wait_slot_free(SGTaskQueue* sq, uint64_t slot
     if (slot < (uint64_t)MAX_SG_LISTS) return true;
     const uint64_t want = slot - MAX_SG_LISTS + 1;
     const SGList& l = sq->lists[slot % MAX_SG_LISTS];
-    for (uint64_t n = 0; n < wave::kSpinLimit; n++) {
+    const uint64_t dl = launch_deadline(sq);
+    for (uint64_t n = 0; n < wave::kSpinLimit && !past(dl); n++) {
         if (wave::load_system(&l.done) >= want) return true;
         __builtin_amdgcn_s_sleep(32);
     }
@@ -142,19 +155,37 @@ __device__ __forceinline__ uint64_t sg_submit_list(SGTaskQueue* sq, const Device
     return slot;
 }
 
-// Wait until at least `expected` lists of this launch have landed in HBM.
+// Wait until at least `expected` lists have landed in HBM during this launch
+// (host-submitted lists queued before it included, as the reference's
+// lists_completed counts every list).
 __device__ __forceinline__ bool sg_wait_list_done(SGTaskQueue* sq, uint64_t expected) {
-    for (uint64_t n = 0; n < wave::kSpinLimit; n++) {
+    const uint64_t dl = launch_deadline(sq);
+    for (uint64_t n = 0; n < wave::kSpinLimit && !past(dl); n++) {
         if (load_dev(&counters(sq)->lists_done) >= expected) return true;
         __builtin_amdgcn_s_sleep(2);
     }
     return false;
 }
 
+// Lists host submitters had queued when this launch started; they land
+// during the launch and lists_done counts them.
+__device__ __forceinline__ uint64_t sg_host_lists(SGTaskQueue* sq) {
+    return __hip_atomic_load(&counters(sq)->host_lists, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait until the `gpu_lists` lists this launch's GPU submitters post have
+// landed, on top of the host lists queued before the launch.  Only then is
+// every list of the launch known to have landed (the precondition of
+// sg_terminate_all_landed).
+__device__ __forceinline__ bool sg_wait_gpu_lists_done(SGTaskQueue* sq, uint64_t gpu_lists) {
+    return sg_wait_list_done(sq, sg_host_lists(sq) + gpu_lists);
+}
+
 // Wait until list `list_id` has landed (d_list_done[list_id] != 0).
 __device__ __forceinline__ bool sg_wait_list_id_done(SGTaskQueue* sq, uint32_t list_id) {
     if (list_id >= (uint32_t)MAX_SG_LISTS) return false;
-    for (uint64_t n = 0; n < wave::kSpinLimit; n++) {
+    const uint64_t dl = launch_deadline(sq);
+    for (uint64_t n = 0; n < wave::kSpinLimit && !past(dl); n++) {
         if (load_dev(&sq->d_list_done[list_id]) != 0) return true;
         __builtin_amdgcn_s_sleep(2);
     }

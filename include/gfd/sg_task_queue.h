@@ -93,7 +93,17 @@ struct SGDeviceCounters {
     uint64_t trace;
     uint64_t trace_cap;
     uint64_t trace_blocks;
-    uint64_t _pad;
+    // Lists host submitters had queued before this launch.  They land during
+    // it, so lists_done counts them: a GPU submitter waiting for its own
+    // `total` lists waits for lists_done >= host_lists + total.
+    uint64_t host_lists;
+    // Launch-wide deadline on the GPU's 100 MHz wall clock (wall_clock64()),
+    // or 0 for none.  Launches whose lists all come from GPU submitters set
+    // it: every wait of the launch (transfer, helper and compute waves, and
+    // the sg:: submitter waits) gives up once it has passed, so a protocol
+    // stall ends the kernel with an error bit instead of spinning.
+    uint64_t deadline;
+    uint64_t _pad[7];
 };
 
 // One list of a traced launch, in wall-clock ticks (100 MHz): when its
@@ -128,7 +138,8 @@ constexpr uint64_t SG_ERR_RING_WAIT = 4;     // GPU submitter: a ring slot never
 constexpr uint64_t SG_ERR_HELPER_WAIT = 8;   // transfer waves: a copy job's hand-off stalled
 constexpr uint64_t SG_ERR_BAD_ROW = 16;      // GPU submitter: a routing entry out of range (skipped)
 constexpr uint64_t SG_ERR_LIST_WAIT = 32;    // GPU submitter: its lists did not all land in time
-static_assert(sizeof(SGDeviceCounters) == 128, "SGDeviceCounters is two cache lines");
+constexpr uint64_t SG_ERR_DEADLINE = 64;     // transfer wave: gave up at the launch's deadline
+static_assert(sizeof(SGDeviceCounters) == 192, "SGDeviceCounters is three cache lines");
 
 GFD_HD inline SGDeviceCounters* sg_device_counters(const SGTaskQueue* sq) {
     return reinterpret_cast<SGDeviceCounters*>(sq->d_list_done + MAX_SG_LISTS);

@@ -91,10 +91,14 @@ __device__ __forceinline__ uint64_t _idle_limit_ticks(const SGTaskQueue* sq) {
     return (uint64_t)(ms ? ms : 30000u) * 100000ull;  // 100 MHz wall clock
 }
 
-// Wait until ring index idx is committed.  False once terminate (or the idle
-// limit) ends the wait with nothing committed.
-__device__ __forceinline__ bool _wait_committed(SGTaskQueue* sq, SGDeviceCounters* cnt, uint64_t idx,
-                                                uint64_t idle_ticks) {
+// _wait_committed's outcomes.
+enum : int { kSgStopped = 0, kSgCommitted = 1, kSgDeadline = 2 };
+
+// Wait until ring index idx is committed: kSgCommitted.  kSgStopped once
+// terminate (or the idle limit) ends the wait with nothing committed;
+// kSgDeadline once the launch's deadline (0: none) has passed.
+__device__ __forceinline__ int _wait_committed(SGTaskQueue* sq, SGDeviceCounters* cnt, uint64_t idx,
+                                               uint64_t idle_ticks, uint64_t deadline) {
     const int lane = wave::lane_id();
     const SGList& mine = sq->lists[idx % MAX_SG_LISTS];
     const uint64_t t0 = wall_clock64();
@@ -105,7 +109,7 @@ __device__ __forceinline__ bool _wait_committed(SGTaskQueue* sq, SGDeviceCounter
             // its release when it raised list_known, so the header and
             // entries read next are those written before that commit.
             wave::acquire_agent();
-            return true;
+            return kSgCommitted;
         }
         if (idx == known) {
             // Leader.  terminate is read before the sequence.  Whoever sets
@@ -128,17 +132,17 @@ __device__ __forceinline__ bool _wait_committed(SGTaskQueue* sq, SGDeviceCounter
                 if (lane == 0)
                     __hip_atomic_fetch_max(&cnt->list_known, idx + (run ? run : 1), __ATOMIC_RELEASE,
                                            __HIP_MEMORY_SCOPE_AGENT);
-                return true;
+                return kSgCommitted;
             }
             if (term) {
                 if (lane == 0) __hip_atomic_store(&cnt->stop, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                return false;
+                return kSgStopped;
             }
             // A GPU submitter that saw every list land raises stop directly.
-            if (__hip_atomic_load(&cnt->stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+            if (__hip_atomic_load(&cnt->stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return kSgStopped;
             __builtin_amdgcn_s_sleep(4);
         } else {
-            if (__hip_atomic_load(&cnt->stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+            if (__hip_atomic_load(&cnt->stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return kSgStopped;
             // Back off in proportion to how many commits this wave is still
             // waiting for, up to ~3.5 us between polls: device-scope loads
             // bypass the XCD-local L2, so hundreds of idle waves polling at
@@ -152,7 +156,8 @@ __device__ __forceinline__ bool _wait_committed(SGTaskQueue* sq, SGDeviceCounter
                 __builtin_amdgcn_s_sleep(127);
             }
         }
-        if (wall_clock64() - t0 > idle_ticks) return false;
+        if (sg::past(deadline)) return kSgDeadline;
+        if (wall_clock64() - t0 > idle_ticks) return kSgStopped;
     }
 }
 
@@ -245,6 +250,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
     if (w == 0) {
         // ---------------- transfer wave (leader)
         const uint64_t idle_ticks = _idle_limit_ticks(sq);
+        const uint64_t deadline = sg::launch_deadline(sq);
         // Timeline of this launch's lists, when the session asks for one.
         const uint64_t t_start = (uint64_t)wall_clock64();
         SGTraceList* const trace =
@@ -262,7 +268,12 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             uint64_t idx = 0;
             if (lane == 0) idx = sg::atomic_add_dev(&cnt->list_claim, 1);
             idx = wave::broadcast0(idx);
-            if (!_wait_committed(sq, cnt, idx, idle_ticks)) break;
+            const int got = _wait_committed(sq, cnt, idx, idle_ticks, deadline);
+            if (got != kSgCommitted) {
+                if (got == kSgDeadline && lane == 0)
+                    __hip_atomic_fetch_or(&cnt->error, SG_ERR_DEADLINE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
             SGList& l = sq->lists[idx % MAX_SG_LISTS];
             const uint32_t pool_offset = l.pool_offset, count = l.count, list_id = l.list_id, flags = l.flags;
             if (lane == 0) wave::store_system(&l.sequence, 0);  // claimed
@@ -326,13 +337,16 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
         // ---------------- transfer helper: copies batches of the leader's
         // jobs; bounded like the compute wave.
         const uint64_t limit = _idle_limit_ticks(sq) + 100000000ull;
+        const uint64_t deadline = sg::launch_deadline(sq);
         for (int want = 1;;) {
             int seq = 0;
             const uint64_t t0 = wall_clock64();
             for (;;) {
                 seq = wave::lds_load(&job.seq);
                 if (seq < 0 || seq >= want) break;
-                if (wall_clock64() - t0 > limit) {
+                // The leader publishes -1 when it stops, deadline included;
+                // a second past it means the leader itself is stuck.
+                if (wall_clock64() - t0 > limit || (deadline && sg::past(deadline + 100000000ull))) {
                     if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_HELPER_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     seq = -1;
                     break;
@@ -356,6 +370,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
         // ---------------- compute wave(s): bounded by the transfer wave's
         // idle limit (plus 1 s), the longest the transfer wave can stay silent.
         const uint64_t limit = _idle_limit_ticks(sq) + 100000000ull;
+        const uint64_t deadline = sg::launch_deadline(sq);
         for (uint64_t k = 0;; k++) {
             const int s = (int)(k & 1);
             const int want = (int)(k / 2) + 1;
@@ -370,7 +385,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
                     ready = wave::lds_load(&slots[s].seq) == want;
                     break;
                 }
-                if (wall_clock64() - t0 > limit) {
+                if (wall_clock64() - t0 > limit || (deadline && sg::past(deadline + 100000000ull))) {
                     if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_COMPUTE_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
                 }

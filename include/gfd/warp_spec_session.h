@@ -6,8 +6,15 @@
 //
 // MI355X design: the kernels move the data themselves (zero-copy loads from
 // pinned host memory, see include/gfd/warp_spec.h and sg_warp_spec.h), so a
-// session owns queues and HBM counters but no CPU poller; get_poller()
-// returns nullptr.  launch() is a template defined for HIP translation units.
+// session's launches need no CPU poller.  get_poller() still returns a live
+// CpuPollingThread owned by the session, created on first use over the
+// session's own descriptor ring (WarpSpecSession: tiled mode over its
+// TiledQueue; SGWarpSpecSession: queue mode over its DescriptorQueue).  Its
+// start()/stop() bracket a kernel the caller launches itself, its stats
+// count what the session's transfer waves landed as well as what it copied
+// itself, and after a caller-launched SG kernel its stop() leaves the session
+// ready for the next launch.  launch() is a template defined for HIP
+// translation units.
 #include <chrono>
 #include <cstdint>
 #include <deque>
@@ -125,7 +132,9 @@ public:
     Stats get_stats() const;
 
     TiledQueue* get_queue() const { return tq_; }
-    CpuPollingThread* get_poller() const { return nullptr; }
+    // The session's poller (created on first call; nullptr if the session
+    // failed to construct).  reset() clears its stats, as the reference's does.
+    CpuPollingThread* get_poller() const;
     // The configuration in effect (helper waves resolved).
     const WarpSpecConfig& config() const { return config_; }
     bool ok() const { return ok_; }
@@ -149,6 +158,10 @@ private:
     double last_elapsed_ms_ = 0;
     void* trace_buf_ = nullptr;  // HBM: trace_cap_ SGTraceList + num_blocks_ SGTraceBlock
     uint32_t trace_cap_ = 0;
+    mutable CpuPollingThread* poller_ = nullptr;
+    // Tiles landed by this session's launches since reset(): a poller created
+    // later starts from them.
+    uint64_t landed_tiles_total_ = 0;
 };
 
 struct SGWarpSpecConfig {
@@ -185,7 +198,15 @@ public:
 
     SGTaskQueue* get_sg_queue() const { return sq_; }
     DescriptorQueue* get_desc_queue() const { return dq_; }
-    CpuPollingThread* get_poller() const { return nullptr; }
+    // The session's poller (created on first call; nullptr if the session
+    // failed to construct).  For a kernel the caller launches itself
+    // (test/test_sg_gpu_submit.cu's flow: launch, get_poller()->start(),
+    // device synchronize, get_poller()->stop()), stop() reads back what the
+    // launch landed (get_stats(), the poller's stats) and prepares the
+    // session's counters for the next launch.  Such a kernel starts on the
+    // state a new session, reset(), that stop(), or synchronize() once the
+    // poller exists, leave: no helper waves, one compute wave, no deadline.
+    CpuPollingThread* get_poller() const;
 
     // Launch a GFD_SG_WARP_SPEC_KERNEL kernel: (DescriptorQueue*, SGTaskQueue*, fn).
     template <typename KernelFn, typename ComputeFn>
@@ -215,8 +236,14 @@ public:
     // Internal: called by launch().  helper_waves < 0: the configured count;
     // kernels whose extra waves have other work (a GPU submitter) pass their own.
     // compute_waves < 0: num_compute_warps (used only by functors that share
-    // lists between compute waves).
-    void before_launch(gfd_stream_t stream, int helper_waves = -1, int compute_waves = -1);
+    // lists between compute waves).  deadline_ms > 0: every wait of the
+    // launch gives up that long after it starts (launches whose lists all
+    // come from GPU submitters; see SGDeviceCounters::deadline).
+    void before_launch(gfd_stream_t stream, int helper_waves = -1, int compute_waves = -1,
+                       uint32_t deadline_ms = 0);
+    // The idle limit in effect (idle_limit_ms, 0 meaning 30 s), which GPU
+    // submitter launches also take as their deadline.
+    uint32_t idle_limit_ms() const { return config_.idle_limit_ms ? config_.idle_limit_ms : 30000u; }
     int compute_waves() const { return config_.num_compute_warps > 0 ? config_.num_compute_warps : 1; }
     // True when GPU submitters posting at most `lists` lists and `entries`
     // entries in the next launch can never find the ring, a ring slot or the
@@ -242,6 +269,14 @@ private:
     void retire_done();
     bool wait_until(const std::function<bool()>& cond, double limit_ms);
     double wait_limit_ms() const;
+    // Take in a finished launch's device counters: stats, consumed ring and
+    // pool positions, error bits, the poller's stats.
+    void absorb(const SGDeviceCounters& c);
+    // Device counters for a kernel the caller launches itself, written with
+    // blocking copies.
+    void prepare_raw_launch();
+    // The poller's stop hook: a caller-launched kernel has finished.
+    void after_raw_launch();
 
     SGWarpSpecConfig config_;
     SGTaskQueue* sq_ = nullptr;
@@ -259,6 +294,9 @@ private:
     double last_elapsed_ms_ = 0;
     void* trace_buf_ = nullptr;  // HBM: trace_cap_ SGTraceList + num_blocks_ SGTraceBlock
     uint32_t trace_cap_ = 0;
+    mutable CpuPollingThread* poller_ = nullptr;
+    // Landed since reset(), so a poller created later starts from them.
+    uint64_t landed_entries_total_ = 0, landed_bytes_total_ = 0, landed_lists_total_ = 0;
 };
 
 // The spelling SgWarpSpecSession, which callers also use for this class.

@@ -193,6 +193,17 @@ int gfd_zero_copy_scatter_tokens_signal(const uint64_t* dst_addrs, const void* s
                                         uint64_t done_value, void* stream);
 int gfd_zero_copy_gather_signal(const gfd_sg_entry* entries, int count, unsigned int* done_counter,
                                 uint64_t* done_word, uint64_t done_value, void* stream);
+/* gfd_zero_copy_gather_signal for a table the caller has already cut into
+ * pieces (no reference counterpart; used by submit_direct, whose
+ * zc_fill_sg_table cuts a short list of large entries by size): the kernel
+ * does not slice the entries again by count, so each record stays one wave's
+ * work. */
+int gfd_zero_copy_gather_signal_presliced(const gfd_sg_entry* entries, int count, unsigned int* done_counter,
+                                          uint64_t* done_word, uint64_t done_value, void* stream);
+/* Waves the zero-copy gather kernels give a short list (no reference
+ * counterpart): GFD_ZC_WAVES when set, else 64.  A caller that cuts a list
+ * into pieces for them sizes the pieces for this many waves. */
+int gfd_zero_copy_target_waves(void);
 /* GPU-built SG list for submit_direct (the pattern of examples/03_gpu_planned_transfer.cu:32-66,
  * plan_compact_kernel + plan_build_sg_kernel): the tokens t with routing[t] == expert, in token
  * order, become entries[k] = {gpu_dst + k*token_size, cpu_base + t*stride, token_size}, and

@@ -12,8 +12,10 @@
 // functors stride over 64-lane waves.  Added: eight lists on a session with
 // three compute waves, where a functor declaring kSharesLists has each list
 // split between the three and one without it sees each list once; every
-// entry must be marked exactly once either way.  Prints PASSED and exits 0 on
-// success.
+// entry must be marked exactly once either way.  After each tile case the
+// session poller's stats are printed as examples/07_warp_spec_simple.cu:283
+// does, and must count the tokens the launch landed.  Prints PASSED and
+// exits 0 on success.
 #include <gfd/gfd.h>
 #include <gfd/sg_warp_spec.cuh>
 #include <gfd/warp_spec.cuh>
@@ -196,6 +198,20 @@ static bool sg_compute_waves(Kernel kernel, unsigned int want_parts, const char*
     return ok && wrong == 0 && h_parts == want_parts && bytes_ok;
 }
 
+// The per-poller summary of the reference's examples/07_warp_spec_simple.cu.
+static void print_poller_stats(gfd::CpuPollingThread& poller, double elapsed_ms) {
+    const uint64_t descs = poller.get_descriptors_processed();
+    const double bytes = poller.get_total_bytes_copied();
+    std::printf("    [Poller] descs=%llu, batches=%llu, coalesced=%llu\n", (unsigned long long)descs,
+                (unsigned long long)poller.get_batches_submitted(), (unsigned long long)poller.get_coalesced_entries());
+    std::printf("    [Poller] bytes=%.2f MB, gather=%llu us, submit=%llu us, wait=%llu us\n", bytes / (1024.0 * 1024.0),
+                (unsigned long long)poller.get_gather_us(), (unsigned long long)poller.get_dma_submit_us(),
+                (unsigned long long)poller.get_dma_wait_us());
+    if (elapsed_ms > 0 && descs > 0)
+        std::printf("    [Poller] effective BW=%.2f GB/s, descs/ms=%.0f\n", bytes / (elapsed_ms * 1e6),
+                    (double)descs / elapsed_ms);
+}
+
 static bool db_tiles(int total_tokens, int tokens_per_tile, int tokens_per_chunk, int token_dim, int num_cus) {
     const int num_tiles = total_tokens / tokens_per_tile;
     const size_t token_size = (size_t)token_dim * sizeof(float);
@@ -225,6 +241,12 @@ static bool db_tiles(int total_tokens, int tokens_per_tile, int tokens_per_chunk
         gfd::WarpSpecSession session(config);
         session.launch(test_kernel_db, SimpleReduce{d_output, token_dim});
         ok = session.synchronize();
+        gfd::CpuPollingThread* poller = session.get_poller();
+        if (!poller) return false;
+        print_poller_stats(*poller, session.get_stats().elapsed_ms);
+        if (poller->get_descriptors_processed() != (uint64_t)total_tokens ||
+            poller->get_total_bytes_copied() != (double)total_size)
+            ok = false;
     }
     std::vector<float> h((size_t)total_tokens);
     HIP_OK(hipMemcpy(h.data(), d_output, h.size() * sizeof(float), hipMemcpyDeviceToHost));

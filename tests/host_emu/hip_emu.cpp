@@ -84,6 +84,18 @@ int g_handle = 0;
 
 namespace {
 std::atomic<unsigned> g_zc_launches{0};
+
+// A GPU kernel that reads a host address the runtime has not mapped for the
+// GPU takes a page fault (XNACK is off): the emulated kernels end the process
+// the same way, so a scenario sees any source handed to them unchecked.
+void require_gpu_readable(const void* p, size_t n, const char* what) {
+    uintptr_t b;
+    size_t s;
+    if (n == 0 || emu::find_alloc(p, n, emu::Kind::Pinned, &b, &s) || emu::find_alloc(p, n, emu::Kind::Device, &b, &s))
+        return;
+    std::fprintf(stderr, "emulated GPU fault: %s reads %zu bytes at %p, not pinned or device memory\n", what, n, p);
+    std::abort();
+}
 }
 namespace emu {
 unsigned zero_copy_launches() { return g_zc_launches.load(); }
@@ -213,6 +225,7 @@ int gfd_zero_copy_gather_tokens_signal(const uint64_t* src_addrs, void* dst, uin
     if (!done_counter || !done_word || num_tokens < 0 || (num_tokens > 0 && (!src_addrs || !dst || !token_size)))
         return 1;
     g_zc_launches++;
+    for (int j = 0; j < num_tokens; j++) require_gpu_readable((const void*)(uintptr_t)src_addrs[j], token_size, "zc_gather_tokens");
     for (int j = 0; j < num_tokens; j++)
         std::memcpy((char*)dst + (size_t)j * token_size, (const void*)(uintptr_t)src_addrs[j], token_size);
     __atomic_store_n(done_counter, 0u, __ATOMIC_RELAXED);
@@ -225,10 +238,19 @@ int gfd_zero_copy_gather_signal(const gfd_sg_entry* entries, int count, unsigned
     if (!done_counter || !done_word || count < 0 || (count > 0 && !entries)) return 1;
     g_zc_launches++;
     for (int i = 0; i < count; i++)
+        require_gpu_readable((const void*)(uintptr_t)entries[i].src, entries[i].size, "zc_gather_sg");
+    for (int i = 0; i < count; i++)
         std::memcpy((void*)(uintptr_t)entries[i].dst, (const void*)(uintptr_t)entries[i].src, entries[i].size);
     __atomic_store_n(done_counter, 0u, __ATOMIC_RELAXED);
     __atomic_store_n(done_word, done_value, __ATOMIC_RELEASE);
     return 0;
 }
+
+int gfd_zero_copy_gather_signal_presliced(const gfd_sg_entry* entries, int count, unsigned int* done_counter,
+                                          uint64_t* done_word, uint64_t done_value, void* stream) {
+    return gfd_zero_copy_gather_signal(entries, count, done_counter, done_word, done_value, stream);
+}
+
+int gfd_zero_copy_target_waves(void) { return 64; }
 
 }  // extern "C"

@@ -732,10 +732,55 @@ int run_locked_source() {
     return 0;
 }
 
+// A pinned source found by one submit_direct call is looked up again by the
+// next: between the calls its registration goes away while the addresses stay
+// readable to the CPU (a freed pinned buffer whose range a pageable
+// allocation now holds).  The second call must not hand those addresses to
+// the zero-copy kernel, whose emulation aborts on a source that is not
+// pinned, as the GPU faults on one; it takes the staged route instead.
+int run_stale_pinned(uint64_t seed) {
+    constexpr uint32_t n = 256, t = 4096;  // 1 MiB: the zero-copy route's size
+    Rng rng(seed);
+    const size_t host_bytes = (size_t)2 * n * t;
+    auto* host = (uint8_t*)host_alloc(host_bytes);
+    for (size_t i = 0; i < host_bytes; i++) host[i] = (uint8_t)rng.next();
+    auto* dst = (uint8_t*)dev_alloc((size_t)n * t);
+    std::vector<SGEntry> sg(n);
+    std::vector<uint8_t> want((size_t)n * t);
+    for (uint32_t i = 0; i < n; i++) {
+        const size_t k = (size_t)((i * 37u + 11u) % n);
+        sg[i] = SGEntry{(uint64_t)(uintptr_t)dst + (size_t)i * t, host + k * 2 * t, t};
+        std::memcpy(&want[(size_t)i * t], host + k * 2 * t, t);
+    }
+    int rc = 0;
+    {
+        CpuPollingThread p(nullptr, nullptr, nullptr, 4u << 20, true, -1);
+        if (!p.init_direct_ce()) return 4;
+        for (int call = 0; call < 3 && rc == 0; call++) {
+            if (call == 1) emu::note_free(host);  // registration gone, memory still there
+            std::memset(dst, kSentinel, want.size());
+            const unsigned zc0 = emu::zero_copy_launches();
+            if (p.submit_direct(sg.data(), (int)n) < 0) return 3;
+            const unsigned zc = emu::zero_copy_launches() - zc0;
+            std::printf("stale pinned: call %d, zero-copy launches %u\n", call, zc);
+            if ((call == 0) != (zc == 1)) {
+                std::printf("stale pinned: call %d took the %s route\n", call, zc ? "zero-copy" : "staged");
+                rc = 3;
+            }
+            if (rc == 0) rc = check_image(dst, want, "stale pinned", call);
+        }
+    }
+    gfd_hip_free(dst);
+    std::free(host);  // its registration was dropped above
+    if (rc == 0) std::printf("stale pinned: pass\n");
+    return rc;
+}
+
 int main(int argc, char** argv) {
     setvbuf(stdout, nullptr, _IOLBF, 0);
     if (argc >= 2 && std::string(argv[1]) == "sdma_slot_reuse") return run_sdma_slot_reuse();
     if (argc >= 2 && std::string(argv[1]) == "locked_source") return run_locked_source();
+    if (argc >= 2 && std::string(argv[1]) == "stale_pinned") return run_stale_pinned(7);
     if (argc >= 4 && std::string(argv[1]) == "staging_pool")
         return run_staging_pool(std::atoi(argv[2]), std::strtoull(argv[3], nullptr, 0));
     if (argc >= 10 && std::string(argv[1]) == "tiled")

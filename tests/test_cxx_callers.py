@@ -7,8 +7,11 @@ submit_direct); it is compiled with g++ and linked against libgfd_amd.so.
 tests/cxx/sessions_e2e.hip is device code written like the reference's
 test/test_sg_e2e.cu and test/test_db_small_tiles.cu (<gfd/sg_warp_spec.cuh>,
 <gfd/warp_spec.cuh>, GFD_SG_WARP_SPEC_KERNEL, GFD_WARP_SPEC_KERNEL_DB, the
-sessions' launch templates); it is compiled with hipcc for gfx950.  Both are
-built into a temporary directory here; the GPU test runs the copies that
+sessions' launch templates); it is compiled with hipcc for gfx950.
+tests/cxx/sg_gpu_submit.hip follows test/test_sg_gpu_submit.cu: a
+caller-written transfer / compute / submitter kernel launched with
+hipLaunchKernelGGL and bracketed by session.get_poller()->start() / stop().
+All are built into a temporary directory here; the GPU test runs the copies that
 build() leaves in tests/cxx/_build.  Also: every reference header name
 exists and <gfd/gfd.h> compiles on its own in plain C++17."""
 import os
@@ -62,7 +65,7 @@ def test_reference_style_callers_build(tmp_path):
                        capture_output=True, text=True, timeout=600)
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and "recognized feature" not in l)
     assert r.returncode == 0, err
-    for name in ("direct_transfer", "sessions_e2e"):
+    for name in ("direct_transfer", "sessions_e2e", "sg_gpu_submit"):
         assert os.path.isfile(tmp_path / name), name
     # The host program resolves the library's C++ API from libgfd_amd.so.
     nm = subprocess.run(["nm", "-D", "--undefined-only", str(tmp_path / "direct_transfer")], capture_output=True,

@@ -7,7 +7,12 @@ compared) through submit_direct, in order and in a seeded random order, with
 the poller's Queue staging taken from the StagingPool.
 sessions_e2e: the reference's test/test_sg_e2e.cu (floats i + 1 landed by an
 SGWarpSpecSession, every one compared) and test/test_db_small_tiles.cu
-(double-buffered tiles, per-token sums (t + 1) * dim at 1-7 tiles)."""
+(double-buffered tiles, per-token sums (t + 1) * dim at 1-7 tiles), with the
+session poller's stats printed as examples/07_warp_spec_simple.cu:283 does.
+sg_gpu_submit: the reference's test/test_sg_gpu_submit.cu flow: a
+caller-launched transfer / compute / submitter kernel bracketed by
+session.get_poller()->start() and stop(), floats i + 1 checked, twice on one
+session, then a launch through the session."""
 import os
 import subprocess
 import sys
@@ -20,7 +25,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BUILD = os.path.join(ROOT, "tests", "cxx", "_build")
 
 
-@pytest.mark.parametrize("prog", ["direct_transfer", "sessions_e2e"])
+@pytest.mark.parametrize("prog", ["direct_transfer", "sessions_e2e", "sg_gpu_submit"])
 def test_reference_style_program(prog):
     path = os.path.join(BUILD, prog)
     assert os.path.isfile(path), "%s is not built: run __graft_entry__.build()" % path

@@ -76,6 +76,52 @@ def test_moe_through_session(T, E, dim, rpl, blocks, cw):
         sess.close()
 
 
+def test_moe_session_with_host_lists_queued_before_launch():
+    """Host lists queued before launch_moe land in the same launch, and the
+    session's lists_done counts them: the GPU submitter must wait for those
+    and its own lists before it raises stop, or transfer waves holding later
+    GPU lists would leave them uncopied.  Two host lists of 32 tokens each go
+    ahead of a launch whose rows must all land byte-exact, with the host
+    lists' tokens and every count exact."""
+    T, E, dim, rpl = 1000, 16, 2048, 4
+    m = Moe(T, E, dim)
+    m.route()
+    n = 2 * T
+    rows = m.expected_rows()
+    total = expected_lists(m.offsets, rpl)
+    k, t = 32, 4096
+    side_host = gfd_amd.HostBuffer(2 * k * t)
+    side_host.array[:] = np.random.default_rng(9).integers(0, 256, 2 * k * t, dtype=np.uint8)
+    side_dst = gfd_amd.DeviceBuffer(2 * k * t)
+    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=8, idle_limit_ms=10000)
+    try:
+        for launch in range(2):
+            print("moe session with 2 host lists queued, launch %d" % launch, flush=True)
+            sess.reset()
+            m.d_dst.fill(0xCD)
+            side_dst.fill(0)
+            for l in range(2):
+                idx = np.arange(l * k, (l + 1) * k, dtype=np.uint64)
+                ent = np.zeros(k, dtype=gfd_amd.DEVICE_SG_ENTRY_DTYPE)
+                ent["src"] = side_host.ptr + idx * t
+                ent["dst"] = side_dst.ptr + idx * t
+                ent["size"] = t
+                sess.submit_sg_list(ent, 1000 + l)
+            sess.launch_moe(m.host.ptr, m.stride, m.T, m.d_offsets.ptr, m.d_rows.ptr, m.E, n, m.row_bytes,
+                            m.d_dst.ptr, None, m.d_weight.ptr, 1e-6, rpl)
+            gfd_amd.synchronize()
+            sess.synchronize(0)
+            st = sess.stats()
+            assert st["error_bits"] == 0
+            assert st["lists_done"] == total + 2
+            assert st["units_done"] == n + 2 * k and st["bytes"] == n * m.row_bytes + 2 * k * t
+            got = m.d_dst.download()
+            assert (got[:n * m.row_bytes].view(np.uint16).reshape(n, dim) == rows).all()
+            assert (side_dst.download() == side_host.array).all()
+    finally:
+        sess.close()
+
+
 def test_moe_session_trace():
     """The per-list device timeline: every list of the launch is recorded once,
     in ring order, with claimed <= ready <= landed; each workgroup's record

@@ -485,6 +485,54 @@ def test_sg_gpu_submit(blocks, n_lists, epl, t, helpers):
     s.close()
 
 
+def test_gpu_submit_launch_ends_at_its_deadline_when_a_list_is_withheld():
+    """A launch whose lists come from GPU submitters has a deadline (the
+    session's idle limit, 2 s here).  The host reserves ring index 0 and never
+    commits it, as a host submitter that stopped between allocating and
+    committing its list would: the GPU lists queue behind it and none can land.
+    The kernel must end by itself at the deadline (the device synchronisation
+    returns, in well under the test's limit) with SG_ERR_LIST_WAIT (its
+    submitter gave up waiting for the lists) and SG_ERR_DEADLINE (transfer
+    waves gave up at the deadline).  After reset() the session works again."""
+    import time
+    n_lists, epl, t = 8, 16, 4096
+    n = n_lists * epl
+    log("sg gpu submit with a withheld list, deadline 2 s")
+    host = gfd_amd.HostBuffer(n * t)
+    host.array[:] = np.random.default_rng(5).integers(0, 256, n * t, dtype=np.uint8)
+    dst = gfd_amd.DeviceBuffer(n * t)
+    arr = entries_array(host.ptr + np.arange(n, dtype=np.uint64) * t, dst.ptr + np.arange(n, dtype=np.uint64) * t, t)
+    d_ent = gfd_amd.DeviceBuffer(arr.nbytes)
+    d_ent.upload(arr.view(np.uint8))
+    s = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=8, idle_limit_ms=2000, helper_waves=0)
+    try:
+        alloc = ctypes.c_uint64.from_address(s.queue_ptr() + gfd_amd.SG_QUEUE_LIST_ALLOC_IDX_OFFSET)
+        assert alloc.value == 0
+        alloc.value = 1  # ring index 0 reserved by the host, never committed
+        dst.fill(0)
+        t0 = time.monotonic()
+        s.launch_gpu_submit(d_ent.ptr, epl, n_lists)
+        gfd_amd.synchronize()  # returns once the kernel has ended itself
+        elapsed = time.monotonic() - t0
+        log("kernel ended after %.2f s" % elapsed)
+        with pytest.raises(gfd_amd.GfdError):
+            s.synchronize(0)
+        st = s.stats()
+        assert st["error_bits"] & gfd_amd.SG_ERR_LIST_WAIT, hex(st["error_bits"])
+        assert st["error_bits"] & gfd_amd.SG_ERR_DEADLINE, hex(st["error_bits"])
+        assert st["lists_done"] == 0
+        assert 1.5 < elapsed < 8.0
+        s.reset()
+        dst.fill(0)
+        s.launch_gpu_submit(d_ent.ptr, epl, n_lists)
+        s.synchronize(extra_gpu_lists=n_lists)
+        assert (dst.download() == host.array).all()
+        st = s.stats()
+        assert st["lists_done"] == n_lists and st["error_bits"] == 0
+    finally:
+        s.close()
+
+
 @pytest.mark.parametrize("blocks,helpers", [(0, 0), (8, 3)])
 def test_sg_gpu_submit_offload(blocks, helpers):
     """Eviction lists posted by GPU submitter waves (test/test_sg_gpu_submit.cu's

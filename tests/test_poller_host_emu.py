@@ -173,6 +173,16 @@ def test_registered_host_memory_at_another_gpu_address_is_not_a_copy_source(poll
     run(poller_emu, ["locked_source"])
 
 
+def test_direct_looks_up_pinned_sources_on_every_call(poller_emu):
+    """A source range found pinned by one submit_direct call whose
+    registration is gone by the next (freed, its addresses reused by pageable
+    memory) must not reach the zero-copy kernel: the second call looks it up
+    again and takes the staged route.  The emulated kernel aborts on a source
+    that is not pinned, as the GPU would fault."""
+    out = run(poller_emu, ["stale_pinned"])
+    assert "call 0, zero-copy launches 1" in out and "call 1, zero-copy launches 0" in out, out[-2000:]
+
+
 # The same stack built with ThreadSanitizer instead: the poller, gather
 # workers, copy engines and the host threads that play the kernels' protocols
 # must show no data race (a report makes the run exit 66).
