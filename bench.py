@@ -120,6 +120,20 @@ def host_info():
     except OSError:
         pass
     info["machine"] = platform.machine()
+    # SMT: hardware threads per physical core among the CPUs this process may use.
+    cores = set()
+    allowed = sorted(os.sched_getaffinity(0))
+    for c in allowed:
+        try:
+            base = "/sys/devices/system/cpu/cpu%d/topology/" % c
+            cores.add((open(base + "physical_package_id").read().strip(), open(base + "core_id").read().strip()))
+        except OSError:
+            cores = set()
+            break
+    if cores:
+        info["physical_cores"] = len(cores)
+        info["threads_per_core"] = round(len(allowed) / len(cores), 2)
+        info["smt"] = len(allowed) > len(cores)
     return info
 
 
@@ -187,6 +201,13 @@ def cpu_baseline(oracle, seconds, info):
                        "P50 %.1f us" % (len(warm), us_warm),
     }
     out["product_gather"] = product
+    # Flat copies of the figures the record keeps (it drops nested objects).
+    out["restated_gather_us"] = round(us, 2)
+    out["product_gather_us"] = product["us_p50"]
+    out["product_gather_GBps"] = product["GBps"]
+    for k in ("physical_cores", "threads_per_core", "smt"):
+        if k in info:
+            out[k] = info[k]
     for b in srcs:
         b.free()
     # The CPU-only layout: 256 x 4 KiB from a 2 MiB source into 1 MiB of
@@ -221,6 +242,9 @@ def cpu_baseline(oracle, seconds, info):
         pg = product_gather([src1.ptr], perm1, n1, t, stg1, wcpus, w, lambda k: expect1, iters=2000)
         c1["W%d" % w]["product_gather"] = {"us_p50": pg["us_p50"], "GBps": pg["GBps"]}
     out["c1_256x4KB"] = c1
+    for w in (15, 7):
+        out["c1_256x4KB_W%d_us" % w] = c1["W%d" % w]["us_p50"]
+        out["c1_256x4KB_W%d_product_us" % w] = c1["W%d" % w]["product_gather"]["us_p50"]
     log("  cpu baseline 256 x 4KiB: %s" % c1)
     return out
 
@@ -662,9 +686,11 @@ def session_timeline(lists, blocks, nlists):
 
 def _pmc_pass(exe, counter, workdir, timeout_s):
     """One rocprofv3 --pmc pass over `bench.py --only zc,calib` (5 device-to-
-    device copies of 32 MiB, then 12 launches of the 8192 x 4 KiB gather), in
-    its own process group under a time limit.  Per-dispatch counter values
-    (KiB): (calibration copies, gather launches), or a reason string."""
+    device copies of 32 MiB, 5 launches of the gather kernel over one
+    contiguous 32 MiB pinned range, then 12 launches of the 8192 x 4 KiB
+    gather), in its own process group under a time limit.  Per-dispatch
+    counter values (KiB): (calibration copies, contiguous calibration
+    gathers, gather launches), or a reason string."""
     out = os.path.join(workdir, counter)
     cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "p", "--", sys.executable,
            os.path.join(ROOT, "bench.py"), "--only", "zc,calib", "--cpu-seconds", "0", "--steps", "5", "--warmup", "1"]
@@ -680,21 +706,23 @@ def _pmc_pass(exe, counter, workdir, timeout_s):
     files = glob.glob(os.path.join(out, "**", "p_counter_collection.csv"), recursive=True)
     if not files:
         return "%s pass wrote no counter file (exit %d)" % (counter, rc)
-    copies, gathers = parse_pmc_counters(files[0], counter)
-    if len(copies) < 5 or not gathers:
-        return "%s pass: %d calibration copies, %d gathers counted (exit %d)" % (counter, len(copies),
-                                                                                 len(gathers), rc)
-    return copies, gathers
+    copies, contig, gathers = parse_pmc_counters(files[0], counter)
+    if len(copies) < 5 or len(contig) < 5 or not gathers:
+        return "%s pass: %d calibration copies, %d contiguous gathers, %d gathers counted (exit %d)" % (
+            counter, len(copies), len(contig), len(gathers), rc)
+    return copies, contig, gathers
 
 
 def parse_pmc_counters(path, counter):
     """Per-dispatch values of `counter` in a rocprofv3 counter_collection.csv:
-    (the calibration copies, the gather launches).  The calibration copies
-    run before anything else that could use the runtime's copy kernel: the
-    first five dispatches of it.  The gathers: the launches of the 8192 x 4
-    KiB job, the largest grid (the poller's set-up also launches the kernel
-    once on 16 bytes)."""
-    copies, gathers = [], []
+    (the calibration copies, the contiguous calibration gathers, the gather
+    launches).  The calibration copies run before anything else that could
+    use the runtime's copy kernel: the first five dispatches of it.  The
+    contiguous gathers are the first five dispatches of the gather kernel
+    (they run before the poller exists).  The gathers: the later launches of
+    the 8192 x 4 KiB job, the largest grid (the poller's set-up also launches
+    the kernel once on 16 bytes)."""
+    copies, zc = [], []
     with open(path) as f:
         for row in csv.DictReader(f):
             if row.get("Counter_Name") != counter:
@@ -703,18 +731,30 @@ def parse_pmc_counters(path, counter):
             if "copyBuffer" in name:
                 copies.append((int(row["Dispatch_Id"]), v))
             elif "zc_gather_tokens" in name:
-                gathers.append((int(row["Grid_Size"]), v))
+                zc.append((int(row["Dispatch_Id"]), int(row["Grid_Size"]), v))
     copies = [v for _, v in sorted(copies)[:5]]
-    big = max((g for g, _ in gathers), default=0)
-    return copies, [v for g, v in gathers if g == big]
+    zc.sort()
+    contig, rest = [v for _, _, v in zc[:5]], zc[5:]
+    big = max((g for _, g, _ in rest), default=0)
+    return copies, contig, [v for _, g, v in rest if g == big]
+
+
+# Bytes the contiguous calibration gather moves per launch: reads are the
+# 32 MiB over the host link plus the 64 KiB page table in HBM, writes the
+# 32 MiB into HBM (the same algorithmic bytes as one 8192 x 4 KiB gather).
+CALIB_READ_BYTES = (32 << 20) + 8192 * 8
+CALIB_WRITE_BYTES = 32 << 20
 
 
 def measure_traffic(timeout_s=150):
     """HBM-side traffic of one 8192 x 4 KiB zc_gather_tokens launch, measured
     in this run: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) from two
-    rocprofv3 --pmc passes, each scaled by the same counter on a 32 MiB
-    device-to-device copy of known size.  (read_bytes, write_bytes, detail) or
-    (None, None, reason)."""
+    rocprofv3 --pmc passes, each scaled by the same counter on the same
+    kernel reading one contiguous 32 MiB pinned range (bytes known:
+    CALIB_READ_BYTES / CALIB_WRITE_BYTES), so host-link reads are calibrated
+    on host-link reads.  The factor a 32 MiB device-to-device copy gives is
+    kept beside it.  (read_bytes, write_bytes, detail) or (None, None,
+    reason)."""
     exe = shutil.which("rocprofv3")
     if not exe:
         return None, None, "rocprofv3 not on PATH"
@@ -728,14 +768,17 @@ def measure_traffic(timeout_s=150):
             got[counter] = r
     detail = {}
     val = {}
-    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        copies, gathers = got[counter]
-        cal = float(np.median(copies))
-        scale = 32768.0 / cal  # KiB the 32 MiB copy moves through that interface per KiB counted
+    for counter, known in (("FETCH_SIZE", CALIB_READ_BYTES), ("WRITE_SIZE", CALIB_WRITE_BYTES)):
+        copies, contig, gathers = got[counter]
+        cal = float(np.median(contig))
+        scale = known / 1024.0 / cal  # KiB the contiguous gather moves per KiB counted
+        copy_scale = 32768.0 / float(np.median(copies))
         val[counter] = float(np.mean(gathers)) * scale * 1024.0
         detail[counter] = {"gather_kib_per_dispatch": round(float(np.mean(gathers)), 2),
-                           "gather_dispatches": len(gathers), "copy_kib_per_dispatch": round(cal, 2),
-                           "scale": round(scale, 5)}
+                           "gather_dispatches": len(gathers),
+                           "contiguous_gather_kib_per_dispatch": round(cal, 2), "scale": round(scale, 5),
+                           "copy_kib_per_dispatch": round(float(np.median(copies)), 2),
+                           "d2d_copy_scale": round(copy_scale, 5)}
     return int(round(val["FETCH_SIZE"])), int(round(val["WRITE_SIZE"])), detail
 
 
@@ -1160,6 +1203,52 @@ class QueueRig:
         self.q.free()
 
 
+def flat_metric_fields(roofline, results, r_moe):
+    """The metric's figures as flat scalars in `roofline` (a record that keeps
+    only scalar fields keeps these): per layout, Direct, the zero-copy kernel,
+    Queue and per-token copies (us, GB/s, fraction of 63.02 GB/s); the
+    Direct / per-token ratio at 4 KiB (target >= 10); the Direct call's SDMA
+    occupancy; and config 5 with and without its routing step."""
+    for r in results:
+        if not r:
+            continue
+        tag = "%dx%s" % (r["tokens"], ("%dKB" % (r["token_bytes"] // 1024)) if r["token_bytes"] >= 1024
+                         else "%dB" % r["token_bytes"])
+        for key, name in (("direct", "direct"), ("zero_copy", "zc"), ("queue", "queue"),
+                          ("memcpy_per_token", "memcpy_per_token")):
+            m = r.get(key)
+            if not m:
+                continue
+            roofline["%s_%s_us" % (name, tag)] = m["us_p50"]
+            roofline["%s_%s_GBps" % (name, tag)] = m["GBps"]
+            roofline["%s_%s_frac" % (name, tag)] = round(m["GBps"] / PCIE_GEN5_X16_GBPS, 4)
+            if key == "zero_copy":
+                roofline["zc_%s_kernel_GBps" % tag] = m["kernel_GBps"]
+            if key == "direct" and "route" in m:
+                roofline["direct_%s_route" % tag] = m["route"]
+        d, c = r.get("direct"), r.get("memcpy_per_token")
+        if d and c:
+            roofline["direct_over_memcpy_per_token_%s" % tag] = round(c["us_p50"] / d["us_p50"], 2)
+        sd = (d or {}).get("sdma")
+        if sd:
+            roofline["direct_sdma_%s_GBps_over_call" % tag] = round(r["bytes"] / (sd["window_us"] * 1e3), 3)
+            roofline["direct_sdma_%s_GBps_while_busy" % tag] = sd["link_GBps_while_busy"]
+            roofline["direct_sdma_%s_busy_frac" % tag] = sd["busy_frac_any"]
+            roofline["direct_sdma_%s_first_copy_us" % tag] = sd["first_copy_start_us"]
+    if r_moe:
+        route = r_moe["route_and_lists_us_p50"]
+        roofline["moe_route_and_lists_us"] = route
+        for key, name in (("transfer_only", "moe_bespoke_transfer"), ("overlapped_rmsnorm", "moe_bespoke_rmsnorm"),
+                          ("session_transfer_only", "moe_session_transfer"),
+                          ("session_overlapped_rmsnorm", "moe_session_rmsnorm")):
+            m = r_moe.get(key)
+            if not m:
+                continue
+            roofline[name + "_us"] = m["us_p50"]
+            roofline[name + "_GBps"] = m["GBps"]
+            roofline[name + "_with_route_GBps"] = round(gbps(r_moe["bytes"], m["us_p50"] + route), 3)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1195,15 +1284,27 @@ def main():
     gfd_amd.lib().gfd_set_device(0)
 
     if "calib" in only:
-        # Reference kernel for the FETCH_SIZE / WRITE_SIZE counters: a device
-        # to device copy of 32 MiB (the runtime's blit kernel), 5 launches.
+        # Reference kernels for the FETCH_SIZE / WRITE_SIZE counters: a device
+        # to device copy of 32 MiB (the runtime's blit kernel), 5 launches;
+        # then the gather kernel itself over one contiguous 32 MiB pinned range
+        # (8192 tokens of 4 KiB in order), 5 launches: the same algorithmic
+        # bytes as the scattered gather, read over the host link.
         a = gfd_amd.DeviceBuffer(32 << 20)
         b = gfd_amd.DeviceBuffer(32 << 20)
         a.fill(1)
         for _ in range(5):
             gfd_amd.lib().gfd_memcpy_d2d(b.ptr, a.ptr, 32 << 20)
         gfd_amd.synchronize()
-        log("calibration copies done: 5 x 32 MiB device-to-device")
+        contig = gfd_amd.HostBuffer(32 << 20)
+        contig.array[:] = 7
+        tab = gfd_amd.DeviceBuffer(8192 * 8)
+        tab.upload(np.uint64(contig.ptr) + np.arange(8192, dtype=np.uint64) * np.uint64(4096))
+        for _ in range(5):
+            gfd_amd.zero_copy_gather_tokens(tab.ptr, b.ptr, 4096, 8192)
+        gfd_amd.synchronize()
+        if not (b.download() == 7).all():
+            raise SystemExit("PARITY FAILURE: contiguous calibration gather")
+        log("calibration done: 5 x 32 MiB device-to-device copies, 5 contiguous 32 MiB gathers")
 
     peak = {}
     if want("peak"):
@@ -1321,7 +1422,8 @@ def main():
             rd, wr, tdetail = measure_traffic()
             log("traffic:", rd, wr, tdetail)
         if rd is not None:
-            source = "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes of this run, each scaled by a 32 MiB D2D copy"
+            source = ("rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes of this run, each scaled by the same kernel "
+                      "reading one contiguous 32 MiB pinned range")
         else:
             source = ("profiles/zc_gather_tokens_8192x4KB.md (an earlier run's --pmc passes); this run: %s"
                       % tdetail)
@@ -1360,6 +1462,8 @@ def main():
         for k in ("zero_copy", "direct", "queue", "memcpy_per_token"):
             if k in r:
                 r[k].update(frac(r[k]["GBps"]))
+    if roofline is not None:
+        flat_metric_fields(roofline, [r_main, r_kv] + r_small, r_moe)
     result = {
         "metric": METRIC, "value": round(value, 3), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(head.get("us_p50", 0.0) / 1e3, 4), "higher_is_better": True, "scaling": "weak",

@@ -157,6 +157,9 @@ def _declare(L):
         "gfd_poller_set_direct_zero_copy_max_bytes": ([vp, c_u64], None),
         "gfd_poller_set_direct_zero_copy_min_bytes": ([vp, c_u64], c_u64),
         "gfd_poller_set_direct_zero_copy_head_bytes": ([vp, c_u64], c_u64),
+        "gfd_poller_set_zero_copy_worker": ([vp, c_int], c_int),
+        "gfd_poller_zero_copy_worker_stats": ([vp, ctypes.POINTER(c_u64), ctypes.POINTER(c_u64)], c_int),
+        "gfd_poller_set_worker_queue_max_bytes": ([vp, c_u64], c_u64),
         "gfd_bench_zero_copy_tokens_signal": ([vp, vp, c_u32, c_int, c_int, c_int, pd], c_int),
         "gfd_zero_copy_gather_tokens_signal": ([vp, vp, c_u32, c_int, vp, vp, c_u64, vp], c_int),
         "gfd_zero_copy_scatter_tokens_signal": ([vp, vp, c_u32, c_int, vp, vp, c_u64, vp], c_int),
@@ -438,6 +441,23 @@ class CpuPollingThread:
         """Lists of at most b bytes take the staged SDMA route (default
         64 KiB).  Returns the previous value."""
         return int(lib().gfd_poller_set_direct_zero_copy_min_bytes(self._h, b))
+
+    def set_zero_copy_worker(self, on=True):
+        """The persistent zero-copy worker (CpuPollingThread::set_zero_copy_worker):
+        Direct lists up to the zero-copy limit and Queue batches up to
+        set_worker_queue_max_bytes() with pinned sources go through it."""
+        _check(lib().gfd_poller_set_zero_copy_worker(self._h, int(bool(on))), "gfd_poller_set_zero_copy_worker")
+
+    def zero_copy_worker_stats(self):
+        """{"jobs": ..., "launches": ...} of the worker (0 while it is off)."""
+        j, l = ctypes.c_uint64(), ctypes.c_uint64()
+        _check(lib().gfd_poller_zero_copy_worker_stats(self._h, ctypes.byref(j), ctypes.byref(l)),
+               "gfd_poller_zero_copy_worker_stats")
+        return {"jobs": j.value, "launches": l.value}
+
+    def set_worker_queue_max_bytes(self, b):
+        """Queue batches of at most b bytes go to the worker; returns the previous limit."""
+        return int(lib().gfd_poller_set_worker_queue_max_bytes(self._h, b))
 
     def set_direct_zero_copy_head_bytes(self, b):
         """Larger lists (destination-contiguous, pinned sources): the zero-copy

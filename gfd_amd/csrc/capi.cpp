@@ -265,6 +265,24 @@ uint64_t gfd_poller_set_direct_zero_copy_head_bytes(gfd_poller_t p, uint64_t b) 
     P(p)->set_direct_zero_copy_head_bytes(b);
     return prev;
 }
+int gfd_poller_set_zero_copy_worker(gfd_poller_t p, int on) {
+    if (!p) return fail(-1, "gfd_poller_set_zero_copy_worker: NULL poller");
+    return P(p)->set_zero_copy_worker(on != 0) == 0
+               ? 0
+               : fail(-1, "gfd_poller_set_zero_copy_worker: set-up failed or the polling thread is running");
+}
+int gfd_poller_zero_copy_worker_stats(gfd_poller_t p, uint64_t* jobs, uint64_t* launches) {
+    if (!p || !jobs || !launches) return fail(-1, "gfd_poller_zero_copy_worker_stats: invalid argument");
+    *jobs = P(p)->zero_copy_worker_jobs();
+    *launches = P(p)->zero_copy_worker_launches();
+    return 0;
+}
+uint64_t gfd_poller_set_worker_queue_max_bytes(gfd_poller_t p, uint64_t b) {
+    if (!p) return 0;
+    const uint64_t prev = P(p)->worker_queue_max_bytes();
+    P(p)->set_worker_queue_max_bytes(b);
+    return prev;
+}
 void gfd_poller_set_direct_chunk_bytes(gfd_poller_t p, uint64_t b) {
     if (p) P(p)->set_direct_chunk_bytes(b);
 }

@@ -38,6 +38,7 @@
 #include "gfd/pcie_topology.h"
 #include "gfd/sg_task_queue.h"
 #include "gfd/staging_pool.h"
+#include "zc_worker.h"
 
 namespace gfd {
 
@@ -113,6 +114,8 @@ CpuPollingThread::CpuPollingThread(DescriptorQueue* queue, void* gpu_base, void*
     direct_zc_max_bytes_ = env_size("GFD_DIRECT_ZC_MAX_BYTES", direct_zc_max_bytes_);
     direct_zc_min_bytes_ = env_size("GFD_DIRECT_ZC_MIN_BYTES", direct_zc_min_bytes_);
     direct_zc_head_bytes_ = env_size("GFD_DIRECT_ZC_HEAD_BYTES", direct_zc_head_bytes_);
+    worker_wanted_ = env_size("GFD_ZC_WORKER", 0) != 0;
+    worker_queue_max_bytes_ = env_size("GFD_ZC_WORKER_QUEUE_MAX_BYTES", worker_queue_max_bytes_);
     fifo_ = new CompletionFifo();
     if (env_size("GFD_TRACE", 0)) set_trace(true);
 }
@@ -120,6 +123,8 @@ CpuPollingThread::CpuPollingThread(DescriptorQueue* queue, void* gpu_base, void*
 CpuPollingThread::~CpuPollingThread() {
     stop_hook_ = nullptr;  // its owner may be half destroyed
     stop();
+    delete worker_;  // ends its grid
+    worker_ = nullptr;
     delete gather_;
     gather_ = nullptr;
     gfd_hip_set_device(device_);
@@ -156,6 +161,70 @@ CpuPollingThread::~CpuPollingThread() {
 }
 
 int CpuPollingThread::num_gather_workers() const { return gather_ ? gather_->num_workers() : 0; }
+
+// The worker's grid: 16 workgroups of 4 waves (64 waves, the zero-copy
+// kernels' short-list width); 8192 records per job.
+bool CpuPollingThread::ensure_worker() {
+    if (worker_) return true;
+    auto* w = new ZcWorker();
+    const uint32_t idle_ms = (uint32_t)env_size("GFD_ZC_WORKER_IDLE_MS", 100);
+    if (gfd_hip_set_device(device_) != 0 || w->init(device_, 16, idle_ms, 8192) != 0) {
+        GFD_LOG_ERROR("zero-copy worker set-up failed; it stays off\n");
+        delete w;
+        return false;
+    }
+    worker_ = w;
+    return true;
+}
+
+int CpuPollingThread::set_zero_copy_worker(bool on) {
+    if (running_.load(std::memory_order_acquire)) {
+        GFD_LOG_ERROR("set_zero_copy_worker: stop the polling thread first\n");
+        return -1;
+    }
+    std::lock_guard<std::mutex> direct_lock(direct_mutex_);
+    if (!on) {
+        delete worker_;
+        worker_ = nullptr;
+        worker_wanted_ = false;
+        return 0;
+    }
+    worker_wanted_ = true;
+    return ensure_worker() ? 0 : -1;
+}
+
+uint64_t CpuPollingThread::zero_copy_worker_jobs() const { return worker_ ? worker_->jobs() : 0; }
+uint64_t CpuPollingThread::zero_copy_worker_launches() const { return worker_ ? worker_->launches() : 0; }
+
+// Queue path: a batch whose sources are pinned and whose destinations lie in
+// device memory goes to the worker as one job (blocking until it has
+// landed).  False if it does not qualify; the caller then stages it.
+bool CpuPollingThread::queue_worker_copy(const SGEntry* e, int count, size_t total) {
+    if (!worker_ || total > worker_queue_max_bytes_ || count > worker_->capacity()) return false;
+    uintptr_t lo = 1, hi = 0;
+    for (int i = 0; i < count; i++) {
+        if (e[i].size == 0) continue;
+        const uintptr_t a = (uintptr_t)e[i].src, b = a + e[i].size;
+        if (a < lo || b > hi) {
+            if (!ce_manager_.host_source_ok(e[i].src, e[i].size)) return false;
+            ce_manager_.last_pinned_range(&lo, &hi);
+            if (a < lo || b > hi) lo = a, hi = b;
+        }
+        const uint64_t d = e[i].dst, de = d + e[i].size;
+        if (d < queue_dst_lo_ || de > queue_dst_hi_) {
+            uint64_t base = 0, size = 0;
+            if (!gfd_hip_device_range(d, &base, &size) || de > base + size) return false;
+            queue_dst_lo_ = base;
+            queue_dst_hi_ = base + size;
+        }
+    }
+    static const uint64_t timeout_us = (uint64_t)env_size("GFD_DIRECT_TIMEOUT_MS", 10000) * 1000ull;
+    std::lock_guard<std::mutex> lock(worker_->mutex());
+    bool cut = false;
+    const int n = zc_fill_sg_table(e, count, total, worker_->table(), worker_->capacity(), &cut, worker_->waves());
+    if (worker_->run(n, timeout_us) != 0) GFD_LOG_ERROR("zero-copy worker: queue batch failed\n");
+    return true;
+}
 
 void CpuPollingThread::set_trace(bool on) {
     std::lock_guard<std::mutex> lock(trace_mutex_);
@@ -301,6 +370,7 @@ bool CpuPollingThread::init_copy_engine() {
     num_staging_bufs_ = got;
     for (int b = 0; b < NUM_STAGING_BUFS; b++) staging_fence_[b] = 0;
     for (int b = 0; b < got; b++) ce_manager_.trust_range(staging_bufs_[b], staging_buffer_size_);
+    if (worker_wanted_) ensure_worker();
     GFD_LOG_INFO("queue staging: %d x %zu bytes (NUMA %d), %d copy channel(s), SDMA engines 0x%x\n", got,
                  staging_buffer_size_, numa_node_, ce_manager_.num_channels(), ce_manager_.sdma_engine_mask());
     return start_workers();
@@ -475,8 +545,10 @@ void CpuPollingThread::polling_loop() {
 void CpuPollingThread::flush_batch(Descriptor* batch, int& count, uint32_t& or_flags) {
     if (count == 0) return;
     // A source range found pinned for an earlier batch may have been freed
-    // and reused since: batches look their caller-owned sources up again.
+    // and reused since: batches look their caller-owned sources up again
+    // (and device ranges too).
     ce_manager_.forget_pinned_range();
+    queue_dst_lo_ = queue_dst_hi_ = 0;
     const uint64_t cur_read = queue_->read_idx;
     if (trace_on_.load(std::memory_order_relaxed)) {
         uint64_t bytes = 0;
@@ -585,7 +657,9 @@ void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total) {
 void CpuPollingThread::submit_list(const SGEntry* e, int count, size_t total, bool dst_contig, bool src_contig,
                                    bool uniform) {
     const uint64_t t0 = now_us();
-    if (count == 1 || (dst_contig && src_contig)) {
+    if (queue_worker_copy(e, count, total)) {
+        coalesced_entries_.fetch_add((uint64_t)count, std::memory_order_relaxed);
+    } else if (count == 1 || (dst_contig && src_contig)) {
         SGEntry one{e[0].dst, e[0].src, total};
         ce_manager_.submit_scatter_gather(&one, 1);
         coalesced_entries_.fetch_add(1, std::memory_order_relaxed);

@@ -23,6 +23,7 @@
 #include "gfd/cpu_polling.h"
 #include "gfd/staging_pool.h"
 #include "gfd_capi.h"
+#include "zc_worker.h"
 
 namespace gfd {
 
@@ -49,25 +50,26 @@ constexpr int kZcNotTaken = INT_MIN;               // direct_zero_copy: the list
 
 void no_chunk(void*, int, size_t, size_t) {}
 
-// The zero-copy SG kernel gives each entry of a short list a wave of its own,
-// so a list of fewer entries than its target waves (W, the kernel's own
-// figure: gfd_zero_copy_target_waves) leaves waves idle while a few stream
-// whole large entries.  Such a list's entries are cut into pieces of at least
-// 4 KiB, a multiple of 16 bytes each (an entry's last piece takes what is
-// left), so the pieces keep each entry's alignment.  The piece size is set for
-// W - count waves, since each entry's last piece may be a short one: the table
-// then has at most W records, one per wave, and goes to the kernel's
-// presliced launch (*presliced = true), which does not cut them again.  Writes
-// the table to out (at most cap records) and returns its length, or copies
-// the entries unchanged (*presliced = false) when the list is long enough or
-// the pieces would not fit.
-int zc_fill_sg_table(const SGEntry* in, int count, size_t total, SGEntry* out, int cap, bool* presliced) {
-    static const int kWaves = gfd_zero_copy_target_waves();
+}  // namespace
+
+// The zero-copy SG kernel (and the zero-copy worker) gives each entry of a
+// short list a wave of its own, so a list of fewer entries than its `waves`
+// waves leaves waves idle while a few stream whole large entries.  Such a
+// list's entries are cut into pieces of at least 4 KiB, a multiple of 16
+// bytes each (an entry's last piece takes what is left), so the pieces keep
+// each entry's alignment.  The piece size is set for waves - count waves,
+// since each entry's last piece may be a short one: the table then has at
+// most `waves` records, one per wave (*presliced = true; the kernel's
+// presliced launch does not cut them again).  Writes the table to out (at
+// most cap records) and returns its length, or copies the entries unchanged
+// (*presliced = false) when the list is long enough or the pieces would not
+// fit.  The caller guarantees count <= cap.
+int zc_fill_sg_table(const SGEntry* in, int count, size_t total, SGEntry* out, int cap, bool* presliced, int waves) {
     constexpr size_t kMinPiece = 4096;
     *presliced = false;
-    if (count < kWaves && total / (size_t)count >= 2 * kMinPiece) {
-        const size_t waves = (size_t)(kWaves - count);
-        const size_t piece = std::max(kMinPiece, ((total + waves - 1) / waves + 15) & ~(size_t)15);
+    if (count < waves && total / (size_t)count >= 2 * kMinPiece) {
+        const size_t free_waves = (size_t)(waves - count);
+        const size_t piece = std::max(kMinPiece, ((total + free_waves - 1) / free_waves + 15) & ~(size_t)15);
         int n = 0;
         for (int i = 0; i < count && n >= 0; i++) {
             for (size_t off = 0; off < in[i].size; off += piece) {
@@ -87,8 +89,6 @@ int zc_fill_sg_table(const SGEntry* in, int count, size_t total, SGEntry* out, i
     std::memcpy(out, in, (size_t)count * sizeof(SGEntry));
     return count;
 }
-
-}  // namespace
 
 void run_copy_chunk(void* p, int chunk, size_t off, size_t len) {
     RunCopyCtx* c = (RunCopyCtx*)p;
@@ -257,7 +257,8 @@ int CpuPollingThread::direct_zero_copy(const SGEntry* entries, int count, size_t
             zc_table_cap_ = cap;
         }
         bool cut = false;
-        const int n = zc_fill_sg_table(entries, count, total, zc_table_, zc_table_cap_, &cut);
+        static const int kWaves = gfd_zero_copy_target_waves();
+        const int n = zc_fill_sg_table(entries, count, total, zc_table_, zc_table_cap_, &cut, kWaves);
         rc = (cut ? gfd_zero_copy_gather_signal_presliced : gfd_zero_copy_gather_signal)(
             reinterpret_cast<const gfd_sg_entry*>(zc_table_), n, zc_counter_, zc_done_, gen, zc_stream_);
     }
@@ -265,6 +266,27 @@ int CpuPollingThread::direct_zero_copy(const SGEntry* entries, int count, size_t
     trace(TRACE_ZC_LAUNCH, (uint32_t)count, total);
     rc = zc_wait(gen);
     trace(TRACE_ZC_DONE, 0, gen);
+    return rc;
+}
+
+// The persistent zero-copy worker copies a destination-contiguous list whose
+// sources were checked pinned: the list (cut into pieces when it is short and
+// its entries large) becomes the worker's next job.  Returns 0, kZcNotTaken
+// (the destination is not device memory, or the list does not fit the
+// worker's table) or an error.
+int CpuPollingThread::direct_worker(const SGEntry* entries, int count, size_t total) {
+    if (count > worker_->capacity() || !zc_dst_in_device(entries[0].dst, entries[0].dst + total)) return kZcNotTaken;
+    static const uint64_t timeout_us = [] {
+        const char* v = std::getenv("GFD_DIRECT_TIMEOUT_MS");
+        return (uint64_t)std::max(1ll, v && *v ? std::atoll(v) : 10000ll) * 1000ull;
+    }();
+    std::lock_guard<std::mutex> lock(worker_->mutex());
+    bool cut = false;
+    const int n = zc_fill_sg_table(entries, count, total, worker_->table(), worker_->capacity(), &cut,
+                                   worker_->waves());
+    trace(TRACE_ZC_LAUNCH, (uint32_t)count, total);
+    const int rc = worker_->run(n, timeout_us);
+    trace(TRACE_ZC_DONE, 0, worker_->jobs());
     return rc;
 }
 
@@ -300,7 +322,8 @@ int CpuPollingThread::zc_launch_head(const SGEntry* entries, int k, bool uniform
         size_t bytes = 0;
         for (int i = 0; i < k; i++) bytes += entries[i].size;
         bool cut = false;
-        const int n = zc_fill_sg_table(entries, k, bytes, zc_table_, zc_table_cap_, &cut);
+        static const int kWaves = gfd_zero_copy_target_waves();
+        const int n = zc_fill_sg_table(entries, k, bytes, zc_table_, zc_table_cap_, &cut, kWaves);
         rc = (cut ? gfd_zero_copy_gather_signal_presliced : gfd_zero_copy_gather_signal)(
             reinterpret_cast<const gfd_sg_entry*>(zc_table_), n, zc_counter_, zc_done_, g, zc_stream_);
     }
@@ -392,6 +415,7 @@ bool CpuPollingThread::init_direct_ce() {
         GFD_LOG_ERROR("zero-copy route set-up failed; submit_direct uses the copy engines only\n");
         direct_zc_max_bytes_ = 0;
     }
+    if (worker_wanted_) ensure_worker();
     return start_workers();
 }
 
@@ -460,7 +484,11 @@ double CpuPollingThread::submit_direct(const SGEntry* entries, int count) {
              TRACE_DIRECT_BEGIN, (uint32_t)count, total);
     int err = 0;
     const int nch = direct_ce_manager_.num_channels();
-    if (dst_contig && src_contig) {
+    if (worker_ && dst_contig && zc_pinned == 1 && total <= direct_zc_max_bytes_ &&
+        (err = direct_worker(entries, count, total)) != kZcNotTaken) {
+        // done by the persistent zero-copy worker (err 0) or failed
+    } else if (dst_contig && src_contig) {
+        err = 0;
         // One range: split it over the channels when it is large.
         int parts = total >= kContiguousSplitMin ? nch : 1;
         size_t per = ((total + parts - 1) / parts + 4095) & ~(size_t)4095;

@@ -66,6 +66,25 @@ inline hsa_signal_t sig(uint64_t h) {
 
 }  // namespace
 
+int find_hsa_agents(int device, uint64_t* gpu_agent, uint64_t* cpu_agent) {
+    AgentSearch s;
+    s.want_index = device;
+    char bus[64] = {0};
+    unsigned dom = 0, b = 0, d = 0, f = 0;
+    if (gfd_hip_pci_bus_id(bus, sizeof(bus), device) == 0 && std::sscanf(bus, "%x:%x:%x.%x", &dom, &b, &d, &f) == 4) {
+        s.bdf = (b << 8) | (d << 3) | f;
+        s.domain = dom;
+    } else {
+        s.bdf = 0xFFFFFFFFu;
+        s.domain = 0xFFFFFFFFu;
+    }
+    hsa_iterate_agents(visit_agent, &s);
+    if (!s.have_cpu || !(s.have_gpu || s.have_nth)) return (int)HSA_STATUS_ERROR_INVALID_AGENT;
+    *gpu_agent = s.have_gpu ? s.gpu.handle : s.nth_gpu.handle;
+    *cpu_agent = s.cpu.handle;
+    return 0;
+}
+
 SdmaQueue::SdmaQueue() = default;
 
 SdmaQueue::~SdmaQueue() {
@@ -87,26 +106,12 @@ int SdmaQueue::init(int device, int channels, int pin_engines) {
         own_hsa_ = true;
     }
     hsa_status_t st = HSA_STATUS_SUCCESS;
-    AgentSearch s;
-    s.want_index = device;
-    char bus[64] = {0};
-    unsigned dom = 0, b = 0, d = 0, f = 0;
-    if (gfd_hip_pci_bus_id(bus, sizeof(bus), device) == 0 && std::sscanf(bus, "%x:%x:%x.%x", &dom, &b, &d, &f) == 4) {
-        s.bdf = (b << 8) | (d << 3) | f;
-        s.domain = dom;
-    } else {
-        s.bdf = 0xFFFFFFFFu;
-        s.domain = 0xFFFFFFFFu;
-    }
-    hsa_iterate_agents(visit_agent, &s);
-    if (!s.have_cpu || !(s.have_gpu || s.have_nth)) {
+    if (find_hsa_agents(device, &gpu_agent_, &cpu_agent_) != 0) {
         GFD_LOG_ERROR("SDMA: HSA agents for device %d not found\n", device);
         if (own_hsa_) hsa_shut_down();
         own_hsa_ = false;
         return (int)HSA_STATUS_ERROR_INVALID_AGENT;
     }
-    gpu_agent_ = s.have_gpu ? s.gpu.handle : s.nth_gpu.handle;
-    cpu_agent_ = s.cpu.handle;
     hsa_agent_t gpu{gpu_agent_}, cpu{cpu_agent_};
     engine_mask_ = 0;
     hsa_amd_memory_copy_engine_status(gpu, cpu, &engine_mask_);

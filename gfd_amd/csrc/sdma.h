@@ -23,6 +23,11 @@
 
 namespace gfd {
 
+// The HSA agents (handles) of HIP device `device` and of the host: the GPU
+// whose PCI bus id HIP reports for the device, else the device-th GPU agent.
+// Returns 0 or an HSA status.
+int find_hsa_agents(int device, uint64_t* gpu_agent, uint64_t* cpu_agent);
+
 class SdmaQueue {
 public:
     SdmaQueue();

@@ -34,6 +34,7 @@ constexpr int NUM_GATHER_WORKERS = 7;
 
 struct SGTaskQueue;
 class GatherEngine;
+class ZcWorker;
 
 class CpuPollingThread {
 public:
@@ -150,6 +151,24 @@ public:
     // GFD_DIRECT_ZC_HEAD_BYTES; needs the zero-copy route enabled).
     void set_direct_zero_copy_head_bytes(size_t b) { direct_zc_head_bytes_ = b; }
     size_t direct_zero_copy_head_bytes() const { return direct_zc_head_bytes_; }
+    // The persistent zero-copy worker (off by default; GFD_ZC_WORKER=1 turns
+    // it on for new pollers): a grid of 64 waves that stays resident on an
+    // AQL queue of this poller's own and copies a list when the host rings
+    // its doorbell, ending itself after GFD_ZC_WORKER_IDLE_MS (100 ms)
+    // without a job.  While it is on, submit_direct sends every destination-
+    // contiguous list of at most direct_zero_copy_max_bytes() with pinned
+    // sources to it (short ones included), and the Queue path sends batches
+    // of at most worker_queue_max_bytes() with pinned sources and device
+    // destinations to it instead of staging them for the copy engines.
+    // Returns 0, or nonzero if the worker cannot be set up (it then stays
+    // off).  Not while the polling thread runs.
+    int set_zero_copy_worker(bool on);
+    bool zero_copy_worker() const { return worker_ != nullptr; }
+    // Jobs the worker ran and grids dispatched for them (0 when off).
+    uint64_t zero_copy_worker_jobs() const;
+    uint64_t zero_copy_worker_launches() const;
+    void set_worker_queue_max_bytes(size_t b) { worker_queue_max_bytes_ = b; }
+    size_t worker_queue_max_bytes() const { return worker_queue_max_bytes_; }
     // Chunk size of the pipelined gather (payload bytes per copy).
     void set_direct_chunk_bytes(size_t b) { direct_chunk_bytes_ = b ? b : 1; }
     size_t direct_chunk_bytes() const { return direct_chunk_bytes_; }
@@ -233,6 +252,9 @@ private:
                                 int nruns = 0, int uniform_hint = -1);
     int direct_scattered(const SGEntry* entries, int count, size_t total, bool uniform);
     int direct_zero_copy(const SGEntry* entries, int count, size_t total, bool uniform, bool sources_checked);
+    int direct_worker(const SGEntry* entries, int count, size_t total);
+    bool queue_worker_copy(const SGEntry* e, int count, size_t total);
+    bool ensure_worker();
     int zc_plan_head(const SGEntry* entries, int count, size_t total, bool uniform, size_t* head_bytes);
     int zc_launch_head(const SGEntry* entries, int k, bool uniform, uint64_t* gen);
     bool zc_sources_pinned(const SGEntry* entries, int count, bool fill_src_table);
@@ -328,6 +350,10 @@ private:
     size_t direct_zc_min_bytes_ = 64u << 10;
     size_t direct_zc_head_bytes_ = 2u << 20;
     uint64_t zc_dst_lo_ = 0, zc_dst_hi_ = 0;  // last device allocation found for a destination
+    ZcWorker* worker_ = nullptr;
+    bool worker_wanted_ = false;  // GFD_ZC_WORKER=1: set up with the copy engines
+    size_t worker_queue_max_bytes_ = 4u << 20;
+    uint64_t queue_dst_lo_ = 0, queue_dst_hi_ = 0;  // Queue path: last device allocation found
     std::vector<uint32_t> tile_scratch_;
     size_t slice_bytes_ = 0;
 

@@ -151,6 +151,18 @@ uint64_t gfd_poller_set_direct_zero_copy_min_bytes(gfd_poller_t p, uint64_t byte
  * kernel moves the first entries, up to `bytes`, while the rest is staged
  * for the copy engines (0 = staged only).  Returns the previous value. */
 uint64_t gfd_poller_set_direct_zero_copy_head_bytes(gfd_poller_t p, uint64_t bytes);
+/* The persistent zero-copy worker (no reference counterpart; it stands in for
+ * the kernel launch and the copy-engine start of short copies,
+ * CpuPollingThread::set_zero_copy_worker): on = 1 sets it up and routes
+ * Direct lists of at most the zero-copy limit and Queue batches of at most
+ * gfd_poller_set_worker_queue_max_bytes (4 MiB) with pinned sources through
+ * it; 0 removes it.  Returns 0 or an error.  Not while the polling thread
+ * runs. */
+int gfd_poller_set_zero_copy_worker(gfd_poller_t p, int on);
+/* Jobs the worker has run and grids dispatched for them (both 0 while off). */
+int gfd_poller_zero_copy_worker_stats(gfd_poller_t p, uint64_t* jobs, uint64_t* launches);
+/* Returns the previous limit. */
+uint64_t gfd_poller_set_worker_queue_max_bytes(gfd_poller_t p, uint64_t bytes);
 void gfd_poller_set_gather_slice_bytes(gfd_poller_t p, uint64_t bytes);
 
 /* Host-only gather (no GPU): the staging step of the pipelined direct path.

@@ -39,6 +39,10 @@ uintptr_t locked_agent_base(uintptr_t base);
 // route), so a scenario can tell which route a call took.
 unsigned zero_copy_launches();
 
+// Aborts the process, as a GPU page fault would end it, unless [p, p + n) is
+// pinned host memory or device memory (n = 0 passes).
+void require_gpu_access(const void* p, size_t n, const char* what);
+
 // Engine stall watchdog: an engine that has polled one dependency for longer
 // than this (GFD_EMU_STALL_MS, default 5000) prints what it waits on and ends
 // the process with kStallExit, since in-order engines that wait on each other

@@ -85,18 +85,22 @@ int g_handle = 0;
 namespace {
 std::atomic<unsigned> g_zc_launches{0};
 
+void require_gpu_readable(const void* p, size_t n, const char* what) { emu::require_gpu_access(p, n, what); }
+}
+
+namespace emu {
 // A GPU kernel that reads a host address the runtime has not mapped for the
 // GPU takes a page fault (XNACK is off): the emulated kernels end the process
-// the same way, so a scenario sees any source handed to them unchecked.
-void require_gpu_readable(const void* p, size_t n, const char* what) {
+// the same way, so a scenario sees any address handed to them unchecked.
+void require_gpu_access(const void* p, size_t n, const char* what) {
     uintptr_t b;
     size_t s;
     if (n == 0 || emu::find_alloc(p, n, emu::Kind::Pinned, &b, &s) || emu::find_alloc(p, n, emu::Kind::Device, &b, &s))
         return;
-    std::fprintf(stderr, "emulated GPU fault: %s reads %zu bytes at %p, not pinned or device memory\n", what, n, p);
+    std::fprintf(stderr, "emulated GPU fault: %s touches %zu bytes at %p, not pinned or device memory\n", what, n, p);
     std::abort();
 }
-}
+}  // namespace emu
 namespace emu {
 unsigned zero_copy_launches() { return g_zc_launches.load(); }
 }  // namespace emu

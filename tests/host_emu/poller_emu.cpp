@@ -357,6 +357,7 @@ int run_queue(uint32_t n, uint32_t t, bool scattered, int rounds, uint64_t seed)
             rc = queue_round(q, ent, dst, want, seed, rnd, "queue");
         }
         p.stop();
+        std::printf("zero-copy worker jobs: %llu\n", (unsigned long long)p.zero_copy_worker_jobs());
     }
     if (rc == 0) std::printf("queue %ux%u scattered=%d: pass\n", n, t, (int)scattered);
     gfd_hip_host_free(q);
@@ -732,6 +733,76 @@ int run_locked_source() {
     return 0;
 }
 
+// submit_direct with the zero-copy worker on: destination-contiguous lists
+// with pinned sources (short, long, ragged, one entry, contiguous) become
+// worker jobs; a list with pageable sources and one larger than the route's
+// limit take the staged route.  Every call's bytes are compared.
+int run_worker_direct(uint64_t seed) {
+    Rng rng(seed);
+    const size_t host_bytes = 24u << 20;
+    auto* host = (uint8_t*)host_alloc(host_bytes);
+    for (size_t i = 0; i < host_bytes; i += 8) {
+        const uint64_t v = rng.next();
+        std::memcpy(host + i, &v, 8);
+    }
+    std::vector<uint8_t> pageable(1u << 20);
+    for (auto& b : pageable) b = (uint8_t)rng.next();
+    const size_t dst_bytes = 12u << 20;
+    auto* dst = (uint8_t*)dev_alloc(dst_bytes);
+    struct Case {
+        const char* name;
+        std::vector<uint32_t> sizes;
+        bool pageable, contiguous, want_worker;
+    };
+    std::vector<Case> cases = {
+        {"16 x 4 KiB", std::vector<uint32_t>(16, 4096), false, false, true},
+        {"2048 x 512 B", std::vector<uint32_t>(2048, 512), false, false, true},
+        {"4 x 256 KiB", std::vector<uint32_t>(4, 256u << 10), false, false, true},
+        {"ragged", {}, false, false, true},
+        {"one 64 KiB entry", {65536}, false, true, true},
+        {"contiguous 32 x 4 KiB", std::vector<uint32_t>(32, 4096), false, true, true},
+        {"pageable 64 x 4 KiB", std::vector<uint32_t>(64, 4096), true, false, false},
+        {"10 MiB, above the limit", std::vector<uint32_t>(160, 65536), false, false, false},
+    };
+    for (int i = 0; i < 50; i++) cases[3].sizes.push_back(1 + (uint32_t)rng.below(20000));
+    int rc = 0;
+    {
+        CpuPollingThread p(nullptr, nullptr, nullptr, 16u << 20, true, -1);
+        if (!p.init_direct_ce() || p.set_zero_copy_worker(true) != 0) return 4;
+        for (const Case& c : cases) {
+            if (rc) break;
+            std::vector<SGEntry> sg;
+            size_t off = 0, src_off = 0;
+            for (uint32_t sz : c.sizes) {
+                const uint8_t* base = c.pageable ? pageable.data() : host;
+                const size_t span = c.pageable ? pageable.size() : host_bytes;
+                size_t so = c.contiguous ? src_off : (size_t)rng.below(span - sz);
+                if (!c.contiguous && ((sz & 15) == 0)) so &= ~(size_t)15;
+                sg.push_back(SGEntry{(uint64_t)(uintptr_t)dst + off, base + so, sz});
+                off += sz;
+                src_off += sz;
+            }
+            if (off > dst_bytes) return 4;
+            std::vector<uint8_t> want(off + 4096, kSentinel);
+            for (const SGEntry& e : sg) std::memcpy(&want[e.dst - (uint64_t)(uintptr_t)dst], e.src, e.size);
+            std::memset(dst, kSentinel, want.size());
+            const uint64_t jobs0 = p.zero_copy_worker_jobs();
+            if (p.submit_direct(sg.data(), (int)sg.size()) < 0) return 3;
+            const bool took = p.zero_copy_worker_jobs() == jobs0 + 1;
+            std::printf("worker direct %s: %s\n", c.name, took ? "worker" : "other route");
+            if (took != c.want_worker) {
+                std::printf("worker direct %s: expected the %s route\n", c.name, c.want_worker ? "worker" : "other");
+                rc = 3;
+            }
+            if (rc == 0) rc = check_image(dst, want, c.name, 0);
+        }
+    }
+    gfd_hip_free(dst);
+    gfd_hip_host_free(host);
+    if (rc == 0) std::printf("worker direct: pass\n");
+    return rc;
+}
+
 // A pinned source found by one submit_direct call is looked up again by the
 // next: between the calls its registration goes away while the addresses stay
 // readable to the CPU (a freed pinned buffer whose range a pageable
@@ -781,6 +852,7 @@ int main(int argc, char** argv) {
     if (argc >= 2 && std::string(argv[1]) == "sdma_slot_reuse") return run_sdma_slot_reuse();
     if (argc >= 2 && std::string(argv[1]) == "locked_source") return run_locked_source();
     if (argc >= 2 && std::string(argv[1]) == "stale_pinned") return run_stale_pinned(7);
+    if (argc >= 2 && std::string(argv[1]) == "worker_direct") return run_worker_direct(11);
     if (argc >= 4 && std::string(argv[1]) == "staging_pool")
         return run_staging_pool(std::atoi(argv[2]), std::strtoull(argv[3], nullptr, 0));
     if (argc >= 10 && std::string(argv[1]) == "tiled")

@@ -23,24 +23,28 @@ def row(dispatch, grid, name, counter, value):
                                                                             value)
 
 
-def test_pmc_parser_keeps_the_calibration_copies_and_the_full_size_gathers(tmp_path):
+def test_pmc_parser_keeps_the_calibration_launches_and_the_full_size_gathers(tmp_path):
     rows = [row(1, 65536, "__amd_rocclr_fillBufferAligned", "FETCH_SIZE", 16.0)]
     # Five calibration copies first, then a later copy that must not count.
     rows += [row(2 + i, 131072, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 16390.0 + i) for i in range(5)]
+    # Five contiguous calibration gathers on the full grid, before anything else launches the kernel.
+    rows += [row(7 + i, 16384, "void (anonymous namespace)::zc_gather_tokens<false>(...)", "FETCH_SIZE",
+                 16440.0 + i) for i in range(5)]
     # The set-up launch on 16 bytes (one workgroup), then 12 launches of the job.
-    rows.append(row(7, 256, "void (anonymous namespace)::zc_gather_tokens<false>(...)", "FETCH_SIZE", 1.0))
-    rows += [row(8 + i, 16384, "void (anonymous namespace)::zc_gather_tokens<false>(...)", "FETCH_SIZE",
+    rows.append(row(12, 256, "void (anonymous namespace)::zc_gather_tokens<false>(...)", "FETCH_SIZE", 1.0))
+    rows += [row(13 + i, 16384, "void (anonymous namespace)::zc_gather_tokens<false>(...)", "FETCH_SIZE",
                  16457.0 + i) for i in range(12)]
-    rows.append(row(20, 131072, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 99999.0))
+    rows.append(row(25, 131072, "__amd_rocclr_copyBuffer", "FETCH_SIZE", 99999.0))
     # Another counter's rows are ignored.
-    rows.append(row(21, 16384, "void (anonymous namespace)::zc_gather_tokens<false>(...)", "WRITE_SIZE", 5.0))
+    rows.append(row(26, 16384, "void (anonymous namespace)::zc_gather_tokens<false>(...)", "WRITE_SIZE", 5.0))
     p = tmp_path / "p_counter_collection.csv"
     p.write_text("\n".join([HEADER] + rows) + "\n")
-    copies, gathers = bench.parse_pmc_counters(str(p), "FETCH_SIZE")
+    copies, contig, gathers = bench.parse_pmc_counters(str(p), "FETCH_SIZE")
     assert copies == [16390.0 + i for i in range(5)]
+    assert contig == [16440.0 + i for i in range(5)]
     assert gathers == [16457.0 + i for i in range(12)]
-    copies, gathers = bench.parse_pmc_counters(str(p), "WRITE_SIZE")
-    assert copies == [] and gathers == [5.0]
+    copies, contig, gathers = bench.parse_pmc_counters(str(p), "WRITE_SIZE")
+    assert copies == [] and contig == [5.0] and gathers == []
 
 
 def test_session_timeline_summary():

@@ -215,3 +215,24 @@ def test_sg_mode_abort_workloads_under_stack_protector(poller_emu_protect, case)
     a stack canary and glibc's checked copies (-fstack-protector-all
     -D_FORTIFY_SOURCE=3, -O3): no canary is overwritten and every byte lands."""
     run(poller_emu_protect, ["sg", case, 3, 1])
+
+
+def test_direct_routes_through_the_zero_copy_worker(poller_emu):
+    """submit_direct with the persistent zero-copy worker on (emulated: the
+    records are copied on the calling thread, each side checked to be pinned
+    or device memory): short, ragged, one-entry and contiguous lists with
+    pinned sources become worker jobs; pageable sources and a list above the
+    zero-copy limit take the other routes.  Every byte is compared."""
+    out = run(poller_emu, ["worker_direct"])
+    assert out.count(": worker") == 6 and out.count(": other route") == 2, out[-2000:]
+
+
+@pytest.mark.parametrize("n,t,scattered,want_jobs", [(2048, 512, 0, True), (2048, 2048, 1, True),
+                                                      (2048, 65536, 0, False)])
+def test_queue_batches_through_the_zero_copy_worker(poller_emu, n, t, scattered, want_jobs):
+    """Queue mode with the worker on: batches of at most 4 MiB (small tokens,
+    contiguous or scattered destinations) become worker jobs, larger ones are
+    staged for the copy engines as before; done_idx and every byte checked."""
+    out = run(poller_emu, ["queue", n, t, scattered, 2, 1], env={"GFD_ZC_WORKER": "1"})
+    jobs = int(out.split("zero-copy worker jobs: ")[1].split()[0])
+    assert (jobs > 0) == want_jobs, out[-2000:]
