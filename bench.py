@@ -503,6 +503,40 @@ def run_direct_sizes(oracle, poller, iters, warmup):
     return out
 
 
+def run_worker_direct(oracle, iters, warmup):
+    """submit_direct through the persistent zero-copy worker (a poller with
+    set_zero_copy_worker on): the reference's published short lists (4 KiB
+    tokens, 16 ... 1024; 64 KiB tokens, 16), few large tokens, and the
+    config-4 sizes; each output checked byte for byte."""
+    p = gfd_amd.CpuPollingThread(None, None, None, 16 << 20, numa_node=-1)
+    out = {}
+    try:
+        assert p.init_direct_ce(), "init_direct_ce failed"
+        p.set_zero_copy_worker(True)
+        shapes = [(n, 4096) for n in (16, 64, 256, 1024)] + [(4, 65536), (16, 65536), (2048, 512), (2048, 1024),
+                                                              (2048, 2048)]
+        for n, t in shapes:
+            L = Layout(oracle, n, t)
+            tt = np.zeros(iters)
+            jobs0 = p.zero_copy_worker_stats()["jobs"]
+            rc = gfd_amd.lib().gfd_bench_submit_direct(p._h, ctypes.cast(L.entries, ctypes.c_void_p), n, warmup, iters,
+                                                       tt.ctypes.data_as(PD))
+            assert rc == 0, gfd_amd.lib().gfd_last_error()
+            L.verify("direct through the worker %d x %d" % (n, t))
+            assert p.zero_copy_worker_stats()["jobs"] == jobs0 + warmup + iters, "not through the worker"
+            key = "%dx%s" % (n, ("%dKB" % (t // 1024)) if t >= 1024 else "%dB" % t)
+            out[key] = {"us_p50": round(p50(tt), 2), "GBps": round(gbps(n * t, p50(tt)), 3)}
+            ref = (REFERENCE_DIRECT_4KB_US if t == 4096 else REFERENCE_DIRECT_64KB_US if t == 65536 else {}).get(n)
+            if ref:
+                out[key]["reference_us"] = ref
+            log("  direct through the worker %s: %s" % (key, out[key]))
+            del L
+        out["worker"] = p.zero_copy_worker_stats()
+    finally:
+        p.close()
+    return out
+
+
 def run_direct_scattered(oracle, poller, iters, warmup):
     """GFD Direct with non-contiguous destinations, 8192 x 4 KiB tokens
     (scattered sources as in the main layout): 'pages' = a paged KV cache,
@@ -1022,7 +1056,7 @@ def run_helper_waves(oracle, iters, warmup):
 TRACE_NAMES = {1: "batch_first_read", 2: "flush", 3: "copies_issued", 4: "done_published", 5: "gap_flush",
                7: "chunk_copy_issued", 8: "direct_end", 9: "gather_entry", 10: "gather_idle",
                11: "gather_published", 12: "gather_first_slice", 13: "gather_built", 14: "zc_kernel_launched",
-               15: "zc_done_seen"}
+               15: "zc_done_seen", 16: "zc_checked"}
 
 
 def _phase_medians(rows):
@@ -1105,9 +1139,21 @@ def run_timeline(oracle, calls=30):
         del L
     direct.close()
 
+    for worker in (False, True):
+        out.update(_queue_timeline(oracle, shapes if not worker else shapes[:3], calls, worker))
+    return out
+
+
+def _queue_timeline(oracle, shapes, calls, worker):
+    """The Queue half of run_timeline; with `worker`, the poller's persistent
+    zero-copy worker copies the batches (keys queue_worker_<n>x<t>)."""
+    L_ = gfd_amd.lib()
+    out = {}
     q = gfd_amd.DescriptorQueue()
     p = gfd_amd.CpuPollingThread(q, None, None, 8192 * 4096 * 2, numa_node=-1)
     assert p.init_copy_engine(), "queue poller init failed"
+    if worker:
+        p.set_zero_copy_worker(True)
     p.start()
     st = ctypes.c_void_p()
     L_.gfd_stream_create(ctypes.byref(st))
@@ -1137,9 +1183,9 @@ def run_timeline(oracle, calls=30):
             p.set_trace(False)
             p.set_copy_timing(False)
             L.verify("queue (timeline)")
-            out["queue_%dx%d" % (n, t)] = _phase_medians([_call_phases(tr, cp[cp["path"] == 0], a, b)
-                                                          for a, b in rows])
-            log("  timeline queue %dx%d: %s" % (n, t, out["queue_%dx%d" % (n, t)]))
+            key = "queue%s_%dx%d" % ("_worker" if worker else "", n, t)
+            out[key] = _phase_medians([_call_phases(tr, cp[cp["path"] == 0], a, b) for a, b in rows])
+            log("  timeline %s: %s" % (key, out[key]))
             del L
     finally:
         L_.gfd_stream_destroy(st)
@@ -1166,10 +1212,12 @@ def first_call_latency(oracle):
 
 
 class QueueRig:
-    def __init__(self, region_bytes):
+    def __init__(self, region_bytes, worker=False):
         self.q = gfd_amd.DescriptorQueue()
         self.p = gfd_amd.CpuPollingThread(self.q, None, None, region_bytes, numa_node=-1)
         assert self.p.init_copy_engine(), "queue poller init failed"
+        if worker:
+            self.p.set_zero_copy_worker(True)
         self.p.start()
         self.base = ctypes.c_uint64(0)
 
@@ -1181,6 +1229,9 @@ class QueueRig:
         L.verify("queue")
         out = {"us_p50": round(p50(t), 2), "GBps": round(gbps(L.bytes, p50(t)), 3),
                "descriptors_per_s": round(L.n / (p50(t) * 1e-6))}
+        w = self.p.zero_copy_worker_stats()
+        if w["jobs"]:
+            out["worker"] = w
         # SDMA timeline over a few more rounds (after the timed loop).
         self.p.set_copy_timing(True)
         t2 = np.zeros(5)
@@ -1203,7 +1254,7 @@ class QueueRig:
         self.q.free()
 
 
-def flat_metric_fields(roofline, results, r_moe):
+def flat_metric_fields(roofline, results, r_moe, r_worker=None):
     """The metric's figures as flat scalars in `roofline` (a record that keeps
     only scalar fields keeps these): per layout, Direct, the zero-copy kernel,
     Queue and per-token copies (us, GB/s, fraction of 63.02 GB/s); the
@@ -1215,7 +1266,7 @@ def flat_metric_fields(roofline, results, r_moe):
         tag = "%dx%s" % (r["tokens"], ("%dKB" % (r["token_bytes"] // 1024)) if r["token_bytes"] >= 1024
                          else "%dB" % r["token_bytes"])
         for key, name in (("direct", "direct"), ("zero_copy", "zc"), ("queue", "queue"),
-                          ("memcpy_per_token", "memcpy_per_token")):
+                          ("queue_worker", "queue_worker"), ("memcpy_per_token", "memcpy_per_token")):
             m = r.get(key)
             if not m:
                 continue
@@ -1235,6 +1286,12 @@ def flat_metric_fields(roofline, results, r_moe):
             roofline["direct_sdma_%s_GBps_while_busy" % tag] = sd["link_GBps_while_busy"]
             roofline["direct_sdma_%s_busy_frac" % tag] = sd["busy_frac_any"]
             roofline["direct_sdma_%s_first_copy_us" % tag] = sd["first_copy_start_us"]
+    for key, m in (r_worker or {}).items():
+        if isinstance(m, dict) and "us_p50" in m:
+            roofline["direct_worker_%s_us" % key] = m["us_p50"]
+            roofline["direct_worker_%s_GBps" % key] = m["GBps"]
+            if "reference_us" in m:
+                roofline["direct_worker_%s_reference_us" % key] = m["reference_us"]
     if r_moe:
         route = r_moe["route_and_lists_us_p50"]
         roofline["moe_route_and_lists_us"] = route
@@ -1256,7 +1313,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=15)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--only", default="",
-                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions,scattered,offload,"
+                    help="comma list: peak,zc,direct,memcpy,queue,cpu,kv,small,moe,sessions,scattered,offload,worker,"
                          "firstcall,sizes,pmc,helpers,timeline (helpers and timeline are not in the default run; pmc: "
                          "the two rocprofv3 --pmc passes behind roofline.traffic, with zc) "
                          "(calib: add a 32 MiB D2D copy)")
@@ -1355,6 +1412,11 @@ def main():
         r_short = run_short_lists(oracle, direct, K, W)
     direct.close()
 
+    r_worker = None
+    if want("worker"):
+        log("submit_direct through the persistent zero-copy worker ...")
+        r_worker = run_worker_direct(oracle, K, W)
+
     r_sessions = None
     if want("sessions"):
         log("wave-specialised sessions ...")
@@ -1398,6 +1460,16 @@ def main():
             log("  %dx%d queue: %s" % (n, t, res[(n, t)]["queue"]))
             del L
         queue.close()
+        if want("worker"):
+            # The same descriptors with the persistent zero-copy worker copying
+            # the batches of at most 4 MiB (config 4).
+            queue = QueueRig(region_max, worker=True)
+            for n, t in small if want("small") else []:
+                L = Layout(oracle, n, t)
+                res[(n, t)]["queue_worker"] = queue.run(L, K, W)
+                log("  %dx%d queue through the worker: %s" % (n, t, res[(n, t)]["queue_worker"]))
+                del L
+            queue.close()
     r_main = res[main_cfg]
     r_kv = res.get(kv_cfg)
     r_small = [res[c] for c in small if c in res]
@@ -1459,11 +1531,11 @@ def main():
     for r in [r_main, r_kv] + r_small:
         if not r:
             continue
-        for k in ("zero_copy", "direct", "queue", "memcpy_per_token"):
+        for k in ("zero_copy", "direct", "queue", "queue_worker", "memcpy_per_token"):
             if k in r:
                 r[k].update(frac(r[k]["GBps"]))
     if roofline is not None:
-        flat_metric_fields(roofline, [r_main, r_kv] + r_small, r_moe)
+        flat_metric_fields(roofline, [r_main, r_kv] + r_small, r_moe, r_worker)
     result = {
         "metric": METRIC, "value": round(value, 3), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(head.get("us_p50", 0.0) / 1e3, 4), "higher_is_better": True, "scaling": "weak",
@@ -1481,6 +1553,7 @@ def main():
         "results_direct_sizes": r_sizes,
         "results_short_lists": r_short,
         "results_offload": r_offload,
+        "results_worker_direct": r_worker,
         "results_helper_waves": r_helpers,
         "results_timeline": r_timeline,
         "first_call_direct_256x4KB": r_first,

@@ -160,6 +160,7 @@ def _declare(L):
         "gfd_poller_set_zero_copy_worker": ([vp, c_int], c_int),
         "gfd_poller_zero_copy_worker_stats": ([vp, ctypes.POINTER(c_u64), ctypes.POINTER(c_u64)], c_int),
         "gfd_poller_set_worker_queue_max_bytes": ([vp, c_u64], c_u64),
+        "gfd_poller_zero_copy_worker_timeline": ([vp, vp, c_int], c_int),
         "gfd_bench_zero_copy_tokens_signal": ([vp, vp, c_u32, c_int, c_int, c_int, pd], c_int),
         "gfd_zero_copy_gather_tokens_signal": ([vp, vp, c_u32, c_int, vp, vp, c_u64, vp], c_int),
         "gfd_zero_copy_scatter_tokens_signal": ([vp, vp, c_u32, c_int, vp, vp, c_u64, vp], c_int),
@@ -454,6 +455,15 @@ class CpuPollingThread:
         _check(lib().gfd_poller_zero_copy_worker_stats(self._h, ctypes.byref(j), ctypes.byref(l)),
                "gfd_poller_zero_copy_worker_stats")
         return {"jobs": j.value, "launches": l.value}
+
+    def zero_copy_worker_timeline(self, max_jobs=64):
+        """The worker's device timeline of its latest jobs, newest first: an
+        (n, 8) uint64 array on the GPU's 100 MHz wall clock (doorbell seen, job
+        seen by the last workgroup, first / last wave with its records, last
+        wave done copying, done raised, doorbell value, unused)."""
+        out = np.zeros((max_jobs, 8), np.uint64)
+        n = lib().gfd_poller_zero_copy_worker_timeline(self._h, out.ctypes.data, max_jobs)
+        return out[:n]
 
     def set_worker_queue_max_bytes(self, b):
         """Queue batches of at most b bytes go to the worker; returns the previous limit."""

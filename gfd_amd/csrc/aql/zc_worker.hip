@@ -10,26 +10,51 @@
 // the hidden kernel arguments zero, so nothing here reads blockDim / gridDim:
 // the workgroup count arrives as an argument and the workgroup size is fixed.
 //
-// Protocol (host side in zc_worker.cpp):
-//   * The host writes a job's records to `table` (pinned memory), then the
-//     doorbell word with a release store: bits 0-15 a generation that changes
-//     every job, bits 16-39 the record count.  The value ~0 asks the grid to
-//     exit.
-//   * Wave 0 of workgroup 0 (the leader) polls the doorbell over PCIe, one
-//     read in flight at a time.  A new value is published to the other
-//     workgroups through HBM (ZcWorkerState::job, an agent-scope release);
-//     wave 0 of every other workgroup polls that word with short naps while
-//     the workgroup's other waves wait at the workgroup barrier.
-//   * Every wave copies its share of the records, releases its stores at
-//     system scope and counts itself in ZcWorkerState::waves_done; the last
-//     wave resets the count and stores the job's doorbell value to `done`
-//     (pinned host memory) with a system-scope release, so every byte is
-//     visible to the host once it reads that value.
-//   * After idle_ticks (100 MHz wall clock) without a new doorbell value the
-//     leader raises ZcWorkerState::exit and the grid ends; the host sees the
-//     dispatch's completion signal and dispatches the worker again for its
-//     next job.  Records of a job are the units of work: the host cuts large
-//     entries of short lists into pieces so that each wave gets one.
+// Protocol (host side in zc_worker.cpp).  Host memory is pinned and coherent:
+//   * Jobs are numbered 1, 2, ... and posted into a ring of job_slots slots
+//     (a power of two).  Slot k holds a header word (one cache line each) and
+//     a region of job_cap records.  The host writes job q's records into
+//     region q mod job_slots, then its header with a release store:
+//     q << 24 | count.  A count of 0xFFFFFF asks the grid to exit.  A slot
+//     is reused only after every workgroup has finished the job before.
+//   * A record is 32 bytes, two 16-byte halves {dst, size, gen} {src, 0,
+//     gen}, gen = the job number's low 24 bits in the last word of each half.
+//   * Wave k of workgroup b is slot k * num_blocks + b (consecutive records
+//     go to different workgroups, and XCDs).  A job of at most one record per
+//     slot gives record s to slot s and stores it at region position b * 8 +
+//     k, so that a workgroup's records are 256 contiguous bytes; a larger job
+//     is stored in order and gives slot s the runs of at most 64 records that
+//     start at s * per, s * per + slots * per, ... (per = ceil(count / slots),
+//     at most 64).
+//   * A workgroup is one prefetch wave and kCopyWaves copy waves; copy wave
+//     k is slot k * num_blocks + b of workgroup b.  The prefetch wave takes
+//     the jobs in order: it polls the header of the next job's ring slot over
+//     PCIe (relaxed loads, one read in flight), reads the records of the
+//     workgroup's slots (the first run of at most 64 records of each), and
+//     stages them in one of two LDS stages, while the copy waves copy the job
+//     staged in the other.  For 200 us after a job (a caller that has just
+//     copied is likely to copy again) each poll also reads as many of the
+//     workgroup's records as its last job had, if that job had at most one
+//     record per slot; later polls read the header alone, with short naps.
+//     A half read in one request is one snapshot of its cache line, and the
+//     host stored the generation after the fields before it, so a half
+//     carrying the job's generation holds the job's fields; other halves are
+//     read again.  Records read after the header are ordered after it by a
+//     system-scope acquire.
+//   * Each copy wave copies its records, waits for its stores, and counts
+//     itself done in the stage; the last of the kCopyWaves releases the
+//     workgroup's stores at agent scope, stores the job number to the
+//     workgroup's progress word (pinned host memory, one cache line per
+//     workgroup) and frees the stage.  Job q and every job before it are
+//     done once every progress word is >= q.
+//   * A prefetch wave that finds no new job for idle_ticks (100 MHz wall
+//     clock) since its last one stores the dispatch's epoch to the closing
+//     word in HBM and stages an exit for its copy waves; every other prefetch
+//     wave reads that word in each poll and does the same, so the grid drains
+//     within a poll.  The dispatch's
+//     completion signal then tells the host, which dispatches the grid again
+//     from the first job not done (a job some workgroups had finished is run
+//     again in full: copies are idempotent).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -38,118 +63,270 @@
 
 namespace {
 
-constexpr int kWaves = 4;  // per workgroup
-constexpr uint64_t kExit = ~0ull;
+constexpr int kCopyWaves = 8;                    // per workgroup, after the prefetch wave
+constexpr int kGroupThreads = (kCopyWaves + 1) * 64;
+constexpr int kStageRecords = 64;                // per copy wave and job: the first run of its records
+constexpr uint64_t kExit = ~0ull;     // no job: the grid drains
+constexpr uint64_t kExitCount = 0xFFFFFF;  // a header count that asks the grid to exit
+constexpr uint64_t kHotTicks = 20000;  // 200 us on the 100 MHz wall clock
 
+// One record: two 16-byte halves, the job's generation in the last word of each.
 struct Record {
     uint64_t dst;
+    uint32_t size;
+    uint32_t gen;
     uint64_t src;
-    uint64_t size;
+    uint32_t pad;
+    uint32_t gen2;
 };
+static_assert(sizeof(Record) == 32, "record layout");
+
+// One 16-byte half, read as a single system-coherent request (a volatile
+// load carries sc0 sc1): no cache line kept from an earlier job can answer it.
+__device__ __forceinline__ gfd::wave::vec4u load_half(const char* p) {
+    return *reinterpret_cast<const volatile gfd::wave::gvec4u*>((uintptr_t)p);
+}
+
+// Per-job device timeline in HBM (zc_worker.cpp reads it): kTraceJobs records
+// of 8 words on the 100 MHz wall clock, record (job mod kTraceJobs).  Each
+// field is the latest over the grid; a record is reused 64 jobs later with
+// larger times, so maxima need no reset:
+//   0 a workgroup found the job, 1 a workgroup had the job and its records,
+//   3 a workgroup had copied its share, 5 a workgroup had stored its
+//   progress word, 6 the job number.
+// Word kTraceJobs * 8 after them is the closing word.
+constexpr int kTraceJobs = 64;
+
+// flags: kTrace records the timeline (off, no timeline atomic sits on a
+// job's path).
+constexpr uint32_t kTrace = 1;
+
+__device__ __forceinline__ void trace_max(uint32_t flags, uint64_t* trace, uint64_t job, int field) {
+    if (flags & kTrace)
+        __hip_atomic_fetch_max(trace + (job & (kTraceJobs - 1)) * 8 + field, (uint64_t)wall_clock64(),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 }  // namespace
 
-// HBM state shared by the grid's workgroups (zc_worker.cpp keeps the same
-// layout: 64 bytes).
-struct ZcWorkerState {
-    uint64_t job;         // the doorbell value the leader published last
-    uint32_t waves_done;  // waves finished with the current job
-    uint32_t exit;        // 1: every wave leaves
-    uint64_t pad[6];
+// An LDS stage: one job's header and the first run of records of each copy
+// wave, as the two 16-byte halves read from the host.
+struct Stage {
+    uint64_t job;  // the job staged here, kExit, or 0 (none yet)
+    uint64_t header;
+    gfd::wave::vec4u rec[kCopyWaves][kStageRecords][2];
 };
 
-// Sets the state a new grid starts from: `last_job` published (already done),
-// no wave counted, no exit.  Dispatched ahead of every gfd_zc_worker grid on
-// the same queue.
-extern "C" __global__ __launch_bounds__(64) void gfd_zc_worker_reset(ZcWorkerState* st, uint64_t last_job) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) {
-        st->job = last_job;
-        st->waves_done = 0;
-        st->exit = 0;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+__device__ __forceinline__ uint64_t lds_load_acquire(uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_store_release(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// The prefetch wave (wave 0 of a workgroup).
+__device__ __forceinline__ void prefetch_wave(const uint64_t* headers, const Record* table, uint64_t* trace,
+                                              uint32_t num_blocks, uint32_t flags, uint64_t first_job,
+                                              uint64_t idle_ticks, uint64_t epoch, uint32_t job_slots,
+                                              uint32_t job_cap, Stage* stage, uint64_t* done_job) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t slots = (uint64_t)num_blocks * kCopyWaves;
+    uint64_t* closing = trace + kTraceJobs * 8;
+    // Lane l < 2 * kCopyWaves reads half l & 1 of copy wave l / 2's record
+    // (slot (l / 2) * num_blocks + blockIdx.x, region position blockIdx.x *
+    // kCopyWaves + l / 2) for jobs of at most one record per slot.
+    const uint32_t lane_wave = (lane >> 1) & (kCopyWaves - 1);
+    const uint64_t lane_slot = (uint64_t)lane_wave * num_blocks + blockIdx.x;
+    const uint64_t lane_pos = (uint64_t)blockIdx.x * kCopyWaves + lane_wave;
+    uint64_t t_last = wall_clock64();
+    uint32_t hot_halves = 0;  // halves the hot polls read: those of the last job's records here
+    for (uint64_t q = first_job;; q++) {
+        Stage& st = stage[q & 1];
+        // The stage last held job q - 2: wait until its copies are done.
+        while (lds_load_acquire(&done_job[q & 1]) + 2 < q) __builtin_amdgcn_s_sleep(1);
+        const uint64_t ring = q & (job_slots - 1);
+        const Record* region = table + ring * job_cap;
+        const char* my_half = reinterpret_cast<const char*>(region + lane_pos) + (lane & 1) * 16;
+        const uint64_t* header = headers + ring * 8;
+        uint64_t h = kExit;
+        gfd::wave::vec4u half = {0, 0, 0, 0};
+        for (;;) {
+            const uint64_t quiet = (uint64_t)wall_clock64() - t_last;
+            const bool hot = quiet < kHotTicks;
+            const uint64_t c = __hip_atomic_load(closing, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t raw =
+                __hip_atomic_load(const_cast<uint64_t*>(header), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (hot && lane < hot_halves) half = load_half(my_half);
+            const uint64_t d = gfd::wave::readlane64(raw, 0);
+            if ((d >> 24) == q) {
+                h = d;
+                break;
+            }
+            if (gfd::wave::readlane64(c, 0) == epoch) break;
+            if (quiet > idle_ticks) {
+                if (lane == 0) __hip_atomic_store(closing, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            if (!hot) __builtin_amdgcn_s_sleep(8);
+        }
+        const uint64_t count = h & 0xFFFFFFull;
+        if (h == kExit || count == kExitCount) {
+            if (lane == 0) lds_store_release(&st.job, kExit);
+            return;
+        }
+        if (lane == 0) trace_max(flags, trace, q, 0);
+        // A launch's dispatch invalidates the caches that may hold pinned
+        // host lines; a resident grid must do it per job, or a source the
+        // host rewrote since an earlier job could be read stale.  The
+        // workgroup's waves share the CU's L1 and the XCD's L2, so one
+        // system-scope acquire here, before the job is staged, does it for
+        // the copy waves too.
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+        hot_halves = 0;
+        if (count <= slots) {
+            // Both halves of each record this workgroup copies must carry the
+            // job's generation; stale ones are read again.
+            const uint32_t gen = (uint32_t)(q & 0xFFFFFFu);
+            const bool want = lane < 2 * kCopyWaves && lane_slot < count;
+            for (uint32_t tries = 0; tries < (1u << 20); tries++) {
+                const bool stale = want && half[3] != gen;
+                if (__ballot(stale) == 0) break;
+                half = load_half(my_half);
+            }
+            if (lane < 2 * kCopyWaves) st.rec[lane_wave][0][lane & 1] = half;
+            hot_halves = 2 * (uint32_t)__popcll(__ballot(want) & 0x5555ull);
+        } else {
+            // The first run of each copy wave: per records from position
+            // slot * per.  Half i (of 2 * per) of copy wave k is flat index
+            // k * 2 * per + i, loaded by lane (index mod 64), eight loads in
+            // flight per lane.
+            uint64_t per = (count + slots - 1) / slots;
+            per = per > kStageRecords ? kStageRecords : per;
+            const uint32_t per32 = (uint32_t)per;
+            const uint32_t total = kCopyWaves * 2 * per32;  // <= 1024
+            for (uint32_t base = 0; base < total; base += 8 * 64) {
+                gfd::wave::vec4u v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const uint32_t idx = base + lane + 64u * u;
+                    const uint32_t k = idx / (2 * per32), r = (idx >> 1) - k * per32;
+                    uint64_t rec = ((uint64_t)k * num_blocks + blockIdx.x) * per + r;
+                    // Branch-free plain loads, all in flight together (a
+                    // lane past the run reads record 0, and its value is not
+                    // kept; volatile loads would be issued one at a time):
+                    // the acquire above has invalidated any line an earlier
+                    // job left cached.
+                    rec = idx < total && rec < count ? rec : 0;
+                    v[u] = gfd::wave::gload((uint64_t)(uintptr_t)(region + rec) + (idx & 1) * 16);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const uint32_t idx = base + lane + 64u * u;
+                    const uint32_t k = idx / (2 * per32), r = (idx >> 1) - k * per32;
+                    const uint64_t rec = ((uint64_t)k * num_blocks + blockIdx.x) * per + r;
+                    if (idx < total && rec < count) st.rec[k][r][idx & 1] = v[u];
+                }
+            }
+        }
+        if (lane == 0) {
+            st.header = h;
+            trace_max(flags, trace, q, 1);
+            lds_store_release(&st.job, q);
+        }
+        t_last = wall_clock64();
     }
 }
 
-extern "C" __global__ __launch_bounds__(kWaves * 64) void gfd_zc_worker(const uint64_t* doorbell, uint64_t* done,
-                                                                       const Record* table, ZcWorkerState* st,
-                                                                       uint32_t num_blocks, uint64_t last_job,
-                                                                       uint64_t idle_ticks) {
-    __shared__ gfd::wave::BatchLds lds[kWaves];
-    __shared__ uint64_t job_lds;
+extern "C" __global__ __launch_bounds__(kGroupThreads) void gfd_zc_worker(const uint64_t* headers, uint64_t* progress,
+                                                                         const Record* table, uint64_t* trace,
+                                                                         uint32_t num_blocks, uint32_t flags,
+                                                                         uint64_t first_job, uint64_t idle_ticks,
+                                                                         uint64_t epoch, uint32_t job_slots,
+                                                                         uint32_t job_cap) {
+    __shared__ Stage stage[2];
+    __shared__ uint64_t done_job[2];   // stage i: the last job all copy waves finished there
+    __shared__ uint32_t done_cnt[2];   // stage i: copy waves done with its current job
+    __shared__ gfd::wave::BatchLds lds[kCopyWaves];
     const uint32_t lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const uint64_t nwaves = (uint64_t)num_blocks * kWaves;
-    const uint64_t wave = (uint64_t)blockIdx.x * kWaves + wid;
-    uint64_t seen = last_job;
-    for (;;) {
-        if (wid == 0) {
-            uint64_t j = kExit;
-            if (blockIdx.x == 0) {
-                // The leader: one PCIe read of the doorbell in flight at a time.
-                const uint64_t t0 = wall_clock64();
-                for (;;) {
-                    const uint64_t d = gfd::wave::readlane64(
-                        __hip_atomic_load(const_cast<uint64_t*>(doorbell), __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM),
-                        0);
-                    if (d != seen) {
-                        j = d;
-                        break;
-                    }
-                    if ((uint64_t)wall_clock64() - t0 > idle_ticks) break;
-                }
+    if (threadIdx.x == 0) {
+        for (int i = 0; i < 2; i++) {
+            stage[i].job = 0;
+            done_job[i] = first_job - 1;
+            done_cnt[i] = 0;
+        }
+    }
+    __syncthreads();
+    if (wid == 0) {
+        prefetch_wave(headers, table, trace, num_blocks, flags, first_job, idle_ticks, epoch, job_slots, job_cap,
+                      stage, done_job);
+        return;
+    }
+    const uint32_t k = wid - 1;  // copy wave index
+    const uint64_t slots = (uint64_t)num_blocks * kCopyWaves;
+    const uint64_t slot = (uint64_t)k * num_blocks + blockIdx.x;
+    for (uint64_t q = first_job;; q++) {
+        Stage& st = stage[q & 1];
+        uint64_t j;
+        while ((j = lds_load_acquire(&st.job)) != q && j != kExit) __builtin_amdgcn_s_sleep(1);
+        if (j == kExit) return;
+        const uint64_t count = st.header & 0xFFFFFFull;
+        const Record* region = table + (q & (job_slots - 1)) * job_cap;
+        if (count <= slots) {
+            // At most one record per slot.
+            if (slot < count) {
+                const gfd::wave::vec4u a = st.rec[k][0][0], b = st.rec[k][0][1];
+                uint64_t md = 0, ms = 0, mn = 0;
                 if (lane == 0) {
-                    if (j == kExit)
-                        __hip_atomic_store(&st->exit, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-                    else
-                        __hip_atomic_store(&st->job, j, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                    md = (uint64_t)a[0] | ((uint64_t)a[1] << 32);
+                    mn = (uint64_t)a[2];
+                    ms = (uint64_t)b[0] | ((uint64_t)b[1] << 32);
                 }
-            } else {
-                for (;;) {
-                    const uint64_t p = __hip_atomic_load(&st->job, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-                    if (p != seen) {
-                        j = p;
-                        break;
+                gfd::wave::copy_batch(16, md, ms, mn, 1, &lds[k]);
+            }
+        } else {
+            uint64_t per = (count + slots - 1) / slots;
+            per = per > kStageRecords ? kStageRecords : per;
+            const uint64_t stride = slots * per;
+            for (uint64_t first = slot * per; first < count; first += stride) {
+                const uint32_t nb = (uint32_t)(count - first < per ? count - first : per);
+                uint64_t md = 0, ms = 0, mn = 0;
+                if (lane < nb) {
+                    if (first == slot * per) {
+                        // The first run is staged.
+                        const gfd::wave::vec4u a = st.rec[k][lane][0], b = st.rec[k][lane][1];
+                        md = (uint64_t)a[0] | ((uint64_t)a[1] << 32);
+                        mn = (uint64_t)a[2];
+                        ms = (uint64_t)b[0] | ((uint64_t)b[1] << 32);
+                    } else {
+                        const Record r = region[first + lane];
+                        md = r.dst;
+                        ms = r.src;
+                        mn = r.size;
                     }
-                    if (__hip_atomic_load(&st->exit, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT)) break;
-                    __builtin_amdgcn_s_sleep(4);
                 }
+                gfd::wave::copy_batch(16, md, ms, mn, nb, &lds[k]);
             }
-            if (lane == 0) job_lds = j;
         }
-        __syncthreads();
-        const uint64_t j = job_lds;
-        __syncthreads();  // job_lds is written again only after every wave has read it
-        if (j == kExit) break;
-        seen = j;
-        // A launch's dispatch invalidates the caches that may hold pinned host
-        // lines; a resident grid must do it per job, or a source the host
-        // rewrote since an earlier job could be read stale from L2.  The
-        // system-scope acquire does that, and orders the record reads after
-        // the doorbell (the host wrote the records first).
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
-        const uint64_t count = (j >> 16) & 0xFFFFFFull;
-        // Wave w takes records [w * per, ...) strided over the grid, at most
-        // 64 at a time; a job of at most nwaves records gives one per wave.
-        uint64_t per = (count + nwaves - 1) / nwaves;
-        per = per < 1 ? 1 : (per > 64 ? 64 : per);
-        const uint64_t stride = nwaves * per;
-        for (uint64_t first = wave * per; first < count; first += stride) {
-            const uint32_t nb = (uint32_t)(count - first < per ? count - first : per);
-            uint64_t md = 0, ms = 0, mn = 0;
-            if (lane < nb) {
-                const Record r = table[first + lane];
-                md = r.dst;
-                ms = r.src;
-                mn = r.size;
-            }
-            gfd::wave::copy_batch(16, md, ms, mn, nb, &lds[wid]);
-        }
-        // System scope: destinations may be pinned host memory as well as HBM.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
-        if (lane == 0) {
-            const uint32_t prev = __hip_atomic_fetch_add(&st->waves_done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            if ((uint64_t)prev + 1 == nwaves) {
-                __hip_atomic_store(&st->waves_done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(done, j, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        // This wave's stores have reached the L2 before it counts itself done.
+        __builtin_amdgcn_s_waitcnt(0);
+        uint32_t prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(&done_cnt[q & 1], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+        prev = __builtin_amdgcn_readfirstlane(prev);
+        if (prev == kCopyWaves - 1) {
+            // The last copy wave of the job here: the workgroup's stores are
+            // visible device-wide before its progress word.
+            gfd::wave::release_agent();
+            if (lane == 0) {
+                done_cnt[q & 1] = 0;
+                trace_max(flags, trace, q, 3);
+                __hip_atomic_store(&progress[(uint64_t)blockIdx.x * 8], q, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+                trace_max(flags, trace, q, 5);
+                if (flags & kTrace)
+                    __hip_atomic_store(&trace[(q & (kTraceJobs - 1)) * 8 + 6], q, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                lds_store_release(&done_job[q & 1], q);
             }
         }
     }

@@ -277,6 +277,10 @@ int gfd_poller_zero_copy_worker_stats(gfd_poller_t p, uint64_t* jobs, uint64_t* 
     *launches = P(p)->zero_copy_worker_launches();
     return 0;
 }
+int gfd_poller_zero_copy_worker_timeline(gfd_poller_t p, uint64_t* out, int max_jobs) {
+    if (!p || (!out && max_jobs > 0)) return 0;
+    return P(p)->zero_copy_worker_timeline(out, max_jobs);
+}
 uint64_t gfd_poller_set_worker_queue_max_bytes(gfd_poller_t p, uint64_t b) {
     if (!p) return 0;
     const uint64_t prev = P(p)->worker_queue_max_bytes();

@@ -162,18 +162,23 @@ CpuPollingThread::~CpuPollingThread() {
 
 int CpuPollingThread::num_gather_workers() const { return gather_ ? gather_->num_workers() : 0; }
 
-// The worker's grid: 16 workgroups of 4 waves (64 waves, the zero-copy
-// kernels' short-list width); 8192 records per job.
+// The worker's grid: by default 8 workgroups of 8 waves (64 waves, the
+// zero-copy kernels' short-list width), one workgroup per XCD; 8192 records
+// per job.  GFD_ZC_WORKER_GROUPS sets the workgroups (1-32),
+// GFD_ZC_WORKER_TRACE=1 records the device timeline.
 bool CpuPollingThread::ensure_worker() {
     if (worker_) return true;
     auto* w = new ZcWorker();
     const uint32_t idle_ms = (uint32_t)env_size("GFD_ZC_WORKER_IDLE_MS", 100);
-    if (gfd_hip_set_device(device_) != 0 || w->init(device_, 16, idle_ms, 8192) != 0) {
+    const int groups = (int)std::min<size_t>(std::max<size_t>(env_size("GFD_ZC_WORKER_GROUPS", 8), 1), 32);
+    const uint32_t flags = env_size("GFD_ZC_WORKER_TRACE", 0) ? ZcWorker::kTrace : 0u;
+    if (gfd_hip_set_device(device_) != 0 || w->init(device_, groups, idle_ms, 8192, flags) != 0) {
         GFD_LOG_ERROR("zero-copy worker set-up failed; it stays off\n");
         delete w;
         return false;
     }
     worker_ = w;
+    worker_posted_ = worker_done_seen_ = 0;
     return true;
 }
 
@@ -187,6 +192,7 @@ int CpuPollingThread::set_zero_copy_worker(bool on) {
         delete worker_;
         worker_ = nullptr;
         worker_wanted_ = false;
+        worker_posted_ = worker_done_seen_ = 0;
         return 0;
     }
     worker_wanted_ = true;
@@ -195,12 +201,19 @@ int CpuPollingThread::set_zero_copy_worker(bool on) {
 
 uint64_t CpuPollingThread::zero_copy_worker_jobs() const { return worker_ ? worker_->jobs() : 0; }
 uint64_t CpuPollingThread::zero_copy_worker_launches() const { return worker_ ? worker_->launches() : 0; }
+int CpuPollingThread::zero_copy_worker_timeline(uint64_t* out, int max_jobs) {
+    return worker_ ? worker_->read_timeline(out, max_jobs) : 0;
+}
 
 // Queue path: a batch whose sources are pinned and whose destinations lie in
-// device memory goes to the worker as one job (blocking until it has
-// landed).  False if it does not qualify; the caller then stages it.
+// device memory goes to the worker as one job.  In plain Queue mode the job
+// is only posted: the batch's completion slot waits for it before done_idx
+// passes the batch.  Tiled and SG modes write their flags with copy-engine
+// packets ordered after the engines' copies only, so there the job is waited
+// for here.  False if the batch does not qualify or the worker failed; the
+// caller then stages it for the copy engines.
 bool CpuPollingThread::queue_worker_copy(const SGEntry* e, int count, size_t total) {
-    if (!worker_ || total > worker_queue_max_bytes_ || count > worker_->capacity()) return false;
+    if (!worker_ || !worker_->ok() || total > worker_queue_max_bytes_ || count > worker_->capacity()) return false;
     uintptr_t lo = 1, hi = 0;
     for (int i = 0; i < count; i++) {
         if (e[i].size == 0) continue;
@@ -218,11 +231,30 @@ bool CpuPollingThread::queue_worker_copy(const SGEntry* e, int count, size_t tot
             queue_dst_hi_ = base + size;
         }
     }
+    trace(TRACE_ZC_CHECKED, (uint32_t)count, total);
     static const uint64_t timeout_us = (uint64_t)env_size("GFD_DIRECT_TIMEOUT_MS", 10000) * 1000ull;
-    std::lock_guard<std::mutex> lock(worker_->mutex());
-    bool cut = false;
-    const int n = zc_fill_sg_table(e, count, total, worker_->table(), worker_->capacity(), &cut, worker_->waves());
-    if (worker_->run(n, timeout_us) != 0) GFD_LOG_ERROR("zero-copy worker: queue batch failed\n");
+    std::lock_guard<std::recursive_mutex> lock(worker_->mutex());
+    uint64_t job = 0;
+    if (count >= worker_->waves()) {
+        // At least one entry per slot: nothing to cut, posted as it is.
+        trace(TRACE_ZC_LAUNCH, (uint32_t)count, total);
+        job = worker_->post(count, timeout_us, e);
+    } else {
+        bool cut = false;
+        const int n =
+            zc_fill_sg_table(e, count, total, worker_->table(), worker_->capacity(), &cut, worker_->waves());
+        trace(TRACE_ZC_LAUNCH, (uint32_t)count, total);
+        job = worker_->post(n, timeout_us);
+    }
+    if (job != 0 && (tiled_queue_ || sg_queue_)) {
+        if (worker_->wait(job, timeout_us) != 0) GFD_LOG_ERROR("zero-copy worker: queue batch failed\n");
+        trace(TRACE_ZC_DONE, 0, job);
+    }
+    if (job == 0) {
+        GFD_LOG_ERROR("zero-copy worker: queue batch not posted; staging it\n");
+        return false;
+    }
+    worker_posted_ = job;
     return true;
 }
 
@@ -419,6 +451,7 @@ void CpuPollingThread::push_completion(uint64_t done_value) {
     while (f.count == CompletionFifo::N) drain_completions(true);
     CompletionSlot& s = f.slots[f.head];
     s.fence = ce_manager_.fence();
+    s.worker_job = worker_posted_;
     s.done_value = done_value;
     s.host_tiles.swap(pending_.host_tiles);
     s.host_lists.swap(pending_.host_lists);
@@ -447,6 +480,15 @@ void CpuPollingThread::drain_completions(bool block) {
         if (!ce_manager_.fence_done(s.fence)) {
             if (!block) return;
             if (ce_manager_.wait_fence(s.fence) != 0) GFD_LOG_ERROR("a copy reported an error\n");
+        }
+        if (s.worker_job && !worker_->done(s.worker_job)) {
+            if (!block) return;
+            static const uint64_t timeout_us = (uint64_t)env_size("GFD_DIRECT_TIMEOUT_MS", 10000) * 1000ull;
+            if (worker_->wait(s.worker_job, timeout_us) != 0) GFD_LOG_ERROR("a worker job did not finish\n");
+        }
+        if (s.worker_job > worker_done_seen_) {
+            worker_done_seen_ = s.worker_job;
+            trace(TRACE_ZC_DONE, 0, s.worker_job);
         }
         finish_slot(s);
         publish_done(s.done_value);

@@ -272,15 +272,15 @@ int CpuPollingThread::direct_zero_copy(const SGEntry* entries, int count, size_t
 // The persistent zero-copy worker copies a destination-contiguous list whose
 // sources were checked pinned: the list (cut into pieces when it is short and
 // its entries large) becomes the worker's next job.  Returns 0, kZcNotTaken
-// (the destination is not device memory, or the list does not fit the
-// worker's table) or an error.
+// (the worker is off after a failure, the destination is not device memory,
+// or the list does not fit the worker's table) or an error.
 int CpuPollingThread::direct_worker(const SGEntry* entries, int count, size_t total) {
-    if (count > worker_->capacity() || !zc_dst_in_device(entries[0].dst, entries[0].dst + total)) return kZcNotTaken;
+    if (!worker_->ok() || count > worker_->capacity() || !zc_dst_in_device(entries[0].dst, entries[0].dst + total)) return kZcNotTaken;
     static const uint64_t timeout_us = [] {
         const char* v = std::getenv("GFD_DIRECT_TIMEOUT_MS");
         return (uint64_t)std::max(1ll, v && *v ? std::atoll(v) : 10000ll) * 1000ull;
     }();
-    std::lock_guard<std::mutex> lock(worker_->mutex());
+    std::lock_guard<std::recursive_mutex> lock(worker_->mutex());
     bool cut = false;
     const int n = zc_fill_sg_table(entries, count, total, worker_->table(), worker_->capacity(), &cut,
                                    worker_->waves());

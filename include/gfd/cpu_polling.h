@@ -167,6 +167,9 @@ public:
     // Jobs the worker ran and grids dispatched for them (0 when off).
     uint64_t zero_copy_worker_jobs() const;
     uint64_t zero_copy_worker_launches() const;
+    // The worker's device timeline of its latest jobs (see ZcWorker::
+    // read_timeline): up to max_jobs records of 8 words, newest first.
+    int zero_copy_worker_timeline(uint64_t* out, int max_jobs);
     void set_worker_queue_max_bytes(size_t b) { worker_queue_max_bytes_ = b; }
     size_t worker_queue_max_bytes() const { return worker_queue_max_bytes_; }
     // Chunk size of the pipelined gather (payload bytes per copy).
@@ -196,8 +199,9 @@ public:
         TRACE_GATHER_PUBLISHED = 11,   // job visible to the workers: a = workers asleep at that moment
         TRACE_GATHER_FIRST_SLICE = 12, // first slice copied: a = threads that copied
         TRACE_GATHER_BUILT = 13,       // job state built (slices cut)
-        TRACE_ZC_LAUNCH = 14,          // Direct: zero-copy kernel launched: a = entries, b = bytes
-        TRACE_ZC_DONE = 15,            // Direct: its completion word seen by the host
+        TRACE_ZC_LAUNCH = 14,          // zero-copy kernel launched or worker job posted: a = entries, b = bytes
+        TRACE_ZC_DONE = 15,            // its completion word(s) seen by the host
+        TRACE_ZC_CHECKED = 16,         // Queue: a batch's sources and destinations checked for the worker
     };
     struct TraceEvent {
         uint64_t t_ns;
@@ -225,6 +229,7 @@ public:
     // Host-side effects applied once a batch's copies have completed.
     struct CompletionSlot {
         uint64_t fence = 0;       // every copy below this fence belongs to the batch or earlier
+        uint64_t worker_job = 0;  // and every zero-copy worker job up to this one (0: none)
         uint64_t done_value = 0;  // done_idx to publish
         std::vector<std::pair<uint32_t, uint64_t>> host_tiles;  // (tile, progress) for host flags
         std::vector<uint32_t> host_lists;                       // list ids for host flags
@@ -354,6 +359,8 @@ private:
     bool worker_wanted_ = false;  // GFD_ZC_WORKER=1: set up with the copy engines
     size_t worker_queue_max_bytes_ = 4u << 20;
     uint64_t queue_dst_lo_ = 0, queue_dst_hi_ = 0;  // Queue path: last device allocation found
+    uint64_t worker_posted_ = 0;     // Queue path: the last job posted to the worker
+    uint64_t worker_done_seen_ = 0;  // and the last one the completion slots saw done
     std::vector<uint32_t> tile_scratch_;
     size_t slice_bytes_ = 0;
 

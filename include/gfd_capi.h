@@ -163,6 +163,12 @@ int gfd_poller_set_zero_copy_worker(gfd_poller_t p, int on);
 int gfd_poller_zero_copy_worker_stats(gfd_poller_t p, uint64_t* jobs, uint64_t* launches);
 /* Returns the previous limit. */
 uint64_t gfd_poller_set_worker_queue_max_bytes(gfd_poller_t p, uint64_t bytes);
+/* The worker's device timeline of its latest jobs, newest first: up to
+ * max_jobs records of 8 words on the GPU's 100 MHz wall clock (doorbell seen,
+ * job seen by the last workgroup, first and last wave with its records, last
+ * wave done copying, done raised, the job's doorbell value, unused).  Returns
+ * the number of records (0 while the worker is off). */
+int gfd_poller_zero_copy_worker_timeline(gfd_poller_t p, uint64_t* out, int max_jobs);
 void gfd_poller_set_gather_slice_bytes(gfd_poller_t p, uint64_t bytes);
 
 /* Host-only gather (no GPU): the staging step of the pipelined direct path.
