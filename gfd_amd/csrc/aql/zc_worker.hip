@@ -23,14 +23,14 @@
 //     go to different workgroups, and XCDs).  A job of at most one record per
 //     slot gives record s to slot s and stores it at region position b * 8 +
 //     k, so that a workgroup's records are 256 contiguous bytes; a larger job
-//     is stored in order and gives slot s the runs of at most 64 records that
-//     start at s * per, s * per + slots * per, ... (per = ceil(count / slots),
-//     at most 64).
+//     is stored in order and gives slot s the run of per = ceil(count /
+//     slots) records at s * per (per <= 64: a job holds at most 64 records
+//     per slot).
 //   * A workgroup is one prefetch wave and kCopyWaves copy waves; copy wave
 //     k is slot k * num_blocks + b of workgroup b.  The prefetch wave takes
 //     the jobs in order: it polls the header of the next job's ring slot over
 //     PCIe (relaxed loads, one read in flight), reads the records of the
-//     workgroup's slots (the first run of at most 64 records of each), and
+//     workgroup's slots (at most 64 each), and
 //     stages them in one of two LDS stages, while the copy waves copy the job
 //     staged in the other.  For 200 us after a job (a caller that has just
 //     copied is likely to copy again) each poll also reads as many of the
@@ -65,7 +65,7 @@ namespace {
 
 constexpr int kCopyWaves = 8;                    // per workgroup, after the prefetch wave
 constexpr int kGroupThreads = (kCopyWaves + 1) * 64;
-constexpr int kStageRecords = 64;                // per copy wave and job: the first run of its records
+constexpr int kStageRecords = 64;                // per copy wave and job: at most this many records
 constexpr uint64_t kExit = ~0ull;     // no job: the grid drains
 constexpr uint64_t kExitCount = 0xFFFFFF;  // a header count that asks the grid to exit
 constexpr uint64_t kHotTicks = 20000;  // 200 us on the 100 MHz wall clock
@@ -109,8 +109,8 @@ __device__ __forceinline__ void trace_max(uint32_t flags, uint64_t* trace, uint6
 
 }  // namespace
 
-// An LDS stage: one job's header and the first run of records of each copy
-// wave, as the two 16-byte halves read from the host.
+// An LDS stage: one job's header and the records of each copy wave, as the
+// two 16-byte halves read from the host.
 struct Stage {
     uint64_t job;  // the job staged here, kExit, or 0 (none yet)
     uint64_t header;
@@ -196,10 +196,11 @@ __device__ __forceinline__ void prefetch_wave(const uint64_t* headers, const Rec
             if (lane < 2 * kCopyWaves) st.rec[lane_wave][0][lane & 1] = half;
             hot_halves = 2 * (uint32_t)__popcll(__ballot(want) & 0x5555ull);
         } else {
-            // The first run of each copy wave: per records from position
-            // slot * per.  Half i (of 2 * per) of copy wave k is flat index
-            // k * 2 * per + i, loaded by lane (index mod 64), eight loads in
-            // flight per lane.
+            // Each copy wave's run: per records from position slot * per
+            // (per <= kStageRecords: the host posts at most kStageRecords
+            // records per slot).  Half i (of 2 * per) of copy wave k is flat
+            // index k * 2 * per + i, loaded by lane (index mod 64), eight
+            // loads in flight per lane.
             uint64_t per = (count + slots - 1) / slots;
             per = per > kStageRecords ? kStageRecords : per;
             const uint32_t per32 = (uint32_t)per;
@@ -270,7 +271,6 @@ extern "C" __global__ __launch_bounds__(kGroupThreads) void gfd_zc_worker(const 
         while ((j = lds_load_acquire(&st.job)) != q && j != kExit) __builtin_amdgcn_s_sleep(1);
         if (j == kExit) return;
         const uint64_t count = st.header & 0xFFFFFFull;
-        const Record* region = table + (q & (job_slots - 1)) * job_cap;
         if (count <= slots) {
             // At most one record per slot.
             if (slot < count) {
@@ -284,25 +284,18 @@ extern "C" __global__ __launch_bounds__(kGroupThreads) void gfd_zc_worker(const 
                 gfd::wave::copy_batch(16, md, ms, mn, 1, &lds[k]);
             }
         } else {
-            uint64_t per = (count + slots - 1) / slots;
-            per = per > kStageRecords ? kStageRecords : per;
-            const uint64_t stride = slots * per;
-            for (uint64_t first = slot * per; first < count; first += stride) {
+            // This slot's run of per records, staged (a job holds at most
+            // kStageRecords records per slot).
+            const uint64_t per = (count + slots - 1) / slots;
+            const uint64_t first = slot * per;
+            if (first < count) {
                 const uint32_t nb = (uint32_t)(count - first < per ? count - first : per);
                 uint64_t md = 0, ms = 0, mn = 0;
                 if (lane < nb) {
-                    if (first == slot * per) {
-                        // The first run is staged.
-                        const gfd::wave::vec4u a = st.rec[k][lane][0], b = st.rec[k][lane][1];
-                        md = (uint64_t)a[0] | ((uint64_t)a[1] << 32);
-                        mn = (uint64_t)a[2];
-                        ms = (uint64_t)b[0] | ((uint64_t)b[1] << 32);
-                    } else {
-                        const Record r = region[first + lane];
-                        md = r.dst;
-                        ms = r.src;
-                        mn = r.size;
-                    }
+                    const gfd::wave::vec4u a = st.rec[k][lane][0], b = st.rec[k][lane][1];
+                    md = (uint64_t)a[0] | ((uint64_t)a[1] << 32);
+                    mn = (uint64_t)a[2];
+                    ms = (uint64_t)b[0] | ((uint64_t)b[1] << 32);
                 }
                 gfd::wave::copy_batch(16, md, ms, mn, nb, &lds[k]);
             }

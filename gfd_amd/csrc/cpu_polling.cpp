@@ -162,17 +162,19 @@ CpuPollingThread::~CpuPollingThread() {
 
 int CpuPollingThread::num_gather_workers() const { return gather_ ? gather_->num_workers() : 0; }
 
-// The worker's grid: by default 8 workgroups of 8 waves (64 waves, the
-// zero-copy kernels' short-list width), one workgroup per XCD; 8192 records
-// per job.  GFD_ZC_WORKER_GROUPS sets the workgroups (1-32),
-// GFD_ZC_WORKER_TRACE=1 records the device timeline.
+// The worker's grid: by default 8 workgroups of 8 copy waves (64 waves, the
+// zero-copy kernels' short-list width), one workgroup per XCD; up to 64
+// records per copy wave in a job (4096: a Queue batch holds at most
+// BATCH_THRESHOLD entries).  GFD_ZC_WORKER_GROUPS sets the workgroups
+// (1-32), GFD_ZC_WORKER_TRACE=1 records the device timeline.
 bool CpuPollingThread::ensure_worker() {
     if (worker_) return true;
     auto* w = new ZcWorker();
     const uint32_t idle_ms = (uint32_t)env_size("GFD_ZC_WORKER_IDLE_MS", 100);
     const int groups = (int)std::min<size_t>(std::max<size_t>(env_size("GFD_ZC_WORKER_GROUPS", 8), 1), 32);
     const uint32_t flags = env_size("GFD_ZC_WORKER_TRACE", 0) ? ZcWorker::kTrace : 0u;
-    if (gfd_hip_set_device(device_) != 0 || w->init(device_, groups, idle_ms, 8192, flags) != 0) {
+    const int capacity = groups * ZcWorker::kWavesPerGroup * ZcWorker::kStageRecords;
+    if (gfd_hip_set_device(device_) != 0 || w->init(device_, groups, idle_ms, capacity, flags) != 0) {
         GFD_LOG_ERROR("zero-copy worker set-up failed; it stays off\n");
         delete w;
         return false;

@@ -165,8 +165,9 @@ ZcWorker::~ZcWorker() {
 int ZcWorker::init(int device, int workgroups, uint32_t idle_ms, int capacity, uint32_t flags) {
     std::lock_guard<std::recursive_mutex> lock(mu_);
     if (ok_) return 0;
+    // A job holds at least one and at most kStageRecords records per slot.
     if (workgroups < 1 || workgroups > kMaxGroups || capacity < workgroups * kWavesPerGroup ||
-        capacity >= (1 << 24) - 1)
+        capacity > workgroups * kWavesPerGroup * kStageRecords)
         return -1;
     workgroups_ = workgroups;
     flags_ = flags;

@@ -35,7 +35,8 @@ int zc_fill_sg_table(const SGEntry* in, int count, size_t total, SGEntry* out, i
 class ZcWorker {
 public:
     static constexpr int kWavesPerGroup = 8;
-    static constexpr int kJobSlots = 4;  // jobs that can be posted and not yet done
+    static constexpr int kJobSlots = 4;       // jobs that can be posted and not yet done
+    static constexpr int kStageRecords = 64;  // records per slot a job may hold
     // Record the device timeline (read_timeline); off, no timeline atomic
     // sits on a job's path.
     static constexpr uint32_t kTrace = 1;
@@ -46,8 +47,8 @@ public:
     ZcWorker& operator=(const ZcWorker&) = delete;
 
     // Load the worker for HIP device `device`: code object, AQL queue,
-    // completion signal, kJobSlots job slots of `capacity` records each (at
-    // least one record per slot), the job timeline in HBM.  workgroups: grid
+    // completion signal, kJobSlots job slots of `capacity` records each
+    // (between 1 and kStageRecords per slot), the job timeline in HBM.  workgroups: grid
     // size (8 waves each, at most 32 workgroups); idle_ms: idle time after
     // which the grid ends; flags: kTrace or 0.  Returns 0 or an error.  The
     // grid is dispatched by the first post().

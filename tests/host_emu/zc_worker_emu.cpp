@@ -26,7 +26,8 @@ ZcWorker::~ZcWorker() {
 
 int ZcWorker::init(int, int workgroups, uint32_t, int capacity, uint32_t flags) {
     std::lock_guard<std::recursive_mutex> lock(mu_);
-    if (workgroups < 1 || workgroups > 32 || capacity < workgroups * kWavesPerGroup || capacity >= (1 << 24) - 1)
+    if (workgroups < 1 || workgroups > 32 || capacity < workgroups * kWavesPerGroup ||
+        capacity > workgroups * kWavesPerGroup * kStageRecords)
         return -1;
     list_ = new SGEntry[capacity];
     records_ = new SGEntry[(size_t)kJobSlots * capacity];

@@ -52,10 +52,11 @@ def scattered(n, t):
 
 # Short lists (below the copy engines' 64 KiB crossover), the config-4 sizes,
 # few large tokens that are cut into pieces, sizes that are no multiple of 16,
-# and an 8 MiB list at the zero-copy route's limit.
-@pytest.mark.parametrize("n,t", [(1, 4096), (2, 4096), (16, 4096), (64, 4096), (256, 4096), (2048, 512),
-                                 (2048, 1024), (2048, 2048), (4, 65536), (2, 32768), (3, 1 << 20), (97, 1000),
-                                 (5, 12), (2048, 4096)])
+# an 8 MiB list at the zero-copy route's limit, and 4096 records (64 per copy
+# wave, the most a job holds).
+@pytest.mark.parametrize("n,t", [(1, 4096), (2, 4096), (16, 4096), (64, 4096), (65, 4096), (256, 4096),
+                                 (2048, 512), (2048, 1024), (2048, 2048), (4, 65536), (2, 32768), (3, 1 << 20),
+                                 (97, 1000), (5, 12), (2048, 4096), (4096, 256)])
 def test_direct_through_the_worker(worker_poller, n, t):
     log("worker direct n=%d t=%d" % (n, t))
     host, perm, want = scattered(n, t)
@@ -153,12 +154,14 @@ def test_worker_ends_when_idle_and_starts_again(monkeypatch):
 
 
 @pytest.mark.parametrize("n,t,through_worker", [(2048, 512, True), (2048, 1024, True), (2048, 2048, True),
-                                                (300, 1000, True), (1, 4096, True), (8192, 4096, False)])
+                                                (300, 1000, True), (1, 4096, True), (9000, 512, True),
+                                                (8192, 4096, False)])
 def test_queue_batches_through_the_worker(n, t, through_worker):
     """Queue mode with the worker on: GPU-submitted descriptors whose batches
     hold at most 4 MiB are copied by the worker (8192 x 4 KiB batches of 16
     MiB are staged for the copy engines as before); two rounds each, done_idx
-    and every byte checked."""
+    and every byte checked.  9000 x 512 B is 9 batches a round: more jobs than
+    the worker's ring of 4, posted while earlier ones run."""
     log("worker queue n=%d t=%d" % (n, t))
     host, perm, want = scattered(n, t)
     src_addrs = np.uint64(host.ptr) + perm.astype(np.uint64) * np.uint64(2 * t)
