@@ -60,6 +60,7 @@ DIRECT_ZC_HEAD = 2 << 20  # and the zero-copy head of larger staged lists
 # in the RMSNorm, rows per GPU-built list (swept: 24-128 workgroups, 1-3
 # compute waves, 2-64 rows per list).
 MOE_SESSION_BLOCKS, MOE_SESSION_COMPUTE_WAVES, MOE_SESSION_ROWS_PER_LIST = 32, 3, 24
+MOE_SESSION_HELPERS = -1  # transfer helper waves per workgroup (negative: the session's default rule)
 PD = ctypes.POINTER(ctypes.c_double)
 
 
@@ -657,7 +658,8 @@ def run_moe(oracle, iters, warmup, tokens=4096, experts=64, dim=7168):
     for name, with_norm, cw in (("session_transfer_only", False, 1),
                                 ("session_overlapped_rmsnorm", True, MOE_SESSION_COMPUTE_WAVES),
                                 ("session_overlapped_rmsnorm_1_compute_wave", True, 1)):
-        sess = gfd_amd.SGWarpSpecSession(num_compute_warps=cw, num_blocks=MOE_SESSION_BLOCKS, idle_limit_ms=10000)
+        sess = gfd_amd.SGWarpSpecSession(num_compute_warps=cw, num_blocks=MOE_SESSION_BLOCKS, idle_limit_ms=10000,
+                                         helper_waves=MOE_SESSION_HELPERS)
         try:
             t = []
             for i in range(-warmup, iters):

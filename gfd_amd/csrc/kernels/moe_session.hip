@@ -152,6 +152,9 @@ struct MoeLists {
     // The launch's lists and entries fit the ring and the pool
     // (SGWarpSpecSession::gpu_lists_fit): no space or slot waits.
     int fits;
+    // Where the lists' headers and entries go: the session's HBM queue
+    // (SGDeviceCounters::dev_ring) when they fit, else the host queue.
+    gfd::SGTaskQueue* ring;
 };
 
 // Submitter wave: posts this workgroup's share of the lists (list L goes to
@@ -225,7 +228,7 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
         if ((uint32_t)lane < n) {
             const uint32_t r = r0 + (uint32_t)lane;
             const int tok = m.row_token[r];
-            DeviceSGEntry& d = sq->entries[(pool + (uint32_t)lane) % MAX_SG_POOL_ENTRIES];
+            DeviceSGEntry& d = m.ring->entries[(pool + (uint32_t)lane) % MAX_SG_POOL_ENTRIES];
             d.dst_addr = m.dst + (uint64_t)r * m.row_bytes;
             d.tag = r;
             if (tok >= 0 && tok < m.num_tokens) {
@@ -238,7 +241,7 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
             }
         }
         const uint64_t slot = sg::sg_alloc_list(sq);
-        if (!sg::sg_commit_list(sq, slot, (uint32_t)(pool % MAX_SG_POOL_ENTRIES), n, L, SG_FLAG_NONE, fits))
+        if (!sg::sg_commit_list(m.ring, slot, (uint32_t)(pool % MAX_SG_POOL_ENTRIES), n, L, SG_FLAG_NONE, fits))
             break;
     }
     if (blockIdx.x == 0) {
@@ -285,12 +288,17 @@ extern "C" int gfd_sg_session_launch_moe(gfd_sg_session_t s, const void* host_ba
     // The RMSNorm consumer shares each list between the session's compute
     // waves (num_compute_warps, at most SG_MAX_COMPUTE); transfer only needs one.
     const int compute = out ? std::min(p->compute_waves(), gfd::sg_warp_spec::SG_MAX_COMPUTE) : 1;
-    p->before_launch(stream, helpers, compute, p->idle_limit_ms());
-    // At most one list more per expert than whole lists of rows.
+    // At most one list more per expert than whole lists of rows.  When they
+    // fit the ring and the pool, their headers and entries stay in HBM: the
+    // transfer waves read them without a PCIe round trip per list.
     const uint64_t max_lists = (uint64_t)num_experts + (uint64_t)num_rows / rows_per_list;
+    if (p->running()) p->synchronize();  // as before_launch would: the ring positions are then current
+    const bool fits = p->gpu_lists_fit(max_lists, (uint64_t)num_rows);
+    gfd::SGTaskQueue* ring = fits ? p->device_ring() : nullptr;
+    if (!ring) ring = p->get_sg_queue();
+    p->before_launch(stream, helpers, compute, p->idle_limit_ms(), ring);
     const MoeLists m{(uint64_t)(uintptr_t)host_base, token_stride, (uint64_t)(uintptr_t)dst, offsets, row_token,
-                     num_experts, num_tokens, num_rows, row_bytes, rows_per_list,
-                     p->gpu_lists_fit(max_lists, (uint64_t)num_rows) ? 1 : 0};
+                     num_experts, num_tokens, num_rows, row_bytes, rows_per_list, fits ? 1 : 0, ring};
     const dim3 grid((unsigned)p->num_blocks()), block((unsigned)(2 + compute + helpers) * 64);
     if (out)
         hipLaunchKernelGGL(sg_moe_kernel<RowRMSNorm>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),

@@ -9,6 +9,7 @@
 // kernels the caller launches around its start()/stop().
 #include <algorithm>
 #include <chrono>
+#include <cstddef>
 #include <cstring>
 #include <thread>
 
@@ -241,11 +242,28 @@ SGWarpSpecSession::~SGWarpSpecSession() {
     delete poller_;  // clears its stop hook first
     poller_ = nullptr;
     if (trace_buf_) gfd_hip_free(trace_buf_);
+    if (dev_ring_) gfd_hip_free(dev_ring_);
     if (sq_) {
         if (sq_->d_list_done) gfd_hip_free(sq_->d_list_done);
         gfd_hip_host_free(sq_);
     }
     if (dq_) gfd_hip_host_free(dq_);
+}
+
+SGTaskQueue* SGWarpSpecSession::device_ring() {
+    if (dev_ring_ || !ok_) return dev_ring_;
+    void* d = nullptr;
+    if (gfd_hip_malloc(&d, sizeof(SGTaskQueue)) != 0) return nullptr;
+    // Zeroed (no list committed in any slot), sharing the host queue's
+    // d_list_done and device counters.
+    uint64_t* done = sq_->d_list_done;
+    if (gfd_hip_memset_d8((uint64_t)(uintptr_t)d, 0, sizeof(SGTaskQueue)) != 0 ||
+        gfd_hip_memcpy_h2d((uint64_t)(uintptr_t)d + offsetof(SGTaskQueue, d_list_done), &done, sizeof(done)) != 0) {
+        gfd_hip_free(d);
+        return nullptr;
+    }
+    dev_ring_ = static_cast<SGTaskQueue*>(d);
+    return dev_ring_;
 }
 
 bool SGWarpSpecSession::list_done(uint64_t idx) const {
@@ -310,7 +328,8 @@ uint64_t SGWarpSpecSession::submit_sg_list(const DeviceSGEntry* entries, uint32_
     return idx;
 }
 
-void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int compute_waves, uint32_t deadline_ms) {
+void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int compute_waves, uint32_t deadline_ms,
+                                      SGTaskQueue* gpu_ring) {
     if (running_) synchronize();
     if (!ok_) return;
     __atomic_store_n(&sq_->terminate, 0u, __ATOMIC_RELEASE);
@@ -330,6 +349,7 @@ void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int
     c.host_lists = sq_->list_alloc_idx - consumed_lists_;
     // Relative here (100 MHz ticks); the set-up kernel adds the GPU clock.
     c.deadline = (uint64_t)deadline_ms * 100000ull;
+    c.dev_ring = gpu_ring && gpu_ring == dev_ring_ ? (uint64_t)(uintptr_t)gpu_ring : 0;
     uint64_t trace_words = 0;
     if (trace_buf_) {
         c.trace = (uint64_t)(uintptr_t)trace_buf_;

@@ -6,8 +6,10 @@
 //
 // MI355X differences: allocation counters are device-scope atomics on
 // SGDeviceCounters in HBM (never atomics across PCIe into host memory);
-// entries and headers are written to the host-resident SGTaskQueue with plain
-// stores and committed with a system-scope release store of `sequence`;
+// entries and headers are written to an SGTaskQueue (the host-resident one,
+// or the session's HBM queue for a launch that sets
+// SGDeviceCounters::dev_ring; the caller passes the one it posts to) with
+// plain stores and committed with a system-scope release store of `sequence`;
 // waits are bounded (a poll count, and the launch's deadline when it has one)
 // and return false when they give up.
 //

@@ -103,7 +103,13 @@ struct SGDeviceCounters {
     // the sg:: submitter waits) gives up once it has passed, so a protocol
     // stall ends the kernel with an error bit instead of spinning.
     uint64_t deadline;
-    uint64_t _pad[7];
+    // Device address of an SGTaskQueue in HBM (0: none) holding the lists
+    // that this launch's GPU submitters post: ring indices from list_base +
+    // host_lists on.  Their headers and entries are then written and read in
+    // HBM, never across PCIe; the header's `done` marker is still raised in
+    // the host queue too, where host code and host submitters look for it.
+    uint64_t dev_ring;
+    uint64_t _pad[6];
 };
 
 // One list of a traced launch, in wall-clock ticks (100 MHz): when its

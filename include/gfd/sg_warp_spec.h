@@ -29,8 +29,13 @@
 // one.  The reference routes each list through descriptors and the CPU poller
 // instead; the DescriptorQueue argument is kept for the interface and unused.
 //
-// Waiting for commits: only the wave holding the lowest index whose commit no
-// wave has seen (SGDeviceCounters::list_known) reads host memory.  When its
+// Lists that a launch's GPU submitters post into the session's HBM queue
+// (SGDeviceCounters::dev_ring) are read there: each waiting wave polls its
+// own list's header in HBM, and no header or entry crosses PCIe.
+//
+// Waiting for commits in the host queue: only the wave holding the lowest
+// index whose commit no wave has seen (SGDeviceCounters::list_known) reads
+// host memory.  When its
 // list is committed it reads the next 64 sequences at once (one per lane) and
 // advances list_known past the committed run, releasing that many waiting
 // waves; the others poll list_known in HBM.  Idle waves thus put one read at
@@ -68,6 +73,7 @@ struct SGListView {
 };
 
 struct _SGSlot {
+    const SGTaskQueue* ring;  // where the list's entries are
     uint32_t list_id, count, pool_offset, flags;
     int seq;         // k + 1 once the k-th list of this slot is ready
     int free;        // 1 while the slot may be (re)filled
@@ -91,6 +97,13 @@ __device__ __forceinline__ uint64_t _idle_limit_ticks(const SGTaskQueue* sq) {
     return (uint64_t)(ms ? ms : 30000u) * 100000ull;  // 100 MHz wall clock
 }
 
+// Where ring index idx's header and entries are: the HBM queue of the
+// launch's GPU-submitted lists (SGDeviceCounters::dev_ring, from index
+// gpu_first on) or the host queue.
+__device__ __forceinline__ SGTaskQueue* _ring(SGTaskQueue* sq, SGTaskQueue* dev, uint64_t gpu_first, uint64_t idx) {
+    return dev && idx >= gpu_first ? dev : sq;
+}
+
 // _wait_committed's outcomes.
 enum : int { kSgStopped = 0, kSgCommitted = 1, kSgDeadline = 2 };
 
@@ -98,10 +111,34 @@ enum : int { kSgStopped = 0, kSgCommitted = 1, kSgDeadline = 2 };
 // terminate (or the idle limit) ends the wait with nothing committed;
 // kSgDeadline once the launch's deadline (0: none) has passed.
 __device__ __forceinline__ int _wait_committed(SGTaskQueue* sq, SGDeviceCounters* cnt, uint64_t idx,
-                                               uint64_t idle_ticks, uint64_t deadline) {
+                                               uint64_t idle_ticks, uint64_t deadline, SGTaskQueue* dev,
+                                               uint64_t gpu_first) {
     const int lane = wave::lane_id();
-    const SGList& mine = sq->lists[idx % MAX_SG_LISTS];
+    const SGList& mine = _ring(sq, dev, gpu_first, idx)->lists[idx % MAX_SG_LISTS];
     const uint64_t t0 = wall_clock64();
+    if (dev && idx >= gpu_first) {
+        // A GPU-submitted list in HBM: the wave polls its own header there
+        // (no host read per poll, so no leader is needed) with relaxed loads
+        // (an acquire per poll would invalidate the L2 each time) and one
+        // acquire once it is committed; the host queue's terminate is read
+        // only every 32nd poll, before the sequence, for the reason given for
+        // the leader below.
+        for (uint32_t n = 0;; n++) {
+            const uint32_t term = (n & 31) == 31 ? wave::load_system32(&sq->terminate) : 0u;
+            if (__hip_atomic_load(const_cast<uint64_t*>(&mine.sequence), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                idx + 1) {
+                wave::acquire_agent();  // the header and entries written before the commit
+                return kSgCommitted;
+            }
+            if (term || __hip_atomic_load(&cnt->stop, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                if (term && lane == 0) __hip_atomic_store(&cnt->stop, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return kSgStopped;
+            }
+            if (sg::past(deadline)) return kSgDeadline;
+            if (wall_clock64() - t0 > idle_ticks) return kSgStopped;
+            __builtin_amdgcn_s_sleep(8);
+        }
+    }
     for (;;) {
         const uint64_t known = __hip_atomic_load(&cnt->list_known, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (idx < known) {
@@ -123,7 +160,8 @@ __device__ __forceinline__ int _wait_committed(SGTaskQueue* sq, SGDeviceCounters
             if (wave::load_system(&mine.sequence) == idx + 1) {
                 // Find the committed run idx, idx+1, ... and publish it.
                 const uint64_t j = idx + (uint64_t)lane;
-                const bool c = wave::load_system(&sq->lists[j % MAX_SG_LISTS].sequence) == j + 1;
+                const bool c =
+                    wave::load_system(&_ring(sq, dev, gpu_first, j)->lists[j % MAX_SG_LISTS].sequence) == j + 1;
                 const uint64_t mask = __ballot(c);
                 const uint64_t run = (~mask == 0) ? 64 : (uint64_t)__builtin_ctzll(~mask);
                 // Release: the 64 sequence loads above (all lanes, one
@@ -171,6 +209,7 @@ constexpr int SG_MAX_HELPERS = 3;
 // leader publish the next one, so no helper ever reads a job's fields while
 // they change.
 struct _SGJob {
+    const SGTaskQueue* ring;  // where the list's entries are
     uint32_t pool_offset, count;
     int seq;           // k + 1 once the k-th job is published; -1: no more jobs
     int next_batch;    // batches claimed
@@ -179,15 +218,16 @@ struct _SGJob {
     unsigned long long bytes;
 };
 
-// Claim and copy batches of the current job (pool_offset, count); adds the
-// batches and bytes copied.  The caller passes the job's fields in registers:
-// wave 0 has them from the list header, a helper read them after every
-// lane's acquire of job->seq.  (Lanes 1..63 of wave 0 must not read them back
-// from LDS: lane 0's plain stores there are not ordered before other lanes'
-// loads, and the compiler does schedule such loads ahead of the stores.)
-__device__ __forceinline__ void _sg_copy_batches(_SGJob* job, const SGTaskQueue* sq, uint32_t pool_offset,
-                                                 uint32_t count, int unroll, wave::BatchLds* lds, int* nbatches_done,
-                                                 uint64_t* bytes) {
+// Claim and copy 64-entry batches of the current job (pool_offset, count);
+// adds the batches and bytes copied and returns the job's number of batches.
+// The caller passes the job's fields in registers: wave 0 has them from the
+// list header, a helper read them after every lane's acquire of job->seq.
+// (Lanes 1..63 of wave 0 must not read them back from LDS: lane 0's plain
+// stores there are not ordered before other lanes' loads, and the compiler
+// does schedule such loads ahead of the stores.)
+__device__ __forceinline__ int _sg_copy_batches(_SGJob* job, const SGTaskQueue* sq, uint32_t pool_offset,
+                                                uint32_t count, int unroll, wave::BatchLds* lds, int* nbatches_done,
+                                                uint64_t* bytes) {
     const int lane = wave::lane_id();
     const int nbatches = (int)((count + wave::kWidth - 1) / wave::kWidth);
     for (;;) {
@@ -207,6 +247,7 @@ __device__ __forceinline__ void _sg_copy_batches(_SGJob* job, const SGTaskQueue*
         *bytes += wave::copy_batch(unroll, md, ms, mn, nb, lds);
         (*nbatches_done)++;
     }
+    return nbatches;
 }
 
 template <typename ComputeFn>
@@ -257,6 +298,10 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             reinterpret_cast<SGTraceList*>(__hip_atomic_load(&cnt->trace, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
         const uint64_t trace_cap = __hip_atomic_load(&cnt->trace_cap, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const uint64_t list_base = __hip_atomic_load(&cnt->list_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        SGTaskQueue* const dev =
+            reinterpret_cast<SGTaskQueue*>(__hip_atomic_load(&cnt->dev_ring, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        const uint64_t gpu_first =
+            list_base + __hip_atomic_load(&cnt->host_lists, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         uint64_t nlists = 0;
         for (uint64_t iter = 0;; iter++) {
             const int s = (int)(iter & 1);
@@ -268,13 +313,14 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             uint64_t idx = 0;
             if (lane == 0) idx = sg::atomic_add_dev(&cnt->list_claim, 1);
             idx = wave::broadcast0(idx);
-            const int got = _wait_committed(sq, cnt, idx, idle_ticks, deadline);
+            const int got = _wait_committed(sq, cnt, idx, idle_ticks, deadline, dev, gpu_first);
             if (got != kSgCommitted) {
                 if (got == kSgDeadline && lane == 0)
                     __hip_atomic_fetch_or(&cnt->error, SG_ERR_DEADLINE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
-            SGList& l = sq->lists[idx % MAX_SG_LISTS];
+            SGTaskQueue* const ring = _ring(sq, dev, gpu_first, idx);
+            SGList& l = ring->lists[idx % MAX_SG_LISTS];
             const uint32_t pool_offset = l.pool_offset, count = l.count, list_id = l.list_id, flags = l.flags;
             if (lane == 0) wave::store_system(&l.sequence, 0);  // claimed
             const uint64_t t_ready = (uint64_t)wall_clock64();
@@ -282,6 +328,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             // Publish the copy job, copy batches with the helpers, wait for
             // every batch and every helper's acknowledgement.
             if (lane == 0) {
+                job.ring = ring;
                 job.pool_offset = pool_offset;
                 job.count = count;
                 job.next_batch = 0;
@@ -292,8 +339,8 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             }
             int mine = 0;
             uint64_t bytes = 0;
-            _sg_copy_batches(&job, sq, pool_offset, count, unroll, &batch_lds[0], &mine, &bytes);
-            const int nbatches = (int)((count + wave::kWidth - 1) / wave::kWidth);
+            const int nbatches =
+                _sg_copy_batches(&job, ring, pool_offset, count, unroll, &batch_lds[0], &mine, &bytes);
             if (lane == 0) {
                 __hip_atomic_fetch_add(&job.bytes, (unsigned long long)bytes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 wave::lds_add(&job.batches_done, mine);
@@ -316,7 +363,10 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
                 sg::atomic_add_dev(&cnt->bytes_done, bytes);
                 __hip_atomic_fetch_add(&cnt->lists_done, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
                 wave::store_system(&l.done, idx + 1);
+                // Host code and host submitters read the marker in the host queue.
+                if (ring != sq) wave::store_system(&sq->lists[idx % MAX_SG_LISTS].done, idx + 1);
                 if (has_compute) {
+                    slots[s].ring = ring;
                     slots[s].list_id = list_id;
                     slots[s].count = count;
                     slots[s].pool_offset = pool_offset;
@@ -356,8 +406,8 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             if (seq < 0) break;
             int mine = 0;
             uint64_t bytes = 0;
-            _sg_copy_batches(&job, sq, job.pool_offset, job.count, unroll, &batch_lds[1 + w - first_helper], &mine,
-                             &bytes);
+            _sg_copy_batches(&job, job.ring, job.pool_offset, job.count, unroll, &batch_lds[1 + w - first_helper],
+                             &mine, &bytes);
             wave::release_agent();  // this wave's stores are visible device-wide before it reports
             if (lane == 0) {
                 __hip_atomic_fetch_add(&job.bytes, (unsigned long long)bytes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -399,7 +449,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             view.flags = slots[s].flags;
             view.lane_id = lane;
             view.pool_offset = slots[s].pool_offset;
-            view.sq = sq;
+            view.sq = slots[s].ring;
             view.part = (uint32_t)(w - 1);
             view.parts = (uint32_t)ncompute;
             compute_fn(view);

@@ -227,6 +227,7 @@ public:
     Stats get_stats() const;
 
     bool ok() const { return ok_; }
+    bool running() const { return running_; }  // launched and not yet synchronized
     uint64_t error_bits() const { return error_bits_; }
     uint64_t lists_landed() const { return lists_done_; }  // during the last launch
     int num_blocks() const { return num_blocks_; }
@@ -240,7 +241,11 @@ public:
     // launch gives up that long after it starts (launches whose lists all
     // come from GPU submitters; see SGDeviceCounters::deadline).
     void before_launch(gfd_stream_t stream, int helper_waves = -1, int compute_waves = -1,
-                       uint32_t deadline_ms = 0);
+                       uint32_t deadline_ms = 0, SGTaskQueue* gpu_ring = nullptr);
+    // An SGTaskQueue in HBM for GPU-submitted lists (allocated on first call;
+    // nullptr if that fails).  A launch whose GPU submitters post there
+    // passes it to before_launch as gpu_ring (SGDeviceCounters::dev_ring).
+    SGTaskQueue* device_ring();
     // The idle limit in effect (idle_limit_ms, 0 meaning 30 s), which GPU
     // submitter launches also take as their deadline.
     uint32_t idle_limit_ms() const { return config_.idle_limit_ms ? config_.idle_limit_ms : 30000u; }
@@ -280,6 +285,7 @@ private:
 
     SGWarpSpecConfig config_;
     SGTaskQueue* sq_ = nullptr;
+    SGTaskQueue* dev_ring_ = nullptr;  // HBM: lists posted by GPU submitters
     DescriptorQueue* dq_ = nullptr;
     int num_blocks_ = 0;
     bool ok_ = false;
