@@ -79,6 +79,9 @@ struct TokenSum {
 struct TokenRmsSin {
     float* out;
     static constexpr int kRegVecs = 16;  // float4 per lane: 16 KiB per wave
+    // Each token's result depends on that token alone: the framework may
+    // hand a chunk's tokens to several compute waves in groups.
+    static constexpr bool kSplitsChunks = true;
 
     __device__ void operator()(ChunkView c) const {
         const uint32_t nf = c.token_size / 4;

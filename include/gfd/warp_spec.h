@@ -79,9 +79,92 @@ __device__ __forceinline__ TileDeviceCounters* tile_counters(TiledQueue* tq) {
 struct _TileSlot {
     uint32_t tile;  // TILE_END: no more tiles
     int seq;        // n + 1 once the n-th tile of this slot is assigned
-    int done;       // compute waves finished with the current tile
+    int done;       // chunks whose compute has finished for the current tile
     int chunk_done[MAX_CHUNKS_PER_TILE];  // pieces of chunk k already in HBM
+    // Functors with kSplitsChunks: chunk k's token groups, claimed as
+    // (epoch << 16 | next token) with epoch = the tile's seq (so a claim can
+    // never take a token of the slot's next tile), and tokens computed.
+    int claim[MAX_CHUNKS_PER_TILE];
+    int toks_done[MAX_CHUNKS_PER_TILE];
 };
+
+// A compute functor that declares `static constexpr bool kSplitsChunks =
+// true` processes every token on its own (its result for a token does not
+// depend on the chunk's other tokens).  Its chunks are then computed in
+// groups of tokens by any compute wave: a wave takes its own chunk, then
+// helps with the tile's other chunks as they land, and the compute waves of a
+// slot left without tiles help finish the other slot's last tile, so the
+// compute of a tile's last chunk is not left to one wave after the copy
+// ends.  The functor sees each group as a ChunkView of that group's tokens.
+// Functors without the declaration see each chunk once, on its own wave, as
+// with the reference.
+template <typename F, typename = void>
+struct _splits_chunks {
+    static constexpr bool value = false;
+};
+template <typename F>
+struct _splits_chunks<F, decltype((void)F::kSplitsChunks)> {
+    static constexpr bool value = F::kSplitsChunks;
+};
+
+// Wait until chunk k of the slot's tile at `epoch` has landed while some of
+// its tokens are still unclaimed: 1 (landed, after an acquire), 0 (nothing
+// left to claim there: all claimed, or the slot has moved past the epoch), or
+// -1 (the bounded wait gave up).
+__device__ __forceinline__ int _wait_claimable(_TileSlot& sl, int epoch, uint32_t k, uint32_t P, uint32_t C) {
+    for (uint64_t t = 0; t < wave::kSpinLimit; t++) {
+        const int c = wave::lds_load(&sl.claim[k]);
+        if ((c >> 16) != (epoch & 0x7FFF) || (uint32_t)(c & 0xFFFF) >= C) return 0;
+        if (wave::lds_load(&sl.chunk_done[k]) == (int)P) {
+            wave::acquire_agent();
+            return 1;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return -1;
+}
+
+// Claim and compute token groups (G tokens) of chunk k of `tile`, the tile of
+// slot `sl` at epoch `epoch` (its seq), until none is left.  The chunk must
+// have landed (the caller saw chunk_done[k] == P and made an acquire).  The
+// group that completes the chunk counts it in `done`.
+template <typename ComputeFn>
+__device__ __forceinline__ void _compute_groups(_TileSlot& sl, int epoch, uint32_t tile, uint32_t k, uint32_t T,
+                                                uint32_t C, uint32_t G, uint32_t token_size, void* gpu_buffer,
+                                                ComputeFn& compute_fn) {
+    const int lane = wave::lane_id();
+    for (;;) {
+        // The retry loop is wave-uniform and only the compare-and-swap is
+        // lane 0's: the functor then runs with every lane active.  (A retry
+        // loop inside lane 0's branch left the functor's cross-lane sums
+        // wrong on every group after a wave's first.)
+        const int w = __builtin_amdgcn_readfirstlane(wave::lds_load(&sl.claim[k]));
+        if ((w >> 16) != (epoch & 0x7FFF) || (uint32_t)(w & 0xFFFF) >= C) return;
+        bool won = false;
+        if (lane == 0) {
+            int expect = w;
+            won = __hip_atomic_compare_exchange_strong(&sl.claim[k], &expect, w + (int)G, __ATOMIC_ACQ_REL,
+                                                       __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        if (__ballot(won) == 0) continue;
+        const int got = w & 0xFFFF;
+        const uint32_t n = C - (uint32_t)got < G ? C - (uint32_t)got : G;
+        ChunkView v;
+        v.global_token_offset = tile * T + k * C + (uint32_t)got;
+        v.base_ptr = (char*)gpu_buffer + (uint64_t)v.global_token_offset * token_size;
+        v.token_size = token_size;
+        v.size = n;
+        v.tile_id = tile;
+        v.chunk_id = k;
+        v.lane_id = lane;
+        compute_fn(v);
+        if (lane == 0) {
+            const int before =
+                __hip_atomic_fetch_add(&sl.toks_done[k], (int)n, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if ((uint32_t)before + n == C) wave::lds_add(&sl.done, 1);
+        }
+    }
+}
 
 // The tile the transfer waves copy together: wave 0 publishes it, every
 // transfer wave claims its pieces, each helper acknowledges it (even with no
@@ -151,6 +234,10 @@ __device__ __forceinline__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, con
         slots[threadIdx.x].seq = 0;
         slots[threadIdx.x].done = (int)K;  // free
         slots[threadIdx.x].tile = 0;
+        for (int k = 0; k < MAX_CHUNKS_PER_TILE; k++) {
+            slots[threadIdx.x].claim[k] = (int)C;  // epoch 0: nothing to claim
+            slots[threadIdx.x].toks_done[k] = 0;
+        }
     }
     if (threadIdx.x == 0) job.seq = 0;
     __syncthreads();
@@ -178,10 +265,17 @@ __device__ __forceinline__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, con
             tile = wave::broadcast0(tile);
             const bool last = tile >= total_tiles;
             if (lane == 0) {
+                const int epoch = (int)(n / NSLOTS) + 1;
                 slots[s].tile = last ? TILE_END : (uint32_t)tile;
-                for (uint32_t k = 0; k < K; k++) slots[s].chunk_done[k] = 0;
+                for (uint32_t k = 0; k < K; k++) {
+                    slots[s].chunk_done[k] = 0;
+                    if (!last) {
+                        slots[s].claim[k] = (epoch & 0x7FFF) << 16;
+                        slots[s].toks_done[k] = 0;
+                    }
+                }
                 slots[s].done = 0;
-                wave::lds_store(&slots[s].seq, (int)(n / NSLOTS) + 1);
+                wave::lds_store(&slots[s].seq, epoch);
             }
             if (last) {
                 // Hand TILE_END to the other slot(s) as well, once they are free.
@@ -244,6 +338,52 @@ __device__ __forceinline__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, con
                 wave::lds_add(&job.acks, 1);
             }
             want = seq + 1;
+        }
+    } else if ((uint32_t)(w - 1) < NSLOTS * K && _splits_chunks<ComputeFn>::value) {
+        // ---------------- compute waves sharing the chunks: slot g, chunk k first
+        const int g = (int)((uint32_t)(w - 1) / K);
+        const uint32_t k = (uint32_t)(w - 1) % K;
+        uint32_t G = C / (NSLOTS * K);
+        G = G ? G : 1u;
+        for (int n = 1;; n++) {
+            if (!wave::wait_lds_eq(&slots[g].seq, n)) {
+                if (lane == 0) __hip_atomic_fetch_or(&cnt->error, WS_ERR_CHUNK_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            const uint32_t tile = slots[g].tile;
+            if (tile == TILE_END) {
+                // No more tiles for this slot: help with the other slot's
+                // tile while it is still the same one.
+                for (int o = 1; o < NSLOTS; o++) {
+                    _TileSlot& other = slots[(g + o) % NSLOTS];
+                    const int epoch = wave::lds_load(&other.seq);
+                    const uint32_t otile = other.tile;
+                    if (epoch == 0 || otile == TILE_END) continue;
+                    for (uint32_t i = 0; i < K; i++) {
+                        const uint32_t k2 = (k + i) % K;
+                        const int r = _wait_claimable(other, epoch, k2, P, C);
+                        if (r < 0) break;  // its own waves report a stall
+                        if (r > 0) _compute_groups(other, epoch, otile, k2, T, C, G, token_size, gpu_buffer, compute_fn);
+                    }
+                }
+                break;
+            }
+            // This wave's chunk, then the tile's later chunks as they land,
+            // then the earlier ones, each while tokens are left to claim (the
+            // slot is refilled only once all of the tile's chunks are done,
+            // so waiting here costs nothing).
+            bool ok = true;
+            for (uint32_t i = 0; i < K && ok; i++) {
+                const uint32_t k2 = (k + i) % K;
+                const int r = _wait_claimable(slots[g], n, k2, P, C);
+                if (r < 0) {
+                    if (lane == 0) __hip_atomic_fetch_or(&cnt->error, WS_ERR_CHUNK_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ok = false;
+                } else if (r > 0) {
+                    _compute_groups(slots[g], n, tile, k2, T, C, G, token_size, gpu_buffer, compute_fn);
+                }
+            }
+            if (!ok) break;
         }
     } else if ((uint32_t)(w - 1) < NSLOTS * K) {
         // ---------------- compute waves: slot g, chunk k

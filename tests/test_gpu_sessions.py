@@ -178,15 +178,21 @@ def rms_sin_reference(tokens):
     return terms.sum(axis=1), np.abs(terms).sum(axis=1)
 
 
-@pytest.mark.parametrize("total,ts,tile,chunk,db", [(256, 16384, 128, 32, False), (256, 16384, 128, 32, True),
-                                                    (200, 4100, 64, 16, False), (128, 256, 64, 16, True)])
-def test_warp_spec_rms_sin(total, ts, tile, chunk, db):
+@pytest.mark.parametrize("total,ts,tile,chunk,db,blocks", [(256, 16384, 128, 32, False, 0),
+                                                           (256, 16384, 128, 32, True, 0),
+                                                           (200, 4100, 64, 16, False, 0), (128, 256, 64, 16, True, 0),
+                                                           (1024, 4096, 64, 16, True, 3),
+                                                           (1000, 4096, 78, 26, False, 2)])
+def test_warp_spec_rms_sin(total, ts, tile, chunk, db, blocks):
     """The RMSNorm + sinf consumer of examples/07_warp_spec_simple.cu through
     WarpSpecSession: every landed token's bytes, and out[t] within fp32
     rounding of a float64 restatement (tolerance 1e-4 of the sum of the
     terms' magnitudes).  Tokens past the last whole tile are not moved and
-    their out slots stay untouched."""
-    log("warp spec rms+sin total=%d ts=%d tile=%d chunk=%d db=%d" % (total, ts, tile, chunk, db))
+    their out slots stay untouched.  The consumer lets the framework share a
+    chunk's tokens between compute waves (kSplitsChunks); few workgroups
+    give each several tiles, so both slots' waves share chunks in steady
+    state and at the end, with chunks that do not split evenly into groups."""
+    log("warp spec rms+sin total=%d ts=%d tile=%d chunk=%d db=%d blocks=%d" % (total, ts, tile, chunk, db, blocks))
     nf = ts // 4
     host = gfd_amd.HostBuffer(total * ts)
     host.array.view(np.float32)[:] = np.random.default_rng(ts + total).standard_normal(total * nf).astype(np.float32)
@@ -194,7 +200,7 @@ def test_warp_spec_rms_sin(total, ts, tile, chunk, db):
     dst.fill(0)
     out = gfd_amd.DeviceBuffer(total * 4)
     out.fill(0xCD)
-    res, _ = gfd_amd.warp_spec_run_rms_sin(host.ptr, dst.ptr, total, ts, out.ptr, tile, chunk, db)
+    res, _ = gfd_amd.warp_spec_run_rms_sin(host.ptr, dst.ptr, total, ts, out.ptr, tile, chunk, db, num_blocks=blocks)
     moved = (total // tile) * tile
     assert res["error_bits"] == 0 and res["units_done"] == moved
     assert (dst.download()[:moved * ts] == host.array[:moved * ts]).all()
