@@ -306,8 +306,6 @@ void record_chunk(void* p, int chunk, size_t, size_t) {
     c->n++;
 }
 
-void no_chunk_report(void*, int, size_t, size_t) {}
-
 }  // namespace
 
 int gfd_host_gather(const gfd_sg_entry* entries, int count, void* out, uint64_t chunk_bytes,
@@ -369,7 +367,7 @@ int gfd_bench_host_gather(const gfd_sg_entry* const* lists, int nlists, int coun
         const int k = (it + warmup) % nlists;
         const auto t0 = std::chrono::steady_clock::now();
         engine.run(reinterpret_cast<const gfd::SGEntry*>(lists[k]), count, scans[(size_t)k].total, (char*)out,
-                   chunk_bytes, no_chunk_report, nullptr);
+                   chunk_bytes, nullptr, nullptr);
         const auto t1 = std::chrono::steady_clock::now();
         if (it >= 0) times_us[it] = std::chrono::duration<double, std::micro>(t1 - t0).count();
     }

@@ -48,8 +48,6 @@ void direct_chunk(void* p, int chunk, size_t off, size_t len) {
 constexpr size_t kContiguousSplitMin = 8u << 20;  // split one contiguous copy above this
 constexpr int kZcNotTaken = INT_MIN;               // direct_zero_copy: the list does not qualify
 
-void no_chunk(void*, int, size_t, size_t) {}
-
 }  // namespace
 
 // The zero-copy SG kernel (and the zero-copy worker) gives each entry of a
@@ -376,7 +374,7 @@ int CpuPollingThread::direct_scattered(const SGEntry* entries, int count, size_t
         if (!direct_staging_ || total > direct_staging_size_ || !gather_) return -1;
         {
             std::lock_guard<std::mutex> lock(gather_mutex_);
-            gather_->run(entries, count, total, direct_staging_, direct_chunk_bytes_, no_chunk, nullptr,
+            gather_->run(entries, count, total, direct_staging_, direct_chunk_bytes_, nullptr, nullptr,
                          uniform ? 1 : 0);
         }
         size_t off = 0;

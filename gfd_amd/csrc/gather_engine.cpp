@@ -160,7 +160,7 @@ void GatherEngine::worker_main(int w, int cpu) {
         if (g != seen) {
             seen = g;
             mb.in_job.store(1, std::memory_order_seq_cst);
-            if (open_.load(std::memory_order_seq_cst) && running_.load(std::memory_order_relaxed)) do_job();
+            if (open_.load(std::memory_order_seq_cst) && running_.load(std::memory_order_relaxed)) do_job(w);
             mb.in_job.store(0, std::memory_order_seq_cst);
             continue;
         }
@@ -247,9 +247,33 @@ void GatherEngine::copy_slice(const Slice& s) {
     }
 }
 
-void GatherEngine::do_job() {
+void GatherEngine::do_job(int w) {
     if (scan_job_) do_scan_parts();
+    else if (whole_) do_whole(w + 1, false);
     else do_slices();
+}
+
+// Whole-list job: slice s is claimed once (the thread of the static split
+// that owns it, or any thread that finds it unclaimed) and marked done.
+bool GatherEngine::take_whole_slice(int s) {
+    SliceFlag& f = slice_flag_[s];
+    const uint32_t job = job_epoch_;
+    if (f.claimed.load(std::memory_order_relaxed) == job || f.claimed.exchange(job, std::memory_order_acq_rel) == job)
+        return false;
+    copy_slice(slice_at(s));
+    store_fence();
+    f.done.store(job, std::memory_order_release);
+    return true;
+}
+
+// A thread's own slice of the static split (slice `first`: the caller has 0,
+// worker w has w + 1); with `any` (the caller), then every slice nobody has
+// claimed, so a worker that is late or asleep leaves its share to the caller.
+void GatherEngine::do_whole(int first, bool any) {
+    const int ns = num_slices_;
+    if (first < ns) take_whole_slice(first);
+    if (any)
+        for (int s = 0; s < ns; s++) take_whole_slice(s);
 }
 
 // Scan job: claim parts of kScanPartEntries entries; part k checks the pairs
@@ -367,7 +391,11 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
                        size_t chunk_bytes, ChunkFn on_chunk, void* ctx, int uniform_hint) {
     if (count <= 0 || total == 0) return;
     times_.entry = mono_ns();
-    if (chunk_bytes == 0 || chunk_bytes > total) chunk_bytes = total;
+    // No copy to pipeline: one chunk of num_workers() + 1 equal slices, the
+    // static split of the reference's parallel_gather, claimed so that a
+    // worker that is late or asleep leaves its share to the others.
+    const bool whole = on_chunk == nullptr;
+    if (whole || chunk_bytes == 0 || chunk_bytes > total) chunk_bytes = total;
     // Workers still inside the previous job must leave before its state changes.
     wait_workers_out();
     times_.idle = mono_ns();
@@ -381,7 +409,7 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     // the link drains).
     size_t first = first_chunk_bytes_ ? first_chunk_bytes_ : chunk_bytes / 8;
     if (first < 64 * 1024) first = 64 * 1024;
-    if (first > chunk_bytes) first = chunk_bytes;
+    if (first > chunk_bytes || whole) first = chunk_bytes;
 
     chunk_end_.clear();
     size_t size = first;
@@ -409,7 +437,8 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     const size_t threads = (size_t)num_workers() + 1;
     const size_t job_slice = std::max<size_t>(
         16 * 1024, std::min(slice_bytes_, ((total / (2 * threads)) + 4095) & ~(size_t)4095));
-    const size_t first_slice = std::max<size_t>(16 * 1024, std::min(job_slice, chunk_end_[0] / 16));
+    const size_t first_slice = whole ? (((total + threads - 1) / threads) + 63) & ~(size_t)63
+                                     : std::max<size_t>(16 * 1024, std::min(job_slice, chunk_end_[0] / 16));
     if (remaining_cap_ < nchunks) {
         remaining_.reset(new std::atomic<int>[nchunks]);
         remaining_cap_ = nchunks;
@@ -467,12 +496,19 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
         nslices = (int)slices_.size();
     }
 
+    if (whole && slice_flag_cap_ < nslices) {
+        slice_flag_.reset(new SliceFlag[nslices]);
+        slice_flag_cap_ = nslices;
+    }
+    // The number publish() gives this job (only this thread bumps epoch_).
+    job_epoch_ = epoch_.load(std::memory_order_relaxed) + 1;
     entries_ = entries;
     count_ = count;
     staging_ = staging;
     num_slices_ = nslices;
     next_slice_.store(0, std::memory_order_relaxed);
     scan_job_ = false;
+    whole_ = whole;
 
     // The caller copies slices too: workers are helpers (one that is asleep
     // or late sits the job out), so the caller alone can always finish it.
@@ -488,6 +524,16 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     times_.published = mono_ns();
     bool counted = false;
 
+    if (whole) {
+        // Slice 0, then any slice left unclaimed; then wait for the rest.
+        do_whole(0, true);
+        for (int i = 0; i < ns; i++)
+            while (slice_flag_[i].done.load(std::memory_order_acquire) != job_epoch_) cpu_relax();
+        open_.store(false, std::memory_order_seq_cst);
+        times_.first_slice = 0;
+        times_.copiers = 0;
+        return;
+    }
     int ready = 0;
     while (ready < nchunks) {
         if (remaining_[ready].load(std::memory_order_acquire) == 0) {

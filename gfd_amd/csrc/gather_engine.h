@@ -77,7 +77,10 @@ public:
     // [0, total) is cut into chunks (a short first chunk, then chunk_bytes
     // each); on_chunk(ctx, c, off, len) is called on the calling thread, in
     // chunk order, once chunk c's bytes are written and fenced.  Returns as
-    // soon as every chunk has been handed to on_chunk.  Not reentrant: one
+    // soon as every chunk has been handed to on_chunk.  A null on_chunk (no
+    // copy to pipeline) gathers the whole list as one chunk split into
+    // num_workers() + 1 equal slices, the reference's static split, and
+    // returns once every byte is written and fenced.  Not reentrant: one
     // caller at a time.
     // uniform_hint: 1 = every entry has the same size (slices are placed by
     // division), 0 = not, -1 = check.
@@ -93,8 +96,10 @@ private:
         int chunk;
     };
     void worker_main(int w, int cpu);
-    void do_job();
+    void do_job(int w);
     void do_slices();
+    void do_whole(int first, bool any);
+    bool take_whole_slice(int s);
     void do_scan_parts();
     void copy_slice(const Slice& s);
     void note_slice(bool& counted);
@@ -138,6 +143,18 @@ private:
     std::vector<size_t> chunk_slice_;  // slice length inside each chunk
     std::unique_ptr<std::atomic<int>[]> remaining_;
     int remaining_cap_ = 0;
+    // Whole-list jobs (no chunk callback): slice s is claimed and reported
+    // done on a cache line of its own, so the threads of a static split never
+    // meet on one contended counter.  Both words hold the number of the job
+    // that last claimed / finished the slice, so no job has to clear them.
+    bool whole_ = false;
+    uint32_t job_epoch_ = 0;
+    struct alignas(64) SliceFlag {
+        std::atomic<uint32_t> claimed{0};
+        std::atomic<uint32_t> done{0};
+    };
+    std::unique_ptr<SliceFlag[]> slice_flag_;
+    int slice_flag_cap_ = 0;
 
     // scan job
     struct ScanPart {
