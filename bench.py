@@ -535,6 +535,36 @@ def run_worker_direct(oracle, iters, warmup):
         out["worker"] = p.zero_copy_worker_stats()
     finally:
         p.close()
+    out["device_timeline"] = worker_device_timeline(oracle, iters)
+    return out
+
+
+def worker_device_timeline(oracle, calls):
+    """The worker's own per-job timeline (GFD_ZC_WORKER_TRACE=1, a poller of
+    its own; untimed): median us, after the last workgroup found the job, at
+    which the last one held its records, the last one had copied its share
+    and the last progress word was stored."""
+    os.environ["GFD_ZC_WORKER_TRACE"] = "1"
+    p = gfd_amd.CpuPollingThread(None, None, None, 16 << 20, numa_node=-1)
+    out = {}
+    try:
+        assert p.init_direct_ce(), "init_direct_ce failed"
+        p.set_zero_copy_worker(True)
+        for n, t in ((16, 4096), (64, 4096), (2048, 512), (2048, 2048)):
+            L = Layout(oracle, n, t)
+            for _ in range(max(calls, 40)):
+                assert p.submit_direct(L.entries, L.n) > 0
+            L.verify("direct through the traced worker %d x %d" % (n, t))
+            tl = p.zero_copy_worker_timeline(40).astype(np.int64)
+            rel = (tl[:, :6] - tl[:, :1]) / 100.0  # 100 MHz ticks -> us
+            m = np.median(rel, axis=0)
+            out["%dx%d" % (n, t)] = {"records_us": round(float(m[1]), 2), "copied_us": round(float(m[3]), 2),
+                                     "progress_us": round(float(m[5]), 2), "jobs": int(len(tl))}
+            log("  worker device timeline %dx%d: %s" % (n, t, out["%dx%d" % (n, t)]))
+            del L
+    finally:
+        p.close()
+        os.environ.pop("GFD_ZC_WORKER_TRACE", None)
     return out
 
 

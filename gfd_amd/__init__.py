@@ -102,7 +102,7 @@ COPY_TIME_DTYPE = np.dtype([("seq", np.uint64), ("bytes", np.uint64), ("start_ns
 TRACE_DTYPE = np.dtype([("t_ns", np.uint64), ("kind", np.uint32), ("a", np.uint32), ("b", np.uint64)])
 TRACE_KINDS = {1: "batch_first", 2: "flush", 3: "issued", 4: "done", 5: "gap_flush", 6: "direct_begin",
                7: "chunk", 8: "direct_end", 9: "gather_entry", 10: "gather_idle", 11: "gather_published",
-               12: "gather_first_slice", 13: "gather_built"}
+               12: "gather_first_slice", 13: "gather_built", 14: "zc_launch", 15: "zc_done", 16: "zc_checked"}
 
 _lib = None
 _SIGNATURES = {}
@@ -458,9 +458,11 @@ class CpuPollingThread:
 
     def zero_copy_worker_timeline(self, max_jobs=64):
         """The worker's device timeline of its latest jobs, newest first: an
-        (n, 8) uint64 array on the GPU's 100 MHz wall clock (doorbell seen, job
-        seen by the last workgroup, first / last wave with its records, last
-        wave done copying, done raised, doorbell value, unused)."""
+        (n, 8) uint64 array on the GPU's 100 MHz wall clock (the last
+        workgroup to find the job, the last to hold it and its records,
+        unused, the last done copying, unused, the last progress word stored,
+        the job number, unused).  Empty unless GFD_ZC_WORKER_TRACE=1 was set
+        when the worker started."""
         out = np.zeros((max_jobs, 8), np.uint64)
         n = lib().gfd_poller_zero_copy_worker_timeline(self._h, out.ctypes.data, max_jobs)
         return out[:n]

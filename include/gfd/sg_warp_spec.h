@@ -449,7 +449,9 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             view.flags = slots[s].flags;
             view.lane_id = lane;
             view.pool_offset = slots[s].pool_offset;
-            view.sq = slots[s].ring;
+            // Uniform across the wave: kept in scalar registers.
+            view.sq = reinterpret_cast<const SGTaskQueue*>(
+                wave::readlane64((uint64_t)(uintptr_t)slots[s].ring, 0));
             view.part = (uint32_t)(w - 1);
             view.parts = (uint32_t)ncompute;
             compute_fn(view);

@@ -159,15 +159,16 @@ uint64_t gfd_poller_set_direct_zero_copy_head_bytes(gfd_poller_t p, uint64_t byt
  * it; 0 removes it.  Returns 0 or an error.  Not while the polling thread
  * runs. */
 int gfd_poller_set_zero_copy_worker(gfd_poller_t p, int on);
-/* Jobs the worker has run and grids dispatched for them (both 0 while off). */
+/* Jobs posted to the worker and grids dispatched for them (both 0 while off). */
 int gfd_poller_zero_copy_worker_stats(gfd_poller_t p, uint64_t* jobs, uint64_t* launches);
 /* Returns the previous limit. */
 uint64_t gfd_poller_set_worker_queue_max_bytes(gfd_poller_t p, uint64_t bytes);
 /* The worker's device timeline of its latest jobs, newest first: up to
- * max_jobs records of 8 words on the GPU's 100 MHz wall clock (doorbell seen,
- * job seen by the last workgroup, first and last wave with its records, last
- * wave done copying, done raised, the job's doorbell value, unused).  Returns
- * the number of records (0 while the worker is off). */
+ * max_jobs records of 8 words on the GPU's 100 MHz wall clock (the last
+ * workgroup to find the job, the last to hold it and its records, unused, the
+ * last done copying, unused, the last progress word stored, the job number,
+ * unused).  Returns the number of records (0 while the worker is off, or when
+ * GFD_ZC_WORKER_TRACE=1 was not set as it started). */
 int gfd_poller_zero_copy_worker_timeline(gfd_poller_t p, uint64_t* out, int max_jobs);
 void gfd_poller_set_gather_slice_bytes(gfd_poller_t p, uint64_t bytes);
 
