@@ -129,7 +129,8 @@ GatherEngine::~GatherEngine() {
 // flag and then checks open_; the caller rebuilds job state only after every
 // in_job flag is down.  With sequentially consistent operations on open_ and
 // the flags, a worker either is seen inside (and the caller waits for it) or
-// sees open_ cleared and leaves without touching the job.
+// sees open_ cleared and leaves without touching the job.  (Whole-list jobs
+// keep their state in the mailboxes and do not come through here.)
 void GatherEngine::publish() {
     open_.store(true, std::memory_order_seq_cst);
     const uint32_t e = epoch_.fetch_add(1, std::memory_order_seq_cst) + 1;
@@ -159,6 +160,10 @@ void GatherEngine::worker_main(int w, int cpu) {
         const uint32_t g = mb.go.load(std::memory_order_acquire);
         if (g != seen) {
             seen = g;
+            if (mb.tag.load(std::memory_order_relaxed) == g) {  // a whole-list slice of job g
+                take_mailbox_slice(mb, g, prefetch_bytes_);
+                continue;
+            }
             mb.in_job.store(1, std::memory_order_seq_cst);
             if (open_.load(std::memory_order_seq_cst) && running_.load(std::memory_order_relaxed)) do_job(w);
             mb.in_job.store(0, std::memory_order_seq_cst);
@@ -175,9 +180,11 @@ void GatherEngine::worker_main(int w, int cpu) {
             if ((i & 255) == 0 && mono_ns() >= t_end) break;
         }
         if (moved) continue;
-        // Dekker handshake with publish(): either the caller sees sleepers_ > 0
-        // and wakes us after bumping epoch_, or we see the new job here and
-        // do not sleep.  futex_wait returns at once if epoch_ has moved on.
+        // Dekker handshake with publish() and run_whole() (each stores go,
+        // then bumps epoch_ with a full fence, then reads sleepers_): either
+        // the caller sees sleepers_ > 0 and wakes us after the bump, or we see
+        // the new job here and do not sleep.  futex_wait returns at once if
+        // epoch_ has moved on.
         sleepers_.fetch_add(1, std::memory_order_seq_cst);
         const uint32_t e = epoch_.load(std::memory_order_seq_cst);
         if (mb.go.load(std::memory_order_seq_cst) == seen && running_.load(std::memory_order_seq_cst))
@@ -191,17 +198,17 @@ void GatherEngine::prewake() {
     if (sleepers_.load(std::memory_order_seq_cst) > 0) futex_wake_all(&epoch_);
 }
 
-void GatherEngine::copy_slice(const Slice& s) {
-    size_t left = s.len;
-    int e = s.entry;
-    size_t eo = s.entry_off;
-    char* d = staging_ + s.off;
+namespace {
+
+// Copy `left` bytes of the list, starting at byte eo of entry e, to d.
+void copy_span(const SGEntry* entries_, int count_, int e, size_t eo, char* d, size_t left,
+               size_t prefetch_bytes) {
     // Source prefetch runs kPrefetchAhead bytes of this slice ahead of the
     // copy, every line of each token it passes (scattered small tokens miss
     // in cache on every line; one line per token left 512 B tokens latency
     // bound).  Tokens longer than kPrefetchLines lines get their first lines
     // only: the hardware stream prefetcher covers the rest.
-    const size_t kPrefetchAhead = prefetch_bytes_;
+    const size_t kPrefetchAhead = prefetch_bytes;
     constexpr size_t kPrefetchLines = 16;
     if (kPrefetchAhead == 0) {  // one line of the token four entries ahead
         while (left) {
@@ -247,33 +254,29 @@ void GatherEngine::copy_slice(const Slice& s) {
     }
 }
 
+}  // namespace
+
+void GatherEngine::copy_slice(const Slice& s) {
+    copy_span(entries_, count_, s.entry, s.entry_off, staging_ + s.off, s.len, prefetch_bytes_);
+}
+
 void GatherEngine::do_job(int w) {
     if (scan_job_) do_scan_parts();
-    else if (whole_) do_whole(w + 1, false);
     else do_slices();
 }
 
-// Whole-list job: slice s is claimed once (the thread of the static split
-// that owns it, or any thread that finds it unclaimed) and marked done.
-bool GatherEngine::take_whole_slice(int s) {
-    SliceFlag& f = slice_flag_[s];
-    const uint32_t job = job_epoch_;
-    if (f.claimed.load(std::memory_order_relaxed) == job || f.claimed.exchange(job, std::memory_order_acq_rel) == job)
-        return false;
-    copy_slice(slice_at(s));
+// Whole-list job: take the slice described in mb if job `job` is still open
+// there (nobody has claimed it for this job), copy it and mark it done.
+bool GatherEngine::take_mailbox_slice(Mailbox& mb, uint32_t job, size_t prefetch_bytes) {
+    uint32_t c = mb.claimed.load(std::memory_order_relaxed);
+    for (;;) {
+        if ((int32_t)(job - c) <= 0) return false;  // taken for this job (or a later one)
+        if (mb.claimed.compare_exchange_weak(c, job, std::memory_order_acq_rel, std::memory_order_relaxed)) break;
+    }
+    copy_span(mb.entries, mb.count, mb.entry, mb.entry_off, mb.dst, mb.len, prefetch_bytes);
     store_fence();
-    f.done.store(job, std::memory_order_release);
+    mb.done.store(job, std::memory_order_release);
     return true;
-}
-
-// A thread's own slice of the static split (slice `first`: the caller has 0,
-// worker w has w + 1); with `any` (the caller), then every slice nobody has
-// claimed, so a worker that is late or asleep leaves its share to the caller.
-void GatherEngine::do_whole(int first, bool any) {
-    const int ns = num_slices_;
-    if (first < ns) take_whole_slice(first);
-    if (any)
-        for (int s = 0; s < ns; s++) take_whole_slice(s);
 }
 
 // Scan job: claim parts of kScanPartEntries entries; part k checks the pairs
@@ -390,12 +393,12 @@ void GatherEngine::note_slice(bool& counted) {
 void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* staging,
                        size_t chunk_bytes, ChunkFn on_chunk, void* ctx, int uniform_hint) {
     if (count <= 0 || total == 0) return;
+    if (on_chunk == nullptr) {
+        run_whole(entries, count, total, staging, uniform_hint);
+        return;
+    }
     times_.entry = mono_ns();
-    // No copy to pipeline: one chunk of num_workers() + 1 equal slices, the
-    // static split of the reference's parallel_gather, claimed so that a
-    // worker that is late or asleep leaves its share to the others.
-    const bool whole = on_chunk == nullptr;
-    if (whole || chunk_bytes == 0 || chunk_bytes > total) chunk_bytes = total;
+    if (chunk_bytes == 0 || chunk_bytes > total) chunk_bytes = total;
     // Workers still inside the previous job must leave before its state changes.
     wait_workers_out();
     times_.idle = mono_ns();
@@ -409,7 +412,7 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     // the link drains).
     size_t first = first_chunk_bytes_ ? first_chunk_bytes_ : chunk_bytes / 8;
     if (first < 64 * 1024) first = 64 * 1024;
-    if (first > chunk_bytes || whole) first = chunk_bytes;
+    if (first > chunk_bytes) first = chunk_bytes;
 
     chunk_end_.clear();
     size_t size = first;
@@ -437,8 +440,7 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     const size_t threads = (size_t)num_workers() + 1;
     const size_t job_slice = std::max<size_t>(
         16 * 1024, std::min(slice_bytes_, ((total / (2 * threads)) + 4095) & ~(size_t)4095));
-    const size_t first_slice = whole ? (((total + threads - 1) / threads) + 63) & ~(size_t)63
-                                     : std::max<size_t>(16 * 1024, std::min(job_slice, chunk_end_[0] / 16));
+    const size_t first_slice = std::max<size_t>(16 * 1024, std::min(job_slice, chunk_end_[0] / 16));
     if (remaining_cap_ < nchunks) {
         remaining_.reset(new std::atomic<int>[nchunks]);
         remaining_cap_ = nchunks;
@@ -496,19 +498,12 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
         nslices = (int)slices_.size();
     }
 
-    if (whole && slice_flag_cap_ < nslices) {
-        slice_flag_.reset(new SliceFlag[nslices]);
-        slice_flag_cap_ = nslices;
-    }
-    // The number publish() gives this job (only this thread bumps epoch_).
-    job_epoch_ = epoch_.load(std::memory_order_relaxed) + 1;
     entries_ = entries;
     count_ = count;
     staging_ = staging;
     num_slices_ = nslices;
     next_slice_.store(0, std::memory_order_relaxed);
     scan_job_ = false;
-    whole_ = whole;
 
     // The caller copies slices too: workers are helpers (one that is asleep
     // or late sits the job out), so the caller alone can always finish it.
@@ -524,16 +519,6 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     times_.published = mono_ns();
     bool counted = false;
 
-    if (whole) {
-        // Slice 0, then any slice left unclaimed; then wait for the rest.
-        do_whole(0, true);
-        for (int i = 0; i < ns; i++)
-            while (slice_flag_[i].done.load(std::memory_order_acquire) != job_epoch_) cpu_relax();
-        open_.store(false, std::memory_order_seq_cst);
-        times_.first_slice = 0;
-        times_.copiers = 0;
-        return;
-    }
     int ready = 0;
     while (ready < nchunks) {
         if (remaining_[ready].load(std::memory_order_acquire) == 0) {
@@ -563,6 +548,91 @@ void GatherEngine::run(const SGEntry* entries, int count, size_t total, char* st
     open_.store(false, std::memory_order_seq_cst);
     times_.first_slice = first_slice_ns_.load(std::memory_order_relaxed);
     times_.copiers = copiers_.load(std::memory_order_relaxed);
+}
+
+// No copy to pipeline: num_workers() + 1 equal slices of 64-byte multiples,
+// the static split of the reference's parallel_gather
+// (src/parallel_gather.cpp:90-116), the caller's first.  Each worker finds
+// its slice in its mailbox; the caller copies its own, takes any slice whose
+// worker has not claimed it yet (a worker that is late or asleep leaves its
+// share to the caller) and returns once every slice is written and fenced.
+void GatherEngine::run_whole(const SGEntry* entries, int count, size_t total, char* staging, int uniform_hint) {
+    const int nw = num_workers();
+    const size_t threads = (size_t)nw + 1;
+    const size_t slice = (((total + threads - 1) / threads) + 63) & ~(size_t)63;
+    const int ns = (int)((total + slice - 1) / slice);  // at most threads
+    const size_t esz = entries[0].size;
+    bool uniform = uniform_hint > 0;
+    if (uniform_hint < 0) {
+        uniform = true;
+        for (int i = 1; i < count && uniform; i++) uniform = entries[i].size == esz;
+    }
+    uniform = uniform && esz > 0;
+    // Only this thread bumps epoch_ (after its own slice, below).
+    const uint32_t job = epoch_.load(std::memory_order_relaxed) + 1;
+    // (e, eo): the list position of byte pos.  Uniform lists step by whole
+    // slices (a slice is q entries and r bytes); ragged ones walk the sizes.
+    int e = 0;
+    size_t eo = 0, pos = 0;
+    const size_t q = uniform ? slice / esz : 0, r = uniform ? slice % esz : 0;
+    for (int s = 1; s < ns; s++) {
+        const size_t off = (size_t)s * slice;
+        if (uniform) {
+            e += (int)q;
+            eo += r;
+            if (eo >= esz) {
+                eo -= esz;
+                e++;
+            }
+        } else {
+            while (pos < off) {
+                const size_t adv = std::min(entries[e].size - eo, off - pos);
+                eo += adv;
+                pos += adv;
+                if (eo == entries[e].size) {
+                    e++;
+                    eo = 0;
+                }
+            }
+            while (e < count && eo == entries[e].size) {  // skip empty entries
+                e++;
+                eo = 0;
+            }
+        }
+        // Fields, tag and go share the line: the worker can start on it as
+        // soon as this line reaches it, while the next ones are written.
+        Mailbox& mb = mail_[s - 1];
+        mb.entries = entries;
+        mb.count = count;
+        mb.entry = e;
+        mb.entry_off = eo;
+        mb.dst = staging + off;
+        mb.len = std::min(slice, total - off);
+        mb.tag.store(job, std::memory_order_relaxed);
+        mb.go.store(job, std::memory_order_release);
+    }
+    for (int w = ns - 1; w < nw; w++) mail_[w].go.store(job, std::memory_order_release);
+    // Sleeping workers are woken now if there are any, so they can still
+    // help; otherwise the job counter is bumped after the caller's slice,
+    // where the full fence it implies (the other half of the handshake with a
+    // worker about to sleep) no longer holds back the caller's first copy.
+    // A worker that falls asleep in between is woken then, and its slice is
+    // the caller's to take.
+    bool bumped = false;
+    if (sleepers_.load(std::memory_order_relaxed) > 0) {
+        epoch_.fetch_add(1, std::memory_order_seq_cst);
+        bumped = true;
+        if (mono_ns() - last_prewake_ns_.load(std::memory_order_relaxed) > 200000ull) futex_wake_all(&epoch_);
+    }
+    copy_span(entries, count, 0, 0, staging, std::min(slice, total), prefetch_bytes_);
+    store_fence();
+    if (!bumped) {
+        epoch_.fetch_add(1, std::memory_order_seq_cst);
+        if (sleepers_.load(std::memory_order_seq_cst) > 0) futex_wake_all(&epoch_);
+    }
+    for (int s = 1; s < ns; s++) take_mailbox_slice(mail_[s - 1], job, prefetch_bytes_);
+    for (int s = 1; s < ns; s++)
+        while (mail_[s - 1].done.load(std::memory_order_acquire) != job) cpu_relax();
 }
 
 }  // namespace gfd

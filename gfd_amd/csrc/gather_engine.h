@@ -60,9 +60,10 @@ public:
     ListScan scan(const SGEntry* entries, int count);
     static constexpr int kCallerScanMax = 4096;
 
-    // CLOCK_MONOTONIC ns of the last run(): entry, after the wait for the
-    // previous job's workers, job published, first slice finished (by any
-    // thread), and number of threads that copied at least one slice.
+    // CLOCK_MONOTONIC ns of the last run() with a chunk callback: entry, after
+    // the wait for the previous job's workers, job published, first slice
+    // finished (by any thread), and number of threads that copied at least
+    // one slice.  Whole-list runs (no callback) leave them as they were.
     struct RunTimes {
         uint64_t entry, idle, built, published, first_slice;
         int copiers, sleepers;
@@ -98,8 +99,9 @@ private:
     void worker_main(int w, int cpu);
     void do_job(int w);
     void do_slices();
-    void do_whole(int first, bool any);
-    bool take_whole_slice(int s);
+    struct Mailbox;
+    void run_whole(const SGEntry* entries, int count, size_t total, char* staging, int uniform_hint);
+    static bool take_mailbox_slice(Mailbox& mb, uint32_t job, size_t prefetch_bytes);
     void do_scan_parts();
     void copy_slice(const Slice& s);
     void note_slice(bool& counted);
@@ -114,9 +116,30 @@ private:
     // it to join, and whether it is inside a job.  Each line has two users
     // (the caller and that worker), so publishing a job and joining it cost
     // one line transfer per worker, not a queue of them on one shared line.
+    //
+    // A whole-list job (no chunk callback) also describes the worker's slice
+    // in the line: tag is the job the fields belong to (written before go),
+    // claimed the last job whose slice someone took, done the last job whose
+    // slice is written and fenced.  The worker reads go, finds tag equal to it
+    // and claims the slice with one compare-exchange on claimed; the caller
+    // can always finish the job alone, taking any slice still unclaimed.  A
+    // slice is claimed only while its job is open (claimed older than the
+    // job), and the job stays open until that slice is done, so the fields a
+    // claimer reads are never rewritten under it.  Such a job touches no
+    // other shared job state, so it needs neither open_ nor in_job: workers
+    // still leaving an earlier chunked job see none of it change.
     struct alignas(64) Mailbox {
         std::atomic<uint32_t> go{0};
         std::atomic<uint32_t> in_job{0};
+        std::atomic<uint32_t> tag{0};
+        std::atomic<uint32_t> claimed{0};
+        std::atomic<uint32_t> done{0};
+        int entry = 0;                     // entry holding the slice's first byte
+        const SGEntry* entries = nullptr;  // the list
+        char* dst = nullptr;               // staging address of the slice
+        size_t entry_off = 0;              // offset of that byte inside the entry
+        size_t len = 0;                    // slice bytes
+        int count = 0;                     // list entries
     };
     std::unique_ptr<Mailbox[]> mail_;
     // Job counter; 32-bit so idle workers can sleep on it with a futex.
@@ -143,18 +166,6 @@ private:
     std::vector<size_t> chunk_slice_;  // slice length inside each chunk
     std::unique_ptr<std::atomic<int>[]> remaining_;
     int remaining_cap_ = 0;
-    // Whole-list jobs (no chunk callback): slice s is claimed and reported
-    // done on a cache line of its own, so the threads of a static split never
-    // meet on one contended counter.  Both words hold the number of the job
-    // that last claimed / finished the slice, so no job has to clear them.
-    bool whole_ = false;
-    uint32_t job_epoch_ = 0;
-    struct alignas(64) SliceFlag {
-        std::atomic<uint32_t> claimed{0};
-        std::atomic<uint32_t> done{0};
-    };
-    std::unique_ptr<SliceFlag[]> slice_flag_;
-    int slice_flag_cap_ = 0;
 
     // scan job
     struct ScanPart {

@@ -25,6 +25,10 @@
 //       pollers on pool sets and on their own staging.
 //   locked_source
 //       SdmaQueue::host_source_ok on registered host memory.
+//   gather_mix <workers> <rounds> <seed>
+//       GatherEngine alone: whole-list runs (no chunk callback), pipelined
+//       runs and parallel list scans in random order on one engine (see the
+//       function).
 //
 // Every landed byte is compared with the expected image (the entries applied
 // by plain memcpy), and list checksums exactly.  Exit status: 0 pass,
@@ -36,6 +40,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <thread>
 #include <vector>
@@ -47,6 +52,7 @@
 #include "gfd/sg_task_queue.h"
 #include "gfd/staging_pool.h"
 #include "gfd/tiled_queue.h"
+#include "gather_engine.h"
 #include "sdma.h"
 
 using namespace gfd;
@@ -847,12 +853,129 @@ int run_stale_pinned(uint64_t seed) {
     return rc;
 }
 
+// GatherEngine on its own.  Each round builds a list (uniform tokens, ragged
+// sizes, ragged with empty entries, or a long list of small entries that the
+// workers scan in parallel), gathers it into one of two staging buffers at a
+// random alignment, as a whole-list run (the static split, slices handed over
+// in the workers' mailboxes) or a pipelined run whose callback checks each
+// chunk as it is reported, and compares every byte and the guard bytes after
+// it.  Then the list's source bytes are inverted: a worker copying after
+// run() returned would write the inverted bytes, which the check of the same
+// image after the next round finds (under ThreadSanitizer that late read is
+// also a reported race).  Some rounds pause 3 ms first, past the workers'
+// spin limit (GFD_GATHER_SPIN_US), so that jobs also meet sleeping workers.
+struct MixChunkCtx {
+    const uint8_t* out;
+    const uint8_t* want;
+    int next;
+    bool bad;
+};
+
+void mix_check_chunk(void* p, int chunk, size_t off, size_t len) {
+    MixChunkCtx* c = (MixChunkCtx*)p;
+    if (chunk != c->next || std::memcmp(c->out + off, c->want + off, len) != 0) c->bad = true;
+    c->next++;
+}
+
+int run_gather_mix(int workers, int rounds, uint64_t seed) {
+    Rng rng(seed);
+    const size_t src_bytes = 3u << 20, max_total = 1u << 20, guard = 64;
+    std::vector<uint8_t> src(src_bytes);
+    for (auto& b : src) b = (uint8_t)rng.next();
+    std::vector<int> cpus((size_t)workers, -1);
+    // On the heap: the engine's 64-byte-aligned members need an aligned
+    // object, which ASan's detached stack frames do not guarantee.
+    auto engp = std::make_unique<GatherEngine>(cpus);
+    GatherEngine& eng = *engp;
+    std::vector<uint8_t> stg[2] = {std::vector<uint8_t>(max_total + 2 * guard),
+                                   std::vector<uint8_t>(max_total + 2 * guard)};
+    std::vector<uint8_t> want[2] = {std::vector<uint8_t>(max_total), std::vector<uint8_t>(max_total)};
+    size_t want_len[2] = {0, 0}, want_at[2] = {0, 0};
+    int whole_runs = 0, chunk_runs = 0, scans = 0;
+    for (int r = 0; r < rounds; r++) {
+        const int kind = (int)rng.below(4);
+        std::vector<SGEntry> e;
+        size_t total = 0;
+        const uint64_t dst0 = 0x100000 + rng.below(1 << 20);
+        auto add = [&](size_t size) {
+            const size_t so = rng.below(src_bytes - size + 1);
+            e.push_back(SGEntry{dst0 + total, src.data() + so, size});
+            total += size;
+        };
+        if (kind == 0) {  // uniform tokens
+            const size_t t = (size_t)64 << rng.below(7);
+            const int n = 1 + (int)rng.below((int)std::min<size_t>(700, max_total / t));
+            for (int i = 0; i < n; i++) add(t);
+        } else if (kind == 1 || kind == 2) {  // ragged, with empty entries in kind 2
+            const int n = 1 + (int)rng.below(600);
+            for (int i = 0; i < n; i++) add(kind == 2 && rng.below(5) == 0 ? 0 : 1 + rng.below(1500));
+        } else {  // long list of small entries: scanned by the workers
+            const int n = GatherEngine::kCallerScanMax + 1 + (int)rng.below(3000);
+            for (int i = 0; i < n; i++) add(1 + rng.below(120));
+        }
+        if (total == 0) add(1 + rng.below(100));
+        const int b = r & 1;
+        const size_t at = guard + rng.below(guard);
+        uint8_t* out = stg[b].data() + at;
+        std::memset(stg[b].data(), kSentinel, stg[b].size());
+        uint8_t* w = want[b].data();
+        for (const SGEntry& x : e)
+            if (x.size) std::memcpy(w + (x.dst - dst0), x.src, x.size);
+        want_len[b] = total;
+        want_at[b] = at;
+        if (rng.below(8) == 0) std::this_thread::sleep_for(std::chrono::milliseconds(3));
+        int uniform_hint = -1;
+        if (kind == 0) uniform_hint = (int)rng.below(2);  // 1 (uniform) or 0 (check per entry)
+        if (kind == 3 || rng.below(4) == 0) {
+            const GatherEngine::ListScan sc = eng.scan(e.data(), (int)e.size());
+            scans++;
+            if (sc.total != total || !sc.dst_contig) {
+                std::fprintf(stderr, "gather mix: round %d scan total %zu (want %zu) dst_contig %d\n", r, sc.total,
+                             total, (int)sc.dst_contig);
+                return 3;
+            }
+        }
+        if (rng.below(2) == 0) {
+            eng.run(e.data(), (int)e.size(), total, (char*)out, 0, nullptr, nullptr, uniform_hint);
+            whole_runs++;
+        } else {
+            eng.set_slice_bytes(4096u << rng.below(4));
+            const size_t chunk = 16384u << rng.below(5);
+            MixChunkCtx ctx{out, w, 0, false};
+            eng.run(e.data(), (int)e.size(), total, (char*)out, chunk, mix_check_chunk, &ctx, uniform_hint);
+            chunk_runs++;
+            if (ctx.bad) {
+                std::fprintf(stderr, "gather mix: round %d a chunk was reported out of order or incomplete\n", r);
+                return 3;
+            }
+        }
+        for (int k = 0; k < 2; k++) {  // this round's image, and the previous round's again
+            if (k == 1 && r == 0) break;
+            const int bb = k == 0 ? b : b ^ 1;
+            const uint8_t* o = stg[bb].data() + want_at[bb];
+            bool ok = std::memcmp(o, want[bb].data(), want_len[bb]) == 0;
+            for (size_t i = 0; i < guard && ok; i++) ok = o[want_len[bb] + i] == kSentinel && o[-(ptrdiff_t)i - 1] == kSentinel;
+            if (!ok) {
+                std::fprintf(stderr, "gather mix: round %d image of round %d differs (%zu entries, %zu bytes)\n", r,
+                             k == 0 ? r : r - 1, e.size(), want_len[bb]);
+                return 3;
+            }
+        }
+        for (const SGEntry& x : e)  // the caller may reuse its sources once run() returns
+            for (size_t i = 0; i < x.size; i++) ((uint8_t*)x.src)[i] ^= 0xFF;
+    }
+    std::printf("gather mix: pass (%d whole, %d pipelined, %d scans)\n", whole_runs, chunk_runs, scans);
+    return 0;
+}
+
 int main(int argc, char** argv) {
     setvbuf(stdout, nullptr, _IOLBF, 0);
     if (argc >= 2 && std::string(argv[1]) == "sdma_slot_reuse") return run_sdma_slot_reuse();
     if (argc >= 2 && std::string(argv[1]) == "locked_source") return run_locked_source();
     if (argc >= 2 && std::string(argv[1]) == "stale_pinned") return run_stale_pinned(7);
     if (argc >= 2 && std::string(argv[1]) == "worker_direct") return run_worker_direct(11);
+    if (argc >= 5 && std::string(argv[1]) == "gather_mix")
+        return run_gather_mix(std::atoi(argv[2]), std::atoi(argv[3]), std::strtoull(argv[4], nullptr, 0));
     if (argc >= 4 && std::string(argv[1]) == "staging_pool")
         return run_staging_pool(std::atoi(argv[2]), std::strtoull(argv[3], nullptr, 0));
     if (argc >= 10 && std::string(argv[1]) == "tiled")

@@ -194,15 +194,29 @@ def test_direct_looks_up_pinned_sources_on_every_call(poller_emu):
     assert "call 0, zero-copy launches 1" in out and "call 1, zero-copy launches 0" in out, out[-2000:]
 
 
+@pytest.mark.parametrize("workers", [0, 1, 3, 15])
+def test_gather_engine_whole_and_pipelined_runs(poller_emu, workers):
+    """GatherEngine alone: whole-list runs (the reference's static W+1 split,
+    src/parallel_gather.cpp:90-116, each worker's slice handed over in its
+    mailbox line), pipelined runs and parallel list scans in random order on
+    one engine, over uniform, ragged and empty entries; every byte of every
+    run is compared with the memcpy image, and again after the next run with
+    the sources inverted in between, so a worker still copying after run()
+    returned would show.  A 200 us spin limit makes some jobs meet sleeping
+    workers."""
+    out = run(poller_emu, ["gather_mix", workers, 300, workers + 5], env={"GFD_GATHER_SPIN_US": "200"})
+    assert "gather mix: pass" in out, out[-2000:]
+
+
 # The same stack built with ThreadSanitizer instead: the poller, gather
 # workers, copy engines and the host threads that play the kernels' protocols
 # must show no data race (a report makes the run exit 66).
 @pytest.mark.parametrize("args", [["sg", "split_small_tokens", 2, 1], ["sg", "pages", 2, 1],
                                   ["queue", 4096, 1000, 1, 2, 3], ["ragged", "direct", 700, 1, 2, 3],
                                   ["tiled", 8, 128, 32, 4096, 1, 1, 2, 5], ["staging_pool", 2, 5],
-                                  ["sdma_slot_reuse"]])
+                                  ["sdma_slot_reuse"], ["gather_mix", 7, 60, 16]])
 def test_no_data_race_under_tsan(poller_emu_tsan, args):
-    out = run(poller_emu_tsan, args, env={"TSAN_OPTIONS": "halt_on_error=0 exitcode=66"})
+    out = run(poller_emu_tsan, args, env={"TSAN_OPTIONS": "halt_on_error=0 exitcode=66", "GFD_GATHER_SPIN_US": "200"})
     assert "ThreadSanitizer" not in out, out[-3000:]
 
 
