@@ -280,13 +280,15 @@ bool GatherEngine::take_mailbox_slice(Mailbox& mb, uint32_t job, size_t prefetch
 }
 
 // Scan job: claim parts of kScanPartEntries entries; part k checks the pairs
-// (i-1, i) for i in its range, so every adjacent pair is checked once.
+// (i-1, i) for i in its range, so every adjacent pair is checked once.  The
+// list is read only after a claim: a worker can reach this loop just as the
+// caller, having seen every part done, returns and the list is freed.
 void GatherEngine::do_scan_parts() {
     const SGEntry* e = entries_;
-    const size_t size0 = e[0].size;
     for (;;) {
         const int k = next_slice_.fetch_add(1, std::memory_order_relaxed);
         if (k >= scan_parts_) break;
+        const size_t size0 = e[0].size;
         const int b = k * kScanPartEntries, end = std::min(count_, b + kScanPartEntries);
         size_t sum = 0;
         bool dc = true, sc = true, un = true;

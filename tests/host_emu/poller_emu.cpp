@@ -887,8 +887,9 @@ int run_gather_mix(int workers, int rounds, uint64_t seed) {
     // object, which ASan's detached stack frames do not guarantee.
     auto engp = std::make_unique<GatherEngine>(cpus);
     GatherEngine& eng = *engp;
-    std::vector<uint8_t> stg[2] = {std::vector<uint8_t>(max_total + 2 * guard),
-                                   std::vector<uint8_t>(max_total + 2 * guard)};
+    // Room for the image at an offset of up to 2 * guard - 1 and the guard after it.
+    std::vector<uint8_t> stg[2] = {std::vector<uint8_t>(max_total + 3 * guard),
+                                   std::vector<uint8_t>(max_total + 3 * guard)};
     std::vector<uint8_t> want[2] = {std::vector<uint8_t>(max_total), std::vector<uint8_t>(max_total)};
     size_t want_len[2] = {0, 0}, want_at[2] = {0, 0};
     int whole_runs = 0, chunk_runs = 0, scans = 0;
