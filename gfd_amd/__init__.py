@@ -713,7 +713,7 @@ def device_sg_entries(src, dst, size, tag=0):
 # gfd_sg_trace_list / gfd_sg_trace_block (include/gfd_capi.h).
 SG_TRACE_LIST_DTYPE = np.dtype([("claimed", "<u8"), ("ready", "<u8"), ("landed", "<u8"), ("block", "<u4"),
                                 ("list_id", "<u4")])
-SG_TRACE_BLOCK_DTYPE = np.dtype([("start", "<u8"), ("exit", "<u8"), ("lists", "<u8"), ("_pad", "<u8")])
+SG_TRACE_BLOCK_DTYPE = np.dtype([("start", "<u8"), ("exit", "<u8"), ("lists", "<u8"), ("hw", "<u8")])
 SG_TRACE_TICKS_PER_US = 100  # the device wall clock runs at 100 MHz
 
 

@@ -4,8 +4,11 @@
 // with the sg:: primitives (the pattern of examples/09_sg_warp_spec.cu:78-294
 // and test/test_sg_gpu_submit.cu:20-213), the session's transfer waves copy
 // each list from pinned host memory to HBM (include/gfd/sg_warp_spec.h), and
-// the compute wave runs the consumer on every landed list: a per-row bf16
-// RMSNorm, or nothing (pure transfer).
+// the compute waves run the consumer: a per-row bf16 RMSNorm, or nothing
+// (pure transfer).  The RMSNorm takes each row from the LDS ring the transfer
+// wave stages it in (the session's staged-row mode) as soon as the row is
+// copied; with GFD_SG_STAGED_ROWS=0 it runs per landed list instead, reading
+// the rows back from HBM.
 //
 // Lists: expert e's rows [offsets[e], offsets[e+1]) in the expert-major order
 // of gfd_moe_route, cut into lists of at most rows_per_list (<= 64) rows, so
@@ -21,6 +24,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 
 #include "bf16_ops.h"
 #include "capi_error.h"
@@ -37,15 +41,19 @@ using gfd::sg_warp_spec::SGListView;
 // round-to-nearest-even out, to out + row * row_bytes (the entry's tag is the
 // row).  V = row_bytes / 1 KiB vectors per lane.
 //
-// The entries live in host memory and the rows were just written to HBM by
-// the transfer waves of this workgroup, so a row's own arithmetic is short
-// and its latency is what counts.  Per list: up to 64 entries are read in one
-// request (lane i reads entry i) instead of one host round trip per row, and
-// the weights are loaded once per list and parked in LDS, each lane reading
-// back only the vectors it stored itself (in registers they would not fit
-// beside a row and its fp32 values).  Entries whose
-// size is not row_bytes (rows skipped for a bad token id have size 0) are
-// left alone.
+// Staged rows: the row is read from the LDS slot, the slot handed back, and
+// the weights (loaded on the wave's first row and parked in LDS, each lane
+// reading back only the vectors it stored itself: in registers they would
+// not fit beside a row and its fp32 values) applied on the way out.
+//
+// List mode: the rows were just written to HBM by the transfer waves of this
+// workgroup, so a row's own arithmetic is short and its latency is what
+// counts.  Per list: up to 64 entries are read in one request (lane i reads
+// entry i) instead of one round trip per row, and the weights are loaded
+// once per list into the same LDS copy.
+//
+// In both, entries whose size is not row_bytes (rows skipped for a bad token
+// id have size 0) are left alone.
 template <int V>
 __device__ __forceinline__ float sum_squares(const gfd::wave::vec4u (&x)[V]) {
     float ss = 0.f;
@@ -116,17 +124,63 @@ __device__ __forceinline__ void rmsnorm_list(const SGListView& view, uint8_t* ou
     }
 }
 
+// The weights, one copy per compute wave: each lane reads back only the
+// vectors it stored itself, so no wave waits for another's copy.
+__device__ __forceinline__ gfd::wave::vec4u* rms_weights_lds(uint32_t wave_part) {
+    __shared__ gfd::wave::vec4u w_lds[gfd::sg_warp_spec::SG_MAX_COMPUTE][14 * 64];
+    return w_lds[wave_part < (uint32_t)gfd::sg_warp_spec::SG_MAX_COMPUTE ? wave_part : 0];
+}
+
+// One staged row (in LDS) normalised to out + tag * kRow; the slot is handed
+// back as soon as the row is in registers.
+template <int V>
+__device__ __forceinline__ void rmsnorm_staged_row(const gfd::sg_warp_spec::SGRowView& r, uint8_t* out,
+                                                   const uint16_t* weight, float eps, gfd::wave::vec4u* w_lds) {
+    using gfd::wave::vec4u;
+    constexpr uint32_t kRow = (uint32_t)V * 1024;
+    const uint32_t lane = (uint32_t)r.lane_id;
+    if (r.first) {
+#pragma unroll
+        for (int k = 0; k < V; k++)
+            w_lds[k * 64 + lane] = gfd::wave::gload((uint64_t)(uintptr_t)weight + (uint64_t)(k * 64 + lane) * 16);
+    }
+    vec4u x[V];
+#pragma unroll
+    for (int k = 0; k < V; k++) x[k] = r.data[k * 64 + lane];
+    r.release();
+    float ss = sum_squares<V>(x);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    store_normalised<V>(x, w_lds, 1.0f / sqrtf(ss / (float)(V * 512) + eps),
+                        (uint64_t)(uintptr_t)out + (uint64_t)r.tag * kRow, lane);
+}
+
 struct RowRMSNorm {
-    // Up to SG_MAX_COMPUTE compute waves share each list, row by row.
+    // Up to SG_MAX_COMPUTE compute waves take the workgroup's rows as the
+    // transfer wave stages them in LDS (stage_rows), or share each landed
+    // list row by row (list mode).
     static constexpr bool kSharesLists = true;
+    static constexpr bool kStagesRows = true;
     uint8_t* out;
     const uint16_t* weight;
     float eps;
     uint32_t row_bytes;
+    int stage_rows;
+    __device__ uint32_t staged_row_bytes() const { return stage_rows ? row_bytes : 0u; }
+    __device__ void row(const gfd::sg_warp_spec::SGRowView& r) const {
+        gfd::wave::vec4u* w = rms_weights_lds((uint32_t)gfd::wave::wave_id() - 1);
+        switch (row_bytes) {
+#define GFD_RMS_CASE(n) \
+    case n * 1024: rmsnorm_staged_row<n>(r, out, weight, eps, w); break;
+            GFD_RMS_CASE(1) GFD_RMS_CASE(2) GFD_RMS_CASE(3) GFD_RMS_CASE(4) GFD_RMS_CASE(5) GFD_RMS_CASE(6)
+            GFD_RMS_CASE(7) GFD_RMS_CASE(8) GFD_RMS_CASE(9) GFD_RMS_CASE(10) GFD_RMS_CASE(11) GFD_RMS_CASE(12)
+            GFD_RMS_CASE(13) GFD_RMS_CASE(14)
+#undef GFD_RMS_CASE
+            default: r.release(); break;
+        }
+    }
     __device__ void operator()(SGListView v) const {
-        // Weights of rows up to 14 KiB, one copy per compute wave.
-        __shared__ gfd::wave::vec4u w_lds[gfd::sg_warp_spec::SG_MAX_COMPUTE][14 * 64];
-        gfd::wave::vec4u* w = w_lds[v.part < (uint32_t)gfd::sg_warp_spec::SG_MAX_COMPUTE ? v.part : 0];
+        gfd::wave::vec4u* w = rms_weights_lds(v.part);
         switch (row_bytes) {
 #define GFD_RMS_CASE(n) \
     case n * 1024: rmsnorm_list<n>(v, out, weight, eps, w); break;
@@ -158,8 +212,9 @@ struct MoeLists {
 };
 
 // Submitter wave: posts this workgroup's share of the lists (list L goes to
-// workgroup L mod grid); workgroup 0 then waits for every list to land and
-// terminates the transfer waves.  Routing entries out of range are reported
+// workgroup L mod grid); workgroup 0 also tells the transfer waves how many
+// lists the launch holds, so that the one landing the last of them ends the
+// launch.  Routing entries out of range are reported
 // (SG_ERR_BAD_ROW) and become empty entries: nothing outside the host buffer
 // is ever read.
 __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
@@ -208,6 +263,23 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
         const uint32_t rj = (uint32_t)__shfl((int)rem, j, 64);
         rank += rj > rem || (rj == rem && j < lane);
     }
+    // When the launch's lists fit the ring and the pool, list L sits at ring
+    // index gpu_first + L and its entries at pool index entry_first + (rows
+    // of the lists before it): the transfer waves, which claim ring indices
+    // in order, then take the lists in id order (full lists first, the
+    // remainders longest first) whatever order the submitters commit them
+    // in.  No submitter ever waits for anything here (no slot is reused, no
+    // space is short), so a transfer wave waiting for index gpu_first + L
+    // always sees it committed.  Workgroup 0 advances the allocation
+    // counters past all of them once, for the host's accounting.
+    const uint64_t gpu_first =
+        __hip_atomic_load(&cnt->list_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) +
+        __hip_atomic_load(&cnt->host_lists, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t entry_first = __hip_atomic_load(&cnt->entry_first, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (fits && blockIdx.x == 0 && lane == 0) {
+        sg::atomic_add_dev(&cnt->list_alloc, total);
+        sg::atomic_add_dev(&cnt->entry_alloc, (uint64_t)rows);
+    }
     for (uint32_t L = blockIdx.x; L < total; L += gridDim.x) {
         // The expert of list L.  A full list: the highest expert whose first
         // full-list id is <= L.  A remainder: the expert of that rank.
@@ -224,7 +296,21 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
             if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_RING_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
-        const uint64_t pool = sg::sg_alloc_entries(sq, n);
+        uint64_t pool, slot;
+        if (fits) {
+            uint32_t before = is_full ? k * m.rows_per_list : nfull * m.rows_per_list;
+            if (!is_full) {  // the remainders ranked ahead of this one
+                uint32_t mine = part && (uint32_t)rank < k ? rem : 0u;
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) mine += (uint32_t)__shfl_xor((int)mine, o, 64);
+                before += mine;
+            }
+            pool = entry_first + before;
+            slot = gpu_first + L;
+        } else {
+            pool = sg::sg_alloc_entries(sq, n);
+            slot = 0;
+        }
         if ((uint32_t)lane < n) {
             const uint32_t r = r0 + (uint32_t)lane;
             const int tok = m.row_token[r];
@@ -240,22 +326,16 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
                 d.size = 0;
             }
         }
-        const uint64_t slot = sg::sg_alloc_list(sq);
+        if (!fits) slot = sg::sg_alloc_list(sq);
         if (!sg::sg_commit_list(m.ring, slot, (uint32_t)(pool % MAX_SG_POOL_ENTRIES), n, L, SG_FLAG_NONE, fits))
             break;
     }
-    if (blockIdx.x == 0) {
-        // Host lists queued before the launch land in it too: wait for those
-        // and this launch's `total`, so stop is raised only once nothing is
-        // left to copy.
-        if (sg::sg_wait_gpu_lists_done(sq, total)) {
-            sg::sg_terminate_all_landed(sq);
-        } else {
-            if (lane == 0)
-                __hip_atomic_fetch_or(&cnt->error, SG_ERR_LIST_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            sg::sg_terminate(sq);
-        }
-    }
+    // Host lists queued before the launch land in it too: the transfer wave
+    // that lands the last of those and this launch's `total` ends the launch,
+    // so stop is raised only once nothing is left to copy, and no wave polls
+    // for it meanwhile.  (A list that never lands leaves the transfer waves
+    // to the launch's deadline.)
+    if (blockIdx.x == 0) sg::sg_stop_when_landed(sq, total);
 }
 
 // Wave 0 transfer, waves 1 .. C compute (C = 1 unless the functor shares
@@ -300,9 +380,12 @@ extern "C" int gfd_sg_session_launch_moe(gfd_sg_session_t s, const void* host_ba
     const MoeLists m{(uint64_t)(uintptr_t)host_base, token_stride, (uint64_t)(uintptr_t)dst, offsets, row_token,
                      num_experts, num_tokens, num_rows, row_bytes, rows_per_list, fits ? 1 : 0, ring};
     const dim3 grid((unsigned)p->num_blocks()), block((unsigned)(2 + compute + helpers) * 64);
+    const char* sr = std::getenv("GFD_SG_STAGED_ROWS");
+    const int stage_rows = !(sr && sr[0] == '0');
     if (out)
         hipLaunchKernelGGL(sg_moe_kernel<RowRMSNorm>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),
-                           p->get_sg_queue(), RowRMSNorm{(uint8_t*)out, weight, eps, row_bytes}, m, 1 + compute);
+                           p->get_sg_queue(), RowRMSNorm{(uint8_t*)out, weight, eps, row_bytes, stage_rows}, m,
+                           1 + compute);
     else
         hipLaunchKernelGGL(sg_moe_kernel<NoCompute>, grid, block, 0, (hipStream_t)stream, p->get_desc_queue(),
                            p->get_sg_queue(), NoCompute{}, m, 2);

@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) void sg_poller_kernel(gfd::DescriptorQueue* q,
             const volatile uint64_t* flag = sq->d_list_done + l;
             const uint64_t t0 = wall_clock64();
             for (uint32_t n = 0;; n++) {
-                if (gfd::device::load_acquire_system(flag) != 0) break;
+                if (gfd::device::load_relaxed_system(flag) != 0) break;  // every lane acquires below
                 if (wall_clock64() - t0 > max_ticks) {
                     ok = 0;
                     break;

@@ -340,7 +340,7 @@ void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int
     SGDeviceCounters c{};
     c.list_claim = consumed_lists_;
     c.list_alloc = sq_->list_alloc_idx;
-    c.entry_alloc = sq_->entry_alloc_idx;
+    c.entry_alloc = c.entry_first = sq_->entry_alloc_idx;
     c.entries_done = consumed_entries_;
     c.list_known = consumed_lists_;
     c.list_base = consumed_lists_;
@@ -441,7 +441,7 @@ void SGWarpSpecSession::prepare_raw_launch() {
     SGDeviceCounters c{};
     c.list_claim = c.list_known = c.list_base = consumed_lists_;
     c.list_alloc = sq_->list_alloc_idx;
-    c.entry_alloc = sq_->entry_alloc_idx;
+    c.entry_alloc = c.entry_first = sq_->entry_alloc_idx;
     c.entries_done = consumed_entries_;
     c.compute_waves = 1;  // the caller's kernel layout is its own: no helpers, one compute wave
     c.host_lists = sq_->list_alloc_idx - consumed_lists_;

@@ -23,6 +23,13 @@ constexpr uint64_t kDefaultWaitTicks = 10ull * kWallClockHz;  // 10 s
 __device__ __forceinline__ uint64_t load_acquire_system(const volatile uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
+// Polls read with relaxed loads and make one acquire (fence) once their
+// condition holds: an acquire invalidates the caches of the wave's XCD every
+// time it runs, which slows every other wave there.
+__device__ __forceinline__ uint64_t load_relaxed_system(const volatile uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void acquire_system() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, ""); }
 
 __device__ __forceinline__ void store_release_system(volatile uint64_t* p, uint64_t v) {
     __hip_atomic_store(const_cast<uint64_t*>(p), v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -84,8 +91,10 @@ __device__ __forceinline__ bool write_descriptor_safe(DescriptorQueue* queue, ui
                                                       uint64_t src_addr, void* gpu_dst, uint32_t token_size,
                                                       int num_tokens, uint64_t user_data = 0) {
     const uint64_t slot = base_slot + (uint64_t)token_idx;
-    if (slot >= (uint64_t)QUEUE_SIZE && load_acquire_system(&queue->read_idx) <= slot - (uint64_t)QUEUE_SIZE)
-        return false;
+    if (slot >= (uint64_t)QUEUE_SIZE) {
+        if (load_relaxed_system(&queue->read_idx) <= slot - (uint64_t)QUEUE_SIZE) return false;
+        acquire_system();  // the slot's consumption before this lane's writes
+    }
     write_descriptor(queue, base_slot, token_idx, src_addr, gpu_dst, token_size, num_tokens, user_data);
     return true;
 }
@@ -96,7 +105,10 @@ __device__ __forceinline__ bool wait_for_completion(DescriptorQueue* queue, uint
                                                     uint64_t max_ticks = kDefaultWaitTicks) {
     const uint64_t t0 = wall_clock64();
     for (;;) {
-        if (load_acquire_system(&queue->done_idx) >= expected_done) return true;
+        if (load_relaxed_system(&queue->done_idx) >= expected_done) {
+            acquire_system();
+            return true;
+        }
         if (wall_clock64() - t0 > max_ticks) return false;
         __builtin_amdgcn_s_sleep(4);
     }

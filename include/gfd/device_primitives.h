@@ -76,7 +76,10 @@ __device__ __forceinline__ bool wait_chunk_done(TiledQueue* tq, uint32_t tile_id
         tq->d_tile_chunk_done ? tq->d_tile_chunk_done + tile_id : &tq->tile_chunk_done[tile_id];
     const uint64_t t0 = wall_clock64();
     for (uint32_t n = 0;; n++) {
-        if (load_acquire_system(signal) >= expected) return true;
+        if (load_relaxed_system(signal) >= expected) {
+            acquire_system();
+            return true;
+        }
         if (wall_clock64() - t0 > max_ticks) return false;
         if (n >= 64) __builtin_amdgcn_s_sleep(8);
     }
@@ -88,9 +91,12 @@ __device__ __forceinline__ bool wait_queue_space(TiledQueue* tq, uint32_t needed
     const uint64_t t0 = wall_clock64();
     bool ok = true;
     for (;;) {
-        const uint64_t w = load_acquire_system(&tq->base.write_idx);
-        const uint64_t r = load_acquire_system(&tq->base.read_idx);
-        if (w - r + 2ull * needed <= (uint64_t)QUEUE_SIZE) break;
+        const uint64_t w = load_relaxed_system(&tq->base.write_idx);
+        const uint64_t r = load_relaxed_system(&tq->base.read_idx);
+        if (w - r + 2ull * needed <= (uint64_t)QUEUE_SIZE) {
+            acquire_system();
+            break;
+        }
         if (wall_clock64() - t0 > max_ticks) {
             ok = false;
             break;

@@ -36,6 +36,14 @@ __device__ __forceinline__ uint64_t atomic_add_dev(uint64_t* p, uint64_t v) {
 __device__ __forceinline__ uint64_t load_dev(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
 }
+// For polls: an agent-scope acquire invalidates the XCD's caches every time
+// it runs, under every other wave on that XCD.  (With one wave polling this
+// way through a 2 ms MoE launch, the three other workgroups on its XCD moved
+// ~115 rows each; with relaxed polls ~155.)  The waits below poll with
+// relaxed loads and make one acquire once their condition holds.
+__device__ __forceinline__ uint64_t poll_dev(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // The launch's deadline (SGDeviceCounters::deadline; 0: none), read once per
 // wait, and whether it has passed.
@@ -53,9 +61,12 @@ __device__ __forceinline__ bool sg_wait_entry_space(SGTaskQueue* sq, uint32_t ne
     SGDeviceCounters* c = counters(sq);
     const uint64_t dl = launch_deadline(sq);
     for (uint64_t n = 0; n < wave::kSpinLimit && !past(dl); n++) {
-        const uint64_t alloc = load_dev(&c->entry_alloc);
-        const uint64_t done = load_dev(&c->entries_done);
-        if (alloc - done <= (uint64_t)(MAX_SG_POOL_ENTRIES - needed)) return true;
+        const uint64_t alloc = poll_dev(&c->entry_alloc);
+        const uint64_t done = poll_dev(&c->entries_done);
+        if (alloc - done <= (uint64_t)(MAX_SG_POOL_ENTRIES - needed)) {
+            wave::acquire_agent();
+            return true;
+        }
         __builtin_amdgcn_s_sleep(2);
     }
     return false;
@@ -66,8 +77,11 @@ __device__ __forceinline__ bool sg_wait_list_space(SGTaskQueue* sq) {
     SGDeviceCounters* c = counters(sq);
     const uint64_t dl = launch_deadline(sq);
     for (uint64_t n = 0; n < wave::kSpinLimit && !past(dl); n++) {
-        const uint64_t in_flight = load_dev(&c->list_alloc) - load_dev(&c->list_base) - load_dev(&c->lists_done);
-        if (in_flight < (uint64_t)(MAX_SG_LISTS - 1)) return true;
+        const uint64_t in_flight = poll_dev(&c->list_alloc) - poll_dev(&c->list_base) - poll_dev(&c->lists_done);
+        if (in_flight < (uint64_t)(MAX_SG_LISTS - 1)) {
+            wave::acquire_agent();
+            return true;
+        }
         __builtin_amdgcn_s_sleep(2);
     }
     return false;
@@ -114,7 +128,10 @@ __device__ __forceinline__ bool sg_wait_slot_free(SGTaskQueue* sq, uint64_t slot
     const SGList& l = sq->lists[slot % MAX_SG_LISTS];
     const uint64_t dl = launch_deadline(sq);
     for (uint64_t n = 0; n < wave::kSpinLimit && !past(dl); n++) {
-        if (wave::load_system(&l.done) >= want) return true;
+        if (__hip_atomic_load(const_cast<uint64_t*>(&l.done), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) >= want) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");  // system scope
+            return true;
+        }
         __builtin_amdgcn_s_sleep(32);
     }
     return false;
@@ -163,8 +180,14 @@ __device__ __forceinline__ uint64_t sg_submit_list(SGTaskQueue* sq, const Device
 __device__ __forceinline__ bool sg_wait_list_done(SGTaskQueue* sq, uint64_t expected) {
     const uint64_t dl = launch_deadline(sq);
     for (uint64_t n = 0; n < wave::kSpinLimit && !past(dl); n++) {
-        if (load_dev(&counters(sq)->lists_done) >= expected) return true;
-        __builtin_amdgcn_s_sleep(2);
+        const uint64_t done = poll_dev(&counters(sq)->lists_done);
+        if (done >= expected) {
+            wave::acquire_agent();
+            return true;
+        }
+        // Many lists still to land: a slower poll (~1 us) costs nothing.
+        if (expected - done > 8) __builtin_amdgcn_s_sleep(32);
+        else __builtin_amdgcn_s_sleep(2);
     }
     return false;
 }
@@ -188,7 +211,10 @@ __device__ __forceinline__ bool sg_wait_list_id_done(SGTaskQueue* sq, uint32_t l
     if (list_id >= (uint32_t)MAX_SG_LISTS) return false;
     const uint64_t dl = launch_deadline(sq);
     for (uint64_t n = 0; n < wave::kSpinLimit && !past(dl); n++) {
-        if (load_dev(&sq->d_list_done[list_id]) != 0) return true;
+        if (poll_dev(&sq->d_list_done[list_id]) != 0) {
+            wave::acquire_agent();
+            return true;
+        }
         __builtin_amdgcn_s_sleep(2);
     }
     return false;
@@ -211,6 +237,23 @@ __device__ __forceinline__ void sg_terminate_all_landed(SGTaskQueue* sq) {
     sg_terminate(sq);
     if (wave::lane_id() == 0)
         __hip_atomic_store(&counters(sq)->stop, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// sg_wait_gpu_lists_done + sg_terminate_all_landed without a wave waiting:
+// the transfer wave whose landing brings lists_done to host lists +
+// gpu_lists ends the launch (SGDeviceCounters::stop_at).  Both sides are
+// sequentially consistent (this wave stores stop_at, then reads lists_done;
+// a lander adds to lists_done, then reads stop_at), so one of them sees the
+// launch complete even when every list lands before stop_at is set.
+__device__ __forceinline__ void sg_stop_when_landed(SGTaskQueue* sq, uint64_t gpu_lists) {
+    SGDeviceCounters* c = counters(sq);
+    const uint64_t want = sg_host_lists(sq) + gpu_lists;
+    int now = 0;
+    if (wave::lane_id() == 0) {
+        __hip_atomic_store(&c->stop_at, want, __ATOMIC_SEQ_CST, __HIP_MEMORY_SCOPE_AGENT);
+        now = __hip_atomic_load(&c->lists_done, __ATOMIC_SEQ_CST, __HIP_MEMORY_SCOPE_AGENT) >= want;
+    }
+    if (__builtin_amdgcn_readfirstlane(now)) sg_terminate_all_landed(sq);
 }
 
 }  // namespace sg

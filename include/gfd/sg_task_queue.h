@@ -109,7 +109,15 @@ struct SGDeviceCounters {
     // HBM, never across PCIe; the header's `done` marker is still raised in
     // the host queue too, where host code and host submitters look for it.
     uint64_t dev_ring;
-    uint64_t _pad[6];
+    // Pool index of this launch's first GPU-submitted entry (entry_alloc as
+    // the launch starts), for submitters that place their lists at fixed
+    // positions instead of allocating them.
+    uint64_t entry_first;
+    // lists_done at which the transfer wave that lands that list ends the
+    // launch (terminate + stop), as sg_terminate_all_landed would; 0: off.
+    // Set by a GPU submitter with sg_stop_when_landed.
+    uint64_t stop_at;
+    uint64_t _pad[4];
 };
 
 // One list of a traced launch, in wall-clock ticks (100 MHz): when its
@@ -132,7 +140,9 @@ struct SGTraceBlock {
     uint64_t start;
     uint64_t exit;
     uint64_t lists;
-    uint64_t _pad;
+    // Where the workgroup ran: XCC_ID << 32 | HW_ID of its transfer wave
+    // (HW_ID: CU id in bits 8-11, shader array 12, shader engine 13-15).
+    uint64_t hw;
 };
 static_assert(sizeof(SGTraceBlock) == 32, "SGTraceBlock must be 32 bytes");
 constexpr int SG_DEVICE_COUNTER_WORDS = (int)(sizeof(SGDeviceCounters) / sizeof(uint64_t));

@@ -18,6 +18,23 @@
 // free again once every part is done.  Functors without the declaration see
 // each list exactly once, on wave 1, as with the reference.
 //
+// A functor may instead take the rows of each list one by one, as the
+// transfer wave copies them, straight from an LDS ring of SG_ROW_SLOTS rows,
+// by declaring `static constexpr bool kStagesRows = true` and
+//
+//   __device__ uint32_t staged_row_bytes() const;  // R: 1 .. 14 KiB in whole KiB (else: list mode)
+//   __device__ void row(const SGRowView& r) const; // must call r.release() once it has read r.data
+//
+// besides operator() (used when R is not a size the ring takes).  Entries of
+// exactly R bytes, 16-byte aligned on both sides, are then loaded by the
+// transfer wave, stored to HBM and written into the ring; compute wave c of C
+// gets the workgroup's staged rows c, c + C, ... in order.  Other entries are
+// copied as usual and not shown to the functor, and lists are still marked
+// done once all their bytes have landed.  The rows reach the compute waves
+// through LDS instead of being loaded again from HBM, so the compute waves
+// put no loads on the vector memory path that the transfer wave's host
+// reads take.
+//
 // The transfer wave claims the next ring index (device-scope atomic on an
 // HBM counter), waits for that list to be committed, copies every entry's
 // bytes from pinned host memory into HBM itself together with the helpers
@@ -41,6 +58,8 @@
 // waves; the others poll list_known in HBM.  Idle waves thus put one read at
 // a time on PCIe instead of one per wave, and a wave whose index is already
 // below list_known goes straight to the list's header.
+#include <type_traits>
+
 #include "gfd/descriptor_queue.h"
 #include "gfd/sg_device_primitives.h"
 #include "gfd/sg_task_queue.h"
@@ -92,6 +111,58 @@ struct _shares_lists<F, decltype((void)F::kSharesLists)> {
     static constexpr bool value = F::kSharesLists;
 };
 
+template <typename F, typename = void>
+struct _stages_rows {
+    static constexpr bool value = false;
+};
+template <typename F>
+struct _stages_rows<F, decltype((void)F::kStagesRows)> {
+    static constexpr bool value = F::kStagesRows;
+};
+
+// Staged rows: ring depth and the largest row the ring holds.
+constexpr int SG_ROW_SLOTS = 4;
+constexpr uint32_t SG_MAX_STAGED_ROW = 14 * 1024;
+
+// One staged row as a compute wave sees it.
+struct SGRowView {
+    const wave::vec4u* data;  // the row in LDS: this lane's vectors are data[k * 64 + lane_id]
+    uint64_t dst;             // where the row landed in HBM
+    uint32_t bytes, tag, list_id;
+    int lane_id;
+    bool first;  // this wave's first row of the launch
+    int* slot;
+    // Hand the slot back to the transfer wave once data has been read (the
+    // workgroup-scope release waits for this wave's LDS reads).
+    __device__ __forceinline__ void release() const {
+        if (lane_id == 0) __hip_atomic_store(slot, 0, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+};
+
+struct _SGRowRing {
+    wave::vec4u data[SG_ROW_SLOTS][SG_MAX_STAGED_ROW / 16];
+    uint64_t dst[SG_ROW_SLOTS];
+    uint32_t tag[SG_ROW_SLOTS], list_id[SG_ROW_SLOTS];
+    int flag[SG_ROW_SLOTS];  // r + 1 while the slot holds the workgroup's staged row r; 0 once free
+};
+struct _SGNoRowRing {
+    wave::vec4u data[1][1];
+    uint64_t dst[1];
+    uint32_t tag[1], list_id[1];
+    int flag[1];
+};
+
+// The functor's staged row size, or 0 for list mode.
+template <typename F>
+__device__ __forceinline__ uint32_t _staged_row_bytes(const F& f) {
+    if constexpr (_stages_rows<F>::value) {
+        const uint32_t r = f.staged_row_bytes();
+        return (r >= 1024 && r <= SG_MAX_STAGED_ROW && r % 1024 == 0) ? r : 0u;
+    } else {
+        return 0u;
+    }
+}
+
 __device__ __forceinline__ uint64_t _idle_limit_ticks(const SGTaskQueue* sq) {
     const uint32_t ms = wave::load_system32(&sq->idle_limit_ms);
     return (uint64_t)(ms ? ms : 30000u) * 100000ull;  // 100 MHz wall clock
@@ -103,6 +174,11 @@ __device__ __forceinline__ uint64_t _idle_limit_ticks(const SGTaskQueue* sq) {
 __device__ __forceinline__ SGTaskQueue* _ring(SGTaskQueue* sq, SGTaskQueue* dev, uint64_t gpu_first, uint64_t idx) {
     return dev && idx >= gpu_first ? dev : sq;
 }
+
+// The waits read the wall clock (s_memrealtime) for their time limits only
+// once every kClockPolls polls: the limits are seconds long, so a clock read
+// on every poll of every idle wave would buy nothing.
+constexpr uint32_t kClockPolls = 64;
 
 // _wait_committed's outcomes.
 enum : int { kSgStopped = 0, kSgCommitted = 1, kSgDeadline = 2 };
@@ -124,7 +200,12 @@ __device__ __forceinline__ int _wait_committed(SGTaskQueue* sq, SGDeviceCounters
         // only every 32nd poll, before the sequence, for the reason given for
         // the leader below.
         for (uint32_t n = 0;; n++) {
-            const uint32_t term = (n & 31) == 31 ? wave::load_system32(&sq->terminate) : 0u;
+            uint32_t term = 0;
+            if ((n & 31) == 31) {
+                term = __hip_atomic_load(const_cast<uint32_t*>(&sq->terminate), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_SYSTEM);
+                if (term) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");  // then the sequence, as below
+            }
             if (__hip_atomic_load(const_cast<uint64_t*>(&mine.sequence), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                 idx + 1) {
                 wave::acquire_agent();  // the header and entries written before the commit
@@ -134,8 +215,10 @@ __device__ __forceinline__ int _wait_committed(SGTaskQueue* sq, SGDeviceCounters
                 if (term && lane == 0) __hip_atomic_store(&cnt->stop, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 return kSgStopped;
             }
-            if (sg::past(deadline)) return kSgDeadline;
-            if (wall_clock64() - t0 > idle_ticks) return kSgStopped;
+            if ((n & (kClockPolls - 1)) == kClockPolls - 1) {
+                if (sg::past(deadline)) return kSgDeadline;
+                if (wall_clock64() - t0 > idle_ticks) return kSgStopped;
+            }
             __builtin_amdgcn_s_sleep(8);
         }
     }
@@ -151,13 +234,20 @@ __device__ __forceinline__ int _wait_committed(SGTaskQueue* sq, SGDeviceCounters
         if (idx == known) {
             // Leader.  terminate is read before the sequence.  Whoever sets
             // terminate does so after every list it expects has been
-            // committed, with a release store; the acquire load that reads it
-            // orders the sequence load after those commits.  So a list still
-            // uncommitted once terminate reads 1 was never submitted, and the
-            // wave can stop at once.  (Read the other way round, a commit
-            // could land between the two loads and be dropped.)
-            const uint32_t term = wave::load_system32(&sq->terminate);
-            if (wave::load_system(&mine.sequence) == idx + 1) {
+            // committed, with a release store; the acquire (fence) after the
+            // load that reads it orders the sequence load after those
+            // commits.  So a list still uncommitted once terminate reads 1
+            // was never submitted, and the wave can stop at once.  (Read the
+            // other way round, a commit could land between the two loads and
+            // be dropped.)  Both are polled with relaxed loads and acquired
+            // only when they count: an acquire per poll would invalidate the
+            // XCD's caches under every other wave there.
+            const uint32_t term =
+                __hip_atomic_load(const_cast<uint32_t*>(&sq->terminate), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (term) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+            if (__hip_atomic_load(const_cast<uint64_t*>(&mine.sequence), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ==
+                idx + 1) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");  // the header and entries written before the commit
                 // Find the committed run idx, idx+1, ... and publish it.
                 const uint64_t j = idx + (uint64_t)lane;
                 const bool c =
@@ -250,6 +340,83 @@ __device__ __forceinline__ int _sg_copy_batches(_SGJob* job, const SGTaskQueue* 
     return nbatches;
 }
 
+// Transfer wave, staged rows of V KiB: copy the list's entries, staging each
+// row of exactly V KiB (16-byte aligned) into the next ring slot once its
+// compute wave has freed it; other entries are copied as they are.  Adds the
+// bytes copied; false if a slot was never freed (the compute waves stalled).
+template <int V>
+__device__ __forceinline__ bool _sg_stage_rows(const SGTaskQueue* ring, uint32_t pool_offset, uint32_t count,
+                                               uint32_t list_id, _SGRowRing* rr, int* nrows, uint64_t* bytes) {
+    using wave::vec4u;
+    constexpr uint32_t kRow = (uint32_t)V * 1024;
+    const int lane = wave::lane_id();
+    for (uint32_t first = 0; first < count; first += wave::kWidth) {
+        uint64_t md = 0, ms = 0, mn = 0;
+        uint32_t tag = 0;
+        if (first + lane < count) {
+            const DeviceSGEntry e = ring->entries[(pool_offset + first + lane) % MAX_SG_POOL_ENTRIES];
+            md = e.dst_addr;
+            ms = e.src_addr;
+            mn = e.size;
+            tag = e.tag;
+        }
+        const bool st = mn == kRow && ((md | ms) & 15) == 0;
+        // Other entries (rare beside the rows: a skipped row has size 0)
+        // are copied one by one with a light loop, which keeps the kernel's
+        // registers within what the row's V vectors leave.
+        for (uint64_t other = __ballot(mn != 0 && !st); other; other &= other - 1) {
+            const int j = __builtin_ctzll(other);
+            const uint64_t n = wave::readlane64(mn, j);
+            wave::copy<4>(wave::readlane64(md, j), wave::readlane64(ms, j), n);
+            *bytes += n;
+        }
+        for (uint64_t rows = __ballot(st); rows; rows &= rows - 1) {
+            const int j = __builtin_ctzll(rows);
+            const uint64_t s0 = wave::readlane64(ms, j), d0 = wave::readlane64(md, j);
+            const uint32_t tj = (uint32_t)__builtin_amdgcn_readlane((int)tag, j);
+            const int r = *nrows;
+            const int slot = r % SG_ROW_SLOTS;
+            if (!wave::wait_lds_eq(&rr->flag[slot], 0)) return false;
+            vec4u v[V];
+#pragma unroll
+            for (int k = 0; k < V; k++) v[k] = wave::gload(s0 + (uint64_t)(k * wave::kWidth + lane) * 16);
+#pragma unroll
+            for (int k = 0; k < V; k++) wave::gstore(d0 + (uint64_t)(k * wave::kWidth + lane) * 16, v[k]);
+#pragma unroll
+            for (int k = 0; k < V; k++) rr->data[slot][k * wave::kWidth + lane] = v[k];
+            if (lane == 0) {
+                rr->dst[slot] = d0;
+                rr->tag[slot] = tj;
+                rr->list_id[slot] = list_id;
+                wave::lds_store(&rr->flag[slot], r + 1);  // release: the row and its fields first
+            }
+            *nrows = r + 1;
+            *bytes += kRow;
+        }
+    }
+    return true;
+}
+
+// (Instantiated only for functors that stage rows.)
+template <bool kOn>
+__device__ __forceinline__ bool _sg_stage_rows_kb(uint32_t kb, const SGTaskQueue* ring, uint32_t pool_offset,
+                                                  uint32_t count, uint32_t list_id, _SGRowRing* rr, int* nrows,
+                                                  uint64_t* bytes) {
+    if constexpr (!kOn) {
+        return false;
+    } else {
+        switch (kb) {
+#define GFD_SG_STAGE_CASE(n) \
+    case n: return _sg_stage_rows<n>(ring, pool_offset, count, list_id, rr, nrows, bytes);
+            GFD_SG_STAGE_CASE(1) GFD_SG_STAGE_CASE(2) GFD_SG_STAGE_CASE(3) GFD_SG_STAGE_CASE(4) GFD_SG_STAGE_CASE(5)
+            GFD_SG_STAGE_CASE(6) GFD_SG_STAGE_CASE(7) GFD_SG_STAGE_CASE(8) GFD_SG_STAGE_CASE(9) GFD_SG_STAGE_CASE(10)
+            GFD_SG_STAGE_CASE(11) GFD_SG_STAGE_CASE(12) GFD_SG_STAGE_CASE(13) GFD_SG_STAGE_CASE(14)
+#undef GFD_SG_STAGE_CASE
+            default: return false;
+        }
+    }
+}
+
 template <typename ComputeFn>
 __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTaskQueue* sq, ComputeFn compute_fn) {
     (void)dq;
@@ -257,6 +424,11 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
     __shared__ int terminated;
     __shared__ _SGJob job;
     __shared__ wave::BatchLds batch_lds[1 + SG_MAX_HELPERS];  // per transfer wave
+    constexpr bool kStaging = _stages_rows<ComputeFn>::value;
+    __shared__ typename std::conditional<kStaging, _SGRowRing, _SGNoRowRing>::type rr;
+    // Staged-row mode (kStagesRows functors with a row size the ring takes).
+    const uint32_t staged_bytes = _staged_row_bytes(compute_fn);
+    const bool staged = staged_bytes != 0;
     const int w = wave::wave_id();
     const int lane = wave::lane_id();
     if (threadIdx.x < 2) {
@@ -268,6 +440,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
         terminated = 0;
         job.seq = 0;
     }
+    if (kStaging && threadIdx.x < SG_ROW_SLOTS) rr.flag[threadIdx.x] = 0;
     __syncthreads();
 
     SGDeviceCounters* cnt = sg_device_counters(sq);
@@ -277,11 +450,12 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
     int helpers = (int)__hip_atomic_load(&cnt->helpers, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (helpers > SG_MAX_HELPERS) helpers = SG_MAX_HELPERS;
     if (helpers > nwaves - 2) helpers = nwaves > 2 ? nwaves - 2 : 0;
+    if (staged) helpers = 0;  // the leader stages rows itself; helper waves return at once
     const int first_helper = nwaves - helpers;
     const int unroll = wave::transfer_unroll(gridDim.x * (1u + (unsigned)helpers));
     // Compute waves 1 .. ncompute (never into the helpers).
     int ncompute = 1;
-    if (_shares_lists<ComputeFn>::value) {
+    if (_shares_lists<ComputeFn>::value || staged) {
         ncompute = (int)__hip_atomic_load(&cnt->compute_waves, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (ncompute > SG_MAX_COMPUTE) ncompute = SG_MAX_COMPUTE;
         if (ncompute > first_helper - 1) ncompute = first_helper - 1;
@@ -303,9 +477,10 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
         const uint64_t gpu_first =
             list_base + __hip_atomic_load(&cnt->host_lists, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         uint64_t nlists = 0;
+        int nrows = 0;  // rows staged (staged-row mode)
         for (uint64_t iter = 0;; iter++) {
             const int s = (int)(iter & 1);
-            if (has_compute && !wave::wait_lds_eq(&slots[s].free, 1)) {
+            if (has_compute && !staged && !wave::wait_lds_eq(&slots[s].free, 1)) {
                 if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_SLOT_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
@@ -325,6 +500,17 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             if (lane == 0) wave::store_system(&l.sequence, 0);  // claimed
             const uint64_t t_ready = (uint64_t)wall_clock64();
 
+            uint64_t bytes = 0;
+            if (staged) {
+                if (!_sg_stage_rows_kb<kStaging>(staged_bytes / 1024, ring, pool_offset, count, list_id,
+                                                 reinterpret_cast<_SGRowRing*>(&rr), &nrows, &bytes)) {
+                    if (lane == 0)
+                        __hip_atomic_fetch_or(&cnt->error, SG_ERR_SLOT_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                wave::acquire_agent();
+                wave::release_agent();  // the list's bytes are visible device-wide
+            } else {
             // Publish the copy job, copy batches with the helpers, wait for
             // every batch and every helper's acknowledgement.
             if (lane == 0) {
@@ -338,7 +524,6 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
                 wave::lds_store(&job.seq, (int)iter + 1);
             }
             int mine = 0;
-            uint64_t bytes = 0;
             const int nbatches =
                 _sg_copy_batches(&job, ring, pool_offset, count, unroll, &batch_lds[0], &mine, &bytes);
             if (lane == 0) {
@@ -353,6 +538,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             bytes = __hip_atomic_load(&job.bytes, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
             wave::acquire_agent();
             wave::release_agent();  // the list's bytes (all transfer waves') are visible device-wide
+            }
             nlists++;
             if (lane == 0) {
                 if (trace && idx - list_base < trace_cap)
@@ -361,11 +547,19 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
                     __hip_atomic_store(&sq->d_list_done[list_id], 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
                 sg::atomic_add_dev(&cnt->entries_done, count);
                 sg::atomic_add_dev(&cnt->bytes_done, bytes);
-                __hip_atomic_fetch_add(&cnt->lists_done, 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t landed =
+                    __hip_atomic_fetch_add(&cnt->lists_done, 1ull, __ATOMIC_SEQ_CST, __HIP_MEMORY_SCOPE_AGENT) + 1;
                 wave::store_system(&l.done, idx + 1);
                 // Host code and host submitters read the marker in the host queue.
                 if (ring != sq) wave::store_system(&sq->lists[idx % MAX_SG_LISTS].done, idx + 1);
-                if (has_compute) {
+                // The launch's last list (sg_stop_when_landed): end the launch.
+                const uint64_t stop_at = __hip_atomic_load(&cnt->stop_at, __ATOMIC_SEQ_CST, __HIP_MEMORY_SCOPE_AGENT);
+                if (stop_at != 0 && landed >= stop_at) {
+                    __hip_atomic_store(const_cast<uint32_t*>(&sq->terminate), 1u, __ATOMIC_RELEASE,
+                                       __HIP_MEMORY_SCOPE_SYSTEM);
+                    __hip_atomic_store(&cnt->stop, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                if (has_compute && !staged) {
                     slots[s].ring = ring;
                     slots[s].list_id = list_id;
                     slots[s].count = count;
@@ -381,7 +575,9 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             wave::lds_store(&terminated, 1);
             if (trace && blockIdx.x < __hip_atomic_load(&cnt->trace_blocks, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
                 reinterpret_cast<SGTraceBlock*>(trace + trace_cap)[blockIdx.x] =
-                    SGTraceBlock{t_start, (uint64_t)wall_clock64(), nlists, 0};
+                    SGTraceBlock{t_start, (uint64_t)wall_clock64(), nlists,
+                                 ((uint64_t)(uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32) |
+                                     (uint32_t)__builtin_amdgcn_s_getreg((31 << 11) | 4)};
         }
     } else if (helpers > 0 && w >= first_helper) {
         // ---------------- transfer helper: copies batches of the leader's
@@ -391,12 +587,13 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
         for (int want = 1;;) {
             int seq = 0;
             const uint64_t t0 = wall_clock64();
-            for (;;) {
+            for (uint32_t n = 1;; n++) {
                 seq = wave::lds_load(&job.seq);
                 if (seq < 0 || seq >= want) break;
                 // The leader publishes -1 when it stops, deadline included;
                 // a second past it means the leader itself is stuck.
-                if (wall_clock64() - t0 > limit || (deadline && sg::past(deadline + 100000000ull))) {
+                if ((n & (kClockPolls - 1)) == 0 &&
+                    (wall_clock64() - t0 > limit || (deadline && sg::past(deadline + 100000000ull)))) {
                     if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_HELPER_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     seq = -1;
                     break;
@@ -416,6 +613,49 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             }
             want = seq + 1;
         }
+    } else if (has_compute && staged && w >= 1 && w <= ncompute) {
+        // ---------------- compute wave(s), staged rows: wave w takes the
+        // workgroup's staged rows w - 1, w - 1 + ncompute, ...; bounded like
+        // the list-mode compute wave below.
+        if constexpr (kStaging) {
+            const uint64_t limit = _idle_limit_ticks(sq) + 100000000ull;
+            const uint64_t deadline = sg::launch_deadline(sq);
+            bool first = true;
+            for (int i = w - 1;; i += ncompute) {
+                const int s = i % SG_ROW_SLOTS;
+                bool ready = false;
+                const uint64_t t0 = wall_clock64();
+                for (uint32_t n = 1;; n++) {
+                    if (wave::lds_load(&rr.flag[s]) == i + 1) {
+                        ready = true;
+                        break;
+                    }
+                    if (wave::lds_load(&terminated)) {  // every row is staged by now: row i is here or never comes
+                        ready = wave::lds_load(&rr.flag[s]) == i + 1;
+                        break;
+                    }
+                    if ((n & (kClockPolls - 1)) == 0 &&
+                        (wall_clock64() - t0 > limit || (deadline && sg::past(deadline + 100000000ull)))) {
+                        if (lane == 0)
+                            __hip_atomic_fetch_or(&cnt->error, SG_ERR_COMPUTE_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                if (!ready) break;
+                SGRowView view;
+                view.data = rr.data[s];
+                view.dst = rr.dst[s];
+                view.bytes = staged_bytes;
+                view.tag = rr.tag[s];
+                view.list_id = rr.list_id[s];
+                view.lane_id = lane;
+                view.first = first;
+                view.slot = &rr.flag[s];
+                compute_fn.row(view);
+                first = false;
+            }
+        }
     } else if (has_compute && w >= 1 && w <= ncompute) {
         // ---------------- compute wave(s): bounded by the transfer wave's
         // idle limit (plus 1 s), the longest the transfer wave can stay silent.
@@ -426,7 +666,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
             const int want = (int)(k / 2) + 1;
             bool ready = false;
             const uint64_t t0 = wall_clock64();
-            for (;;) {
+            for (uint32_t n = 1;; n++) {
                 if (wave::lds_load(&slots[s].seq) == want) {
                     ready = true;
                     break;
@@ -435,7 +675,8 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
                     ready = wave::lds_load(&slots[s].seq) == want;
                     break;
                 }
-                if (wall_clock64() - t0 > limit || (deadline && sg::past(deadline + 100000000ull))) {
+                if ((n & (kClockPolls - 1)) == 0 &&
+                    (wall_clock64() - t0 > limit || (deadline && sg::past(deadline + 100000000ull)))) {
                     if (lane == 0) __hip_atomic_fetch_or(&cnt->error, SG_ERR_COMPUTE_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
                 }

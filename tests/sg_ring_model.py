@@ -14,11 +14,18 @@ Submitter wave (one per workgroup), for each of its lists:
   alloc   slot = list_alloc++                           (sg_alloc_list)
   slot    wait until done[slot % R] >= slot - R + 1     (sg_wait_slot_free)
   commit  seq[slot % R] = slot + 1, a release           (sg_commit_list)
-Submitter 0 then waits until lists_done == total and raises terminate and
-stop (sg_wait_gpu_lists_done + sg_terminate_all_landed).  Lists reach the
-submitters either as the MoE kernel deals them (list L to submitter
-L mod S, each in order: "mod") or from a shared counter ("shared": the
-variant that was tried and taken out).
+With place "fixed" (the MoE kernel when the launch's lists fit the ring:
+total < R), list L goes to ring index L with no space, allocation or slot
+wait: the submitter commits seq[L % R] = L + 1 directly.
+stop "wait": submitter 0 then waits until lists_done == total and raises
+terminate and stop (sg_wait_gpu_lists_done + sg_terminate_all_landed).
+stop "lander" (sg_stop_when_landed): submitter 0 sets stop_at = total and,
+if lists_done >= total already, raises them itself; the transfer wave whose
+landing brings lists_done to stop_at raises them otherwise (each of these
+steps is one atomic move here, as the kernels make them sequentially
+consistent).  Lists reach the submitters either as the MoE kernel deals
+them (list L to submitter L mod S, each in order: "mod") or from a shared
+counter ("shared": the variant that was tried and taken out).
 
 Transfer wave, per list:
   claim   idx = list_claim++
@@ -30,6 +37,8 @@ Transfer wave, per list:
           exits; any wave exits once stop is set
   read    the header is read; the claim store seq[idx % R] = 0
   land    done[idx % R] = idx + 1, a system-scope release; lists_done++
+          (stop "lander": then terminate and stop if lists_done reached a
+          nonzero stop_at)
 
 claim_store "ordered": the claim store is performed before the release of
 done (a store followed by a release in the same wave).  "reorderable": it
@@ -48,29 +57,35 @@ CLAIM, WAIT, READ, LAND, WEND = range(5)                 # transfer wave
 
 
 class State:
-    __slots__ = ("la", "lc", "lk", "ld", "stop", "term", "nid", "seq", "done", "landed", "subs", "waves")
+    __slots__ = ("la", "lc", "lk", "ld", "stop", "term", "nid", "sa", "seq", "done", "landed", "subs", "waves")
 
     def clone(self):
         s = State.__new__(State)
         s.la, s.lc, s.lk, s.ld, s.stop, s.term, s.nid = self.la, self.lc, self.lk, self.ld, self.stop, self.term, self.nid
+        s.sa = self.sa
         s.seq, s.done, s.landed = list(self.seq), list(self.done), list(self.landed)
         s.subs, s.waves = [list(x) for x in self.subs], [list(x) for x in self.waves]
         return s
 
     def key(self):
-        return (self.la, self.lc, self.lk, self.ld, self.stop, self.term, self.nid, tuple(self.seq), tuple(self.done),
+        return (self.la, self.lc, self.lk, self.ld, self.stop, self.term, self.nid, self.sa, tuple(self.seq), tuple(self.done),
                 tuple(self.landed), tuple(map(tuple, self.subs)), tuple(map(tuple, self.waves)))
 
 
 class Model:
-    def __init__(self, ring, submitters, waves, total, assign="mod", claim_store="ordered"):
+    def __init__(self, ring, submitters, waves, total, assign="mod", claim_store="ordered", place="alloc",
+                 stop="wait"):
         assert assign in ("mod", "shared") and claim_store in ("ordered", "reorderable")
+        # "lander_unchecked": a planted mistake for the tests, submitter 0
+        # setting stop_at without checking whether every list has landed.
+        assert place in ("alloc", "fixed") and stop in ("wait", "lander", "lander_unchecked")
+        assert place == "alloc" or total < ring, "fixed places need the launch's lists to fit the ring"
         self.R, self.S, self.W, self.total = ring, submitters, waves, total
-        self.assign, self.claim_store = assign, claim_store
+        self.assign, self.claim_store, self.place, self.stop = assign, claim_store, place, stop
 
     def initial(self):
         s = State()
-        s.la = s.lc = s.lk = s.ld = s.stop = s.term = s.nid = 0
+        s.la = s.lc = s.lk = s.ld = s.stop = s.term = s.nid = s.sa = 0
         s.seq, s.done, s.landed = [0] * self.R, [0] * self.R, [0] * self.total
         s.subs = [[NEXT, -1, k, -1] for k in range(self.S)]  # pc, list, next own list (mod), slot
         s.waves = [[CLAIM, -1, -1] for _ in range(self.W)]   # pc, idx, slot of a claim store in flight
@@ -85,7 +100,12 @@ class Model:
                 sub[1], sub[2] = sub[2], sub[2] + self.S
             else:
                 sub[1], s.nid = s.nid, s.nid + 1
-            sub[0] = SPACE if sub[1] < self.total else (FINAL if i == 0 else END)
+            if sub[1] >= self.total:
+                sub[0] = FINAL if i == 0 else END
+            elif self.place == "fixed":
+                sub[3], sub[0] = sub[1], COMMIT
+            else:
+                sub[0] = SPACE
         elif pc == SPACE:
             if s.la - s.ld >= R - 1:
                 return False
@@ -101,6 +121,12 @@ class Model:
             s.seq[sub[3] % R] = sub[3] + 1
             sub[0], sub[3] = NEXT, -1
         elif pc == FINAL:
+            if self.stop in ("lander", "lander_unchecked"):
+                s.sa = self.total
+                if self.stop == "lander" and s.ld >= self.total:
+                    s.term, s.stop = 1, 1
+                sub[0] = END
+                return True
             if s.ld < self.total:
                 return False
             s.term, s.stop, sub[0] = 1, 1, END
@@ -156,6 +182,8 @@ class Model:
             if idx < self.total:
                 s.landed[idx] += 1
             s.ld += 1
+            if self.stop != "wait" and s.sa and s.ld >= s.sa:
+                s.term, s.stop = 1, 1
             w[0], w[1] = CLAIM, -1
         else:
             return False

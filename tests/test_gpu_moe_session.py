@@ -169,21 +169,26 @@ def test_moe_session_trace():
         sess.close()
 
 
-def test_moe_session_skips_out_of_range_rows():
+@pytest.mark.parametrize("with_norm,cw", [(False, 1), (True, 1), (True, 3)])
+def test_moe_session_skips_out_of_range_rows(with_norm, cw):
     """A routing entry outside the token range is reported (error bit 16) and
-    its row skipped; every other row lands."""
-    m = Moe(64, 8, 512)
+    its row skipped (an empty entry, which the staged-row RMSNorm never
+    sees); every other row lands, and with the RMSNorm every other row is
+    normalised."""
+    print("moe session with one out-of-range row, norm=%s compute waves=%d" % (with_norm, cw), flush=True)
+    m = Moe(64, 8, 1024)
     m.route()
     rt = m.row_token.copy()
     rt[5] = m.T + 3
     m.d_rows.upload(rt)
     n = 2 * m.T
-    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=1, num_blocks=2, idle_limit_ms=10000)
+    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=cw, num_blocks=2, idle_limit_ms=10000)
     try:
         m.d_dst.fill(0xCD)
+        m.d_out.fill(0xCD)
         sess.reset()
         sess.launch_moe(m.host.ptr, m.stride, m.T, m.d_offsets.ptr, m.d_rows.ptr, m.E, n, m.row_bytes, m.d_dst.ptr,
-                        None, None, 1e-6, 16)
+                        m.d_out.ptr if with_norm else None, m.d_weight.ptr, 1e-6, 16)
         gfd_amd.synchronize()
         with pytest.raises(gfd_amd.GfdError):
             sess.synchronize(0)
@@ -193,6 +198,40 @@ def test_moe_session_skips_out_of_range_rows():
         keep = np.arange(n) != 5
         assert (got[keep] == rows[keep]).all()
         assert (got[5].view(np.uint8) == 0xCD).all()
+        out = m.d_out.download()
+        if not with_norm:
+            assert (out == 0xCD).all()
+            return
+        y = out[:n * m.row_bytes].view(np.uint16).reshape(n, m.dim)
+        assert (y[5].view(np.uint8) == 0xCD).all()
+        ref = oracle.rmsnorm_rows(oracle.bf16_to_f32(rows[keep]), oracle.bf16_to_f32(m.weight), 1e-6)
+        yk = oracle.bf16_to_f32(y[keep])
+        assert np.all(np.abs(yk - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-6)
+    finally:
+        sess.close()
+
+
+@pytest.mark.parametrize("staged", ["1", "0"])
+def test_moe_session_rmsnorm_staged_and_list_mode(staged, monkeypatch):
+    """The RMSNorm consumer both ways: rows staged in LDS by the transfer wave
+    (the default) and per landed list read back from HBM
+    (GFD_SG_STAGED_ROWS=0), at the full 14 KiB rows and 3 compute waves;
+    rows byte-exact, RMSNorm within bf16 of the fp32 oracle."""
+    print("moe session RMSNorm, GFD_SG_STAGED_ROWS=%s" % staged, flush=True)
+    monkeypatch.setenv("GFD_SG_STAGED_ROWS", staged)
+    m = Moe(4096, 64, 7168)
+    m.route()
+    n = 2 * m.T
+    rows = m.expected_rows()
+    ref = oracle.rmsnorm_rows(oracle.bf16_to_f32(rows), oracle.bf16_to_f32(m.weight), 1e-6)
+    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=3, num_blocks=32, idle_limit_ms=10000)
+    try:
+        st = run_session(m, sess, True, 24)
+        assert st["error_bits"] == 0 and st["units_done"] == n
+        got = m.d_dst.download()
+        assert (got[:n * m.row_bytes].view(np.uint16).reshape(n, m.dim) == rows).all()
+        y = oracle.bf16_to_f32(m.d_out.download()[:n * m.row_bytes].view(np.uint16).reshape(n, m.dim))
+        assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-6)
     finally:
         sess.close()
 

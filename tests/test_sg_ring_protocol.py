@@ -11,7 +11,13 @@ include/gfd/sg_device_primitives.h and include/gfd/sg_warp_spec.h).
   after the slot's next list was committed and erases that commit.
 - Random interleavings at the shape of the MoE session launch that once hung
   (1088 lists over the 512-slot ring, 64 submitters, 64 transfer waves),
-  with actors of very different speeds, all end."""
+  with actors of very different speeds, all end.
+- The MoE kernel's current form when its lists fit the ring: list L placed
+  at ring index L with no allocation or waits, and the transfer wave that
+  lands the last list ending the launch (sg_stop_when_landed).  Every
+  interleaving ends, also with the lander stop over a reused ring; without
+  the submitter's own check of lists_done (all lists landed before stop_at
+  was set) the search finds the launch that never ends."""
 import pytest
 
 from sg_ring_model import Model
@@ -41,3 +47,26 @@ def test_unordered_claim_store_can_erase_the_next_commit():
 def test_full_size_launch_random_interleavings_end(assign, seed):
     steps, outcome = Model(512, 64, 64, 1088, assign, "ordered").simulate(seed)
     assert outcome == "ok", (assign, seed, steps)
+
+
+@pytest.mark.parametrize("place,ring,total", [("fixed", 8, 7), ("alloc", 3, 7)])
+def test_lander_stop_never_deadlocks(place, ring, total):
+    m = Model(ring, 2, 2, total, "mod", "ordered", place=place, stop="lander")
+    states, problem = m.explore()
+    assert problem is None, (problem[0], m.replay(problem[1])[1])
+    assert states > 1_000
+
+
+def test_lander_stop_needs_the_submitters_own_check():
+    m = Model(8, 2, 2, 3, "mod", "ordered", place="fixed", stop="lander_unchecked")
+    _, problem = m.explore()
+    assert problem is not None and problem[0] == "deadlock"
+    s, lines = m.replay(problem[1])
+    # Every list landed before stop_at was set, so no lander raised stop.
+    assert s.ld == m.total and s.sa == m.total and not s.stop, "\n".join(lines)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_moe_launch_with_fixed_places_random_interleavings_end(seed):
+    steps, outcome = Model(512, 32, 32, 370, "mod", "ordered", place="fixed", stop="lander").simulate(seed)
+    assert outcome == "ok", (seed, steps)
