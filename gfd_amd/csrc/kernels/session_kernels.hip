@@ -86,25 +86,52 @@ struct TokenRmsSin {
     __device__ void operator()(ChunkView c) const {
         const uint32_t nf = c.token_size / 4;
         const uint32_t lane = (uint32_t)c.lane_id;
-        if (((uintptr_t)c.base_ptr & 15) == 0 && (c.token_size & 15) == 0 && nf / 4 <= 64u * kRegVecs) {
+        if (((uintptr_t)c.base_ptr & 15) == 0 && (c.token_size & 15) == 0 && nf >= 4 && nf / 4 <= 64u * kRegVecs) {
             const uint32_t nv = nf / 4;
             for (uint32_t i = 0; i < c.size; i++) {
                 const float4* t4 = c.data<float4>((int)i);
+                // Each pass reads the token in batches of kBatch vectors per
+                // lane, every load of a batch issued before the first is used:
+                // the index is clamped instead of guarded (a guarded load sits
+                // in a block of its own and waits for all earlier loads, which
+                // left one 16-byte load in flight per lane: a token's two
+                // passes took ~32 round trips to memory, 8 now).  Batches of 4:
+                // with 8 (or 8 in the second pass) the compute waves' bursts
+                // slowed the transfer wave's host reads when chunks are small
+                // (64-token tiles of 8-token chunks: 2472-2475 against
+                // 2431-2442 us), while 4 keeps the example's 32-token chunks
+                // at 2470-2475 us (2504-2516 before).
+                constexpr int kBatch = 4;
                 float ss = 0.f;
 #pragma unroll
-                for (int j = 0; j < kRegVecs; j++) {
-                    const uint32_t k = lane + 64u * (uint32_t)j;
-                    const float4 v = k < nv ? t4[k] : make_float4(0.f, 0.f, 0.f, 0.f);
-                    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+                for (int j0 = 0; j0 < kRegVecs; j0 += kBatch) {
+                    float4 x[kBatch];
+#pragma unroll
+                    for (int j = 0; j < kBatch; j++) {
+                        const uint32_t k = lane + 64u * (uint32_t)(j0 + j);
+                        x[j] = t4[k < nv ? k : nv - 1];
+                    }
+#pragma unroll
+                    for (int j = 0; j < kBatch; j++)
+                        if (lane + 64u * (uint32_t)(j0 + j) < nv)
+                            ss += x[j].x * x[j].x + x[j].y * x[j].y + x[j].z * x[j].z + x[j].w * x[j].w;
                 }
                 const float r = rsqrtf(wave_sum(ss) / (float)nf + 1e-6f);
                 float acc = 0.f;
-#pragma unroll 2
-                for (int j = 0; j < kRegVecs; j++) {
-                    const uint32_t k = lane + 64u * (uint32_t)j;
-                    const float4 v = k < nv ? t4[k] : make_float4(0.f, 0.f, 0.f, 0.f);
-                    const float a = v.x * r, b = v.y * r, d = v.z * r, e = v.w * r;
-                    acc += sinf(a) * a + sinf(b) * b + sinf(d) * d + sinf(e) * e;
+#pragma unroll
+                for (int j0 = 0; j0 < kRegVecs; j0 += kBatch) {
+                    float4 x[kBatch];
+#pragma unroll
+                    for (int j = 0; j < kBatch; j++) {
+                        const uint32_t k = lane + 64u * (uint32_t)(j0 + j);
+                        x[j] = t4[k < nv ? k : nv - 1];
+                    }
+#pragma unroll
+                    for (int j = 0; j < kBatch; j++) {
+                        if (lane + 64u * (uint32_t)(j0 + j) >= nv) continue;
+                        const float a = x[j].x * r, b = x[j].y * r, d = x[j].z * r, e = x[j].w * r;
+                        acc += sinf(a) * a + sinf(b) * b + sinf(d) * d + sinf(e) * e;
+                    }
                 }
                 acc = wave_sum(acc);
                 if (lane == 0) out[c.global_idx((int)i)] = acc;
