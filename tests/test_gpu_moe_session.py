@@ -151,6 +151,10 @@ def test_moe_session_trace():
             assert (used["claimed"] <= used["ready"]).all() and (used["ready"] <= used["landed"]).all()
             assert (used["block"] < 32).all()
             assert int(blocks["lists"].sum()) == total
+            # Where each workgroup ran (XCC_ID << 32 | HW_ID): MI355X has 8 XCCs,
+            # and 32 workgroups are spread over more than one.
+            xcc = (blocks["hw"] >> np.uint64(32)) & np.uint64(0xF)
+            assert (xcc < 8).all() and len(set(xcc.tolist())) > 1, blocks["hw"]
             for b in range(32):
                 mine = used[used["block"] == b]
                 assert len(mine) == int(blocks["lists"][b])
