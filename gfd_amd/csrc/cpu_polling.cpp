@@ -534,6 +534,19 @@ void CpuPollingThread::polling_loop() {
             if (n == 0) {
                 if (gather_) gather_->prewake();  // wake workers while the batch is read
                 trace(TRACE_BATCH_FIRST, (uint32_t)(read % QUEUE_SIZE), read);
+                // The batch's ranges are looked up afresh (see flush_batch),
+                // now for its first entry: the runtime lookups (a few us) then
+                // overlap the writing of the rest of the batch instead of
+                // delaying its flush.
+                ce_manager_.forget_pinned_range();
+                ce_manager_.host_source_ok(reinterpret_cast<const void*>((uintptr_t)d->src_addr), d->size);
+                queue_dst_lo_ = queue_dst_hi_ = 0;
+                uint64_t base = 0, bytes = 0;
+                if (gfd_hip_device_range(d->dst_addr, &base, &bytes)) {
+                    queue_dst_lo_ = base;
+                    queue_dst_hi_ = base + bytes;
+                }
+                batch_checked_ = true;
             }
             do {
                 // The ring lines were last written by the GPU, so each is a
@@ -590,9 +603,13 @@ void CpuPollingThread::flush_batch(Descriptor* batch, int& count, uint32_t& or_f
     if (count == 0) return;
     // A source range found pinned for an earlier batch may have been freed
     // and reused since: batches look their caller-owned sources up again
-    // (and device ranges too).
-    ce_manager_.forget_pinned_range();
-    queue_dst_lo_ = queue_dst_hi_ = 0;
+    // (and device ranges too), when their first descriptor is taken in the
+    // polling loop, or here.
+    if (!batch_checked_) {
+        ce_manager_.forget_pinned_range();
+        queue_dst_lo_ = queue_dst_hi_ = 0;
+    }
+    batch_checked_ = false;
     const uint64_t cur_read = queue_->read_idx;
     if (trace_on_.load(std::memory_order_relaxed)) {
         uint64_t bytes = 0;

@@ -359,6 +359,9 @@ private:
     bool worker_wanted_ = false;  // GFD_ZC_WORKER=1: set up with the copy engines
     size_t worker_queue_max_bytes_ = 4u << 20;
     uint64_t queue_dst_lo_ = 0, queue_dst_hi_ = 0;  // Queue path: last device allocation found
+    // The open batch's host and device ranges were looked up when its first
+    // descriptor was taken (the flush then keeps them).
+    bool batch_checked_ = false;
     uint64_t worker_posted_ = 0;     // Queue path: the last job posted to the worker
     uint64_t worker_done_seen_ = 0;  // and the last one the completion slots saw done
     std::vector<uint32_t> tile_scratch_;
