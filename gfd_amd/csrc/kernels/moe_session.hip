@@ -209,6 +209,9 @@ struct MoeLists {
     // Where the lists' headers and entries go: the session's HBM queue
     // (SGDeviceCounters::dev_ring) when they fit, else the host queue.
     gfd::SGTaskQueue* ring;
+    // The session's device counters (sg_device_counters of the host queue),
+    // so no wave reads the host queue to find them.
+    gfd::SGDeviceCounters* cnt;
 };
 
 // Submitter wave: posts this workgroup's share of the lists (list L goes to
@@ -220,7 +223,12 @@ struct MoeLists {
 __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
     using namespace gfd;
     const int lane = wave::lane_id();
-    SGDeviceCounters* cnt = sg_device_counters(sq);
+    SGDeviceCounters* const cnt = m.cnt;
+    // Issued first, beside the offsets' read: the list places depend on them.
+    const uint64_t gpu_first =
+        __hip_atomic_load(&cnt->list_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) +
+        __hip_atomic_load(&cnt->host_lists, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t entry_first = __hip_atomic_load(&cnt->entry_first, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // Lists per expert (one lane per expert, at most 64 experts): `full`
     // lists of rows_per_list rows and at most one shorter one with the rest.
     // Full lists get the first ids (expert-major), the shorter ones the last,
@@ -272,10 +280,6 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
     // space is short), so a transfer wave waiting for index gpu_first + L
     // always sees it committed.  Workgroup 0 advances the allocation
     // counters past all of them once, for the host's accounting.
-    const uint64_t gpu_first =
-        __hip_atomic_load(&cnt->list_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) +
-        __hip_atomic_load(&cnt->host_lists, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t entry_first = __hip_atomic_load(&cnt->entry_first, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (fits && blockIdx.x == 0 && lane == 0) {
         sg::atomic_add_dev(&cnt->list_alloc, total);
         sg::atomic_add_dev(&cnt->entry_alloc, (uint64_t)rows);
@@ -335,7 +339,7 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
     // so stop is raised only once nothing is left to copy, and no wave polls
     // for it meanwhile.  (A list that never lands leaves the transfer waves
     // to the launch's deadline.)
-    if (blockIdx.x == 0) sg::sg_stop_when_landed(sq, total);
+    if (blockIdx.x == 0) sg::sg_stop_when_landed(sq, total, cnt);
 }
 
 // Wave 0 transfer, waves 1 .. C compute (C = 1 unless the functor shares
@@ -343,6 +347,9 @@ __device__ void moe_submit(gfd::SGTaskQueue* sq, const MoeLists& m) {
 template <typename F>
 __global__ __launch_bounds__(8 * 64) void sg_moe_kernel(gfd::DescriptorQueue* dq, gfd::SGTaskQueue* sq, F fn,
                                                         MoeLists m, int submitter_wave) {
+    // (The transfer waves find the counters through sq, one host read per
+    // wave as it starts: passing m.cnt here costs the staged-row loop two
+    // spilled registers.)
     gfd::sg_warp_spec::_sg_transfer_warp_loop(dq, sq, fn);  // the submitter wave returns from it
     if (gfd::wave::wave_id() == submitter_wave) moe_submit(sq, m);
 }
@@ -378,7 +385,8 @@ extern "C" int gfd_sg_session_launch_moe(gfd_sg_session_t s, const void* host_ba
     if (!ring) ring = p->get_sg_queue();
     p->before_launch(stream, helpers, compute, p->idle_limit_ms(), ring);
     const MoeLists m{(uint64_t)(uintptr_t)host_base, token_stride, (uint64_t)(uintptr_t)dst, offsets, row_token,
-                     num_experts, num_tokens, num_rows, row_bytes, rows_per_list, fits ? 1 : 0, ring};
+                     num_experts, num_tokens, num_rows, row_bytes, rows_per_list, fits ? 1 : 0, ring,
+                     gfd::sg_device_counters(p->get_sg_queue())};
     const dim3 grid((unsigned)p->num_blocks()), block((unsigned)(2 + compute + helpers) * 64);
     const char* sr = std::getenv("GFD_SG_STAGED_ROWS");
     const int stage_rows = !(sr && sr[0] == '0');

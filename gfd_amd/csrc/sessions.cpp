@@ -347,6 +347,7 @@ void SGWarpSpecSession::before_launch(gfd_stream_t stream, int helper_waves, int
     c.helpers = (uint64_t)(helper_waves < 0 ? config_.transfer_helper_waves : helper_waves);
     c.compute_waves = (uint64_t)(compute_waves < 0 ? this->compute_waves() : compute_waves);
     c.host_lists = sq_->list_alloc_idx - consumed_lists_;
+    c.idle_ticks = sg_idle_ticks(sq_->idle_limit_ms);
     // Relative here (100 MHz ticks); the set-up kernel adds the GPU clock.
     c.deadline = (uint64_t)deadline_ms * 100000ull;
     c.dev_ring = gpu_ring && gpu_ring == dev_ring_ ? (uint64_t)(uintptr_t)gpu_ring : 0;
@@ -445,6 +446,7 @@ void SGWarpSpecSession::prepare_raw_launch() {
     c.entries_done = consumed_entries_;
     c.compute_waves = 1;  // the caller's kernel layout is its own: no helpers, one compute wave
     c.host_lists = sq_->list_alloc_idx - consumed_lists_;
+    c.idle_ticks = sg_idle_ticks(sq_->idle_limit_ms);
     const uint64_t d = (uint64_t)(uintptr_t)sq_->d_list_done;
     if (gfd_hip_memset_d8(d, 0, MAX_SG_LISTS * sizeof(uint64_t)) != 0 ||
         gfd_hip_memcpy_h2d((uint64_t)(uintptr_t)sg_device_counters(sq_), &c, sizeof(c)) != 0 ||

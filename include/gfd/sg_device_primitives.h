@@ -47,9 +47,10 @@ __device__ __forceinline__ uint64_t poll_dev(const uint64_t* p) {
 
 // The launch's deadline (SGDeviceCounters::deadline; 0: none), read once per
 // wait, and whether it has passed.
-__device__ __forceinline__ uint64_t launch_deadline(SGTaskQueue* sq) {
-    return __hip_atomic_load(&counters(sq)->deadline, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ uint64_t launch_deadline(SGDeviceCounters* c) {
+    return __hip_atomic_load(&c->deadline, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ uint64_t launch_deadline(SGTaskQueue* sq) { return launch_deadline(counters(sq)); }
 __device__ __forceinline__ bool past(uint64_t deadline) {
     return deadline != 0 && (uint64_t)wall_clock64() > deadline;
 }
@@ -233,10 +234,12 @@ __device__ __forceinline__ void sg_terminate(SGTaskQueue* sq) {
 // having one of them read terminate across PCIe.  Not for any other case: a
 // wave waiting for a committed list that no wave has seen yet would stop
 // without copying it.
-__device__ __forceinline__ void sg_terminate_all_landed(SGTaskQueue* sq) {
+// c: the launch's counters, when the caller has their address (else they
+// are found through the host queue, a read across PCIe).
+__device__ __forceinline__ void sg_terminate_all_landed(SGTaskQueue* sq, SGDeviceCounters* c = nullptr) {
     sg_terminate(sq);
     if (wave::lane_id() == 0)
-        __hip_atomic_store(&counters(sq)->stop, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&(c ? c : counters(sq))->stop, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // sg_wait_gpu_lists_done + sg_terminate_all_landed without a wave waiting:
@@ -245,15 +248,16 @@ __device__ __forceinline__ void sg_terminate_all_landed(SGTaskQueue* sq) {
 // sequentially consistent (this wave stores stop_at, then reads lists_done;
 // a lander adds to lists_done, then reads stop_at), so one of them sees the
 // launch complete even when every list lands before stop_at is set.
-__device__ __forceinline__ void sg_stop_when_landed(SGTaskQueue* sq, uint64_t gpu_lists) {
-    SGDeviceCounters* c = counters(sq);
-    const uint64_t want = sg_host_lists(sq) + gpu_lists;
+// c as for sg_terminate_all_landed.
+__device__ __forceinline__ void sg_stop_when_landed(SGTaskQueue* sq, uint64_t gpu_lists, SGDeviceCounters* c = nullptr) {
+    if (!c) c = counters(sq);
+    const uint64_t want = __hip_atomic_load(&c->host_lists, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + gpu_lists;
     int now = 0;
     if (wave::lane_id() == 0) {
         __hip_atomic_store(&c->stop_at, want, __ATOMIC_SEQ_CST, __HIP_MEMORY_SCOPE_AGENT);
         now = __hip_atomic_load(&c->lists_done, __ATOMIC_SEQ_CST, __HIP_MEMORY_SCOPE_AGENT) >= want;
     }
-    if (__builtin_amdgcn_readfirstlane(now)) sg_terminate_all_landed(sq);
+    if (__builtin_amdgcn_readfirstlane(now)) sg_terminate_all_landed(sq, c);
 }
 
 }  // namespace sg

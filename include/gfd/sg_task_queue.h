@@ -117,7 +117,12 @@ struct SGDeviceCounters {
     // launch (terminate + stop), as sg_terminate_all_landed would; 0: off.
     // Set by a GPU submitter with sg_stop_when_landed.
     uint64_t stop_at;
-    uint64_t _pad[4];
+    // The transfer and compute waves' idle limit in 100 MHz wall-clock ticks
+    // (SGTaskQueue::idle_limit_ms, 0 meaning 30 s, as the launch starts), so
+    // they need not read it from the host queue across PCIe; 0: not set,
+    // read it there.
+    uint64_t idle_ticks;
+    uint64_t _pad[3];
 };
 
 // One list of a traced launch, in wall-clock ticks (100 MHz): when its
@@ -159,6 +164,17 @@ static_assert(sizeof(SGDeviceCounters) == 192, "SGDeviceCounters is three cache 
 
 GFD_HD inline SGDeviceCounters* sg_device_counters(const SGTaskQueue* sq) {
     return reinterpret_cast<SGDeviceCounters*>(sq->d_list_done + MAX_SG_LISTS);
+}
+
+// The d_list_done array the counters follow (device code given the counters'
+// address needs no read of the host queue to find it).
+GFD_HD inline uint64_t* sg_list_done_words(SGDeviceCounters* c) {
+    return reinterpret_cast<uint64_t*>(c) - MAX_SG_LISTS;
+}
+
+// SGDeviceCounters::idle_ticks for an idle limit in ms (0 meaning 30 s).
+GFD_HD inline uint64_t sg_idle_ticks(uint32_t idle_limit_ms) {
+    return (uint64_t)(idle_limit_ms ? idle_limit_ms : 30000u) * 100000ull;
 }
 
 namespace sg_compat {

@@ -163,9 +163,11 @@ __device__ __forceinline__ uint32_t _staged_row_bytes(const F& f) {
     }
 }
 
-__device__ __forceinline__ uint64_t _idle_limit_ticks(const SGTaskQueue* sq) {
-    const uint32_t ms = wave::load_system32(&sq->idle_limit_ms);
-    return (uint64_t)(ms ? ms : 30000u) * 100000ull;  // 100 MHz wall clock
+// The idle limit in wall-clock ticks: from the counters in HBM when the
+// launch's set-up wrote it there, else from the host queue.
+__device__ __forceinline__ uint64_t _idle_limit_ticks(const SGTaskQueue* sq, SGDeviceCounters* cnt) {
+    const uint64_t t = __hip_atomic_load(&cnt->idle_ticks, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return t ? t : sg_idle_ticks(wave::load_system32(&sq->idle_limit_ms));
 }
 
 // Where ring index idx's header and entries are: the HBM queue of the
@@ -417,8 +419,12 @@ __device__ __forceinline__ bool _sg_stage_rows_kb(uint32_t kb, const SGTaskQueue
     }
 }
 
+// cnt_arg: the launch's counters (sg_device_counters(sq)) when the kernel
+// was given their address; otherwise each wave finds them through the host
+// queue, one read across PCIe as it starts.
 template <typename ComputeFn>
-__device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTaskQueue* sq, ComputeFn compute_fn) {
+__device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTaskQueue* sq, ComputeFn compute_fn,
+                                                       SGDeviceCounters* cnt_arg = nullptr) {
     (void)dq;
     __shared__ _SGSlot slots[2];
     __shared__ int terminated;
@@ -443,7 +449,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
     if (kStaging && threadIdx.x < SG_ROW_SLOTS) rr.flag[threadIdx.x] = 0;
     __syncthreads();
 
-    SGDeviceCounters* cnt = sg_device_counters(sq);
+    SGDeviceCounters* const cnt = cnt_arg ? cnt_arg : sg_device_counters(sq);
     const int nwaves = (int)(blockDim.x / wave::kWidth);
     const bool has_compute = nwaves > 1;
     // Helpers are the last `helpers` waves of the workgroup (never wave 0 or 1).
@@ -464,8 +470,8 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
 
     if (w == 0) {
         // ---------------- transfer wave (leader)
-        const uint64_t idle_ticks = _idle_limit_ticks(sq);
-        const uint64_t deadline = sg::launch_deadline(sq);
+        const uint64_t idle_ticks = _idle_limit_ticks(sq, cnt);
+        const uint64_t deadline = sg::launch_deadline(cnt);
         // Timeline of this launch's lists, when the session asks for one.
         const uint64_t t_start = (uint64_t)wall_clock64();
         SGTraceList* const trace =
@@ -544,7 +550,7 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
                 if (trace && idx - list_base < trace_cap)
                     trace[idx - list_base] = SGTraceList{t_claimed, t_ready, (uint64_t)wall_clock64(), blockIdx.x, list_id};
                 if (list_id < (uint32_t)MAX_SG_LISTS)
-                    __hip_atomic_store(&sq->d_list_done[list_id], 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(&sg_list_done_words(cnt)[list_id], 1ull, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
                 sg::atomic_add_dev(&cnt->entries_done, count);
                 sg::atomic_add_dev(&cnt->bytes_done, bytes);
                 const uint64_t landed =
@@ -582,8 +588,8 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
     } else if (helpers > 0 && w >= first_helper) {
         // ---------------- transfer helper: copies batches of the leader's
         // jobs; bounded like the compute wave.
-        const uint64_t limit = _idle_limit_ticks(sq) + 100000000ull;
-        const uint64_t deadline = sg::launch_deadline(sq);
+        const uint64_t limit = _idle_limit_ticks(sq, cnt) + 100000000ull;
+        const uint64_t deadline = sg::launch_deadline(cnt);
         for (int want = 1;;) {
             int seq = 0;
             const uint64_t t0 = wall_clock64();
@@ -618,8 +624,8 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
         // workgroup's staged rows w - 1, w - 1 + ncompute, ...; bounded like
         // the list-mode compute wave below.
         if constexpr (kStaging) {
-            const uint64_t limit = _idle_limit_ticks(sq) + 100000000ull;
-            const uint64_t deadline = sg::launch_deadline(sq);
+            const uint64_t limit = _idle_limit_ticks(sq, cnt) + 100000000ull;
+            const uint64_t deadline = sg::launch_deadline(cnt);
             bool first = true;
             for (int i = w - 1;; i += ncompute) {
                 const int s = i % SG_ROW_SLOTS;
@@ -659,8 +665,8 @@ __device__ __forceinline__ void _sg_transfer_warp_loop(DescriptorQueue* dq, SGTa
     } else if (has_compute && w >= 1 && w <= ncompute) {
         // ---------------- compute wave(s): bounded by the transfer wave's
         // idle limit (plus 1 s), the longest the transfer wave can stay silent.
-        const uint64_t limit = _idle_limit_ticks(sq) + 100000000ull;
-        const uint64_t deadline = sg::launch_deadline(sq);
+        const uint64_t limit = _idle_limit_ticks(sq, cnt) + 100000000ull;
+        const uint64_t deadline = sg::launch_deadline(cnt);
         for (uint64_t k = 0;; k++) {
             const int s = (int)(k & 1);
             const int want = (int)(k / 2) + 1;
