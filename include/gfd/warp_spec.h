@@ -75,6 +75,12 @@ struct TileContext {
 __device__ __forceinline__ TileDeviceCounters* tile_counters(TiledQueue* tq) {
     return reinterpret_cast<TileDeviceCounters*>(tq->d_tile_chunk_done + MAX_TILES);
 }
+// The d_tile_chunk_done array the counters follow.  tq lives in host memory:
+// deriving the array from the counters' address instead of reading
+// tq->d_tile_chunk_done again spares a round trip across PCIe per tile.
+__device__ __forceinline__ uint64_t* tile_done_words(TileDeviceCounters* cnt) {
+    return reinterpret_cast<uint64_t*>(cnt) - MAX_TILES;
+}
 
 struct _TileSlot {
     uint32_t tile;  // TILE_END: no more tiles
@@ -308,7 +314,7 @@ __device__ __forceinline__ void _tile_loop(TiledQueue* tq, void* gpu_buffer, con
             }
             if (lane == 0) {
                 if (tile < (uint64_t)MAX_TILES)
-                    __hip_atomic_store(&tq->d_tile_chunk_done[tile], (uint64_t)T, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(&tile_done_words(cnt)[tile], (uint64_t)T, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_fetch_add(&cnt->tiles_done, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
