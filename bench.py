@@ -59,7 +59,7 @@ DIRECT_ZC_HEAD = 2 << 20  # and the zero-copy head of larger staged lists
 # MoE through SGWarpSpecSession: workgroups, compute waves sharing each list
 # in the RMSNorm, rows per GPU-built list (swept: 24-128 workgroups, 1-3
 # compute waves, 2-64 rows per list).
-MOE_SESSION_BLOCKS, MOE_SESSION_COMPUTE_WAVES, MOE_SESSION_ROWS_PER_LIST = 32, 3, 24
+MOE_SESSION_BLOCKS, MOE_SESSION_COMPUTE_WAVES, MOE_SESSION_ROWS_PER_LIST = 40, 3, 48
 MOE_SESSION_HELPERS = -1  # transfer helper waves per workgroup (negative: the session's default rule)
 PD = ctypes.POINTER(ctypes.c_double)
 

@@ -751,7 +751,7 @@ class SGWarpSpecSession:
                                                       stream), "gfd_sg_session_launch_gpu_submit")
 
     def launch_moe(self, host_base, token_stride, num_tokens, d_offsets, d_row_token, num_experts, num_rows,
-                   row_bytes, d_dst, d_out=None, d_weight=None, eps=1e-6, rows_per_list=32, stream=None):
+                   row_bytes, d_dst, d_out=None, d_weight=None, eps=1e-6, rows_per_list=48, stream=None):
         """The MoE-routed gather with GPU-built lists (gfd_sg_session_launch_moe);
         the kernel ends itself once every list has landed."""
         _check(lib().gfd_sg_session_launch_moe(self._h, host_base, token_stride, num_tokens, d_offsets, d_row_token,

@@ -44,7 +44,7 @@ def run_session(m, sess, with_norm, rows_per_list, eps=1e-6):
                                                    (4096, 64, 7168, 2, 0, 1), (64, 8, 512, 4, 2, 1),
                                                    (300, 5, 1024, 7, 0, 1), (1000, 16, 2048, 1, 8, 1),
                                                    (4096, 64, 7168, 32, 0, 3), (4096, 64, 7168, 7, 4, 2),
-                                                   (300, 5, 1024, 1, 2, 3)])
+                                                   (300, 5, 1024, 1, 2, 3), (4096, 64, 7168, 48, 40, 3)])
 def test_moe_through_session(T, E, dim, rpl, blocks, cw):
     print("moe session T=%d E=%d dim=%d rows/list=%d blocks=%d compute waves=%d" % (T, E, dim, rpl, blocks, cw),
           flush=True)
@@ -228,9 +228,9 @@ def test_moe_session_rmsnorm_staged_and_list_mode(staged, monkeypatch):
     n = 2 * m.T
     rows = m.expected_rows()
     ref = oracle.rmsnorm_rows(oracle.bf16_to_f32(rows), oracle.bf16_to_f32(m.weight), 1e-6)
-    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=3, num_blocks=32, idle_limit_ms=10000)
+    sess = gfd_amd.SGWarpSpecSession(num_compute_warps=3, num_blocks=40, idle_limit_ms=10000)
     try:
-        st = run_session(m, sess, True, 24)
+        st = run_session(m, sess, True, 48)
         assert st["error_bits"] == 0 and st["units_done"] == n
         got = m.d_dst.download()
         assert (got[:n * m.row_bytes].view(np.uint16).reshape(n, m.dim) == rows).all()
