@@ -76,7 +76,8 @@ struct TokenSum {
 // (sin(0) * 0 = 0).  Other tokens take two lane-strided passes.  At 8192 x
 // 16 KiB with 128-token tiles of 32-token chunks this took the kernel from
 // 2761 to 2630 us.
-struct TokenRmsSin {
+template <bool kWholeToken>
+struct TokenRmsSinT {
     float* out;
     static constexpr int kRegVecs = 16;  // float4 per lane: 16 KiB per wave
     // Each token's result depends on that token alone: the framework may
@@ -88,6 +89,52 @@ struct TokenRmsSin {
         const uint32_t lane = (uint32_t)c.lane_id;
         if (((uintptr_t)c.base_ptr & 15) == 0 && (c.token_size & 15) == 0 && nf >= 4 && nf / 4 <= 64u * kRegVecs) {
             const uint32_t nv = nf / 4;
+            if constexpr (kWholeToken) {
+                // A kernel with room for 64 more registers per lane reads the
+                // whole token at once for the sum of squares: one round trip
+                // to HBM per token instead of four.  (The sinf pass then reads
+                // the token again from L2 in batches: its unrolled code is too
+                // large to keep the token in registers through it.)  A native
+                // vector type: an array of 16 of HIP's float4 wrappers would
+                // be placed in scratch memory.
+                typedef float f4 __attribute__((ext_vector_type(4)));
+                for (uint32_t i = 0; i < c.size; i++) {
+                    const f4* t4 = c.data<f4>((int)i);
+                    f4 x[kRegVecs];
+#pragma unroll
+                    for (int j = 0; j < kRegVecs; j++) {
+                        const uint32_t k = lane + 64u * (uint32_t)j;
+                        x[j] = t4[k < nv ? k : nv - 1];
+                    }
+                    float ss = 0.f;
+#pragma unroll
+                    for (int j = 0; j < kRegVecs; j++)
+                        if (lane + 64u * (uint32_t)j < nv)
+                            ss += x[j].x * x[j].x + x[j].y * x[j].y + x[j].z * x[j].z + x[j].w * x[j].w;
+                    const float r = rsqrtf(wave_sum(ss) / (float)nf + 1e-6f);
+                    const float4* v4 = c.data<float4>((int)i);
+                    float acc = 0.f;
+                    constexpr int kBatch = 4;
+#pragma unroll
+                    for (int j0 = 0; j0 < kRegVecs; j0 += kBatch) {
+                        float4 y[kBatch];
+#pragma unroll
+                        for (int j = 0; j < kBatch; j++) {
+                            const uint32_t k = lane + 64u * (uint32_t)(j0 + j);
+                            y[j] = v4[k < nv ? k : nv - 1];
+                        }
+#pragma unroll
+                        for (int j = 0; j < kBatch; j++) {
+                            if (lane + 64u * (uint32_t)(j0 + j) >= nv) continue;
+                            const float a = y[j].x * r, b = y[j].y * r, d = y[j].z * r, e = y[j].w * r;
+                            acc += sinf(a) * a + sinf(b) * b + sinf(d) * d + sinf(e) * e;
+                        }
+                    }
+                    acc = wave_sum(acc);
+                    if (lane == 0) out[c.global_idx((int)i)] = acc;
+                }
+                return;
+            }
             for (uint32_t i = 0; i < c.size; i++) {
                 const float4* t4 = c.data<float4>((int)i);
                 // Each pass reads the token in batches of kBatch vectors per
@@ -166,6 +213,7 @@ struct TokenRmsSin {
         }
     }
 };
+using TokenRmsSin = TokenRmsSinT<false>;
 
 struct NullChunk {
     __device__ void operator()(ChunkView) const {}
@@ -229,6 +277,13 @@ GFD_WARP_SPEC_KERNEL(ws_token_sum_kernel, TokenSum)
 GFD_WARP_SPEC_KERNEL_DB(ws_token_sum_kernel_db, TokenSum)
 GFD_WARP_SPEC_KERNEL(ws_rms_sin_kernel, TokenRmsSin)
 GFD_WARP_SPEC_KERNEL_DB(ws_rms_sin_kernel_db, TokenRmsSin)
+// The same for blocks of at most 9 waves (1 transfer + 2 slots of 4 chunks):
+// 3 waves per SIMD leave each ~168 registers, so the consumer holds a whole
+// 16 KiB token per wave.
+__global__ __launch_bounds__(576) __attribute__((amdgpu_waves_per_eu(1, 3))) void ws_rms_sin_kernel_db9(gfd::TiledQueue* tq, void* gpu_buffer, const void* cpu_base,
+                                                             TokenRmsSinT<true> compute_fn) {
+    gfd::warp_spec::_warp_spec_tile_loop_double_buffer(tq, gpu_buffer, cpu_base, compute_fn);
+}
 GFD_WARP_SPEC_KERNEL(ws_null_kernel, NullChunk)
 GFD_WARP_SPEC_KERNEL_DB(ws_null_kernel_db, NullChunk)
 GFD_SG_WARP_SPEC_KERNEL(sg_checksum_kernel, ListChecksum)
@@ -351,7 +406,10 @@ int warp_spec_run(const void* cpu_src, void* gpu_dst, uint32_t total_tokens, uin
                 hipLaunchKernelGGL(ws_token_sum_kernel, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
                                    p.cpu_base, TokenSum{out});
         } else if (consumer == kWsRmsSin) {
-            if (c.double_buffer)
+            if (c.double_buffer && p.block <= 576)
+                hipLaunchKernelGGL(ws_rms_sin_kernel_db9, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
+                                   p.cpu_base, TokenRmsSinT<true>{out});
+            else if (c.double_buffer)
                 hipLaunchKernelGGL(ws_rms_sin_kernel_db, dim3(p.grid), dim3(p.block), 0, nullptr, p.tq, p.gpu_buffer,
                                    p.cpu_base, TokenRmsSin{out});
             else
