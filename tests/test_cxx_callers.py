@@ -96,3 +96,20 @@ def test_exclusive_core_partition_on_synthetic_topologies(tmp_path):
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60, env=env)
     assert r.returncode == 0, r.stderr
     assert "PASSED" in r.stdout
+
+
+def test_sg_counter_layout_and_helpers(tmp_path):
+    """The SG session's device-counter layout and the helpers device code uses
+    to reach it without reading the host queue (tests/cxx/queue_layouts.cpp):
+    counters right after d_list_done[MAX_SG_LISTS], sg_list_done_words() back
+    to that array, sg_idle_ticks() in 100 MHz ticks with 0 meaning 30 s.
+    Header-only host code."""
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    exe = tmp_path / "queue_layouts"
+    r = subprocess.run(["make", "-s", "-B", "-C", os.path.join(ROOT, "tests", "cxx"), "OUT=%s" % tmp_path, str(exe)],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0, r.stderr
+    assert "PASSED" in r.stdout
